@@ -1,0 +1,12 @@
+"""HIP kernel entry points (ctypes over libcab_hip.so)."""
+
+from .coarsening import coarsen_qk_max_l2, coarsen_qk_max_l2_pytorch
+from .frc_kernel import (compute_block_frc, generate_block_index, generate_block_mask,
+                         keep_count, visualize_frc_statistics)
+from .sparse_attention import block_sparse_attention, kept_tile_flops
+
+__all__ = [
+    "coarsen_qk_max_l2", "coarsen_qk_max_l2_pytorch", "compute_block_frc", "generate_block_mask",
+    "generate_block_index", "keep_count", "visualize_frc_statistics", "block_sparse_attention",
+    "kept_tile_flops",
+]

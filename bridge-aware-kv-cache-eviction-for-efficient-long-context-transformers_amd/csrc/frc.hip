@@ -1,0 +1,515 @@
+// Coarse Forman-Ricci curvature (cab_block_frc).
+//
+// Pipeline per (b, h), Mp = M rounded up to 128:
+//  1. affinity_kernel<STATS>: A = qc kc^T * alpha on MFMA (64x64 tile per
+//     workgroup, one 32x32 tile per wave), per-tile min/max partials.
+//  2. minmax_finalize_kernel: per-(b,h) min/max from the partials.
+//  3. affinity_kernel<EMIT>: recomputes the A tile, normalises it, and writes
+//     Ahat as a bf16 hi/lo pair (hi = bf16(Ahat), lo = bf16(Ahat - hi)) in
+//     row-major X and transposed XT planes (zero outside M), the fp32 Ahat
+//     diagnostic and, for the augmented formula, row-sum partials.
+//  4. rowsum_finalize_kernel (augmented only).
+//  5. triangle_kernel: T = Ahat Ahat = X XT^T on MFMA as
+//     hi*hi + hi*lo + lo*hi (fp32 accumulate; the dropped lo*lo term is below
+//     2^-16 relative), 128x128 tile per workgroup, LDS double-buffered, with
+//     the FRC combination fused into the epilogue.
+// Algorithmic work: 2 M^2 D flops (affinity) + 2 M^3 flops (triangles).
+#include "cab_internal.h"
+
+namespace cab {
+namespace {
+
+constexpr int AT = 64;    // affinity tile
+constexpr int TT = 128;   // triangle tile
+constexpr int TK = 32;    // triangle k-step
+
+struct FrcLayout {
+  int64_t Mp, nta;  // padded M, affinity tiles per dim
+  size_t plane;     // bytes of one [BH][Mp][Mp] bf16 plane
+  size_t off_xhi, off_xlo, off_xthi, off_xtlo, off_mmpart, off_mm, off_rspart, off_rs, total;
+};
+
+FrcLayout frc_layout(int64_t BH, int64_t M) {
+  FrcLayout L;
+  L.Mp = round_up(M, TT);
+  L.nta = L.Mp / AT;
+  L.plane = static_cast<size_t>(BH) * L.Mp * L.Mp * 2;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    size_t at = o;
+    o += static_cast<size_t>(round_up(static_cast<int64_t>(bytes), 256));
+    return at;
+  };
+  L.off_xhi = take(L.plane);
+  L.off_xlo = take(L.plane);
+  L.off_xthi = take(L.plane);
+  L.off_xtlo = take(L.plane);
+  L.off_mmpart = take(static_cast<size_t>(BH) * L.nta * L.nta * 2 * sizeof(float));
+  L.off_mm = take(static_cast<size_t>(BH) * 2 * sizeof(float));
+  L.off_rspart = take(static_cast<size_t>(BH) * L.nta * L.Mp * sizeof(float));
+  L.off_rs = take(static_cast<size_t>(BH) * L.Mp * sizeof(float));
+  L.total = o;
+  return L;
+}
+
+struct AffArgs {
+  const void* qc;
+  const void* kc;
+  int64_t M, Mp, nta;
+  int32_t D;
+  float alpha;
+  int normalization;
+  float* mmpart;       // [BH][nta*nta][2]
+  const float* mm;     // [BH][2]
+  uint16_t* xhi;       // [BH][Mp][Mp]
+  uint16_t* xlo;
+  uint16_t* xthi;
+  uint16_t* xtlo;
+  float* affinity;     // [BH][M][M] or null
+  float* rspart;       // [BH][nta][Mp] or null
+};
+
+// One wave computes a 32x32 tile of qc kc^T (fp32 accumulate). Lane l owns
+// column l % 32 and rows 8 * (e / 4) + 4 * (l / 32) + e % 4 of acc[e].
+template <typename T>
+__device__ __forceinline__ f32x16 aff_tile(const void* qcv, const void* kcv, int64_t row0,
+                                           int64_t col0, int64_t M, int D, int lane) {
+  f32x16 acc = {};
+  const int64_t r = row0 + (lane & 31), c = col0 + (lane & 31);
+  const int half = lane >> 5;
+  if constexpr (sizeof(T) == 4) {
+    // fp32: 32x32x2 MFMA; lane half h holds k = 8q + 4h + s in step s.
+    const float* qa = static_cast<const float*>(qcv) + r * D;
+    const float* kb = static_cast<const float*>(kcv) + c * D;
+    const bool ra = r < M, cb = c < M;
+    for (int k0 = 0; k0 < D; k0 += 8) {
+      f32x4 av = {0.f, 0.f, 0.f, 0.f}, bv = {0.f, 0.f, 0.f, 0.f};
+      if (ra) av = *reinterpret_cast<const f32x4*>(qa + k0 + 4 * half);
+      if (cb) bv = *reinterpret_cast<const f32x4*>(kb + k0 + 4 * half);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[s], bv[s], acc, 0, 0, 0);
+    }
+  } else {
+    const uint16_t* qa = static_cast<const uint16_t*>(qcv) + r * D;
+    const uint16_t* kb = static_cast<const uint16_t*>(kcv) + c * D;
+    const bool ra = r < M, cb = c < M;
+    for (int k0 = 0; k0 < D; k0 += 16) {
+      u32x4 av = {0u, 0u, 0u, 0u}, bv = {0u, 0u, 0u, 0u};
+      const bool kin = k0 + 8 * half < D;  // D % 16 == 8: the upper half is past the row
+      if (ra && kin) av = *reinterpret_cast<const u32x4*>(qa + k0 + 8 * half);
+      if (cb && kin) bv = *reinterpret_cast<const u32x4*>(kb + k0 + 8 * half);
+      if constexpr (std::is_same<T, bf16_t>::value)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av),
+                                                      __builtin_bit_cast(bf16x8, bv), acc, 0, 0, 0);
+      else
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, av),
+                                                     __builtin_bit_cast(f16x8, bv), acc, 0, 0, 0);
+    }
+  }
+  return acc;
+}
+
+__device__ __forceinline__ float normalize_minmax(float a, float mn, float mx) {
+  return mx > mn ? (a - mn) / (mx - mn + 1e-8f) : a;
+}
+
+template <typename T, bool EMIT>
+__global__ __launch_bounds__(256) void affinity_kernel(AffArgs a) {
+  const int64_t bh = blockIdx.y;
+  const int64_t tile = blockIdx.x;
+  const int64_t ti = tile / a.nta, tj = tile - (tile / a.nta) * a.nta;
+  const int w = threadIdx.x >> 6, lane = lane_id();
+  const int wi = w >> 1, wj = w & 1;
+  const int64_t row0 = ti * AT + wi * 32, col0 = tj * AT + wj * 32;
+  const size_t esz = sizeof(T) == 4 ? 4 : 2;
+  const char* qcb = static_cast<const char*>(a.qc) + static_cast<size_t>(bh) * a.M * a.D * esz;
+  const char* kcb = static_cast<const char*>(a.kc) + static_cast<size_t>(bh) * a.M * a.D * esz;
+  f32x16 acc = aff_tile<T>(qcb, kcb, row0, col0, a.M, a.D, lane);
+
+  const int64_t j = col0 + (lane & 31);
+  const int half = lane >> 5;
+  if constexpr (!EMIT) {
+    float mn = INFINITY, mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int64_t i = row0 + 8 * (e >> 2) + 4 * half + (e & 3);
+      if (i < a.M && j < a.M) {
+        const float v = acc[e] * a.alpha;
+        mn = fminf(mn, v);
+        mx = fmaxf(mx, v);
+      }
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      mn = fminf(mn, shfl_xor_f32(mn, off));
+      mx = fmaxf(mx, shfl_xor_f32(mx, off));
+    }
+    __shared__ float red[4][2];
+    if (lane == 0) {
+      red[w][0] = mn;
+      red[w][1] = mx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float m0 = fminf(fminf(red[0][0], red[1][0]), fminf(red[2][0], red[3][0]));
+      float m1 = fmaxf(fmaxf(red[0][1], red[1][1]), fmaxf(red[2][1], red[3][1]));
+      float* p = a.mmpart + (bh * a.nta * a.nta + tile) * 2;
+      p[0] = m0;
+      p[1] = m1;
+    }
+  } else {
+    float mn = 0.f, mx = 0.f;
+    if (a.normalization == CAB_NORM_MINMAX) {
+      mn = a.mm[bh * 2 + 0];
+      mx = a.mm[bh * 2 + 1];
+    }
+    const size_t pbase = static_cast<size_t>(bh) * a.Mp * a.Mp;
+    float rowpart[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint32_t hi2[2], lo2[2];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int e = 4 * g + r;
+        const int64_t i = row0 + 8 * g + 4 * half + r;
+        float v = 0.f;
+        if (i < a.M && j < a.M) {
+          v = acc[e] * a.alpha;
+          if (a.normalization == CAB_NORM_MINMAX) v = normalize_minmax(v, mn, mx);
+          if (a.affinity) a.affinity[(static_cast<size_t>(bh) * a.M + i) * a.M + j] = v;
+        }
+        rowpart[e] = v;
+        const uint16_t h = f32_to_bf16(v);
+        const uint16_t l = f32_to_bf16(v - bf16_to_f32(h));
+        a.xhi[pbase + i * a.Mp + j] = h;
+        a.xlo[pbase + i * a.Mp + j] = l;
+        const uint32_t sh = (r & 1) * 16;
+        if ((r & 1) == 0) {
+          hi2[r >> 1] = h;
+          lo2[r >> 1] = l;
+        } else {
+          hi2[r >> 1] |= static_cast<uint32_t>(h) << sh;
+          lo2[r >> 1] |= static_cast<uint32_t>(l) << sh;
+        }
+      }
+      // Transposed planes: XT[j][i .. i+3] as one 8-byte store.
+      const int64_t i0 = row0 + 8 * g + 4 * half;
+      *reinterpret_cast<u32x2*>(a.xthi + pbase + j * a.Mp + i0) = u32x2{hi2[0], hi2[1]};
+      *reinterpret_cast<u32x2*>(a.xtlo + pbase + j * a.Mp + i0) = u32x2{lo2[0], lo2[1]};
+    }
+    if (a.rspart) {
+      // Row sums over the tile's 64 columns: 32 lanes per wave, 2 waves.
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float s = rowpart[e];
+#pragma unroll
+        for (int off = 1; off < 32; off <<= 1) s += shfl_xor_f32(s, off);
+        rowpart[e] = s;
+      }
+      __shared__ float rs[2][32];
+      if ((lane & 31) == 0 && wj == 1) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) rs[wi][8 * (e >> 2) + 4 * half + (e & 3)] = rowpart[e];
+      }
+      __syncthreads();
+      if ((lane & 31) == 0 && wj == 0) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int il = 8 * (e >> 2) + 4 * half + (e & 3);
+          const int64_t i = row0 + il;
+          a.rspart[(static_cast<size_t>(bh) * a.nta + tj) * a.Mp + i] = rowpart[e] + rs[wi][il];
+        }
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void minmax_finalize_kernel(const float* part, int64_t nparts,
+                                                              float* mm) {
+  const int64_t bh = blockIdx.x;
+  float mn = INFINITY, mx = -INFINITY;
+  for (int64_t p = threadIdx.x; p < nparts; p += 256) {
+    mn = fminf(mn, part[(bh * nparts + p) * 2 + 0]);
+    mx = fmaxf(mx, part[(bh * nparts + p) * 2 + 1]);
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    mn = fminf(mn, shfl_xor_f32(mn, off));
+    mx = fmaxf(mx, shfl_xor_f32(mx, off));
+  }
+  __shared__ float red[4][2];
+  const int w = threadIdx.x >> 6;
+  if (lane_id() == 0) {
+    red[w][0] = mn;
+    red[w][1] = mx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    mm[bh * 2 + 0] = fminf(fminf(red[0][0], red[1][0]), fminf(red[2][0], red[3][0]));
+    mm[bh * 2 + 1] = fmaxf(fmaxf(red[0][1], red[1][1]), fmaxf(red[2][1], red[3][1]));
+  }
+}
+
+__global__ __launch_bounds__(256) void rowsum_finalize_kernel(const float* part, int64_t nta,
+                                                              int64_t Mp, float* rs) {
+  const int64_t bh = blockIdx.y;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= Mp) return;
+  float s = 0.f;
+  for (int64_t t = 0; t < nta; ++t) s += part[(bh * nta + t) * Mp + i];
+  rs[bh * Mp + i] = s;
+}
+
+struct TriArgs {
+  const uint16_t* xhi;
+  const uint16_t* xlo;
+  const uint16_t* xthi;
+  const uint16_t* xtlo;
+  const float* rowsum;  // [BH][Mp] (augmented only)
+  float* frc;           // [BH][M][M]
+  float* tri;           // [BH][M][M] or null
+  int64_t M, Mp, nt, BH;
+  float lambda;
+  int formula;
+};
+
+// LDS operand tile in MFMA order: slot (kk, sub, lane) of 16 bytes holds the
+// 8 consecutive k values lane needs for a 32x32x16 MFMA, so every operand
+// read is one contiguous 1 KB wave access.
+constexpr int SLOTS = (TK / 16) * (TT / 32) * 64;  // 512 slots = 8 KB per plane
+
+__device__ __forceinline__ void tri_load(const uint16_t* plane, int64_t row0, int64_t k0, int64_t Mp,
+                                         u32x4 (&reg)[2]) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int cid = threadIdx.x + 256 * q;
+    const int row = cid >> 2, kc = cid & 3;
+    reg[q] = *reinterpret_cast<const u32x4*>(plane + (row0 + row) * Mp + k0 + 8 * kc);
+  }
+}
+
+__device__ __forceinline__ void tri_store(u32x4* lds, const u32x4 (&reg)[2]) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int cid = threadIdx.x + 256 * q;
+    const int row = cid >> 2, kc = cid & 3;
+    const int kk = kc >> 1, hf = kc & 1, sub = row >> 5;
+    lds[(kk * (TT / 32) + sub) * 64 + (row & 31) + 32 * hf] = reg[q];
+  }
+}
+
+__device__ __forceinline__ float frc_combine(int formula, float ahat, float t, float lambda, float si,
+                                             float sj) {
+  float f;
+  if (formula == CAB_FRC_ADDITIVE) {
+    f = ahat - lambda * t;
+    if (!isfinite(f)) f = 0.f;
+  } else if (formula == CAB_FRC_MULTIPLICATIVE) {
+    f = ahat * (1.0f / (1.0f + lambda * (t / (ahat + 1e-8f))));
+    if (!isfinite(f)) f = 0.f;
+  } else {
+    f = ahat > 0.f ? 4.0f * ahat - si - sj + 3.0f * t : 1000.0f;
+  }
+  return f;
+}
+
+__global__ __launch_bounds__(256) void triangle_kernel(TriArgs a) {
+  __shared__ u32x4 lds[2][4][SLOTS];  // [stage][Ahi, Alo, Bhi, Blo][slot] = 64 KB
+  const int64_t total = a.BH * a.nt * a.nt;
+  const int64_t logical = xcd_remap(blockIdx.x, total);
+  const int64_t bh = logical / (a.nt * a.nt);
+  const int64_t rem = logical - bh * a.nt * a.nt;
+  const int64_t ti = rem / a.nt, tj = rem - (rem / a.nt) * a.nt;
+  const size_t pbase = static_cast<size_t>(bh) * a.Mp * a.Mp;
+  const uint16_t* planes[4] = {a.xhi + pbase, a.xlo + pbase, a.xthi + pbase, a.xtlo + pbase};
+  const int64_t rows[4] = {ti * TT, ti * TT, tj * TT, tj * TT};
+
+  const int w = threadIdx.x >> 6, lane = lane_id();
+  const int wi = w >> 1, wj = w & 1;
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) acc[x][y] = f32x16{};
+
+  u32x4 reg[4][2];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) tri_load(planes[p], rows[p], 0, a.Mp, reg[p]);
+  const int nk = static_cast<int>(a.Mp / TK);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int st = kt & 1;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) tri_store(lds[st][p], reg[p]);
+    __syncthreads();
+    if (kt + 1 < nk) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) tri_load(planes[p], rows[p], static_cast<int64_t>(kt + 1) * TK, a.Mp, reg[p]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < TK / 16; ++kk) {
+      bf16x8 ah[2], al[2], bh8[2], bl[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int sa = (kk * (TT / 32) + 2 * wi + s) * 64 + lane;
+        const int sb = (kk * (TT / 32) + 2 * wj + s) * 64 + lane;
+        ah[s] = __builtin_bit_cast(bf16x8, lds[st][0][sa]);
+        al[s] = __builtin_bit_cast(bf16x8, lds[st][1][sa]);
+        bh8[s] = __builtin_bit_cast(bf16x8, lds[st][2][sb]);
+        bl[s] = __builtin_bit_cast(bf16x8, lds[st][3][sb]);
+      }
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) {
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[x], bh8[y], acc[x][y], 0, 0, 0);
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[x], bl[y], acc[x][y], 0, 0, 0);
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[x], bh8[y], acc[x][y], 0, 0, 0);
+        }
+    }
+  }
+
+  // Epilogue: F = combine(Ahat, T) for the wave's 64x64 block.
+  const int half = lane >> 5;
+  const size_t obase = static_cast<size_t>(bh) * a.M * a.M;
+#pragma unroll
+  for (int y = 0; y < 2; ++y) {
+    const int64_t j = tj * TT + wj * 64 + y * 32 + (lane & 31);
+    if (j >= a.M) continue;
+    const float sj = a.formula == CAB_FRC_AUGMENTED ? a.rowsum[bh * a.Mp + j] : 0.f;
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t i = ti * TT + wi * 64 + x * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+        if (i >= a.M) continue;
+        const float t = acc[x][y][e];
+        const float ahat = bf16_to_f32(a.xhi[pbase + i * a.Mp + j]) + bf16_to_f32(a.xlo[pbase + i * a.Mp + j]);
+        const float si = a.formula == CAB_FRC_AUGMENTED ? a.rowsum[bh * a.Mp + i] : 0.f;
+        a.frc[obase + i * a.M + j] = frc_combine(a.formula, ahat, t, a.lambda, si, sj);
+        if (a.tri) a.tri[obase + i * a.M + j] = t;
+      }
+    }
+  }
+}
+
+template <typename T>
+void launch_affinity(const AffArgs& a, int64_t BH, bool emit, hipStream_t s) {
+  dim3 grid(static_cast<unsigned>(a.nta * a.nta), static_cast<unsigned>(BH));
+  if (emit)
+    affinity_kernel<T, true><<<grid, 256, 0, s>>>(a);
+  else
+    affinity_kernel<T, false><<<grid, 256, 0, s>>>(a);
+}
+
+}  // namespace
+}  // namespace cab
+
+using namespace cab;
+
+extern "C" size_t cab_block_frc_workspace_bytes(int64_t B, int64_t H, int64_t M, int64_t D,
+                                                int normalization, int formula) {
+  (void)D;
+  (void)normalization;
+  (void)formula;
+  if (B <= 0 || H <= 0 || M <= 0) return 0;
+  return frc_layout(B * H, M).total;
+}
+
+extern "C" cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_t dtype,
+                                      int64_t B, int64_t H, int64_t M, int64_t D, float scale,
+                                      float temperature, float lambda_redundancy,
+                                      int normalization, int formula, float* frc,
+                                      float* affinity, float* triangles, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  clear_error();
+  CAB_REQUIRE(valid_dtype(dtype), CAB_EDTYPE, "cab_block_frc: unknown dtype %d", (int)dtype);
+  CAB_REQUIRE(B >= 0 && H >= 0 && M >= 0, CAB_ESHAPE, "cab_block_frc: negative size");
+  CAB_REQUIRE(D >= 8 && D <= 512 && D % 8 == 0, CAB_ESHAPE,
+              "cab_block_frc: head dim D=%lld must be a multiple of 8 in [8, 512]", (long long)D);
+  CAB_REQUIRE(normalization == CAB_NORM_NONE || normalization == CAB_NORM_MINMAX, CAB_EINVAL,
+              "cab_block_frc: unsupported normalization %d", normalization);
+  CAB_REQUIRE(formula == CAB_FRC_ADDITIVE || formula == CAB_FRC_MULTIPLICATIVE ||
+                  formula == CAB_FRC_AUGMENTED,
+              CAB_EINVAL, "cab_block_frc: unsupported formula %d", formula);
+  CAB_REQUIRE(temperature != 0.f && std::isfinite(temperature) && std::isfinite(scale) &&
+                  std::isfinite(lambda_redundancy),
+              CAB_EINVAL, "cab_block_frc: scale, temperature and lambda must be finite, temperature != 0");
+  if (B == 0 || H == 0 || M == 0) return CAB_OK;
+  CAB_REQUIRE(qc && kc && frc, CAB_EINVAL, "cab_block_frc: null tensor pointer");
+  CAB_REQUIRE(reinterpret_cast<uintptr_t>(qc) % 16 == 0 && reinterpret_cast<uintptr_t>(kc) % 16 == 0,
+              CAB_ESHAPE, "cab_block_frc: qc/kc not 16-byte aligned");
+  CAB_REQUIRE(M <= 32768, CAB_ESHAPE, "cab_block_frc: M=%lld exceeds 32768", (long long)M);
+  const int64_t BH = B * H;
+  CAB_REQUIRE(BH <= 65535, CAB_ESHAPE, "cab_block_frc: B*H=%lld exceeds 65535", (long long)BH);
+  const FrcLayout L = frc_layout(BH, M);
+  CAB_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, CAB_EWORKSPACE,
+              "cab_block_frc: workspace of %zu bytes given, %zu needed", workspace_bytes, L.total);
+  CAB_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, CAB_EWORKSPACE,
+              "cab_block_frc: workspace not 256-byte aligned");
+
+  char* ws = static_cast<char*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  AffArgs a;
+  a.qc = qc;
+  a.kc = kc;
+  a.M = M;
+  a.Mp = L.Mp;
+  a.nta = L.nta;
+  a.D = static_cast<int32_t>(D);
+  a.alpha = static_cast<float>(static_cast<double>(scale) / static_cast<double>(temperature));
+  a.normalization = normalization;
+  a.mmpart = reinterpret_cast<float*>(ws + L.off_mmpart);
+  a.mm = reinterpret_cast<const float*>(ws + L.off_mm);
+  a.xhi = reinterpret_cast<uint16_t*>(ws + L.off_xhi);
+  a.xlo = reinterpret_cast<uint16_t*>(ws + L.off_xlo);
+  a.xthi = reinterpret_cast<uint16_t*>(ws + L.off_xthi);
+  a.xtlo = reinterpret_cast<uint16_t*>(ws + L.off_xtlo);
+  a.affinity = affinity;
+  a.rspart = formula == CAB_FRC_AUGMENTED ? reinterpret_cast<float*>(ws + L.off_rspart) : nullptr;
+
+  if (normalization == CAB_NORM_MINMAX) {
+    switch (dtype) {
+      case CAB_BF16: launch_affinity<bf16_t>(a, BH, false, s); break;
+      case CAB_F16: launch_affinity<f16_t>(a, BH, false, s); break;
+      default: launch_affinity<float>(a, BH, false, s); break;
+    }
+    cab_status_t st = launch_status("cab_block_frc/affinity_stats");
+    if (st != CAB_OK) return st;
+    minmax_finalize_kernel<<<static_cast<unsigned>(BH), 256, 0, s>>>(
+        a.mmpart, L.nta * L.nta, reinterpret_cast<float*>(ws + L.off_mm));
+    st = launch_status("cab_block_frc/minmax_finalize");
+    if (st != CAB_OK) return st;
+  }
+  switch (dtype) {
+    case CAB_BF16: launch_affinity<bf16_t>(a, BH, true, s); break;
+    case CAB_F16: launch_affinity<f16_t>(a, BH, true, s); break;
+    default: launch_affinity<float>(a, BH, true, s); break;
+  }
+  cab_status_t st = launch_status("cab_block_frc/affinity_emit");
+  if (st != CAB_OK) return st;
+  if (formula == CAB_FRC_AUGMENTED) {
+    dim3 g(static_cast<unsigned>(ceil_div(L.Mp, 256)), static_cast<unsigned>(BH));
+    rowsum_finalize_kernel<<<g, 256, 0, s>>>(a.rspart, L.nta, L.Mp,
+                                             reinterpret_cast<float*>(ws + L.off_rs));
+    st = launch_status("cab_block_frc/rowsum_finalize");
+    if (st != CAB_OK) return st;
+  }
+  TriArgs t;
+  t.xhi = a.xhi;
+  t.xlo = a.xlo;
+  t.xthi = a.xthi;
+  t.xtlo = a.xtlo;
+  t.rowsum = reinterpret_cast<const float*>(ws + L.off_rs);
+  t.frc = frc;
+  t.tri = triangles;
+  t.M = M;
+  t.Mp = L.Mp;
+  t.nt = L.Mp / TT;
+  t.BH = BH;
+  t.lambda = lambda_redundancy;
+  t.formula = formula;
+  const int64_t blocks = BH * t.nt * t.nt;
+  CAB_REQUIRE(blocks <= INT32_MAX, CAB_ESHAPE, "cab_block_frc: problem too large");
+  triangle_kernel<<<static_cast<unsigned>(blocks), 256, 0, s>>>(t);
+  return launch_status("cab_block_frc/triangles");
+}

@@ -1,0 +1,159 @@
+/*
+ * cab_hip.h - C ABI of the MI355X (gfx950) CAB-Attention block-sparse path.
+ *
+ * libcab_hip.so exports the four stages of CAB-Attention's hot path:
+ * Max-L2 coarsening, the coarse Forman-Ricci curvature (FRC) stage, the
+ * per-row block-mask generator and the block-sparse attention executor.
+ *
+ * Conventions
+ *  - Every buffer is device memory owned by the caller. The library never
+ *    allocates, frees or synchronises; work is enqueued on `stream`
+ *    (a hipStream_t, NULL for the default stream).
+ *  - Tensors are [B, H, rows, cols]. Strides are in elements. The last
+ *    dimension must be contiguous (stride 1) and rows 16-byte aligned.
+ *  - All arguments are validated before any launch. A failed check returns
+ *    a non-zero status and leaves a message for cab_last_error(); nothing
+ *    is enqueued. A failed launch returns CAB_EHIP.
+ *  - Calls are re-entrant; cab_last_error() is per host thread.
+ *
+ * The reference implementations these entry points replace are Python
+ * functions that are imported by the reference's callers but are not in its
+ * tree (cab_attention/kernels/coarsening.py, cab_attention/kernels/frc_kernel.py,
+ * cab_attention/coarse_predictor.py, cab_attention/cab_attention.py); each
+ * declaration cites the call sites that fix its contract.
+ */
+#ifndef CAB_HIP_H
+#define CAB_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  CAB_OK = 0,
+  CAB_EINVAL = 1,     /* bad scalar argument or null pointer */
+  CAB_EDTYPE = 2,     /* unsupported element type */
+  CAB_ESHAPE = 3,     /* unsupported or inconsistent shape / stride / alignment */
+  CAB_EWORKSPACE = 4, /* workspace too small */
+  CAB_EHIP = 5        /* HIP runtime error at launch */
+} cab_status_t;
+
+typedef enum { CAB_F32 = 0, CAB_F16 = 1, CAB_BF16 = 2 } cab_dtype_t;
+
+/* Affinity normalisation (experiments/longbench_qa/config.py:466). */
+enum { CAB_NORM_NONE = 0, CAB_NORM_MINMAX = 1 };
+
+/* FRC combination (experiments/longbench_qa/config.py:465; test.ipynb:111-145). */
+enum { CAB_FRC_ADDITIVE = 0, CAB_FRC_MULTIPLICATIVE = 1, CAB_FRC_AUGMENTED = 2 };
+
+#define CAB_ABI_VERSION 1
+
+int cab_abi_version(void);
+const char* cab_last_error(void);
+
+/*
+ * Max-L2 coarsening of Q and K.
+ * Replaces coarsen_qk_max_l2 / coarsen_qk_max_l2_pytorch (q, k, block_size)
+ * -> (q_coarse, k_coarse) of cab_attention/kernels/coarsening.py (absent;
+ * contract: benchmarks/kernel_benchmark.py:23, :82-85;
+ * CAB_Attention_Colab.ipynb:109-141; README.md:30-33).
+ *
+ * For every (b, h, block m) of M = ceil(N / block_size) blocks, separately for
+ * q and k: idx = argmax over the block's tokens of the squared L2 norm, summed
+ * in float64 in a fixed order (chunks of 8 consecutive elements left to right,
+ * then the chunk sums pairwise); ties go to the lowest token, NaN counts as
+ * the largest. q_coarse[b,h,m,:] = q[b,h,idx,:] (bitwise copy).
+ * q, k: [B,H,N,D] of `dtype`, D % 8 == 0, D <= 512. qc, kc: contiguous
+ * [B,H,M,D] of `dtype`. q_idx, k_idx: contiguous int32 [B,H,M] (absolute token
+ * index), may be NULL.
+ */
+cab_status_t cab_coarsen_maxl2(const void* q, const void* k, cab_dtype_t dtype,
+                               int64_t B, int64_t H, int64_t N, int64_t D,
+                               const int64_t q_strides[4], const int64_t k_strides[4],
+                               int32_t block_size, void* qc, void* kc,
+                               int32_t* q_idx, int32_t* k_idx, void* stream);
+
+/*
+ * Workspace bytes cab_block_frc needs for these sizes.
+ */
+size_t cab_block_frc_workspace_bytes(int64_t B, int64_t H, int64_t M, int64_t D,
+                                     int normalization, int formula);
+
+/*
+ * Coarse FRC scores.
+ * Replaces compute_block_frc(q_coarse, k_coarse, temperature, lambda_redundancy,
+ * formula, normalization) -> (frc, affinity, redundancy) of
+ * cab_attention/kernels/frc_kernel.py (absent; contract:
+ * experiments/longbench_qa/methods.py:330-336; benchmarks/kernel_benchmark.py:149,
+ * :253; README.md:34-38).
+ *
+ * A = qc kc^T * scale / temperature (fp32 accumulate on MFMA);
+ * Ahat = minmax(A) per (b,h) ((A-min)/(max-min+1e-8), A unchanged if max==min)
+ * or A; T = Ahat @ Ahat (MFMA, bf16 hi/lo split, fp32 accumulate);
+ * additive: F = Ahat - lambda T; multiplicative: F = Ahat / (1 + lambda T /
+ * (Ahat + 1e-8)); non-finite F -> 0; augmented: 4 Ahat - S_i - S_j + 3 T on
+ * entries with Ahat > 0 and 1000 elsewhere (S = row sums of Ahat).
+ * qc, kc: contiguous [B,H,M,D] of `dtype`, D % 8 == 0, D <= 512.
+ * frc (required), affinity (= Ahat) and triangles (= T) (nullable):
+ * contiguous fp32 [B,H,M,M].
+ */
+cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_t dtype,
+                           int64_t B, int64_t H, int64_t M, int64_t D,
+                           float scale, float temperature, float lambda_redundancy,
+                           int normalization, int formula,
+                           float* frc, float* affinity, float* triangles,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Per-row block selection.
+ * Replaces generate_block_mask(frc, sparsity, select_high, keep_diagonal, causal)
+ * of cab_attention/kernels/frc_kernel.py (absent; contract:
+ * experiments/longbench_qa/methods.py:339-345; benchmarks/kernel_benchmark.py:197-205;
+ * README.md:40-42); the caller computes k = max(1, int(M * (1 - sparsity))).
+ *
+ * Row i keeps min(k, #candidates) blocks: candidates are j <= i when causal,
+ * all j otherwise; lowest scores first (highest when select_high), ties to the
+ * lower j, -0.0 == +0.0, NaN above +inf. keep_diagonal forces j = i in (it
+ * counts toward k).
+ * frc: contiguous fp32 [B,H,M,M]. kv_idx: int32 [B,H,M,k], ascending, tail
+ * filled with -1. kv_cnt: int32 [B,H,M]. dense_mask: uint8 0/1 [B,H,M,M] or NULL.
+ * M <= 8192.
+ */
+cab_status_t cab_block_topk(const float* frc, int64_t B, int64_t H, int64_t M, int32_t k,
+                            int select_high, int keep_diagonal, int causal,
+                            int32_t* kv_idx, int32_t* kv_cnt, uint8_t* dense_mask,
+                            void* stream);
+
+/*
+ * Block-sparse attention forward.
+ * Replaces the executor inside CABAttention.forward of
+ * cab_attention/cab_attention.py (absent; FlexAttention or the manual masked
+ * softmax of README.md:44-46, CAB_Attention_Colab.ipynb:376-382 and
+ * experiments/longbench_qa/methods.py:103-119).
+ *
+ * For query block i: out[t] = softmax_s(q_t . k_s * scale) v_s over the tokens
+ * s of the key blocks kv_idx[b,h,i,0:kv_cnt[b,h,i]] (entries outside [0, M)
+ * are skipped); when causal, keys s > t are dropped; a query with no key
+ * gets 0. fp32 online softmax, bf16/fp16 MFMA.
+ * q, k, v: [B,H,N,D] (strides), out: [B,H,N,D] (strides), dtype bf16 or fp16.
+ * block_size == 64, D == 128. kv_idx: contiguous int32 [B,H,M,kmax],
+ * kv_cnt: contiguous int32 [B,H,M]. lse: fp32 [B,H,N] natural-log
+ * log-sum-exp of the scaled scores (-inf for a query with no key), or NULL.
+ */
+cab_status_t cab_block_sparse_attn_fwd(const void* q, const void* k, const void* v,
+                                       cab_dtype_t dtype, int64_t B, int64_t H,
+                                       int64_t N, int64_t D,
+                                       const int64_t q_strides[4], const int64_t k_strides[4],
+                                       const int64_t v_strides[4], const int64_t o_strides[4],
+                                       int32_t block_size, const int32_t* kv_idx,
+                                       const int32_t* kv_cnt, int32_t kmax, float scale,
+                                       int causal, void* out, float* lse, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CAB_HIP_H */

@@ -1,0 +1,355 @@
+"""float64 numpy restatement of CAB-Attention's block-sparse hot path.
+
+TEST INFRASTRUCTURE ONLY: the checker for the HIP kernels and the CPU
+baseline in ``bench.py``. The shipped package never imports this module.
+
+The reference's hot-path modules (``cab_attention/coarse_predictor.py``,
+``cab_attention/cab_attention.py``, ``cab_attention/kernels/coarsening.py``,
+``cab_attention/kernels/frc_kernel.py``) are absent from the reference tree;
+their behaviour is fixed by their call sites, README prose and notebook
+cells, cited per function below. Inputs are float32 arrays whose values are
+exactly representable in the caller's dtype (bf16 and fp16 values are exact
+in float32), so a gather compares bit-for-bit after widening.
+
+Pinning of each function (tests/test_oracle.py):
+
+- ``canonical_sqnorm``: exact-arithmetic cases (small integers, where every
+  summation order is exact), a brute-force Python loop in the same order, and
+  zero-padding invariance for D not a power of two.
+- ``coarsen_max_l2``: brute-force loop on tiny inputs, planted maximum,
+  exact ties (lowest index wins), NaN handling, block_size 1 = identity,
+  block_size >= N = one global argmax, ragged last block.
+- ``compute_block_frc``: the reference's only stored known answer, the
+  bridge FRC of -85.71 (test.ipynb:19) reproduced through the full
+  coarse-FRC path, plus closed forms (identity, all-ones, rank-1 and
+  block-diagonal affinities), minmax range and temperature invariance.
+- ``generate_block_mask``: brute-force per-row sort, exact counts,
+  causal/diagonal rules, ascending index lists; the global-top-k variant
+  reproduces test.ipynb's stored retrieval booleans (test.ipynb:20-25).
+- ``sparse_attention``: dense masked attention in the reference's manual
+  form (CAB_Attention_Colab.ipynb:376-382), all-kept equals dense softmax
+  attention, constant scores give the mean of the kept V rows.
+- ``estimate_flops``: closed forms.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+__all__ = [
+    "canonical_sqnorm",
+    "coarsen_max_l2",
+    "num_blocks",
+    "keep_count",
+    "compute_block_frc",
+    "order_keys",
+    "generate_block_mask",
+    "expand_block_mask",
+    "effective_sparsity",
+    "sparse_attention",
+    "dense_masked_attention",
+    "global_topk_mask",
+    "estimate_flops",
+    "NORM_CHUNK",
+]
+
+# Elements summed sequentially per partial before the pairwise tree.
+NORM_CHUNK = 8
+
+
+def num_blocks(n: int, block_size: int) -> int:
+    """M = ceil(N / block_size) (CAB_Attention_Colab.ipynb:203; methods.py:446)."""
+    return (n + block_size - 1) // block_size
+
+
+def keep_count(m: int, sparsity: float) -> int:
+    """Blocks kept per row: max(1, int(M * (1 - sparsity))), clamped to M.
+
+    Same integer floor as the H2O block analogue (methods.py:252) and the
+    notebook's k_keep (CAB_Attention_Colab.ipynb:372), applied per row.
+    """
+    return min(m, max(1, int(m * (1.0 - sparsity))))
+
+
+# ---------------------------------------------------------------------------
+# Max-L2 coarsening
+# ---------------------------------------------------------------------------
+
+def canonical_sqnorm(x: np.ndarray) -> np.ndarray:
+    """Squared L2 norm over the last axis, in a fixed float64 order.
+
+    Each element is widened to float64 and squared (exact for fp32/bf16/fp16
+    inputs). The D squares are cut into chunks of 8 consecutive elements,
+    each chunk summed left to right; the chunk sums (zero-padded to a power
+    of two) are then added pairwise, adjacent pairs first. The order is part
+    of the specification so that argmax ties and near-ties resolve the same
+    way on every device.
+    """
+    d = x.shape[-1]
+    if d % NORM_CHUNK:
+        raise ValueError(f"head dim {d} is not a multiple of {NORM_CHUNK}")
+    sq = np.square(x.astype(np.float64))
+    sq = sq.reshape(*x.shape[:-1], d // NORM_CHUNK, NORM_CHUNK)
+    part = sq[..., 0].copy()
+    for e in range(1, NORM_CHUNK):
+        part = part + sq[..., e]
+    nchunk = d // NORM_CHUNK
+    width = 1 << (nchunk - 1).bit_length()
+    if width != nchunk:
+        pad = np.zeros((*part.shape[:-1], width - nchunk), dtype=np.float64)
+        part = np.concatenate([part, pad], axis=-1)
+    while part.shape[-1] > 1:
+        part = part[..., 0::2] + part[..., 1::2]
+    return part[..., 0]
+
+
+def coarsen_max_l2(x: np.ndarray, block_size: int):
+    """Max-L2 pooling: one representative token per block.
+
+    ``idx[b,h,m] = argmax_{t in block m} ||x[b,h,t]||`` (first index on
+    ties, NaN counts as the maximum, a ragged last block looks only at its
+    valid tokens) and ``xc[b,h,m] = x[b,h,idx]``, a bitwise copy.
+    Follows README.md:30-33 (Max-L2 pooling) and the coarsening contract of
+    benchmarks/kernel_benchmark.py:82-85 and CAB_Attention_Colab.ipynb:109-141.
+    Returns ``(xc, idx)``; idx is the absolute token index (int32).
+    """
+    b, h, n, d = x.shape
+    m = num_blocks(n, block_size)
+    norms = canonical_sqnorm(x)
+    padded = np.full((b, h, m * block_size), -np.inf, dtype=np.float64)
+    padded[..., :n] = norms
+    local = np.argmax(padded.reshape(b, h, m, block_size), axis=-1)
+    idx = (local + np.arange(m)[None, None, :] * block_size).astype(np.int32)
+    xc = np.take_along_axis(x, idx[..., None].astype(np.int64), axis=2)
+    return xc, idx
+
+
+# ---------------------------------------------------------------------------
+# Coarse FRC
+# ---------------------------------------------------------------------------
+
+def compute_block_frc(q_coarse, k_coarse, temperature: float = 1.0,
+                      lambda_redundancy: float = 0.5, formula: str = "additive",
+                      normalization: str = "minmax"):
+    """Block-level Forman-Ricci curvature, float64.
+
+    - Affinity ``A = Qc Kc^T / sqrt(D) / temperature``
+      (kernel_benchmark.py:135-137; CAB_Attention_Colab.ipynb:361; methods.py:332).
+    - Normalisation ``minmax``: ``(A - min) / (max - min + 1e-8)`` per (b, h),
+      left unchanged when max == min
+      (CAB_Attention_Colab.ipynb:249, cell 11 src l.75-81); ``none``: A;
+      ``softmax``: row softmax over key blocks (named in TODO.md:114, no
+      reference code).
+    - Redundancy ``T = Ahat @ Ahat`` (README.md:36, :240; kernel_benchmark.py:143-144).
+    - ``additive``: ``F = Ahat - lambda T`` (README.md:37, :236; Colab :367).
+      ``multiplicative``: ``F = Ahat / (1 + lambda T / (Ahat + 1e-8))``
+      (Colab :249, cell 11 src l.83-97). Non-finite F becomes 0 (cell 11
+      src l.100-104).
+      ``augmented``: test.ipynb's graph curvature
+      ``4 Ahat - S_i - S_j + 3 T`` on edges (Ahat > 0), 1000 elsewhere, with
+      ``S`` the row sums of Ahat (test.ipynb:111-145).
+    Returns ``(frc, affinity, redundancy)`` with affinity the normalised Ahat.
+    """
+    qc = np.asarray(q_coarse, dtype=np.float64)
+    kc = np.asarray(k_coarse, dtype=np.float64)
+    d = qc.shape[-1]
+    a = np.matmul(qc, np.swapaxes(kc, -1, -2)) * (1.0 / math.sqrt(d)) / temperature
+    if normalization == "minmax":
+        mn = a.min(axis=(-2, -1), keepdims=True)
+        mx = a.max(axis=(-2, -1), keepdims=True)
+        ahat = np.where(mx > mn, (a - mn) / (mx - mn + 1e-8), a)
+    elif normalization == "none":
+        ahat = a
+    elif normalization == "softmax":
+        z = a - a.max(axis=-1, keepdims=True)
+        e = np.exp(z)
+        ahat = e / e.sum(axis=-1, keepdims=True)
+    else:
+        raise ValueError(f"unknown normalization {normalization!r}")
+    t = np.matmul(ahat, ahat)
+    lam = float(lambda_redundancy)
+    with np.errstate(all="ignore"):
+        if formula == "additive":
+            f = ahat - lam * t
+            f = np.where(np.isfinite(f), f, 0.0)
+        elif formula == "multiplicative":
+            f = ahat * (1.0 / (1.0 + lam * (t / (ahat + 1e-8))))
+            f = np.where(np.isfinite(f), f, 0.0)
+        elif formula == "augmented":
+            s = ahat.sum(axis=-1)
+            f = 4.0 * ahat - s[..., :, None] - s[..., None, :] + 3.0 * t
+            f = np.where(ahat > 0, f, 1000.0)
+        else:
+            raise ValueError(f"unknown formula {formula!r}")
+    return f, ahat, t
+
+
+# ---------------------------------------------------------------------------
+# Block mask
+# ---------------------------------------------------------------------------
+
+def order_keys(values: np.ndarray, select_high: bool) -> np.ndarray:
+    """Unsigned keys whose ascending order is the selection order.
+
+    Ascending float order, -0.0 equal to +0.0, NaN above +inf; inverted when
+    ``select_high`` so that the highest value comes first. float32 input
+    gives uint32 keys, float64 gives uint64.
+    """
+    v = np.asarray(values)
+    if v.dtype == np.float32:
+        u, bits, nan = np.uint32, 32, np.uint32(0x7FC00000)
+    elif v.dtype == np.float64:
+        u, bits, nan = np.uint64, 64, np.uint64(0x7FF8000000000000)
+    else:
+        raise TypeError(f"unsupported dtype {v.dtype}")
+    v = np.where(v == 0, np.zeros((), v.dtype), v)  # -0 -> +0
+    raw = v.view(u).copy()
+    raw = np.where(np.isnan(v), nan, raw)
+    sign = u(1) << u(bits - 1)
+    allones = ~u(0)
+    key = np.where(raw & sign, raw ^ allones, raw | sign)
+    if select_high:
+        key = ~key
+    return key
+
+
+def generate_block_mask(frc, sparsity: float, select_high: bool = False,
+                        keep_diagonal: bool = True, causal: bool = False):
+    """Per-row block selection (README.md:40-42; methods.py:339-345).
+
+    Row i keeps ``k = keep_count(M, sparsity)`` blocks (``min(k, i+1)`` when
+    causal, candidates ``j <= i``) with the lowest FRC (highest when
+    ``select_high``), ties to the lower j. With ``keep_diagonal`` the block
+    ``j = i`` is always kept and counts toward k. Returns
+    ``(mask bool[B,H,M,M], kv_idx int32[B,H,M,k] ascending, -1 padded,
+    kv_cnt int32[B,H,M])``.
+    """
+    f = np.asarray(frc)
+    b, h, m, m2 = f.shape
+    assert m == m2
+    k = keep_count(m, sparsity)
+    keys = order_keys(f, select_high)
+    mask = np.zeros((b, h, m, m), dtype=bool)
+    kv_idx = np.full((b, h, m, k), -1, dtype=np.int32)
+    kv_cnt = np.zeros((b, h, m), dtype=np.int32)
+    for i in range(m):
+        ncand = i + 1 if causal else m
+        krow = min(k, ncand)
+        cand = np.arange(ncand)
+        rowkeys = keys[:, :, i, :ncand]
+        if keep_diagonal:
+            others = cand[cand != i]
+            order = np.argsort(rowkeys[..., others], axis=-1, kind="stable")
+            chosen = others[order[..., :krow - 1]]
+            diag = np.full((b, h, 1), i, dtype=chosen.dtype)
+            chosen = np.concatenate([diag, chosen], axis=-1)
+        else:
+            order = np.argsort(rowkeys, axis=-1, kind="stable")
+            chosen = order[..., :krow]
+        chosen = np.sort(chosen, axis=-1)
+        kv_idx[:, :, i, :krow] = chosen
+        kv_cnt[:, :, i] = krow
+        np.put_along_axis(mask[:, :, i, :], chosen, True, axis=-1)
+    return mask, kv_idx, kv_cnt
+
+
+def expand_block_mask(block_mask: np.ndarray, block_size: int, seq_len: int) -> np.ndarray:
+    """Token-level mask from a block mask (methods.py:103-119)."""
+    t = np.repeat(np.repeat(block_mask, block_size, axis=-2), block_size, axis=-1)
+    return t[..., :seq_len, :seq_len]
+
+
+def effective_sparsity(mask: np.ndarray) -> float:
+    """``1 - mean(mask)`` (methods.py:99-101)."""
+    return 1.0 - float(np.asarray(mask, dtype=np.float64).mean())
+
+
+def global_topk_mask(scores: np.ndarray, sparsity: float, largest: bool) -> np.ndarray:
+    """test.ipynb's whole-matrix top-k with threshold ties kept (test.ipynb:151-175)."""
+    flat = np.sort(np.asarray(scores).ravel())
+    k = max(1, int((1.0 - sparsity) * scores.size))
+    if largest:
+        return scores >= flat[::-1][k - 1]
+    return scores <= flat[k - 1]
+
+
+# ---------------------------------------------------------------------------
+# Block-sparse attention executor
+# ---------------------------------------------------------------------------
+
+def sparse_attention(q, k, v, kv_idx, kv_cnt, block_size: int, scale=None,
+                     causal: bool = False, heads=None, query_blocks=None) -> np.ndarray:
+    """Softmax attention over the kept key blocks of each query block.
+
+    ``O_t = sum_s softmax_s(q_t . k_s * scale) v_s`` over the tokens s of
+    the blocks listed in ``kv_idx[b,h,i,:kv_cnt]`` for the query block i
+    holding t; with ``causal`` keys s > t are dropped; a query with no key
+    gets 0 (the manual path's nan_to_num, CAB_Attention_Colab.ipynb:376-382;
+    methods.py:103-119). ``scale`` defaults to 1/sqrt(D). float64 output
+    ``[B,H,N,D]``; ``heads`` restricts the work to a list of (b, h) pairs and
+    ``query_blocks`` to a list of block rows (other outputs stay 0).
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    b, h, n, d = q.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    m = num_blocks(n, block_size)
+    out = np.zeros_like(q)
+    pairs = heads if heads is not None else [(bb, hh) for bb in range(b) for hh in range(h)]
+    rows = range(m) if query_blocks is None else query_blocks
+    for bb, hh in pairs:
+        for i in rows:
+            t0, t1 = i * block_size, min((i + 1) * block_size, n)
+            cnt = int(kv_cnt[bb, hh, i])
+            if cnt == 0:
+                continue
+            blocks = kv_idx[bb, hh, i, :cnt]
+            toks = np.concatenate([np.arange(j * block_size, min((j + 1) * block_size, n))
+                                   for j in blocks])
+            s = (q[bb, hh, t0:t1] @ k[bb, hh, toks].T) * scale
+            if causal:
+                s = np.where(toks[None, :] > np.arange(t0, t1)[:, None], -np.inf, s)
+            mx = s.max(axis=-1, keepdims=True)
+            valid = np.isfinite(mx)
+            e = np.exp(np.where(valid, s - np.where(valid, mx, 0.0), -np.inf))
+            den = e.sum(axis=-1, keepdims=True)
+            p = np.divide(e, den, out=np.zeros_like(e), where=den > 0)
+            out[bb, hh, t0:t1] = p @ v[bb, hh, toks]
+    return out
+
+
+def dense_masked_attention(q, k, v, token_mask, scale=None) -> np.ndarray:
+    """The reference's manual executor: ``masked_fill(-inf)``, softmax,
+    ``nan_to_num`` (CAB_Attention_Colab.ipynb:376-382), in float64."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    s = np.matmul(q, np.swapaxes(k, -1, -2)) * scale
+    s = np.where(token_mask, s, -np.inf)
+    with np.errstate(invalid="ignore"):
+        mx = s.max(axis=-1, keepdims=True)
+        e = np.exp(s - mx)
+        p = e / e.sum(axis=-1, keepdims=True)
+    p = np.nan_to_num(p, nan=0.0)
+    return np.matmul(p, v)
+
+
+def estimate_flops(n: int, d: int, block_size: int = 64) -> dict:
+    """Per-(b, h) operation counts of the predictor.
+
+    ``coarsening = 2 N D`` (norm squares and adds), ``matmul = 2 M^2 D``
+    (affinity), ``triangles = 2 M^3`` (T = A @ A), ``total`` their sum.
+    Contract: examples/demo_cab_attention.py:192-207,
+    benchmarks/benchmark_predictor.py:114-130.
+    """
+    m = num_blocks(n, block_size)
+    c = 2 * n * d
+    a = 2 * m * m * d
+    t = 2 * m * m * m
+    return {"M": m, "coarsening": c, "matmul": a, "triangles": t, "total": c + a + t}

@@ -1,0 +1,155 @@
+"""C-ABI boundary checks that need no GPU: the library loads, exports every
+symbol include/cab_hip.h declares, and rejects bad arguments with the
+documented status codes before anything is launched."""
+
+import ctypes
+import re
+import subprocess
+
+import pytest
+import torch
+
+from conftest import PKG, ROOT
+
+from cab_attention import _native as nat
+
+HEADER = ROOT / "include" / "cab_hip.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not nat.LIB_PATH.exists():
+        from cab_attention import _build
+        _build.build(verbose=False)
+    return nat.load()
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:[a-z_]+\s*\*?\s*)+\s*\**(cab_[a-z0-9_]+)\(", text, re.M)))
+
+
+def test_header_declares_the_hot_path():
+    syms = declared_symbols()
+    for name in ("cab_abi_version", "cab_last_error", "cab_coarsen_maxl2",
+                 "cab_block_frc_workspace_bytes", "cab_block_frc", "cab_block_topk",
+                 "cab_block_sparse_attn_fwd"):
+        assert name in syms
+    assert set(syms) == set(nat.SIGNATURES), "ctypes table and header disagree"
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(nat.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\sT\s(cab_\w+)$", out, re.M))
+    missing = set(declared_symbols()) - exported
+    assert not missing, f"not exported: {missing}"
+    assert lib.cab_abi_version() == nat.ABI_VERSION
+
+
+def _s4(*v):
+    return (ctypes.c_int64 * 4)(*v)
+
+
+FAKE = 0x7f0000000000  # 16-byte aligned address that is never dereferenced
+
+
+def test_coarsen_validation(lib):
+    st = _s4(8 * 64 * 128, 64 * 128, 128, 1)
+    call = lambda **kw: lib.cab_coarsen_maxl2(
+        kw.get("q", FAKE), FAKE, kw.get("dt", nat.CAB_BF16), kw.get("B", 1), 8, 64,
+        kw.get("D", 128), kw.get("qs", st), st, kw.get("bs", 64), FAKE, FAKE, None, None, None)
+    assert call(dt=7) == nat.CAB_EDTYPE
+    assert call(D=12) == nat.CAB_ESHAPE
+    assert call(D=1024) == nat.CAB_ESHAPE
+    assert call(bs=0) == nat.CAB_EINVAL
+    assert call(q=None) == nat.CAB_EINVAL
+    assert call(q=FAKE + 2) == nat.CAB_ESHAPE
+    assert call(qs=_s4(1, 1, 128, 2)) == nat.CAB_ESHAPE
+    assert call(qs=_s4(8 * 64 * 128, 64 * 128, 12, 1)) == nat.CAB_ESHAPE
+    assert b"stride" in lib.cab_last_error()
+    assert call(B=0) == nat.CAB_OK  # empty batch: nothing to launch
+
+
+def test_frc_validation(lib):
+    need = lib.cab_block_frc_workspace_bytes(2, 8, 2000, 128, 1, 0)
+    assert need >= 4 * 16 * 2048 * 2048 * 2
+    call = lambda **kw: lib.cab_block_frc(
+        FAKE, FAKE, kw.get("dt", nat.CAB_BF16), 1, 1, kw.get("M", 64), kw.get("D", 128), 0.1,
+        kw.get("temp", 1.0), 0.5, kw.get("norm", 1), kw.get("form", 0), FAKE, None, None,
+        kw.get("ws", FAKE), kw.get("wsb", 1 << 40), None)
+    assert call(dt=5) == nat.CAB_EDTYPE
+    assert call(D=100) == nat.CAB_ESHAPE
+    assert call(norm=2) == nat.CAB_EINVAL
+    assert call(form=3) == nat.CAB_EINVAL
+    assert call(temp=0.0) == nat.CAB_EINVAL
+    assert call(wsb=16) == nat.CAB_EWORKSPACE
+    assert call(ws=None) == nat.CAB_EWORKSPACE
+    assert call(ws=FAKE + 16) == nat.CAB_EWORKSPACE
+    assert call(M=40000) == nat.CAB_ESHAPE
+    assert call(M=0) == nat.CAB_OK
+
+
+def test_topk_validation(lib):
+    call = lambda **kw: lib.cab_block_topk(FAKE, 1, 1, kw.get("M", 64), kw.get("k", 3), 0, 1, 0,
+                                           FAKE, FAKE, None, None)
+    assert call(k=0) == nat.CAB_EINVAL
+    assert call(k=65) == nat.CAB_EINVAL
+    assert call(M=9000, k=3) == nat.CAB_ESHAPE
+    assert call(M=0) == nat.CAB_OK
+
+
+def test_attention_validation(lib):
+    st = _s4(8 * 64 * 128, 64 * 128, 128, 1)
+    call = lambda **kw: lib.cab_block_sparse_attn_fwd(
+        FAKE, FAKE, FAKE, kw.get("dt", nat.CAB_BF16), 1, 8, 64, kw.get("D", 128), st, st, st,
+        kw.get("os", st), kw.get("bs", 64), FAKE, FAKE, kw.get("kmax", 3), 0.088, 1, FAKE, None,
+        None)
+    assert call(dt=nat.CAB_F32 + 9) == nat.CAB_EDTYPE
+    assert call(D=96) == nat.CAB_ESHAPE
+    assert call(bs=48) == nat.CAB_ESHAPE
+    assert call(kmax=0) == nat.CAB_EINVAL
+    assert call(os=_s4(1, 1, 1, 3)) == nat.CAB_ESHAPE
+
+
+def test_python_layer_refuses_cpu_tensors(lib):
+    from cab_attention.kernels import (block_sparse_attention, coarsen_qk_max_l2,
+                                       compute_block_frc, generate_block_mask)
+    x = torch.randn(1, 1, 64, 128)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        coarsen_qk_max_l2(x, x, 64)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        compute_block_frc(x, x)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        generate_block_mask(torch.randn(1, 1, 4, 4), 0.5)
+    idx = torch.zeros(1, 1, 1, 1, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        block_sparse_attention(x, x, x, idx, idx[..., 0], 64)
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    code = (
+        "import sys; sys.path.insert(0, %r)\n"
+        "import torch\n"
+        "from cab_attention import _native as n\n"
+        "n.LIB_PATH = n.LIB_PATH.with_name('absent.so')\n"
+        "try:\n    n.load()\nexcept RuntimeError as e:\n    print('RAISED', e)\n" % str(PKG))
+    out = subprocess.run(["python", "-c", code], capture_output=True, text=True, timeout=300)
+    assert "RAISED" in out.stdout and "no fallback" in out.stdout
+
+
+def test_module_contract_on_host():
+    from cab_attention import CABAttention, CoarseCurvaturePredictor
+    p = CoarseCurvaturePredictor(block_size=64, sparsity=0.95, lambda_redundancy=0.5,
+                                 use_triton=False)
+    assert p.block_size == 64 and p.sparsity == 0.95
+    f = p.estimate_flops(131072, 128)
+    assert f["M"] == 2048 and f["triangles"] == 2 * 2048 ** 3
+    assert p.keep_per_row(128000) == 100
+    a = CABAttention(dim=512, num_heads=8, block_size=64, sparsity=0.95)
+    assert a.num_heads == 8 and a.predictor.block_size == 64
+    assert a.predictor.sparsity == 0.95
+    with pytest.raises(ValueError):
+        CABAttention(dim=500, num_heads=8)
+    with pytest.raises(ValueError):
+        CoarseCurvaturePredictor(sparsity=1.5)

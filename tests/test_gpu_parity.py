@@ -1,0 +1,352 @@
+"""Parity of the HIP kernels (through the C ABI, via the package's ctypes
+wrappers) against the CPU oracle on identical seeded inputs."""
+
+import json
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from oracle import cab_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}
+
+
+def seeded(shape, seed, dtype, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g, dtype=torch.float32) * scale).to(dtype)
+
+
+def np32(t):
+    return t.detach().float().cpu().numpy()
+
+
+def bits(t):
+    t = t.detach().cpu()
+    return t.view(torch.int16 if t.element_size() == 2 else torch.int32).numpy()
+
+
+# ---------------------------------------------------------------------------
+# Max-L2 coarsening: indices and gathered rows bit-exact
+# ---------------------------------------------------------------------------
+
+COARSEN_CASES = [
+    # B, H, N, D, bs
+    (2, 8, 1024, 128, 64),   # CAB_Attention_Colab.ipynb:127-141 correctness config
+    (1, 2, 1000, 128, 64),   # ragged last block
+    (1, 3, 333, 64, 16),
+    (1, 1, 96, 256, 32),
+    (1, 1, 40, 8, 1),        # block_size 1: identity
+    (1, 2, 50, 24, 128),     # block_size > N: one global argmax, D not a power of two
+]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp16", "fp32"])
+@pytest.mark.parametrize("case", COARSEN_CASES)
+def test_coarsen_bit_exact(cuda, dt, case):
+    from cab_attention.kernels import coarsen_qk_max_l2
+    B, H, N, D, bs = case
+    q = seeded((B, H, N, D), 1, DTYPES[dt])
+    k = seeded((B, H, N, D), 2, DTYPES[dt])
+    qc, kc, qi, ki = coarsen_qk_max_l2(q.to(cuda), k.to(cuda), bs, return_indices=True)
+    for x, xc, xi in ((q, qc, qi), (k, kc, ki)):
+        oc, oi = O.coarsen_max_l2(np32(x), bs)
+        np.testing.assert_array_equal(xi.cpu().numpy(), oi)
+        np.testing.assert_array_equal(bits(xc), bits(torch.from_numpy(oc).to(x.dtype)))
+
+
+def test_coarsen_ties_nan_and_strided_input(cuda):
+    from cab_attention.kernels import coarsen_qk_max_l2
+    base = seeded((1, 4, 256, 128), 3, torch.bfloat16)
+    base[0, 0, 10] = base[0, 0, 20] = 8.0          # exact tie in block 0
+    base[0, 1, 70] = float("nan")                  # NaN wins block 1
+    base[0, 1, 71] = 100.0
+    base[0, 2, 130] = base[0, 2, 131] = float("nan")
+    # q as a strided view of a [B, N, H, D] buffer, like CABAttention's qkv split
+    qbuf = base.transpose(1, 2).contiguous()
+    q = qbuf.to(cuda).transpose(1, 2)
+    assert not q.is_contiguous()
+    qc, _, qi, _ = coarsen_qk_max_l2(q, q, 64, return_indices=True)
+    _, oi = O.coarsen_max_l2(np32(base), 64)
+    np.testing.assert_array_equal(qi.cpu().numpy(), oi)
+    assert qi[0, 0, 0].item() == 10 and qi[0, 1, 1].item() == 70 and qi[0, 2, 2].item() == 130
+
+
+def test_coarsen_config3_full_size(cuda):
+    """B=2, H=8, N=128000: gather property on every head, oracle on one."""
+    from cab_attention.kernels import coarsen_qk_max_l2
+    B, H, N, D, bs = 2, 8, 128000, 128, 64
+    q = seeded((B, H, N, D), 1, torch.bfloat16).to(cuda)
+    k = seeded((B, H, N, D), 2, torch.bfloat16).to(cuda)
+    qc, kc, qi, ki = coarsen_qk_max_l2(q, k, bs, return_indices=True)
+    M = N // bs
+    blk = torch.arange(M, device=cuda).view(1, 1, M)
+    for x, xc, xi in ((q, qc, qi), (k, kc, ki)):
+        assert torch.equal((xi // bs).long(), blk.expand(B, H, M).long())
+        gathered = torch.gather(x, 2, xi.long()[..., None].expand(B, H, M, D))
+        assert torch.equal(gathered.view(torch.int16), xc.view(torch.int16))
+        _, oi = O.coarsen_max_l2(np32(x[1:2, 5:6]), bs)
+        np.testing.assert_array_equal(xi[1:2, 5:6].cpu().numpy(), oi)
+
+
+# ---------------------------------------------------------------------------
+# Coarse FRC
+# ---------------------------------------------------------------------------
+
+def assert_frc_close(got, want_f, ahat, tri, lam, rtol=1e-3):
+    """|dF| <= rtol * (|Ahat| + lambda (|Ahat| @ |Ahat|)) + 1e-6: relative to
+    the magnitude of the terms F and T are sums of (both can cancel to 0).
+    With minmax normalisation Ahat >= 0 and |Ahat| @ |Ahat| is T itself."""
+    err = np.abs(np32(got) - want_f)
+    absprod = np.matmul(np.abs(ahat), np.abs(ahat))
+    bound = rtol * (np.abs(ahat) + abs(lam) * absprod) + 1e-6
+    worst = (err / bound).max()
+    assert worst <= 1.0, f"FRC error {worst:.3g} x bound"
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp16", "fp32"])
+@pytest.mark.parametrize("M", [100, 257, 512])
+@pytest.mark.parametrize("formula,normalization", [("additive", "minmax"),
+                                                   ("multiplicative", "minmax"),
+                                                   ("additive", "none")])
+def test_frc_parity(cuda, dt, M, formula, normalization):
+    from cab_attention.kernels import compute_block_frc
+    B, H, D, lam = 1, 2, 128, 0.5
+    qc = seeded((B, H, M, D), 11, DTYPES[dt], scale=3.0)
+    kc = seeded((B, H, M, D), 12, DTYPES[dt], scale=3.0)
+    f, a, t = compute_block_frc(qc.to(cuda), kc.to(cuda), lambda_redundancy=lam, formula=formula,
+                                normalization=normalization)
+    of, oa, ot = O.compute_block_frc(np32(qc), np32(kc), lambda_redundancy=lam, formula=formula,
+                                     normalization=normalization)
+    np.testing.assert_allclose(np32(a), oa, rtol=1e-5, atol=1e-5 * max(1.0, np.abs(oa).max()))
+    np.testing.assert_allclose(np32(t), ot, rtol=1e-4, atol=1e-4 * np.abs(ot).max())
+    if formula == "multiplicative":
+        np.testing.assert_allclose(np32(f), of, rtol=1e-3, atol=1e-5)
+    else:
+        assert_frc_close(f, of, oa, ot, lam)
+
+
+def test_frc_no_diagnostics_matches(cuda):
+    from cab_attention.kernels import compute_block_frc
+    qc = seeded((2, 2, 300, 128), 13, torch.bfloat16).to(cuda)
+    kc = seeded((2, 2, 300, 128), 14, torch.bfloat16).to(cuda)
+    f1, a1, t1 = compute_block_frc(qc, kc)
+    f2, a2, t2 = compute_block_frc(qc, kc, diagnostics=False)
+    assert a2 is None and t2 is None
+    assert torch.equal(f1, f2)
+
+
+def test_bridge_known_answer_on_gpu(cuda):
+    """test.ipynb:19-25 through the GPU FRC path: adjacency as qc, identity
+    as kc (fp32, D=104), unit scale, no normalisation, augmented formula."""
+    from cab_attention.kernels import compute_block_frc
+    adj = np.load(GOLDEN / "bridge_sbm_adj.npy")
+    kat = json.loads((GOLDEN / "bridge_kat.json").read_text())
+    n, d = adj.shape[0], 104
+    qc = torch.zeros(1, 1, n, d)
+    qc[0, 0, :, :n] = torch.from_numpy(adj)
+    kc = torch.zeros(1, 1, n, d)
+    kc[0, 0, :, :n] = torch.eye(n)
+    f, a, t = compute_block_frc(qc.to(cuda), kc.to(cuda), temperature=1.0 / math.sqrt(d),
+                                formula="augmented", normalization="none")
+    f = np32(f)[0, 0]
+    u, v = kat["bridge"]
+    assert round(float(f[u, v]), 2) == kat["bridge_frc_2dp"]
+    for sp, cab in zip(kat["sparsities"], kat["cab_found"]):
+        assert bool(O.global_topk_mask(f, sp, largest=False)[u, v]) == cab
+    of, _, _ = O.compute_block_frc(qc.numpy(), kc.numpy(), temperature=1.0 / math.sqrt(d),
+                                   formula="augmented", normalization="none")
+    np.testing.assert_allclose(f, of[0, 0], rtol=1e-4, atol=2e-3)
+
+
+# ---------------------------------------------------------------------------
+# Block selection: bit-exact on identical scores
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("M", [1, 7, 64, 100, 513, 2000])
+@pytest.mark.parametrize("flags", [(False, True, False), (False, True, True), (True, True, True),
+                                   (False, False, False), (True, False, True)])
+def test_topk_bit_exact(cuda, M, flags):
+    from cab_attention.kernels import generate_block_index
+    select_high, keep_diag, causal = flags
+    g = torch.Generator().manual_seed(M)
+    f = torch.randint(-20, 20, (1, 3, M, M), generator=g).float()  # many exact ties
+    f[0, 1] = torch.randn(M, M, generator=g)
+    f[0, 2, :, ::3] = -0.0
+    for sp in (0.95, 0.5):
+        idx, cnt, mask = generate_block_index(f.to(cuda), sp, select_high=select_high,
+                                              keep_diagonal=keep_diag, causal=causal, dense=True)
+        omask, oidx, ocnt = O.generate_block_mask(f.numpy(), sp, select_high, keep_diag, causal)
+        np.testing.assert_array_equal(cnt.cpu().numpy(), ocnt)
+        np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
+        np.testing.assert_array_equal(mask.cpu().numpy(), omask)
+
+
+def test_topk_nan_inf(cuda):
+    from cab_attention.kernels import generate_block_index
+    f = torch.tensor([[[[0.0, float("nan"), -float("inf"), float("inf"), -0.0, 1.0]] * 6]])
+    for high in (False, True):
+        idx, cnt, mask = generate_block_index(f.to(cuda), 0.5, select_high=high,
+                                              keep_diagonal=False, dense=True)
+        omask, oidx, ocnt = O.generate_block_mask(f.numpy(), 0.5, high, False, False)
+        np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
+
+
+# ---------------------------------------------------------------------------
+# Predictor end to end: mask identical except near the row threshold
+# ---------------------------------------------------------------------------
+
+def assert_masks_agree(gpu_mask, gpu_frc, of, omask, k, keep_diag, causal, max_frac=0.01):
+    gm = gpu_mask.cpu().numpy()
+    diff = gm != omask
+    if not diff.any():
+        return
+    gf = np32(gpu_frc)
+    B, H, M, _ = of.shape
+    bad = 0
+    for b, h, i in {(b, h, i) for b, h, i, _ in zip(*np.nonzero(diff))}:
+        ncand = i + 1 if causal else M
+        cand = [j for j in range(ncand) if not (keep_diag and j == i)]
+        need = min(k, ncand) - (1 if keep_diag else 0)
+        vals = np.sort(of[b, h, i, cand])
+        theta = vals[need - 1] if need > 0 else None
+        delta = 8 * np.abs(gf[b, h, i] - of[b, h, i]).max() + 1e-7 * np.abs(of[b, h, i]).max()
+        for j in np.flatnonzero(diff[b, h, i]):
+            if theta is None or abs(of[b, h, i, j] - theta) > delta:
+                bad += 1
+    assert bad == 0, f"{bad} mask entries differ away from the threshold"
+    assert diff.mean() <= max_frac
+
+
+@pytest.mark.parametrize("cfg", [
+    # B, H, N, D, dtype, causal
+    (1, 8, 4096, 128, "fp32", False),   # BASELINE config 1 (CPU config), here on the GPU
+    (1, 4, 8192, 128, "bf16", False),
+    (1, 4, 8192, 128, "bf16", True),
+    (2, 2, 6000, 128, "fp16", False),   # ragged
+])
+def test_predictor_end_to_end(cuda, cfg):
+    from cab_attention import CoarseCurvaturePredictor
+    B, H, N, D, dt, causal = cfg
+    q = seeded((B, H, N, D), 1, DTYPES[dt])
+    k = seeded((B, H, N, D), 2, DTYPES[dt])
+    pred = CoarseCurvaturePredictor(block_size=64, sparsity=0.95, lambda_redundancy=0.5,
+                                    causal=causal)
+    mask, diag = pred(q.to(cuda), k.to(cuda), return_diagnostics=True)
+    qc, _ = O.coarsen_max_l2(np32(q), 64)
+    kc, _ = O.coarsen_max_l2(np32(k), 64)
+    of, oa, ot = O.compute_block_frc(qc, kc, lambda_redundancy=0.5)
+    omask, _, ocnt = O.generate_block_mask(of, 0.95, causal=causal)
+    M = (N + 63) // 64
+    assert tuple(mask.shape) == (B, H, M, M) and mask.dtype == torch.bool
+    assert diag["num_blocks"] == M
+    assert diag["effective_sparsity"] == pytest.approx(O.effective_sparsity(omask))
+    assert_frc_close(diag["frc_scores"], of, oa, ot, 0.5)
+    assert_masks_agree(mask, diag["frc_scores"], of, omask, O.keep_count(M, 0.95), True, causal)
+
+
+# ---------------------------------------------------------------------------
+# Block-sparse attention
+# ---------------------------------------------------------------------------
+
+ATOL = {"bf16": 2e-2, "fp16": 5e-3}
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp16"])
+@pytest.mark.parametrize("N,causal,sp", [(512, False, 0.5), (512, True, 0.5), (500, True, 0.7),
+                                         (1024, False, 0.9), (256, False, 0.0)])
+def test_attention_parity(cuda, dt, N, causal, sp):
+    from cab_attention.kernels import block_sparse_attention
+    B, H, D, bs = 1, 2, 128, 64
+    q = seeded((B, H, N, D), 1, DTYPES[dt])
+    k = seeded((B, H, N, D), 2, DTYPES[dt])
+    v = seeded((B, H, N, D), 3, DTYPES[dt])
+    M = (N + bs - 1) // bs
+    f = np.random.default_rng(N).standard_normal((B, H, M, M)).astype(np.float32)
+    _, idx, cnt = O.generate_block_mask(f, sp, causal=causal)
+    out, lse = block_sparse_attention(q.to(cuda), k.to(cuda), v.to(cuda),
+                                      torch.from_numpy(idx).to(cuda),
+                                      torch.from_numpy(cnt).to(cuda), bs, causal=causal,
+                                      return_lse=True)
+    want = O.sparse_attention(np32(q), np32(k), np32(v), idx, cnt, bs, causal=causal)
+    err = np.abs(np32(out) - want).max()
+    assert err <= ATOL[dt], f"max abs error {err}"
+    # lse against the oracle's softmax normaliser on one head
+    s = np32(q)[0, 0] @ np32(k)[0, 0].T / math.sqrt(D)
+    tok = O.expand_block_mask(O.generate_block_mask(f, sp, causal=causal)[0], bs, N)[0, 0]
+    if causal:
+        tok &= np.tril(np.ones((N, N), bool))
+    s = np.where(tok, s.astype(np.float64), -np.inf)
+    mx = s.max(1)
+    want_lse = mx + np.log(np.exp(s - mx[:, None]).sum(1))
+    np.testing.assert_allclose(np32(lse)[0, 0], want_lse, atol=1e-3, rtol=1e-4)
+
+
+def test_attention_empty_rows_and_bad_indices(cuda):
+    from cab_attention.kernels import block_sparse_attention
+    B, H, N, D, bs = 1, 1, 256, 128, 64
+    q, k, v = (seeded((B, H, N, D), s, torch.bfloat16) for s in (4, 5, 6))
+    idx = torch.tensor([[[[1, 3, -1], [0, 99, 2], [2, -5, 7], [0, 1, 2]]]], dtype=torch.int32)
+    cnt = torch.tensor([[[2, 3, 0, 5]]], dtype=torch.int32)  # row 2 empty, row 3 over kmax
+    out = block_sparse_attention(q.to(cuda), k.to(cuda), v.to(cuda), idx.to(cuda), cnt.to(cuda),
+                                 bs)
+    clean_idx = np.array([[[[1, 3, -1], [0, 2, -1], [0, 0, 0], [0, 1, 2]]]], np.int32)
+    clean_cnt = np.array([[[2, 2, 0, 3]]], np.int32)
+    want = O.sparse_attention(np32(q), np32(k), np32(v), clean_idx, clean_cnt, bs)
+    got = np32(out)
+    assert np.all(got[0, 0, 128:192] == 0)
+    assert np.abs(got - want).max() <= 2e-2
+
+
+def test_attention_strided_output_and_module(cuda):
+    """CABAttention: qkv views in, [B, N, H, D] output buffer, oracle on the
+    GPU's own block lists."""
+    from cab_attention import CABAttention
+    torch.manual_seed(0)
+    B, N, C, H = 1, 1024, 512, 4
+    attn = CABAttention(dim=C, num_heads=H, block_size=64, sparsity=0.8, causal=True)
+    attn = attn.to(cuda, torch.bfloat16)
+    x = seeded((B, N, C), 7, torch.bfloat16).to(cuda)
+    with torch.no_grad():
+        y, diag = attn(x, return_diagnostics=True)
+        qkv = attn.qkv(x).view(B, N, 3, H, C // H)
+        q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
+        idx, cnt = attn.predictor.predict_index(q, k)
+        o = O.sparse_attention(np32(q), np32(k), np32(v), idx.cpu().numpy(), cnt.cpu().numpy(),
+                               64, causal=True)
+        o = torch.from_numpy(o).float().to(cuda).transpose(1, 2).reshape(B, N, C)
+        want = attn.proj.float()(o)
+    assert y.shape == (B, N, C) and not torch.isnan(y).any()
+    assert 0.0 < diag["effective_sparsity"] < 1.0
+    assert (y.float() - want).abs().max().item() <= 5e-2
+
+
+def test_attention_config4_sampled(cuda):
+    """B=1, H=32, N=65536, causal, predictor mask: sampled query blocks of two
+    heads against the oracle."""
+    from cab_attention import CoarseCurvaturePredictor
+    from cab_attention.kernels import block_sparse_attention
+    B, H, N, D = 1, 32, 65536, 128
+    q = seeded((B, H, N, D), 1, torch.bfloat16).to(cuda)
+    k = seeded((B, H, N, D), 2, torch.bfloat16).to(cuda)
+    v = seeded((B, H, N, D), 3, torch.bfloat16).to(cuda)
+    pred = CoarseCurvaturePredictor(block_size=64, sparsity=0.95, causal=True)
+    idx, cnt = pred.predict_index(q, k)
+    M = N // 64
+    assert torch.all(cnt == torch.clamp(torch.arange(M, device=cuda) + 1, max=51))
+    out = block_sparse_attention(q, k, v, idx, cnt, 64, causal=True)
+    heads = [(0, 3), (0, 30)]
+    rows = [0, 1, 50, 51, 700, M - 1]
+    for (_, h) in heads:
+        qs, ks, vs = (np32(t[:, h:h + 1]) for t in (q, k, v))
+        want = O.sparse_attention(qs, ks, vs, idx[:, h:h + 1].cpu().numpy(),
+                                  cnt[:, h:h + 1].cpu().numpy(), 64, causal=True,
+                                  query_blocks=rows)
+        got = np32(out[:, h:h + 1])
+        for i in rows:
+            err = np.abs(got[0, 0, 64 * i:64 * i + 64] - want[0, 0, 64 * i:64 * i + 64]).max()
+            assert err <= 2e-2, f"head {h} block {i}: {err}"

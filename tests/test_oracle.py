@@ -1,0 +1,318 @@
+"""Pins the CPU oracle against the reference's stored answers, closed forms,
+invariants and brute force (CPU only)."""
+
+import json
+import math
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN
+from oracle import cab_oracle as O
+
+
+# ---------------------------------------------------------------------------
+# canonical squared norm
+# ---------------------------------------------------------------------------
+
+def test_sqnorm_exact_on_small_integers():
+    rng = np.random.default_rng(0)
+    x = rng.integers(-8, 9, size=(5, 7, 128)).astype(np.float32)
+    exact = (x.astype(np.int64) ** 2).sum(-1).astype(np.float64)
+    np.testing.assert_array_equal(O.canonical_sqnorm(x), exact)
+
+
+@pytest.mark.parametrize("d", [8, 64, 96, 128, 256])
+def test_sqnorm_within_ulps_of_exactly_rounded_sum(d):
+    rng = np.random.default_rng(d)
+    x = (rng.standard_normal((50, d)) * rng.uniform(0.1, 100, (50, 1))).astype(np.float32)
+    got = O.canonical_sqnorm(x)
+    for r in range(50):
+        ref = math.fsum(float(v) ** 2 for v in x[r].astype(np.float64))
+        assert abs(got[r] - ref) <= 8 * np.spacing(ref)
+
+
+def test_sqnorm_order_is_chunks_then_pairwise():
+    # 2^54 has a float64 spacing of 4, so a lone +1 added to it is lost.
+    # Chunk 0 = [2^27, 1 x 7] sums left to right to 2^54 (every 1 lost);
+    # chunk 1 = [1 x 8] sums to 8; the pairwise step gives 2^54 + 8. A plain
+    # left-to-right sum would give 2^54, the exactly rounded sum 2^54 + 16.
+    x = np.ones(16, dtype=np.float32)
+    x[0] = 2.0 ** 27
+    assert O.canonical_sqnorm(x[None])[0] == 2.0 ** 54 + 8
+    # Dropping the zero padding or reordering chunks must not change the value.
+    x24 = np.concatenate([x, np.ones(8, np.float32)])
+    x32 = np.concatenate([x24, np.zeros(8, np.float32)])
+    assert O.canonical_sqnorm(x24[None])[0] == O.canonical_sqnorm(x32[None])[0]
+
+
+def test_sqnorm_rejects_ragged_dim():
+    with pytest.raises(ValueError):
+        O.canonical_sqnorm(np.zeros((2, 12), np.float32))
+
+
+# ---------------------------------------------------------------------------
+# Max-L2 coarsening
+# ---------------------------------------------------------------------------
+
+def _brute_coarsen(x, bs):
+    b, h, n, d = x.shape
+    m = (n + bs - 1) // bs
+    idx = np.zeros((b, h, m), np.int32)
+    for bb in range(b):
+        for hh in range(h):
+            for mm in range(m):
+                best, bt = -1.0, -1
+                for t in range(mm * bs, min((mm + 1) * bs, n)):
+                    v = math.fsum(float(e) ** 2 for e in x[bb, hh, t].astype(np.float64))
+                    if v > best:
+                        best, bt = v, t
+                idx[bb, hh, mm] = bt
+    return idx
+
+
+@pytest.mark.parametrize("n,bs", [(64, 16), (100, 16), (37, 8)])
+def test_coarsen_matches_brute_force(n, bs):
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal((2, 3, n, 16)).astype(np.float32)
+    xc, idx = O.coarsen_max_l2(x, bs)
+    np.testing.assert_array_equal(idx, _brute_coarsen(x, bs))
+    for bb in range(2):
+        for hh in range(3):
+            np.testing.assert_array_equal(xc[bb, hh], x[bb, hh, idx[bb, hh]])
+    m = (n + bs - 1) // bs
+    blocks = idx // bs
+    np.testing.assert_array_equal(blocks, np.broadcast_to(np.arange(m), blocks.shape))
+
+
+def test_coarsen_planted_max_ties_and_nan():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((1, 1, 64, 8)).astype(np.float32)
+    x[0, 0, 5] *= 50                     # block 0: planted maximum
+    x[0, 0, 20] = x[0, 0, 30] = 40.0     # block 1: exact tie -> lowest
+    x[0, 0, 40] = np.nan                 # block 2: NaN wins
+    x[0, 0, 41] = 1e6
+    x[0, 0, 50] = x[0, 0, 60] = np.nan   # block 3: first NaN
+    _, idx = O.coarsen_max_l2(x, 16)
+    assert idx.ravel().tolist() == [5, 20, 40, 50]
+
+
+def test_coarsen_identity_and_global():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((1, 2, 10, 8)).astype(np.float32)
+    xc, idx = O.coarsen_max_l2(x, 1)
+    np.testing.assert_array_equal(xc, x)
+    np.testing.assert_array_equal(idx[0, 0], np.arange(10))
+    _, idx = O.coarsen_max_l2(x, 64)
+    norms = (x.astype(np.float64) ** 2).sum(-1)
+    np.testing.assert_array_equal(idx[..., 0], norms.argmax(-1))
+
+
+# ---------------------------------------------------------------------------
+# Coarse FRC
+# ---------------------------------------------------------------------------
+
+def _unit_scale_frc(qc, kc, **kw):
+    d = qc.shape[-1]
+    return O.compute_block_frc(qc, kc, temperature=1.0 / math.sqrt(d), **kw)
+
+
+def test_bridge_known_answer():
+    """test.ipynb:19-25: bridge FRC -85.71 and the retrieval flags."""
+    adj = np.load(GOLDEN / "bridge_sbm_adj.npy")
+    kat = json.loads((GOLDEN / "bridge_kat.json").read_text())
+    n, d = adj.shape[0], 104
+    qc = np.zeros((1, 1, n, d), np.float32)
+    qc[0, 0, :, :n] = adj
+    kc = np.zeros((1, 1, n, d), np.float32)
+    kc[0, 0, :, :n] = np.eye(n, dtype=np.float32)
+    f, ahat, t = _unit_scale_frc(qc, kc, normalization="none", formula="augmented")
+    np.testing.assert_allclose(ahat[0, 0], adj, rtol=1e-12)
+    u, v = kat["bridge"]
+    assert round(float(f[0, 0, u, v]), 2) == kat["bridge_frc_2dp"]
+    for sp, h2o, cab in zip(kat["sparsities"], kat["h2o_found"], kat["cab_found"]):
+        assert bool(O.global_topk_mask(adj, sp, largest=True)[u, v]) == h2o
+        assert bool(O.global_topk_mask(f[0, 0], sp, largest=False)[u, v]) == cab
+
+
+def test_frc_identity_affinity():
+    m, d, lam = 8, 16, 0.5
+    eye = np.zeros((1, 1, m, d), np.float32)
+    eye[0, 0, :, :m] = np.eye(m)
+    f, ahat, t = _unit_scale_frc(eye, eye, normalization="none", lambda_redundancy=lam)
+    np.testing.assert_allclose(t[0, 0], np.eye(m), atol=1e-12)
+    np.testing.assert_allclose(f[0, 0], (1 - lam) * np.eye(m), atol=1e-12)
+    fm, _, _ = _unit_scale_frc(eye, eye, normalization="none", formula="multiplicative",
+                               lambda_redundancy=lam)
+    np.testing.assert_allclose(np.diag(fm[0, 0]), 1 / (1 + lam / (1 + 1e-8)), rtol=1e-12)
+    assert np.all(fm[0, 0][~np.eye(m, dtype=bool)] == 0)
+
+
+def test_frc_all_ones_and_rank_one():
+    m, d, lam = 6, 8, 0.3
+    e1 = np.zeros((1, 1, m, d), np.float32)
+    e1[..., 0] = 1
+    f, ahat, t = _unit_scale_frc(e1, e1, normalization="none", lambda_redundancy=lam)
+    np.testing.assert_allclose(t[0, 0], m * np.ones((m, m)), rtol=1e-12)
+    np.testing.assert_allclose(f[0, 0], (1 - lam * m) * np.ones((m, m)), rtol=1e-12)
+    rng = np.random.default_rng(3)
+    uu = rng.uniform(0.5, 2, m).astype(np.float32)
+    vv = rng.uniform(0.5, 2, m).astype(np.float32)
+    qc = np.zeros((1, 1, m, d), np.float32)
+    kc = np.zeros((1, 1, m, d), np.float32)
+    qc[0, 0, :, 0] = uu
+    kc[0, 0, :, 0] = vv
+    _, _, t = _unit_scale_frc(qc, kc, normalization="none")
+    u64, v64 = uu.astype(np.float64), vv.astype(np.float64)
+    np.testing.assert_allclose(t[0, 0], np.dot(v64, u64) * np.outer(u64, v64), rtol=1e-12)
+
+
+def test_frc_block_diagonal_and_permutation():
+    rng = np.random.default_rng(4)
+    m, d = 12, 16
+    qc = np.zeros((1, 1, m, d), np.float32)
+    kc = np.zeros((1, 1, m, d), np.float32)
+    qc[0, 0, :6, :8] = rng.standard_normal((6, 8))
+    qc[0, 0, 6:, 8:] = rng.standard_normal((6, 8))
+    kc[0, 0, :6, :8] = rng.standard_normal((6, 8))
+    kc[0, 0, 6:, 8:] = rng.standard_normal((6, 8))
+    _, _, t = O.compute_block_frc(qc, kc, normalization="none")
+    assert np.all(t[0, 0, :6, 6:] == 0) and np.all(t[0, 0, 6:, :6] == 0)
+    f, _, _ = O.compute_block_frc(qc, kc)
+    perm = rng.permutation(m)
+    fp, _, _ = O.compute_block_frc(qc[:, :, perm], kc[:, :, perm])
+    np.testing.assert_allclose(fp[0, 0], f[0, 0][np.ix_(perm, perm)], rtol=1e-10, atol=1e-12)
+
+
+def test_frc_minmax_range_temperature_and_constant():
+    rng = np.random.default_rng(5)
+    qc = rng.standard_normal((2, 2, 20, 32)).astype(np.float32)
+    kc = rng.standard_normal((2, 2, 20, 32)).astype(np.float32)
+    f1, a1, _ = O.compute_block_frc(qc, kc, temperature=1.0)
+    f2, a2, _ = O.compute_block_frc(qc, kc, temperature=3.0)
+    assert a1.min() == 0 and np.all(a1.max(axis=(-2, -1)) <= 1) and np.all(a1.max(axis=(-2, -1)) > 1 - 1e-6)
+    np.testing.assert_allclose(a1, a2, atol=1e-7)
+    np.testing.assert_allclose(f1, f2, rtol=1e-6, atol=1e-6)
+    const = np.ones((1, 1, 4, 8), np.float32)
+    _, ac, _ = O.compute_block_frc(const, const)
+    np.testing.assert_allclose(ac, 8 / math.sqrt(8))  # max == min: left unnormalised
+
+
+# ---------------------------------------------------------------------------
+# Block mask
+# ---------------------------------------------------------------------------
+
+def _brute_mask(f, k, select_high, keep_diag, causal):
+    m = f.shape[0]
+    rows = []
+    for i in range(m):
+        cand = list(range(i + 1 if causal else m))
+        krow = min(k, len(cand))
+        chosen = [i] if keep_diag else []
+        rest = [j for j in cand if not (keep_diag and j == i)]
+        sign = -1.0 if select_high else 1.0
+        rest.sort(key=lambda j: (sign * (0.0 if f[i, j] == 0 else float(f[i, j])), j))
+        chosen += rest[:krow - len(chosen)]
+        rows.append(sorted(chosen))
+    return rows
+
+
+@pytest.mark.parametrize("select_high", [False, True])
+@pytest.mark.parametrize("keep_diag", [False, True])
+@pytest.mark.parametrize("causal", [False, True])
+def test_mask_matches_brute_force(select_high, keep_diag, causal):
+    rng = np.random.default_rng(6)
+    m = 24
+    f = rng.integers(-3, 4, size=(1, 2, m, m)).astype(np.float32)  # many ties
+    f[0, 0, 3, 4] = -0.0
+    mask, idx, cnt = O.generate_block_mask(f, 0.8, select_high, keep_diag, causal)
+    k = O.keep_count(m, 0.8)
+    for h in range(2):
+        want = _brute_mask(f[0, h], k, select_high, keep_diag, causal)
+        for i in range(m):
+            got = idx[0, h, i, :cnt[0, h, i]].tolist()
+            assert got == want[i]
+            assert np.all(idx[0, h, i, cnt[0, h, i]:] == -1)
+            assert sorted(np.flatnonzero(mask[0, h, i]).tolist()) == want[i]
+            assert cnt[0, h, i] == min(k, i + 1 if causal else m)
+            if keep_diag:
+                assert mask[0, h, i, i]
+            if causal:
+                assert not mask[0, h, i, i + 1:].any()
+    assert O.effective_sparsity(mask) == pytest.approx(1 - cnt.sum() / mask.size)
+
+
+def test_mask_nan_and_signed_zero_order():
+    f = np.array([[[[0.0, -0.0, np.nan, 1.0, -1.0]] * 5]], np.float32)
+    _, idx, cnt = O.generate_block_mask(f, 0.4, keep_diagonal=False)   # k = 3 per row
+    assert idx[0, 0, 0].tolist() == [0, 1, 4]        # -1, then the tied zeros
+    _, idx, _ = O.generate_block_mask(f, 0.8, select_high=True, keep_diagonal=False)  # k = 1
+    assert idx[0, 0, 0].tolist() == [2]              # NaN is the largest
+
+
+def test_keep_count_matches_survey_figures():
+    assert O.keep_count(2000, 0.95) == 100
+    assert O.keep_count(1024, 0.95) == 51
+    assert O.keep_count(64, 0.95) == 3
+    assert O.keep_count(512, 0.95) == 25
+    assert O.keep_count(2048, 0.99) == 20
+    assert O.keep_count(10, 1.0) == 1 and O.keep_count(10, 0.0) == 10
+
+
+# ---------------------------------------------------------------------------
+# Sparse attention
+# ---------------------------------------------------------------------------
+
+def _rand_qkv(rng, b, h, n, d):
+    return [rng.standard_normal((b, h, n, d)).astype(np.float32) for _ in range(3)]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("n", [64, 70])
+def test_sparse_attention_equals_dense_masked(causal, n):
+    rng = np.random.default_rng(7)
+    bs, d = 16, 8
+    q, k, v = _rand_qkv(rng, 1, 2, n, d)
+    m = (n + bs - 1) // bs
+    f = rng.standard_normal((1, 2, m, m)).astype(np.float32)
+    mask, idx, cnt = O.generate_block_mask(f, 0.5, causal=causal)
+    got = O.sparse_attention(q, k, v, idx, cnt, bs, causal=causal)
+    tok = O.expand_block_mask(mask, bs, n)
+    if causal:
+        tok = tok & np.tril(np.ones((n, n), bool))
+    want = O.dense_masked_attention(q, k, v, tok)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_sparse_attention_all_kept_is_softmax_attention():
+    rng = np.random.default_rng(8)
+    q, k, v = _rand_qkv(rng, 1, 1, 32, 8)
+    m = 4
+    idx = np.tile(np.arange(m, dtype=np.int32), (1, 1, m, 1))
+    cnt = np.full((1, 1, m), m, np.int32)
+    got = O.sparse_attention(q, k, v, idx, cnt, 8)
+    s = q[0, 0].astype(np.float64) @ k[0, 0].T.astype(np.float64) / math.sqrt(8)
+    p = np.exp(s - s.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    np.testing.assert_allclose(got[0, 0], p @ v[0, 0], rtol=1e-12, atol=1e-12)
+
+
+def test_sparse_attention_constant_scores_and_empty_rows():
+    rng = np.random.default_rng(9)
+    _, k, v = _rand_qkv(rng, 1, 1, 32, 8)
+    q = np.zeros_like(k)
+    idx = np.array([[[[1, 3], [0, -1], [2, -1], [0, 0]]]], np.int32)
+    cnt = np.array([[[2, 1, 0, 1]]], np.int32)
+    got = O.sparse_attention(q, k, v, idx, cnt, 8)
+    np.testing.assert_allclose(got[0, 0, :8], np.broadcast_to(
+        np.concatenate([v[0, 0, 8:16], v[0, 0, 24:32]]).astype(np.float64).mean(0), (8, 8)),
+        rtol=1e-12)
+    assert np.all(got[0, 0, 16:24] == 0)
+
+
+def test_estimate_flops_closed_form():
+    e = O.estimate_flops(131072, 128)
+    assert e["M"] == 2048
+    assert e["triangles"] == 2 * 2048 ** 3
+    assert e["matmul"] == 2 * 2048 ** 2 * 128
+    assert e["total"] == e["coarsening"] + e["matmul"] + e["triangles"]
