@@ -1,0 +1,269 @@
+"""Benchmark of the CAB-Attention hot path on one MI355X.
+
+Headline metric: "predictor ms @N=128k + block-sparse attn
+TFLOP/s, % of roofline".
+
+- ``value``: block-sparse attention throughput at BASELINE config 4
+  (CABAttention forward, causal, bf16, B=1 H=32 N=65536 D=128, block_size 64,
+  sparsity 0.95): useful kept-tile TFLOP per second of the executor kernel,
+  with Q/K/V and the predictor's block lists resident in HBM. One step = one
+  executor launch over the whole batch.
+- ``predictor``: latency of CoarseCurvaturePredictor.forward (coarsen + FRC +
+  mask, dense bool mask out) at config 3 (B=2 H=8 N=128000 D=128), plus the
+  per-stage times and the config-4 predictor + attention end-to-end time.
+- ``roofline``: the executor against the bf16 dense MFMA peak, from HIP events
+  on the launch stream; ``traffic`` from the committed rocprofv3 PMC summary.
+- ``cpu_baseline``: the float64 numpy oracle on a bounded sample of the same
+  workload, on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import re
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+PKG = ROOT / "bridge-aware-kv-cache-eviction-for-efficient-long-context-transformers_amd"
+for _p in (str(ROOT), str(PKG)):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "predictor ms @N=128k + block-sparse attn TFLOP/s, % of roofline"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+TRAFFIC_FILE = ROOT / "profiles" / "attn_fwd_config4_traffic.md"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def seeded_gpu(shape, seed, dtype, dev):
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return torch.randn(shape, generator=g, device=dev, dtype=torch.float32).to(dtype)
+
+
+def time_events(fn, iters: int):
+    """Average ms of ``fn`` over ``iters`` calls, from events on the current
+    stream (the stream every kernel of this package is launched on)."""
+    import torch
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(iters):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def read_traffic():
+    """HBM bytes per executor launch from the committed PMC summary, if any."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    m = re.search(r"hbm_bytes_per_launch:\s*([0-9.eE+]+)", TRAFFIC_FILE.read_text())
+    return float(m.group(1)) if m else None
+
+
+def blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+        n = [i.get("num_threads", 0) for i in threadpool_info() if i.get("user_api") == "blas"]
+        if n:
+            return max(n)
+    except Exception:
+        pass
+    return os.cpu_count() or 1
+
+
+def cpu_attention_baseline(q, k, v, idx, cnt, heads, rows, flops_fn):
+    """Oracle block-sparse attention on a sample of (head, query block) rows."""
+    import numpy as np
+    from oracle import cab_oracle as O
+    hs = list(heads)
+    qs = q[:, hs].float().cpu().numpy()
+    ks = k[:, hs].float().cpu().numpy()
+    vs = v[:, hs].float().cpu().numpy()
+    ii = idx[:, hs].cpu().numpy()
+    cc = cnt[:, hs].cpu().numpy()
+    t0 = time.perf_counter()
+    O.sparse_attention(qs, ks, vs, ii, cc, 64, causal=True, query_blocks=rows)
+    dt = time.perf_counter() - t0
+    sel = np.zeros_like(cc, dtype=bool)
+    sel[..., rows] = True
+    flops = flops_fn(ii, cc, sel)
+    return flops / dt / 1e12, dt, flops
+
+
+def cpu_predictor_baseline(q, k, block_size, sparsity):
+    """Oracle predictor on one (b, h) unit of config 3; returns seconds."""
+    from oracle import cab_oracle as O
+    q1 = q[:1, :1].float().cpu().numpy()
+    k1 = k[:1, :1].float().cpu().numpy()
+    t0 = time.perf_counter()
+    qc, _ = O.coarsen_max_l2(q1, block_size)
+    kc, _ = O.coarsen_max_l2(k1, block_size)
+    f, _, _ = O.compute_block_frc(qc, kc, lambda_redundancy=0.5)
+    O.generate_block_mask(f, sparsity)
+    return time.perf_counter() - t0
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--attn-only", action="store_true", help="skip the predictor section")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
+              "(the path shards per (b, h) with no collectives; see the design notes).",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from cab_attention import CoarseCurvaturePredictor
+    from cab_attention.kernels import (block_sparse_attention, coarsen_qk_max_l2,
+                                       compute_block_frc, generate_block_index, kept_tile_flops)
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    bs, D = 64, 128
+
+    # ---------------- config 4: predictor (causal) + block-sparse attention
+    B, H, N, sp = 1, 32, 65536, 0.95
+    log(f"config4 inputs B={B} H={H} N={N}")
+    q = seeded_gpu((B, H, N, D), 1, torch.bfloat16, dev)
+    k = seeded_gpu((B, H, N, D), 2, torch.bfloat16, dev)
+    v = seeded_gpu((B, H, N, D), 3, torch.bfloat16, dev)
+    pred4 = CoarseCurvaturePredictor(block_size=bs, sparsity=sp, lambda_redundancy=0.5,
+                                     causal=True)
+    idx, cnt = pred4.predict_index(q, k)
+    torch.cuda.synchronize()
+    flops = kept_tile_flops(idx, cnt, bs, D, N, causal=True)
+    out = torch.empty_like(q)
+    attn = lambda: block_sparse_attention(q, k, v, idx, cnt, bs, causal=True, out=out)
+    for _ in range(args.warmup):
+        attn()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} executor steps ({flops / 1e12:.3f} TFLOP useful each)")
+    attn_ms = time_events(attn, args.steps)
+    attn_tflops = flops / (attn_ms * 1e-3) / 1e12
+    e2e = lambda: block_sparse_attention(q, k, v, *pred4.predict_index(q, k), bs, causal=True,
+                                         out=out)
+    e2e()
+    e2e_ms = time_events(e2e, max(3, args.steps // 4))
+    log(f"attention {attn_ms:.3f} ms = {attn_tflops:.1f} TFLOP/s; e2e {e2e_ms:.3f} ms")
+
+    result_pred = None
+    if not args.attn_only:
+        # ---------------- config 3: predictor latency at N = 128k
+        B3, H3, N3 = 2, 8, 128000
+        q3 = seeded_gpu((B3, H3, N3, D), 1, torch.bfloat16, dev)
+        k3 = seeded_gpu((B3, H3, N3, D), 2, torch.bfloat16, dev)
+        pred3 = CoarseCurvaturePredictor(block_size=bs, sparsity=sp, lambda_redundancy=0.5)
+        for _ in range(args.warmup):
+            pred3(q3, k3)
+        iters = max(5, args.steps)
+        log("timing config3 predictor")
+        pred_ms = time_events(lambda: pred3(q3, k3), iters)
+        qc, kc = coarsen_qk_max_l2(q3, k3, bs)
+        f3, _, _ = compute_block_frc(qc, kc, diagnostics=False)
+        st_coarsen = time_events(lambda: coarsen_qk_max_l2(q3, k3, bs), iters)
+        st_frc = time_events(lambda: compute_block_frc(qc, kc, diagnostics=False), iters)
+        st_mask = time_events(lambda: generate_block_index(f3, sp, dense=True), iters)
+        M3 = (N3 + bs - 1) // bs
+        k3keep = pred3.keep_per_row(N3)
+        coarsen_bytes = 2 * B3 * H3 * N3 * D * 2 + 2 * B3 * H3 * M3 * (D * 2 + 4)
+        tri_flops = 2 * M3 ** 3 * B3 * H3
+        aff_flops = 2 * M3 ** 2 * D * B3 * H3
+        mask_bytes = B3 * H3 * M3 * (M3 * 4 + k3keep * 4 + 4 + M3)
+        result_pred = {
+            "config": "config3: CoarseCurvaturePredictor B=2 H=8 N=128000 D=128 bs=64 "
+                      "s=0.95 lambda=0.5 bf16, dense bool mask out",
+            "ms": round(pred_ms, 4),
+            "target_ms": 5.0,
+            "stages_ms": {"coarsen": round(st_coarsen, 4), "frc": round(st_frc, 4),
+                          "mask": round(st_mask, 4)},
+            "coarsen_GBps": round(coarsen_bytes / (st_coarsen * 1e-3) / 1e9, 1),
+            "frc_TFLOPs": round((tri_flops + aff_flops) / (st_frc * 1e-3) / 1e12, 1),
+            "mask_GBps": round(mask_bytes / (st_mask * 1e-3) / 1e9, 1),
+            "config4_predictor_plus_attention_ms": round(e2e_ms, 4),
+        }
+        log(f"predictor {pred_ms:.3f} ms (coarsen {st_coarsen:.3f}, frc {st_frc:.3f}, "
+            f"mask {st_mask:.3f})")
+        if not args.no_cpu:
+            cpu_s = cpu_predictor_baseline(q3, k3, bs, sp)
+            result_pred["cpu_ms_estimate"] = round(cpu_s * 1e3 * B3 * H3, 1)
+            result_pred["cpu_sample"] = "oracle on 1 of 16 (b,h) units, scaled x16"
+        del q3, k3, qc, kc, f3
+        torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu:
+        M = N // bs
+        rows = list(range(M - 48, M))  # full-length causal rows
+        heads = [0, 17]
+
+        def sample_flops(ii, cc, sel):
+            tiles = 0
+            diag = 0
+            for b in range(ii.shape[0]):
+                for h in range(ii.shape[1]):
+                    for i in np.flatnonzero(sel[b, h]):
+                        js = ii[b, h, i, :cc[b, h, i]]
+                        tiles += len(js)
+                        diag += int((js == i).sum())
+            return (tiles - diag) * 4 * bs * bs * D + diag * 2 * bs * (bs + 1) * D
+
+        log("cpu baseline: oracle attention sample")
+        tfl, secs, fl = cpu_attention_baseline(q, k, v, idx, cnt, heads, rows, sample_flops)
+        cpu = {"value": round(tfl, 6), "unit": "TFLOP/s", "cores": blas_threads(),
+               "kind": "port",
+               "sample": f"float64 numpy oracle, heads {heads} x query blocks {rows[0]}-{rows[-1]} "
+                         f"of config 4 ({fl / 1e9:.1f} GFLOP useful in {secs:.1f} s)"}
+
+    achieved = attn_tflops
+    traffic = read_traffic()
+    line = {
+        "metric": METRIC,
+        "value": round(attn_tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(attn_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "config4: CABAttention causal block-sparse executor, B=1 H=32 "
+                               "N=65536 D=128 bs=64 sparsity=0.95, predictor block lists",
+                   "B": B, "H": H, "N": N, "D": D, "block_size": bs, "sparsity": sp,
+                   "causal": True, "useful_tflop_per_step": round(flops / 1e12, 4)},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic},
+        "cpu_baseline": cpu,
+        "predictor": result_pred,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

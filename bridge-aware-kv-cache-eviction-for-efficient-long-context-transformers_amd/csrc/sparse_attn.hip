@@ -58,29 +58,30 @@ __device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f3
 
 template <bool BF16>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  if constexpr (BF16)
-    return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
-  else
+  if constexpr (BF16) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};  // v_cvt_pk_bf16_f32, RNE
+    return __builtin_bit_cast(uint32_t, v);
+  } else {
     return static_cast<uint32_t>(f32_to_f16(lo)) | (static_cast<uint32_t>(f32_to_f16(hi)) << 16);
+  }
 }
 
 // Global -> register staging of one key block (rows beyond N read as 0).
 struct KVRegs {
-  u32x4 k[4];  // K chunk (key = cid / 16, d = 8 (cid % 16)), cid = tid + 256 r
+  u32x4 k[4];  // K[16 w + l % 16][32 r + 8 (l / 16) .. +8] for wave w, lane l, r = 0..3
   u32x4 v[4];  // V rows 4 kq + r at d = 8 c, kq = tid / 16, c = tid % 16
 };
 
 __device__ __forceinline__ void load_kv(const AttnArgs& a, const uint16_t* kb, const uint16_t* vb,
                                         int64_t j, KVRegs& R) {
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
   const int64_t tok0 = j * BS;
+  const int64_t tk = tok0 + 16 * w + (l & 15);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int cid = tid + 256 * r;
-    const int key = cid >> 4, c = cid & 15;
-    const int64_t t = tok0 + key;
-    R.k[r] = t < a.N ? *reinterpret_cast<const u32x4*>(kb + t * a.ks[2] + 8 * c) : u32x4{0u, 0u, 0u, 0u};
-  }
+  for (int r = 0; r < 4; ++r)
+    R.k[r] = tk < a.N ? *reinterpret_cast<const u32x4*>(kb + tk * a.ks[2] + 32 * r + 8 * (l >> 4))
+                      : u32x4{0u, 0u, 0u, 0u};
   const int kq = tid >> 4, c = tid & 15;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -90,18 +91,17 @@ __device__ __forceinline__ void load_kv(const AttnArgs& a, const uint16_t* kb, c
 }
 
 // Register -> LDS in MFMA operand order.
-//  K slot (tt, ds, lane'): keys 16 tt + lane' % 16, d = 32 ds + 8 (lane' / 16) .. +8.
+//  K slot (tt, ds, lane'): key 16 tt + lane' % 16, d = 32 ds + 8 (lane' / 16) .. +8. Wave w
+//    writes block tt = w, so every store is one linear 1 KB wave access.
 //  V^T slot (dt, s, lane'): d = 16 dt + lane' % 16; 8 bytes per half:
 //    half 0 = keys 32 s + 4 g + 0..3, half 1 = keys 32 s + 16 + 4 g + 0..3, g = lane' / 16.
+//    Stored at lane' ^ dt within its 64-slot row: the transposing 8-byte stores of one
+//    wave then spread over 16 bank groups instead of 2, and a row read stays a
+//    permutation of one contiguous 1 KB block (conflict-free).
 __device__ __forceinline__ void store_kv(u32x4* ks, u32x4* vts, const KVRegs& R) {
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int cid = tid + 256 * r;
-    const int key = cid >> 4, c = cid & 15;
-    const int tt = key >> 4, ds = c >> 2, g = c & 3;
-    ks[(tt * 4 + ds) * 64 + (key & 15) + 16 * g] = R.k[r];
-  }
+  for (int r = 0; r < 4; ++r) ks[(w * 4 + r) * 64 + l] = R.k[r];
   const int kq = tid >> 4, c = tid & 15;
   const int key0 = 4 * kq;
   const int s = key0 >> 5, rem = key0 & 31;
@@ -109,17 +109,17 @@ __device__ __forceinline__ void store_kv(u32x4* ks, u32x4* vts, const KVRegs& R)
   char* vbytes = reinterpret_cast<char*>(vts);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const int w = e >> 1;
+    const int wd = e >> 1;
     uint32_t x0, x1;
     if ((e & 1) == 0) {
-      x0 = (R.v[0][w] & 0xffffu) | (R.v[1][w] << 16);
-      x1 = (R.v[2][w] & 0xffffu) | (R.v[3][w] << 16);
+      x0 = (R.v[0][wd] & 0xffffu) | (R.v[1][wd] << 16);
+      x1 = (R.v[2][wd] & 0xffffu) | (R.v[3][wd] << 16);
     } else {
-      x0 = (R.v[0][w] >> 16) | (R.v[1][w] & 0xffff0000u);
-      x1 = (R.v[2][w] >> 16) | (R.v[3][w] & 0xffff0000u);
+      x0 = (R.v[0][wd] >> 16) | (R.v[1][wd] & 0xffff0000u);
+      x1 = (R.v[2][wd] >> 16) | (R.v[3][wd] & 0xffff0000u);
     }
     const int d = 8 * c + e;
-    const int dt = d >> 4, lanep = (d & 15) + 16 * g;
+    const int dt = d >> 4, lanep = ((d & 15) + 16 * g) ^ dt;
     *reinterpret_cast<u32x2*>(vbytes + ((dt * 2 + s) * 64 + lanep) * 16 + hf * 8) = u32x2{x0, x1};
   }
 }
@@ -158,26 +158,14 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) acc_o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
-
-  KVRegs R;
-  int64_t jn = cnt > 0 ? list[0] : -1;
-  if (jn >= 0 && jn < a.M) load_kv(a, kb, vb, jn, R);
   int stage = 0;
-  for (int n = 0; n < cnt; ++n) {
-    const int64_t j = jn;
-    const bool valid = j >= 0 && j < a.M;  // uniform over the workgroup
-    if (valid) {
-      store_kv(lds[stage][0], lds[stage][1], R);
-      __syncthreads();
-    }
-    jn = n + 1 < cnt ? list[n + 1] : -1;
-    if (jn >= 0 && jn < a.M) load_kv(a, kb, vb, jn, R);
-    if (!valid) continue;
 
-    const u32x4* ks = lds[stage][0];
-    const u32x4* vts = lds[stage][1];
-    stage ^= 1;
+  auto fetch = [&](int n, KVRegs& R) {
+    const int64_t j = list[n];
+    if (j >= 0 && j < a.M) load_kv(a, kb, vb, j, R);
+  };
 
+  auto compute = [&](int64_t j, const u32x4* ks, const u32x4* vts) {
     // S^T[key][query] for the block's 64 keys.
     f32x4 sc[4];
 #pragma unroll
@@ -193,13 +181,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float s = sc[tt][r] * a.scale_log2;
+        float sv = sc[tt][r] * a.scale_log2;
         if (need_mask) {
           const int64_t ktok = j * BS + 16 * tt + 4 * g + r;
-          if (ktok >= a.N || (a.causal && ktok > qtok)) s = -INFINITY;
+          if (ktok >= a.N || (a.causal && ktok > qtok)) sv = -INFINITY;
         }
-        sc[tt][r] = s;
-        mx = fmaxf(mx, s);
+        sc[tt][r] = sv;
+        mx = fmaxf(mx, sv);
       }
     mx = fmaxf(mx, shfl_xor_f32(mx, 16));
     mx = fmaxf(mx, shfl_xor_f32(mx, 32));
@@ -232,7 +220,33 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-      for (int s = 0; s < 2; ++s) acc_o[dt] = mfma16<BF16>(vts[(dt * 2 + s) * 64 + lane], pb[s], acc_o[dt]);
+      for (int s = 0; s < 2; ++s)
+        acc_o[dt] = mfma16<BF16>(vts[(dt * 2 + s) * 64 + (lane ^ dt)], pb[s], acc_o[dt]);
+  };
+
+  // Two blocks in flight in registers: block n is stored to LDS while block
+  // n + 1 is still arriving; block n + 2 is requested as soon as n's
+  // registers are free.
+  auto step = [&](int n, KVRegs& R) {
+    const int64_t j = list[n];
+    const bool valid = j >= 0 && j < a.M;  // uniform over the workgroup
+    if (valid) {
+      store_kv(lds[stage][0], lds[stage][1], R);
+      __syncthreads();
+    }
+    if (n + 2 < cnt) fetch(n + 2, R);
+    if (valid) {
+      compute(j, lds[stage][0], lds[stage][1]);
+      stage ^= 1;
+    }
+  };
+
+  KVRegs R0, R1;
+  if (cnt > 0) fetch(0, R0);
+  if (cnt > 1) fetch(1, R1);
+  for (int n = 0; n < cnt; n += 2) {
+    step(n, R0);
+    if (n + 1 < cnt) step(n + 1, R1);
   }
 
   float l_tot = l_run + shfl_xor_f32(l_run, 16);
