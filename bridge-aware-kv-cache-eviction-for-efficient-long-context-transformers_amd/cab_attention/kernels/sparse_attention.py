@@ -24,7 +24,7 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     ``kv_idx[b, h, i, :kv_cnt[b, h, i]]`` of the query block i holding t.
 
     q, k, v: ``[B, H, N, D]`` bf16 or fp16 (D = 128, block_size = 64); causal
-    drops keys s > t; a query with no key gets 0; ``scale`` defaults to
+    drops keys s > t; a query with no key gets 0; ``scale`` (> 0) defaults to
     ``1/sqrt(D)``. Index entries outside ``[0, M)`` are skipped. ``out`` may be
     a preallocated ``[B, H, N, D]`` view (any strides with a contiguous last
     dim), e.g. a transposed view of a ``[B, N, H, D]`` buffer. With
@@ -59,12 +59,15 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     lse = torch.empty((B, H, N), dtype=torch.float32, device=dev) if return_lse else None
     if scale is None:
         scale = 1.0 / math.sqrt(D)
+    wbytes = lib.cab_block_sparse_attn_workspace_bytes(B, H, N, D, int(block_size))
+    ws = torch.empty(max(int(wbytes), 16), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         st = lib.cab_block_sparse_attn_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, B, H, N, D, nat.strides4(q),
             nat.strides4(k), nat.strides4(v), nat.strides4(out), int(block_size),
             kv_idx.data_ptr(), kv_cnt.data_ptr(), int(kv_idx.shape[-1]), float(scale),
-            int(bool(causal)), out.data_ptr(), nat.ptr(lse), nat.stream_ptr(dev))
+            int(bool(causal)), out.data_ptr(), nat.ptr(lse), ws.data_ptr(), ws.numel(),
+            nat.stream_ptr(dev))
     nat.check("cab_block_sparse_attn_fwd", st)
     return (out, lse) if return_lse else out
 

@@ -1,25 +1,34 @@
 // Block-sparse attention forward (cab_block_sparse_attn_fwd), D = 128,
 // block_size = 64.
 //
-// One workgroup (4 waves) per (b, h, query block i); wave w owns queries
-// 16 w .. 16 w + 15 of the block. The workgroup walks the kept key blocks
-// kv_idx[b, h, i, :cnt] and, per 64-key block, every wave computes
-//   S^T = K Q^T   (16 MFMA 16x16x32: A = K from LDS, B = Q in registers)
-//   online softmax in the log2 domain, fp32
-//   O^T += V^T P^T (16 MFMA 16x16x32: A = V^T from LDS, B = P in registers)
+// Two kernels:
+//  1. pack_vt_kernel: V [B, H, N, D] -> V^T tiles in MFMA operand order
+//     (16 KB per (b, h, key block), zero past N), in the caller's workspace.
+//     One streaming pass; it moves the transposition MFMA needs for P V out
+//     of the attention loop.
+//  2. attn_fwd_kernel: one workgroup (4 waves) per (b, h, query block i);
+//     wave w owns queries 16 w .. 16 w + 15 of the block. For every kept key
+//     block the workgroup stages K and V^T in LDS with gfx950 direct-to-LDS
+//     loads (global_load_lds_dwordx4: each lane supplies its own global
+//     address, the data lands at LDS base + 16 * lane, so K is gathered
+//     straight into MFMA order and staging costs no VALU work), then every
+//     wave computes
+//       S^T = K Q^T    (16 MFMA 16x16x32: A = K from LDS, B = Q in registers)
+//       online softmax in the log2 domain, fp32
+//       O^T += V^T P^T (16 MFMA 16x16x32: A = V^T from LDS, B = P in registers)
 // Computing the transposed products keeps one query per lane (lane l owns
-// query l % 16) in S, P and O alike, so the softmax statistics never cross
-// lanes except for the 4-lane row reductions, and P feeds the second MFMA
-// straight from the first one's accumulators: the k-slots of P^T are the
-// keys {32 s + 4 g + r, 32 s + 16 + 4 g + r} (g = lane / 16, r = 0..3) and V^T
-// is staged in LDS in the same key order.
-//
-// Both operand tiles sit in LDS in MFMA order (16 bytes per lane and slot),
-// so every operand read is one contiguous 1 KB wave access. The next block's
-// K and V are loaded into registers while the current block is computed
-// (two LDS stages, one barrier per block). Workgroups are mapped so that one
-// XCD runs consecutive query blocks of the same heads (their K/V share L2),
-// longest rows first.
+// query l % 16) in S, P and O alike, so softmax statistics only cross the 4
+// lanes of a query, and P feeds the second MFMA straight from the first
+// one's accumulators: the k-slots of P^T are the keys
+// {32 s + 4 g + r, 32 s + 16 + 4 g + r} (g = lane / 16, r = 0..3), the order
+// pack_vt_kernel writes V^T in.
+// The accumulator is rescaled only when some query's running maximum grows
+// by more than 2^8 (P stays below 256, exact in fp32, the final division by
+// the row sum is unchanged). Two LDS stages, one barrier per block; the next
+// block's loads are issued right after the barrier and land while the
+// current block is computed. Workgroups are mapped so that one XCD runs
+// consecutive query blocks of the same heads (their K/V share L2), longest
+// causal rows first.
 //
 // Algorithmic work per kept tile: 4 * 64 * 64 * 128 flops (2 * 64 * 65 * 128
 // on a causal diagonal tile). Bound: MFMA.
@@ -28,22 +37,34 @@
 namespace cab {
 namespace {
 
-constexpr int BS = 64;   // tokens per block
-constexpr int HD = 128;  // head dim
+constexpr int BS = 64;                       // tokens per block
+constexpr int HD = 128;                      // head dim
+constexpr int TILE_SLOTS = 1024;             // 16-byte slots per operand tile
+constexpr size_t TILE_BYTES = TILE_SLOTS * 16;
+constexpr float RESCALE_LOG2 = 8.0f;         // lazy rescale threshold (2^8)
+
+typedef __attribute__((address_space(3))) void lds_void;
 
 struct AttnArgs {
   const uint16_t* q;
   const uint16_t* k;
-  const uint16_t* v;
+  const uint16_t* vt;  // packed V^T tiles [B*H][M][TILE_SLOTS] x 16 bytes
   uint16_t* o;
   float* lse;
-  int64_t qs[3], ks[3], vs[3], os[3];  // b, h, token strides (elements)
+  int64_t qs[3], ks[3], os[3];  // b, h, token strides (elements)
   const int32_t* kv_idx;
   const int32_t* kv_cnt;
   int64_t B, H, N, M;
   int32_t kmax;
   float scale_log2;
   int causal;
+};
+
+struct PackArgs {
+  const uint16_t* v;
+  uint16_t* vt;
+  int64_t vs[3];
+  int64_t H, N, M;
 };
 
 template <bool BF16>
@@ -67,66 +88,70 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   }
 }
 
-// Global -> register staging of one key block (rows beyond N read as 0).
-struct KVRegs {
-  u32x4 k[4];  // K[16 w + l % 16][32 r + 8 (l / 16) .. +8] for wave w, lane l, r = 0..3
-  u32x4 v[4];  // V rows 4 kq + r at d = 8 c, kq = tid / 16, c = tid % 16
-};
-
-__device__ __forceinline__ void load_kv(const AttnArgs& a, const uint16_t* kb, const uint16_t* vb,
-                                        int64_t j, KVRegs& R) {
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-  const int64_t tok0 = j * BS;
-  const int64_t tk = tok0 + 16 * w + (l & 15);
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-    R.k[r] = tk < a.N ? *reinterpret_cast<const u32x4*>(kb + tk * a.ks[2] + 32 * r + 8 * (l >> 4))
-                      : u32x4{0u, 0u, 0u, 0u};
-  const int kq = tid >> 4, c = tid & 15;
+// V^T tile slot (dt, s, L) (index (2 dt + s) * 64 + L) holds, for d = 16 dt + L % 16
+// and g = L / 16, the 8 values V[32 s + 4 g + r][d] (r = 0..3) followed by
+// V[32 s + 16 + 4 g + r][d] (r = 0..3).
+__global__ __launch_bounds__(256) void pack_vt_kernel(PackArgs a) {
+  __shared__ uint16_t vs[BS][HD + 8];  // padded rows
+  const int64_t bh = blockIdx.y, j = blockIdx.x;
+  const int64_t b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const uint16_t* vb = a.v + b * a.vs[0] + h * a.vs[1];
+  const int tid = threadIdx.x;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int64_t t = tok0 + 4 * kq + r;
-    R.v[r] = t < a.N ? *reinterpret_cast<const u32x4*>(vb + t * a.vs[2] + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+    const int cid = tid + 256 * r;  // 1024 chunks of 8 values
+    const int key = cid >> 4, c = cid & 15;
+    const int64_t t = j * BS + key;
+    const u32x4 x = t < a.N ? *reinterpret_cast<const u32x4*>(vb + t * a.vs[2] + 8 * c)
+                            : u32x4{0u, 0u, 0u, 0u};
+    *reinterpret_cast<u32x2*>(&vs[key][8 * c]) = u32x2{x[0], x[1]};
+    *reinterpret_cast<u32x2*>(&vs[key][8 * c + 4]) = u32x2{x[2], x[3]};
+  }
+  __syncthreads();
+  u32x4* out = reinterpret_cast<u32x4*>(a.vt) + (bh * a.M + j) * TILE_SLOTS;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int slot = tid + 256 * r;
+    const int row = slot >> 6, L = slot & 63;
+    const int dt = row >> 1, s = row & 1, g = L >> 4;
+    const int d = 16 * dt + (L & 15);
+    const int k0 = 32 * s + 4 * g;
+    u32x4 x;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      x[2 * p + 0] = static_cast<uint32_t>(vs[k0 + 16 * p + 0][d]) |
+                     (static_cast<uint32_t>(vs[k0 + 16 * p + 1][d]) << 16);
+      x[2 * p + 1] = static_cast<uint32_t>(vs[k0 + 16 * p + 2][d]) |
+                     (static_cast<uint32_t>(vs[k0 + 16 * p + 3][d]) << 16);
+    }
+    out[slot] = x;
   }
 }
 
-// Register -> LDS in MFMA operand order.
-//  K slot (tt, ds, lane'): key 16 tt + lane' % 16, d = 32 ds + 8 (lane' / 16) .. +8. Wave w
-//    writes block tt = w, so every store is one linear 1 KB wave access.
-//  V^T slot (dt, s, lane'): d = 16 dt + lane' % 16; 8 bytes per half:
-//    half 0 = keys 32 s + 4 g + 0..3, half 1 = keys 32 s + 16 + 4 g + 0..3, g = lane' / 16.
-//    Stored at lane' ^ dt within its 64-slot row: the transposing 8-byte stores of one
-//    wave then spread over 16 bank groups instead of 2, and a row read stays a
-//    permutation of one contiguous 1 KB block (conflict-free).
-__device__ __forceinline__ void store_kv(u32x4* ks, u32x4* vts, const KVRegs& R) {
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+// Issues the direct-to-LDS loads of key block j into one stage: wave w
+// fetches K slot rows (tt = w, ds = 0..3) and V^T slot rows 4 w .. 4 w + 3.
+// K slot (tt, ds, L) = K[16 tt + L % 16][32 ds + 8 (L / 16) .. +8]; rows past N
+// are clamped to N - 1 (their scores are masked).
+__device__ __forceinline__ void issue_tile(const AttnArgs& a, const uint16_t* kb, const u32x4* vtb,
+                                           int64_t j, u32x4* kst, u32x4* vst) {
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  int64_t tk = j * BS + 16 * w + (l & 15);
+  tk = tk < a.N ? tk : a.N - 1;
+  const uint16_t* kp = kb + tk * a.ks[2] + 8 * (l >> 4);
+  const u32x4* vp = vtb + j * TILE_SLOTS + w * 256 + l;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) ks[(w * 4 + r) * 64 + l] = R.k[r];
-  const int kq = tid >> 4, c = tid & 15;
-  const int key0 = 4 * kq;
-  const int s = key0 >> 5, rem = key0 & 31;
-  const int hf = rem >> 4, g = (rem & 15) >> 2;
-  char* vbytes = reinterpret_cast<char*>(vts);
+  for (int r = 0; r < 4; ++r)
+    __builtin_amdgcn_global_load_lds(kp + 32 * r, (lds_void*)(kst + (w * 4 + r) * 64),
+                                     16, 0, 0);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int wd = e >> 1;
-    uint32_t x0, x1;
-    if ((e & 1) == 0) {
-      x0 = (R.v[0][wd] & 0xffffu) | (R.v[1][wd] << 16);
-      x1 = (R.v[2][wd] & 0xffffu) | (R.v[3][wd] << 16);
-    } else {
-      x0 = (R.v[0][wd] >> 16) | (R.v[1][wd] & 0xffff0000u);
-      x1 = (R.v[2][wd] >> 16) | (R.v[3][wd] & 0xffff0000u);
-    }
-    const int d = 8 * c + e;
-    const int dt = d >> 4, lanep = ((d & 15) + 16 * g) ^ dt;
-    *reinterpret_cast<u32x2*>(vbytes + ((dt * 2 + s) * 64 + lanep) * 16 + hf * 8) = u32x2{x0, x1};
-  }
+  for (int r = 0; r < 4; ++r)
+    __builtin_amdgcn_global_load_lds(vp + 64 * r, (lds_void*)(vst + (w * 4 + r) * 64),
+                                     16, 0, 0);
 }
 
 template <bool BF16>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
-  __shared__ u32x4 lds[2][2][1024];  // [stage][K, V^T][slot]: 64 KB
+  __shared__ u32x4 lds[2][2][TILE_SLOTS];  // [stage][K, V^T][slot]: 64 KB
 
   const int64_t total = a.B * a.H * a.M;
   const int64_t logical = xcd_remap(blockIdx.x, total);
@@ -140,7 +165,19 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 
   const uint16_t* qb = a.q + b * a.qs[0] + h * a.qs[1];
   const uint16_t* kb = a.k + b * a.ks[0] + h * a.ks[1];
-  const uint16_t* vb = a.v + b * a.vs[0] + h * a.vs[1];
+  const u32x4* vtb = reinterpret_cast<const u32x4*>(a.vt) + bh * a.M * TILE_SLOTS;
+
+  const int64_t row = bh * a.M + i;
+  int cnt = a.kv_cnt[row];
+  cnt = cnt < 0 ? 0 : (cnt > a.kmax ? a.kmax : cnt);
+  const int32_t* list = a.kv_idx + row * a.kmax;
+  auto next_valid = [&](int n) {
+    while (n < cnt && (list[n] < 0 || list[n] >= a.M)) ++n;
+    return n;
+  };
+
+  int n = next_valid(0);
+  if (n < cnt) issue_tile(a, kb, vtb, list[n], lds[0][0], lds[0][1]);
 
   // Q^T as the B operand: lane holds Q[qtok][32 ds + 8 g .. +8].
   u32x4 qreg[4];
@@ -149,24 +186,24 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     qreg[ds] = qtok < a.N ? *reinterpret_cast<const u32x4*>(qb + qtok * a.qs[2] + 32 * ds + 8 * g)
                           : u32x4{0u, 0u, 0u, 0u};
 
-  const int64_t row = bh * a.M + i;
-  int cnt = a.kv_cnt[row];
-  cnt = cnt < 0 ? 0 : (cnt > a.kmax ? a.kmax : cnt);
-  const int32_t* list = a.kv_idx + row * a.kmax;
-
   f32x4 acc_o[8];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) acc_o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
-  int stage = 0;
+  const float c = a.scale_log2;
+  float m_run = -INFINITY;  // running max of the raw scores this lane's query saw
+  float l_run = 0.f;        // partial row sum of exp2((s - m_run) c) over this lane's keys
+  int st = 0;
 
-  auto fetch = [&](int n, KVRegs& R) {
+  while (n < cnt) {
     const int64_t j = list[n];
-    if (j >= 0 && j < a.M) load_kv(a, kb, vb, j, R);
-  };
+    const int nn = next_valid(n + 1);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of block j landed
+    __builtin_amdgcn_s_barrier();        // ... and every other wave's; stage st^1 is free
+    if (nn < cnt) issue_tile(a, kb, vtb, list[nn], lds[st ^ 1][0], lds[st ^ 1][1]);
+    const u32x4* ks = lds[st][0];
+    const u32x4* vts = lds[st][1];
 
-  auto compute = [&](int64_t j, const u32x4* ks, const u32x4* vts) {
-    // S^T[key][query] for the block's 64 keys.
+    // S^T[key][query] for the block's 64 keys: lane holds keys 16 tt + 4 g + r.
     f32x4 sc[4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
@@ -175,38 +212,43 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
       for (int ds = 0; ds < 4; ++ds) acc = mfma16<BF16>(ks[(tt * 4 + ds) * 64 + lane], qreg[ds], acc);
       sc[tt] = acc;
     }
-    const bool need_mask = (a.causal && j >= i) || (j + 1) * BS > a.N;
+    if ((a.causal && j >= i) || (j + 1) * BS > a.N) {
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t ktok = j * BS + 16 * tt + 4 * g + r;
+          if (ktok >= a.N || (a.causal && ktok > qtok)) sc[tt][r] = -INFINITY;
+        }
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float sv = sc[tt][r] * a.scale_log2;
-        if (need_mask) {
-          const int64_t ktok = j * BS + 16 * tt + 4 * g + r;
-          if (ktok >= a.N || (a.causal && ktok > qtok)) sv = -INFINITY;
-        }
-        sc[tt][r] = sv;
-        mx = fmaxf(mx, sv);
-      }
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[tt][r]);
     mx = fmaxf(mx, shfl_xor_f32(mx, 16));
     mx = fmaxf(mx, shfl_xor_f32(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    // Raise the reference point only when P would exceed 2^8 (or on first sight).
+    const bool grow = mx > m_run && (m_run == -INFINITY || (mx - m_run) * c > RESCALE_LOG2);
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      const float m_new = grow ? mx : m_run;
+      const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run - m_new) * c);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) acc_o[dt] *= alpha;
+      m_run = m_new;
+    }
+    const float mc = m_run == -INFINITY ? 0.f : m_run * c;
     float psum = 0.f;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float p = __builtin_amdgcn_exp2f(sc[tt][r] - m_use);
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tt][r], c, -mc));
         sc[tt][r] = p;
         psum += p;
       }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc_o[dt] *= alpha;
+    l_run += psum;
 
     // P^T as the B operand, k-slots {32 s + 4 g + r, 32 s + 16 + 4 g + r}.
     u32x4 pb[2];
@@ -221,32 +263,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
       for (int s = 0; s < 2; ++s)
-        acc_o[dt] = mfma16<BF16>(vts[(dt * 2 + s) * 64 + (lane ^ dt)], pb[s], acc_o[dt]);
-  };
-
-  // Two blocks in flight in registers: block n is stored to LDS while block
-  // n + 1 is still arriving; block n + 2 is requested as soon as n's
-  // registers are free.
-  auto step = [&](int n, KVRegs& R) {
-    const int64_t j = list[n];
-    const bool valid = j >= 0 && j < a.M;  // uniform over the workgroup
-    if (valid) {
-      store_kv(lds[stage][0], lds[stage][1], R);
-      __syncthreads();
-    }
-    if (n + 2 < cnt) fetch(n + 2, R);
-    if (valid) {
-      compute(j, lds[stage][0], lds[stage][1]);
-      stage ^= 1;
-    }
-  };
-
-  KVRegs R0, R1;
-  if (cnt > 0) fetch(0, R0);
-  if (cnt > 1) fetch(1, R1);
-  for (int n = 0; n < cnt; n += 2) {
-    step(n, R0);
-    if (n + 1 < cnt) step(n + 1, R1);
+        acc_o[dt] = mfma16<BF16>(vts[(dt * 2 + s) * 64 + lane], pb[s], acc_o[dt]);
+    st ^= 1;
+    n = nn;
   }
 
   float l_tot = l_run + shfl_xor_f32(l_run, 16);
@@ -262,7 +281,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     }
     if (a.lse && g == 0) {
       a.lse[bh * a.N + qtok] =
-          l_tot > 0.f ? (m_run + __log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
+          l_tot > 0.f ? (m_run * c + __log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
     }
   }
 }
@@ -272,12 +291,18 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 
 using namespace cab;
 
+extern "C" size_t cab_block_sparse_attn_workspace_bytes(int64_t B, int64_t H, int64_t N,
+                                                        int64_t D, int32_t block_size) {
+  if (B <= 0 || H <= 0 || N <= 0 || D != HD || block_size != BS) return 0;
+  return static_cast<size_t>(B * H * ceil_div(N, BS)) * TILE_BYTES;
+}
+
 extern "C" cab_status_t cab_block_sparse_attn_fwd(
     const void* q, const void* k, const void* v, cab_dtype_t dtype, int64_t B, int64_t H,
     int64_t N, int64_t D, const int64_t q_strides[4], const int64_t k_strides[4],
     const int64_t v_strides[4], const int64_t o_strides[4], int32_t block_size,
     const int32_t* kv_idx, const int32_t* kv_cnt, int32_t kmax, float scale, int causal,
-    void* out, float* lse, void* stream) {
+    void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   CAB_REQUIRE(dtype == CAB_BF16 || dtype == CAB_F16, CAB_EDTYPE,
               "cab_block_sparse_attn_fwd: dtype %d unsupported (bf16 or fp16)", (int)dtype);
@@ -287,7 +312,8 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
   CAB_REQUIRE(block_size == BS, CAB_ESHAPE,
               "cab_block_sparse_attn_fwd: block_size %d unsupported (64)", (int)block_size);
   CAB_REQUIRE(kmax >= 1, CAB_EINVAL, "cab_block_sparse_attn_fwd: kmax=%d must be >= 1", (int)kmax);
-  CAB_REQUIRE(std::isfinite(scale), CAB_EINVAL, "cab_block_sparse_attn_fwd: scale not finite");
+  CAB_REQUIRE(std::isfinite(scale) && scale > 0.f, CAB_EINVAL,
+              "cab_block_sparse_attn_fwd: scale must be finite and > 0");
   CAB_REQUIRE(q_strides && k_strides && v_strides && o_strides, CAB_EINVAL,
               "cab_block_sparse_attn_fwd: null stride array");
   const int64_t M = ceil_div(N, BS);
@@ -307,18 +333,37 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
                   "cab_block_sparse_attn_fwd: %s stride[%d]=%lld must keep rows 16-byte aligned",
                   names[t], d, (long long)strides[t][d]);
   }
+  const size_t need = static_cast<size_t>(B * H * M) * TILE_BYTES;
+  CAB_REQUIRE(workspace != nullptr && workspace_bytes >= need, CAB_EWORKSPACE,
+              "cab_block_sparse_attn_fwd: workspace of %zu bytes given, %zu needed",
+              workspace_bytes, need);
+  CAB_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, CAB_EWORKSPACE,
+              "cab_block_sparse_attn_fwd: workspace not 16-byte aligned");
   const int64_t total = B * H * M;
-  CAB_REQUIRE(total <= INT32_MAX, CAB_ESHAPE, "cab_block_sparse_attn_fwd: problem too large");
+  CAB_REQUIRE(total <= INT32_MAX && B * H <= 65535, CAB_ESHAPE,
+              "cab_block_sparse_attn_fwd: problem too large (B*H <= 65535, B*H*M < 2^31)");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  PackArgs p;
+  p.v = static_cast<const uint16_t*>(v);
+  p.vt = static_cast<uint16_t*>(workspace);
+  for (int d = 0; d < 3; ++d) p.vs[d] = v_strides[d];
+  p.H = H;
+  p.N = N;
+  p.M = M;
+  pack_vt_kernel<<<dim3(static_cast<unsigned>(M), static_cast<unsigned>(B * H)), 256, 0, s>>>(p);
+  cab_status_t st = launch_status("cab_block_sparse_attn_fwd/pack_vt");
+  if (st != CAB_OK) return st;
+
   AttnArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k);
-  a.v = static_cast<const uint16_t*>(v);
+  a.vt = static_cast<const uint16_t*>(workspace);
   a.o = static_cast<uint16_t*>(out);
   a.lse = lse;
   for (int d = 0; d < 3; ++d) {
     a.qs[d] = q_strides[d];
     a.ks[d] = k_strides[d];
-    a.vs[d] = v_strides[d];
     a.os[d] = o_strides[d];
   }
   a.kv_idx = kv_idx;
@@ -330,7 +375,6 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
   a.kmax = kmax;
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   a.causal = causal ? 1 : 0;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   dim3 grid(static_cast<unsigned>(total));
   if (dtype == CAB_BF16)
     attn_fwd_kernel<true><<<grid, 256, 0, s>>>(a);

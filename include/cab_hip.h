@@ -128,6 +128,13 @@ cab_status_t cab_block_topk(const float* frc, int64_t B, int64_t H, int64_t M, i
                             void* stream);
 
 /*
+ * Workspace bytes cab_block_sparse_attn_fwd needs: one packed V^T tile
+ * (16 KB) per (b, h, key block). 0 for unsupported sizes.
+ */
+size_t cab_block_sparse_attn_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D,
+                                             int32_t block_size);
+
+/*
  * Block-sparse attention forward.
  * Replaces the executor inside CABAttention.forward of
  * cab_attention/cab_attention.py (absent; FlexAttention or the manual masked
@@ -136,12 +143,14 @@ cab_status_t cab_block_topk(const float* frc, int64_t B, int64_t H, int64_t M, i
  *
  * For query block i: out[t] = softmax_s(q_t . k_s * scale) v_s over the tokens
  * s of the key blocks kv_idx[b,h,i,0:kv_cnt[b,h,i]] (entries outside [0, M)
- * are skipped); when causal, keys s > t are dropped; a query with no key
- * gets 0. fp32 online softmax, bf16/fp16 MFMA.
+ * are skipped, kv_cnt is clamped to [0, kmax]); when causal, keys s > t are
+ * dropped; a query with no key gets 0. fp32 online softmax, bf16/fp16 MFMA.
  * q, k, v: [B,H,N,D] (strides), out: [B,H,N,D] (strides), dtype bf16 or fp16.
- * block_size == 64, D == 128. kv_idx: contiguous int32 [B,H,M,kmax],
- * kv_cnt: contiguous int32 [B,H,M]. lse: fp32 [B,H,N] natural-log
- * log-sum-exp of the scaled scores (-inf for a query with no key), or NULL.
+ * block_size == 64, D == 128, scale > 0. kv_idx: contiguous int32
+ * [B,H,M,kmax], kv_cnt: contiguous int32 [B,H,M]. lse: fp32 [B,H,N]
+ * natural-log log-sum-exp of the scaled scores (-inf for a query with no
+ * key), or NULL. workspace: cab_block_sparse_attn_workspace_bytes() bytes,
+ * 16-byte aligned, overwritten (V is repacked there first).
  */
 cab_status_t cab_block_sparse_attn_fwd(const void* q, const void* k, const void* v,
                                        cab_dtype_t dtype, int64_t B, int64_t H,
@@ -150,7 +159,8 @@ cab_status_t cab_block_sparse_attn_fwd(const void* q, const void* k, const void*
                                        const int64_t v_strides[4], const int64_t o_strides[4],
                                        int32_t block_size, const int32_t* kv_idx,
                                        const int32_t* kv_cnt, int32_t kmax, float scale,
-                                       int causal, void* out, float* lse, void* stream);
+                                       int causal, void* out, float* lse, void* workspace,
+                                       size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -25,15 +25,15 @@ def lib():
 
 
 def declared_symbols():
-    text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:[a-z_]+\s*\*?\s*)+\s*\**(cab_[a-z0-9_]+)\(", text, re.M)))
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)  # drop comments
+    return sorted(set(re.findall(r"\b(cab_[a-z0-9_]+)\s*\(", text)))
 
 
 def test_header_declares_the_hot_path():
     syms = declared_symbols()
     for name in ("cab_abi_version", "cab_last_error", "cab_coarsen_maxl2",
                  "cab_block_frc_workspace_bytes", "cab_block_frc", "cab_block_topk",
-                 "cab_block_sparse_attn_fwd"):
+                 "cab_block_sparse_attn_workspace_bytes", "cab_block_sparse_attn_fwd"):
         assert name in syms
     assert set(syms) == set(nat.SIGNATURES), "ctypes table and header disagree"
 
@@ -100,16 +100,21 @@ def test_topk_validation(lib):
 
 
 def test_attention_validation(lib):
+    assert lib.cab_block_sparse_attn_workspace_bytes(1, 8, 65, 128, 64) == 8 * 2 * 16384
+    assert lib.cab_block_sparse_attn_workspace_bytes(1, 8, 64, 64, 64) == 0
     st = _s4(8 * 64 * 128, 64 * 128, 128, 1)
     call = lambda **kw: lib.cab_block_sparse_attn_fwd(
         FAKE, FAKE, FAKE, kw.get("dt", nat.CAB_BF16), 1, 8, 64, kw.get("D", 128), st, st, st,
-        kw.get("os", st), kw.get("bs", 64), FAKE, FAKE, kw.get("kmax", 3), 0.088, 1, FAKE, None,
-        None)
+        kw.get("os", st), kw.get("bs", 64), FAKE, FAKE, kw.get("kmax", 3), kw.get("scale", 0.088),
+        1, FAKE, None, kw.get("ws", FAKE), kw.get("wsb", 1 << 30), None)
     assert call(dt=nat.CAB_F32 + 9) == nat.CAB_EDTYPE
     assert call(D=96) == nat.CAB_ESHAPE
     assert call(bs=48) == nat.CAB_ESHAPE
     assert call(kmax=0) == nat.CAB_EINVAL
+    assert call(scale=-0.1) == nat.CAB_EINVAL
     assert call(os=_s4(1, 1, 1, 3)) == nat.CAB_ESHAPE
+    assert call(wsb=1024) == nat.CAB_EWORKSPACE
+    assert call(ws=None) == nat.CAB_EWORKSPACE
 
 
 def test_python_layer_refuses_cpu_tensors(lib):
