@@ -32,6 +32,9 @@ HIPCC_FLAGS = [
     "-Wno-unused-function",
     # Keep packed-fp32 instructions out of the device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: no accvgpr moves when the softmax
+    # rescales or the epilogue reads them.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

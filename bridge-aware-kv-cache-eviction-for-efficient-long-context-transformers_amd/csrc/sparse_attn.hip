@@ -141,17 +141,51 @@ __device__ __forceinline__ void issue_tile(const AttnArgs& a, const uint16_t* kb
   const u32x4* vp = vtb + j * TILE_SLOTS + w * 256 + l;
 #pragma unroll
   for (int r = 0; r < 4; ++r)
-    __builtin_amdgcn_global_load_lds(kp + 32 * r, (lds_void*)(kst + (w * 4 + r) * 64),
-                                     16, 0, 0);
+    __builtin_amdgcn_global_load_lds(kp + 32 * r, (lds_void*)(kst + (w * 4 + r) * 64), 16, 0, 0);
 #pragma unroll
   for (int r = 0; r < 4; ++r)
-    __builtin_amdgcn_global_load_lds(vp + 64 * r, (lds_void*)(vst + (w * 4 + r) * 64),
-                                     16, 0, 0);
+    __builtin_amdgcn_global_load_lds(vp + 64 * r, (lds_void*)(vst + (w * 4 + r) * 64), 16, 0, 0);
 }
 
-template <bool BF16>
+// Pulls key block j's 256 cache lines (128 of K rows, 128 of its V^T tile)
+// into L2 ahead of its staging loads: one 16-byte load per lane, each lane a
+// different 128-byte line, landing in a scratch LDS row nobody reads.
+__device__ __forceinline__ void prefetch_tile(const AttnArgs& a, const uint16_t* kb,
+                                              const u32x4* vtb, int64_t j, u32x4* junk) {
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int line = 64 * w + l;
+  const void* p;
+  if (line < 128) {
+    int64_t tk = j * BS + (line >> 1);
+    tk = tk < a.N ? tk : a.N - 1;
+    p = kb + tk * a.ks[2] + 64 * (line & 1);
+  } else {
+    p = vtb + j * TILE_SLOTS + 8 * (line - 128);
+  }
+  __builtin_amdgcn_global_load_lds(p, (lds_void*)junk, 16, 0, 0);
+}
+
+// Waits until at most n of this wave's vector-memory operations are pending.
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  if (n <= 0)
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+  else if (n == 1)
+    __builtin_amdgcn_s_waitcnt(0x0f71);
+  else
+    __builtin_amdgcn_s_waitcnt(0x0f72);
+}
+
+constexpr int LIST_MAX = 2048;  // kv lists up to this length are staged in LDS
+constexpr int PREFETCH = 3;     // L2 prefetch distance in key blocks
+
+template <bool BF16, bool LIST_LDS>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
-  __shared__ u32x4 lds[2][2][TILE_SLOTS];  // [stage][K, V^T][slot]: 64 KB
+  // One LDS object: [stage 0: K, V^T][stage 1: K, V^T][prefetch landing row][list].
+  __shared__ u32x4 smem[4 * TILE_SLOTS + 64 + LIST_MAX / 4];
+  auto stage_k = [&](int s) { return smem + 2 * s * TILE_SLOTS; };
+  auto stage_v = [&](int s) { return smem + (2 * s + 1) * TILE_SLOTS; };
+  u32x4* junk = smem + 4 * TILE_SLOTS;
+  int32_t* slist = reinterpret_cast<int32_t*>(smem + 4 * TILE_SLOTS + 64);
 
   const int64_t total = a.B * a.H * a.M;
   const int64_t logical = xcd_remap(blockIdx.x, total);
@@ -170,21 +204,35 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const int64_t row = bh * a.M + i;
   int cnt = a.kv_cnt[row];
   cnt = cnt < 0 ? 0 : (cnt > a.kmax ? a.kmax : cnt);
-  const int32_t* list = a.kv_idx + row * a.kmax;
-  auto next_valid = [&](int n) {
-    while (n < cnt && (list[n] < 0 || list[n] >= a.M)) ++n;
-    return n;
+  const int32_t* glist = a.kv_idx + row * a.kmax;
+  if constexpr (LIST_LDS) {
+    for (int p = threadIdx.x; p < cnt; p += 256) slist[p] = glist[p];
+    __syncthreads();
+  }
+  // Entry p of the list; an entry outside [0, M) becomes block 0 with every
+  // score masked, so the pipeline below never branches on validity.
+  auto entry = [&](int p) -> int64_t {
+    if constexpr (LIST_LDS)
+      return slist[p];
+    else
+      return glist[p];
   };
+  auto block_of = [&](int64_t j) -> int64_t { return (j >= 0 && j < a.M) ? j : 0; };
 
-  int n = next_valid(0);
-  if (n < cnt) issue_tile(a, kb, vtb, list[n], lds[0][0], lds[0][1]);
-
-  // Q^T as the B operand: lane holds Q[qtok][32 ds + 8 g .. +8].
+  // Q^T as the B operand: lane holds Q[qtok][32 ds + 8 g .. +8]. Issue order:
+  // block 0's staging loads, Q, then the first prefetches; the empty asm makes
+  // Q ready here (it waits past the prefetches only), so no wait for Q is left
+  // inside the loop where it would also stall on the next block's loads.
   u32x4 qreg[4];
+  int pre = 0;  // prefetches issued before the loop, after block 0's loads
+  if (cnt > 0) issue_tile(a, kb, vtb, block_of(entry(0)), stage_k(0), stage_v(0));
 #pragma unroll
   for (int ds = 0; ds < 4; ++ds)
     qreg[ds] = qtok < a.N ? *reinterpret_cast<const u32x4*>(qb + qtok * a.qs[2] + 32 * ds + 8 * g)
                           : u32x4{0u, 0u, 0u, 0u};
+  for (int p = 1; p < PREFETCH && p < cnt; ++p, ++pre)
+    prefetch_tile(a, kb, vtb, block_of(entry(p)), junk);
+  asm volatile("" ::"v"(qreg[0]), "v"(qreg[1]), "v"(qreg[2]), "v"(qreg[3]));
 
   f32x4 acc_o[8];
 #pragma unroll
@@ -192,17 +240,20 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const float c = a.scale_log2;
   float m_run = -INFINITY;  // running max of the raw scores this lane's query saw
   float l_run = 0.f;        // partial row sum of exp2((s - m_run) c) over this lane's keys
-  int st = 0;
-
-  while (n < cnt) {
-    const int64_t j = list[n];
-    const int nn = next_valid(n + 1);
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of block j landed
-    __builtin_amdgcn_s_barrier();        // ... and every other wave's; stage st^1 is free
-    if (nn < cnt) issue_tile(a, kb, vtb, list[nn], lds[st ^ 1][0], lds[st ^ 1][1]);
-    const u32x4* ks = lds[st][0];
-    const u32x4* vts = lds[st][1];
-
+  // One key block; ST (compile-time) is the LDS stage holding it, so the
+  // compiler sees that the loads into stage ST ^ 1 cannot alias its reads.
+  auto step = [&](int p, auto stage_tag) {
+    constexpr int ST = decltype(stage_tag)::value;
+    const int64_t jraw = entry(p);
+    const bool valid = jraw >= 0 && jraw < a.M;
+    const int64_t j = valid ? jraw : 0;
+    // Block p's loads were followed by the prefetches issued after them.
+    wait_vmcnt(p == 0 ? pre : (p + PREFETCH - 1 < cnt ? 1 : 0));
+    __builtin_amdgcn_s_barrier();  // every wave's loads of block p landed; stage ST^1 is free
+    if (p + 1 < cnt) issue_tile(a, kb, vtb, block_of(entry(p + 1)), stage_k(ST ^ 1), stage_v(ST ^ 1));
+    if (p + PREFETCH < cnt) prefetch_tile(a, kb, vtb, block_of(entry(p + PREFETCH)), junk);
+    const u32x4* ks = stage_k(ST);
+    const u32x4* vts = stage_v(ST);
     // S^T[key][query] for the block's 64 keys: lane holds keys 16 tt + 4 g + r.
     f32x4 sc[4];
 #pragma unroll
@@ -212,13 +263,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
       for (int ds = 0; ds < 4; ++ds) acc = mfma16<BF16>(ks[(tt * 4 + ds) * 64 + lane], qreg[ds], acc);
       sc[tt] = acc;
     }
-    if ((a.causal && j >= i) || (j + 1) * BS > a.N) {
+    if (!valid || (a.causal && j >= i) || (j + 1) * BS > a.N) {
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int64_t ktok = j * BS + 16 * tt + 4 * g + r;
-          if (ktok >= a.N || (a.causal && ktok > qtok)) sc[tt][r] = -INFINITY;
+          if (!valid || ktok >= a.N || (a.causal && ktok > qtok)) sc[tt][r] = -INFINITY;
         }
     }
     float mx = -INFINITY;
@@ -244,9 +295,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tt][r], c, -mc));
-        sc[tt][r] = p;
-        psum += p;
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tt][r], c, -mc));
+        sc[tt][r] = pv;
+        psum += pv;
       }
     l_run += psum;
 
@@ -264,9 +315,12 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int s = 0; s < 2; ++s)
         acc_o[dt] = mfma16<BF16>(vts[(dt * 2 + s) * 64 + lane], pb[s], acc_o[dt]);
-    st ^= 1;
-    n = nn;
+  };
+  for (int p = 0; p < cnt; p += 2) {
+    step(p, std::integral_constant<int, 0>{});
+    if (p + 1 < cnt) step(p + 1, std::integral_constant<int, 1>{});
   }
+  wait_vmcnt(0);  // drain the scratch prefetches before the workgroup exits
 
   float l_tot = l_run + shfl_xor_f32(l_run, 16);
   l_tot = l_tot + shfl_xor_f32(l_tot, 32);
@@ -376,9 +430,17 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   a.causal = causal ? 1 : 0;
   dim3 grid(static_cast<unsigned>(total));
-  if (dtype == CAB_BF16)
-    attn_fwd_kernel<true><<<grid, 256, 0, s>>>(a);
-  else
-    attn_fwd_kernel<false><<<grid, 256, 0, s>>>(a);
+  const bool list_lds = kmax <= LIST_MAX;
+  if (dtype == CAB_BF16) {
+    if (list_lds)
+      attn_fwd_kernel<true, true><<<grid, 256, 0, s>>>(a);
+    else
+      attn_fwd_kernel<true, false><<<grid, 256, 0, s>>>(a);
+  } else {
+    if (list_lds)
+      attn_fwd_kernel<false, true><<<grid, 256, 0, s>>>(a);
+    else
+      attn_fwd_kernel<false, false><<<grid, 256, 0, s>>>(a);
+  }
   return launch_status("cab_block_sparse_attn_fwd");
 }
