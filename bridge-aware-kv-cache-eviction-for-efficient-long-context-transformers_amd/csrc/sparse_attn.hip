@@ -6,29 +6,28 @@
 //     (16 KB per (b, h, key block), zero past N), in the caller's workspace.
 //     One streaming pass; it moves the transposition MFMA needs for P V out
 //     of the attention loop.
-//  2. attn_fwd_kernel: one workgroup (4 waves) per (b, h, query block i);
-//     wave w owns queries 16 w .. 16 w + 15 of the block. For every kept key
-//     block the workgroup stages K and V^T in LDS with gfx950 direct-to-LDS
-//     loads (global_load_lds_dwordx4: each lane supplies its own global
-//     address, the data lands at LDS base + 16 * lane, so K is gathered
-//     straight into MFMA order and staging costs no VALU work), then every
-//     wave computes
-//       S^T = K Q^T    (16 MFMA 16x16x32: A = K from LDS, B = Q in registers)
-//       online softmax in the log2 domain, fp32
-//       O^T += V^T P^T (16 MFMA 16x16x32: A = V^T from LDS, B = P in registers)
-// Computing the transposed products keeps one query per lane (lane l owns
-// query l % 16) in S, P and O alike, so softmax statistics only cross the 4
-// lanes of a query, and P feeds the second MFMA straight from the first
-// one's accumulators: the k-slots of P^T are the keys
-// {32 s + 4 g + r, 32 s + 16 + 4 g + r} (g = lane / 16, r = 0..3), the order
-// pack_vt_kernel writes V^T in.
-// The accumulator is rescaled only when some query's running maximum grows
-// by more than 2^8 (P stays below 256, exact in fp32, the final division by
-// the row sum is unchanged). Two LDS stages, one barrier per block; the next
-// block's loads are issued right after the barrier and land while the
-// current block is computed. Workgroups are mapped so that one XCD runs
-// consecutive query blocks of the same heads (their K/V share L2), longest
-// causal rows first.
+//  2. attn_fwd_kernel: one workgroup of 2 waves per (b, h, query block i).
+//     Wave h (h = 0, 1) owns key half h (keys 32 h .. 32 h + 31) of every kept
+//     key block and all 64 queries of the block. Per block it loads its K
+//     half and its packed V^T half straight from memory into registers (each
+//     byte is read by exactly one wave; nothing goes through LDS) and computes
+//       S^T = K_h Q^T    (32 MFMA 16x16x32: A = K rows, B = Q in registers)
+//       online softmax over its 32 keys, fp32, log2 domain
+//       O_h^T += V_h^T P^T (32 MFMA 16x16x32: A = packed V^T, B = P)
+//     The two waves keep separate running maxima, sums and accumulators (a
+//     split of the key dimension), so the loop has no barrier; they are
+//     merged once at the end through LDS.
+// Transposed products keep the query on the lane axis: lane l holds queries
+// 16 qt + l % 16 (qt = 0..3) in S, P and O alike. S^T's accumulator already
+// is the P^T B operand with k-slots {4 g + r, 16 + 4 g + r} (g = lane / 16,
+// r = 0..3), the key order pack_vt_kernel writes V^T in.
+// The loop is software-pipelined: while block p's softmax runs on the vector
+// ALUs, block p + 1's scores run on the matrix cores, and block p + 2's K
+// and block p + 1's V^T are in flight in registers. The accumulator is
+// rescaled only when a query's running maximum grows by more than 2^8 (P
+// stays below 256; the final division by the row sum is unchanged).
+// Workgroups are mapped so that one XCD runs consecutive query blocks of the
+// same heads (their K/V share L2), longest causal rows first.
 //
 // Algorithmic work per kept tile: 4 * 64 * 64 * 128 flops (2 * 64 * 65 * 128
 // on a causal diagonal tile). Bound: MFMA.
@@ -39,11 +38,10 @@ namespace {
 
 constexpr int BS = 64;                       // tokens per block
 constexpr int HD = 128;                      // head dim
-constexpr int TILE_SLOTS = 1024;             // 16-byte slots per operand tile
+constexpr int TILE_SLOTS = 1024;             // 16-byte slots per packed V^T tile
 constexpr size_t TILE_BYTES = TILE_SLOTS * 16;
 constexpr float RESCALE_LOG2 = 8.0f;         // lazy rescale threshold (2^8)
-
-typedef __attribute__((address_space(3))) void lds_void;
+constexpr int LIST_MAX = 2048;               // kv lists up to this length are staged in LDS
 
 struct AttnArgs {
   const uint16_t* q;
@@ -128,77 +126,27 @@ __global__ __launch_bounds__(256) void pack_vt_kernel(PackArgs a) {
   }
 }
 
-// Issues the direct-to-LDS loads of key block j into one stage: wave w
-// fetches K slot rows (tt = w, ds = 0..3) and V^T slot rows 4 w .. 4 w + 3.
-// K slot (tt, ds, L) = K[16 tt + L % 16][32 ds + 8 (L / 16) .. +8]; rows past N
-// are clamped to N - 1 (their scores are masked).
-__device__ __forceinline__ void issue_tile(const AttnArgs& a, const uint16_t* kb, const u32x4* vtb,
-                                           int64_t j, u32x4* kst, u32x4* vst) {
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  int64_t tk = j * BS + 16 * w + (l & 15);
-  tk = tk < a.N ? tk : a.N - 1;
-  const uint16_t* kp = kb + tk * a.ks[2] + 8 * (l >> 4);
-  const u32x4* vp = vtb + j * TILE_SLOTS + w * 256 + l;
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-    __builtin_amdgcn_global_load_lds(kp + 32 * r, (lds_void*)(kst + (w * 4 + r) * 64), 16, 0, 0);
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-    __builtin_amdgcn_global_load_lds(vp + 64 * r, (lds_void*)(vst + (w * 4 + r) * 64), 16, 0, 0);
-}
-
-// Pulls key block j's 256 cache lines (128 of K rows, 128 of its V^T tile)
-// into L2 ahead of its staging loads: one 16-byte load per lane, each lane a
-// different 128-byte line, landing in a scratch LDS row nobody reads.
-__device__ __forceinline__ void prefetch_tile(const AttnArgs& a, const uint16_t* kb,
-                                              const u32x4* vtb, int64_t j, u32x4* junk) {
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int line = 64 * w + l;
-  const void* p;
-  if (line < 128) {
-    int64_t tk = j * BS + (line >> 1);
-    tk = tk < a.N ? tk : a.N - 1;
-    p = kb + tk * a.ks[2] + 64 * (line & 1);
-  } else {
-    p = vtb + j * TILE_SLOTS + 8 * (line - 128);
-  }
-  __builtin_amdgcn_global_load_lds(p, (lds_void*)junk, 16, 0, 0);
-}
-
-// Waits until at most n of this wave's vector-memory operations are pending.
-__device__ __forceinline__ void wait_vmcnt(int n) {
-  if (n <= 0)
-    __builtin_amdgcn_s_waitcnt(0x0f70);
-  else if (n == 1)
-    __builtin_amdgcn_s_waitcnt(0x0f71);
-  else
-    __builtin_amdgcn_s_waitcnt(0x0f72);
-}
-
-constexpr int LIST_MAX = 2048;  // kv lists up to this length are staged in LDS
-constexpr int PREFETCH = 3;     // L2 prefetch distance in key blocks
+// Per-wave register tiles of one key block (this wave's 32-key half).
+struct KTile { u32x4 r[2][4]; };  // K[32 h + 16 tt + l % 16][32 ds + 8 g .. +8]
+struct VTile { u32x4 r[8]; };     // packed V^T slot (dt, s = h, l), dt = 0..7
 
 template <bool BF16, bool LIST_LDS>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
-  // One LDS object: [stage 0: K, V^T][stage 1: K, V^T][prefetch landing row][list].
-  __shared__ u32x4 smem[4 * TILE_SLOTS + 64 + LIST_MAX / 4];
-  auto stage_k = [&](int s) { return smem + 2 * s * TILE_SLOTS; };
-  auto stage_v = [&](int s) { return smem + (2 * s + 1) * TILE_SLOTS; };
-  u32x4* junk = smem + 4 * TILE_SLOTS;
-  int32_t* slist = reinterpret_cast<int32_t*>(smem + 4 * TILE_SLOTS + 64);
+__global__ __launch_bounds__(128) void attn_fwd_kernel(AttnArgs a) {
+  __shared__ int32_t slist[LIST_MAX];
+  __shared__ float xo[8][4][4][64];  // wave 1's O^T [dt][qt][r][lane] for the merge
+  __shared__ float xm[4][64], xl[4][64];
 
   const int64_t total = a.B * a.H * a.M;
   const int64_t logical = xcd_remap(blockIdx.x, total);
   const int64_t bh = logical / a.M;
   const int64_t i = a.M - 1 - (logical - bh * a.M);  // longest causal rows first
-  const int64_t b = bh / a.H, h = bh - (bh / a.H) * a.H;
-  const int w = threadIdx.x >> 6, lane = lane_id();
-  const int g = lane >> 4;
-  const int qi = lane & 15;
-  const int64_t qtok = i * BS + 16 * w + qi;
+  const int64_t b = bh / a.H, hh = bh - (bh / a.H) * a.H;
+  const int kh = threadIdx.x >> 6;  // key half owned by this wave
+  const int lane = lane_id();
+  const int g = lane >> 4, l16 = lane & 15;
 
-  const uint16_t* qb = a.q + b * a.qs[0] + h * a.qs[1];
-  const uint16_t* kb = a.k + b * a.ks[0] + h * a.ks[1];
+  const uint16_t* qb = a.q + b * a.qs[0] + hh * a.qs[1];
+  const uint16_t* kb = a.k + b * a.ks[0] + hh * a.ks[1];
   const u32x4* vtb = reinterpret_cast<const u32x4*>(a.vt) + bh * a.M * TILE_SLOTS;
 
   const int64_t row = bh * a.M + i;
@@ -206,136 +154,213 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   cnt = cnt < 0 ? 0 : (cnt > a.kmax ? a.kmax : cnt);
   const int32_t* glist = a.kv_idx + row * a.kmax;
   if constexpr (LIST_LDS) {
-    for (int p = threadIdx.x; p < cnt; p += 256) slist[p] = glist[p];
+    for (int p = threadIdx.x; p < cnt; p += 128) slist[p] = glist[p];
     __syncthreads();
   }
-  // Entry p of the list; an entry outside [0, M) becomes block 0 with every
-  // score masked, so the pipeline below never branches on validity.
   auto entry = [&](int p) -> int64_t {
     if constexpr (LIST_LDS)
       return slist[p];
     else
       return glist[p];
   };
+  // An entry outside [0, M) is computed as block 0 with every score masked.
   auto block_of = [&](int64_t j) -> int64_t { return (j >= 0 && j < a.M) ? j : 0; };
 
-  // Q^T as the B operand: lane holds Q[qtok][32 ds + 8 g .. +8]. Issue order:
-  // block 0's staging loads, Q, then the first prefetches; the empty asm makes
-  // Q ready here (it waits past the prefetches only), so no wait for Q is left
-  // inside the loop where it would also stall on the next block's loads.
-  u32x4 qreg[4];
-  int pre = 0;  // prefetches issued before the loop, after block 0's loads
-  if (cnt > 0) issue_tile(a, kb, vtb, block_of(entry(0)), stage_k(0), stage_v(0));
+  auto load_k = [&](int64_t j, KTile& t) {
 #pragma unroll
-  for (int ds = 0; ds < 4; ++ds)
-    qreg[ds] = qtok < a.N ? *reinterpret_cast<const u32x4*>(qb + qtok * a.qs[2] + 32 * ds + 8 * g)
-                          : u32x4{0u, 0u, 0u, 0u};
-  for (int p = 1; p < PREFETCH && p < cnt; ++p, ++pre)
-    prefetch_tile(a, kb, vtb, block_of(entry(p)), junk);
-  asm volatile("" ::"v"(qreg[0]), "v"(qreg[1]), "v"(qreg[2]), "v"(qreg[3]));
-
-  f32x4 acc_o[8];
+    for (int tt = 0; tt < 2; ++tt) {
+      int64_t tk = j * BS + 32 * kh + 16 * tt + l16;
+      tk = tk < a.N ? tk : a.N - 1;  // rows past N are masked
+      const uint16_t* kp = kb + tk * a.ks[2] + 8 * g;
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) acc_o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const float c = a.scale_log2;
-  float m_run = -INFINITY;  // running max of the raw scores this lane's query saw
-  float l_run = 0.f;        // partial row sum of exp2((s - m_run) c) over this lane's keys
-  // One key block; ST (compile-time) is the LDS stage holding it, so the
-  // compiler sees that the loads into stage ST ^ 1 cannot alias its reads.
-  auto step = [&](int p, auto stage_tag) {
-    constexpr int ST = decltype(stage_tag)::value;
-    const int64_t jraw = entry(p);
-    const bool valid = jraw >= 0 && jraw < a.M;
-    const int64_t j = valid ? jraw : 0;
-    // Block p's loads were followed by the prefetches issued after them.
-    wait_vmcnt(p == 0 ? pre : (p + PREFETCH - 1 < cnt ? 1 : 0));
-    __builtin_amdgcn_s_barrier();  // every wave's loads of block p landed; stage ST^1 is free
-    if (p + 1 < cnt) issue_tile(a, kb, vtb, block_of(entry(p + 1)), stage_k(ST ^ 1), stage_v(ST ^ 1));
-    if (p + PREFETCH < cnt) prefetch_tile(a, kb, vtb, block_of(entry(p + PREFETCH)), junk);
-    const u32x4* ks = stage_k(ST);
-    const u32x4* vts = stage_v(ST);
-    // S^T[key][query] for the block's 64 keys: lane holds keys 16 tt + 4 g + r.
-    f32x4 sc[4];
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ds = 0; ds < 4; ++ds) acc = mfma16<BF16>(ks[(tt * 4 + ds) * 64 + lane], qreg[ds], acc);
-      sc[tt] = acc;
+      for (int ds = 0; ds < 4; ++ds) t.r[tt][ds] = *reinterpret_cast<const u32x4*>(kp + 32 * ds);
     }
-    if (!valid || (a.causal && j >= i) || (j + 1) * BS > a.N) {
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t ktok = j * BS + 16 * tt + 4 * g + r;
-          if (!valid || ktok >= a.N || (a.causal && ktok > qtok)) sc[tt][r] = -INFINITY;
-        }
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[tt][r]);
-    mx = fmaxf(mx, shfl_xor_f32(mx, 16));
-    mx = fmaxf(mx, shfl_xor_f32(mx, 32));
-    // Raise the reference point only when P would exceed 2^8 (or on first sight).
-    const bool grow = mx > m_run && (m_run == -INFINITY || (mx - m_run) * c > RESCALE_LOG2);
-    if (__builtin_amdgcn_ballot_w64(grow)) {
-      const float m_new = grow ? mx : m_run;
-      const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run - m_new) * c);
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) acc_o[dt] *= alpha;
-      m_run = m_new;
-    }
-    const float mc = m_run == -INFINITY ? 0.f : m_run * c;
-    float psum = 0.f;
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tt][r], c, -mc));
-        sc[tt][r] = pv;
-        psum += pv;
-      }
-    l_run += psum;
-
-    // P^T as the B operand, k-slots {32 s + 4 g + r, 32 s + 16 + 4 g + r}.
-    u32x4 pb[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      pb[s][0] = pack2<BF16>(sc[2 * s][0], sc[2 * s][1]);
-      pb[s][1] = pack2<BF16>(sc[2 * s][2], sc[2 * s][3]);
-      pb[s][2] = pack2<BF16>(sc[2 * s + 1][0], sc[2 * s + 1][1]);
-      pb[s][3] = pack2<BF16>(sc[2 * s + 1][2], sc[2 * s + 1][3]);
-    }
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-        acc_o[dt] = mfma16<BF16>(vts[(dt * 2 + s) * 64 + lane], pb[s], acc_o[dt]);
   };
-  for (int p = 0; p < cnt; p += 2) {
-    step(p, std::integral_constant<int, 0>{});
-    if (p + 1 < cnt) step(p + 1, std::integral_constant<int, 1>{});
-  }
-  wait_vmcnt(0);  // drain the scratch prefetches before the workgroup exits
-
-  float l_tot = l_run + shfl_xor_f32(l_run, 16);
-  l_tot = l_tot + shfl_xor_f32(l_tot, 32);
-  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  if (qtok < a.N) {
-    uint16_t* ob = a.o + b * a.os[0] + h * a.os[1] + qtok * a.os[2];
+  auto load_v = [&](int64_t j, VTile& t) {
+    const u32x4* vp = vtb + j * TILE_SLOTS + kh * 64 + lane;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const u32x2 pk = {pack2<BF16>(acc_o[dt][0] * inv, acc_o[dt][1] * inv),
-                        pack2<BF16>(acc_o[dt][2] * inv, acc_o[dt][3] * inv)};
-      *reinterpret_cast<u32x2*>(ob + 16 * dt + 4 * g) = pk;
+    for (int dt = 0; dt < 8; ++dt) t.r[dt] = vp[dt * 128];
+  };
+
+  // Q^T as the B operand: qreg[qt][ds] = Q[16 qt + l % 16][32 ds + 8 g .. +8].
+  u32x4 qreg[4][4];
+#pragma unroll
+  for (int qt = 0; qt < 4; ++qt) {
+    const int64_t qtok = i * BS + 16 * qt + l16;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds)
+      qreg[qt][ds] = qtok < a.N ? *reinterpret_cast<const u32x4*>(qb + qtok * a.qs[2] + 32 * ds + 8 * g)
+                                : u32x4{0u, 0u, 0u, 0u};
+  }
+
+  f32x4 oacc[8][4];  // O^T[16 dt + 4 g + r][16 qt + l % 16]
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt) oacc[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const float c = a.scale_log2;
+  float m_run[4], l_run[4];  // per query qt: running max of raw scores, partial row sum
+#pragma unroll
+  for (int qt = 0; qt < 4; ++qt) {
+    m_run[qt] = -INFINITY;
+    l_run[qt] = 0.f;
+  }
+
+  // S^T of one block half: sacc[tt][qt][r] = score(key 32 h + 16 tt + 4 g + r, query 16 qt + l % 16).
+  auto scores = [&](const KTile& kt, f32x4 (&sacc)[2][4]) {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int qt = 0; qt < 4; ++qt) sacc[tt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt)
+          sacc[tt][qt] = mfma16<BF16>(kt.r[tt][ds], qreg[qt][ds], sacc[tt][qt]);
+  };
+
+  if (cnt > 0) {
+    // Register pipeline: at the top of step p, sc holds S(p), kt holds
+    // K(p + 1) and vt holds V(p). Each buffer is refilled right after the
+    // MFMAs that read it were issued, about one step ahead of its use.
+    KTile kt;
+    VTile vt;
+    f32x4 sc[2][4];
+    load_k(block_of(entry(0)), kt);
+    load_v(block_of(entry(0)), vt);
+    scores(kt, sc);
+    if (cnt > 1) load_k(block_of(entry(1)), kt);
+
+    for (int p = 0; p < cnt; ++p) {
+      const int64_t jraw = entry(p);
+      const bool valid = jraw >= 0 && jraw < a.M;
+      const int64_t j = valid ? jraw : 0;
+
+      // Mask and running max of block p (rare branches first).
+      if (!valid || (a.causal && j >= i) || (j + 1) * BS > a.N) {
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int qt = 0; qt < 4; ++qt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int64_t ktok = j * BS + 32 * kh + 16 * tt + 4 * g + r;
+              const int64_t qtok = i * BS + 16 * qt + l16;
+              if (!valid || ktok >= a.N || (a.causal && ktok > qtok)) sc[tt][qt][r] = -INFINITY;
+            }
+      }
+      float mx[4];
+      bool any_grow = false;
+      bool grow[4];
+#pragma unroll
+      for (int qt = 0; qt < 4; ++qt) {
+        float m = fmaxf(fmaxf(fmaxf(sc[0][qt][0], sc[0][qt][1]), fmaxf(sc[0][qt][2], sc[0][qt][3])),
+                        fmaxf(fmaxf(sc[1][qt][0], sc[1][qt][1]), fmaxf(sc[1][qt][2], sc[1][qt][3])));
+        m = fmaxf(m, shfl_xor_f32(m, 16));
+        m = fmaxf(m, shfl_xor_f32(m, 32));
+        mx[qt] = m;
+        grow[qt] = m > m_run[qt] && (m_run[qt] == -INFINITY || (m - m_run[qt]) * c > RESCALE_LOG2);
+        any_grow |= grow[qt];
+      }
+      if (__builtin_amdgcn_ballot_w64(any_grow)) {
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt) {
+          const float m_new = grow[qt] ? mx[qt] : m_run[qt];
+          const float alpha =
+              m_run[qt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run[qt] - m_new) * c);
+          l_run[qt] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) oacc[dt][qt] *= alpha;
+          m_run[qt] = m_new;
+        }
+      }
+
+      // Straight-line block: scores of block p + 1 on the matrix cores (on the
+      // last block they read a stale buffer and are discarded) interleaved
+      // with block p's exponentials, then P(p) V(p).
+      f32x4 sn[2][4];
+      scores(kt, sn);
+      if (p + 2 < cnt) load_k(block_of(entry(p + 2)), kt);
+      u32x4 pb[4];
+#pragma unroll
+      for (int qt = 0; qt < 4; ++qt) {
+        const float mc = m_run[qt] == -INFINITY ? 0.f : m_run[qt] * c;
+        float pv[2][4];
+        float ps = 0.f;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            pv[tt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tt][qt][r], c, -mc));
+            ps += pv[tt][r];
+          }
+        l_run[qt] += ps;
+        pb[qt][0] = pack2<BF16>(pv[0][0], pv[0][1]);
+        pb[qt][1] = pack2<BF16>(pv[0][2], pv[0][3]);
+        pb[qt][2] = pack2<BF16>(pv[1][0], pv[1][1]);
+        pb[qt][3] = pack2<BF16>(pv[1][2], pv[1][3]);
+      }
+#pragma unroll
+      for (int qt = 0; qt < 4; ++qt)
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) oacc[dt][qt] = mfma16<BF16>(vt.r[dt], pb[qt], oacc[dt][qt]);
+      if (p + 1 < cnt) load_v(block_of(entry(p + 1)), vt);
+      // Interleave: each score MFMA followed by a few softmax instructions.
+#pragma unroll
+      for (int k = 0; k < 32; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+      }
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt) sc[tt][qt] = sn[tt][qt];
     }
-    if (a.lse && g == 0) {
-      a.lse[bh * a.N + qtok] =
-          l_tot > 0.f ? (m_run * c + __log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
+  }
+
+  // Merge the two key halves: wave 1 hands its maxima, sums and O^T to wave 0.
+#pragma unroll
+  for (int qt = 0; qt < 4; ++qt) {
+    l_run[qt] += shfl_xor_f32(l_run[qt], 16);
+    l_run[qt] += shfl_xor_f32(l_run[qt], 32);
+  }
+  if (kh == 1) {
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt) {
+      xm[qt][lane] = m_run[qt];
+      xl[qt][lane] = l_run[qt];
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xo[dt][qt][r][lane] = oacc[dt][qt][r];
+    }
+  }
+  __syncthreads();
+  if (kh == 0) {
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt) {
+      const float m1 = xm[qt][lane], l1 = xl[qt][lane];
+      const float m = fmaxf(m_run[qt], m1);
+      const float a0 = m_run[qt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run[qt] - m) * c);
+      const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m1 - m) * c);
+      const float l = l_run[qt] * a0 + l1 * a1;
+      const float inv = l > 0.f ? 1.0f / l : 0.f;
+      const int64_t qtok = i * BS + 16 * qt + l16;
+      if (qtok < a.N) {
+        uint16_t* ob = a.o + b * a.os[0] + hh * a.os[1] + qtok * a.os[2];
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          float o[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[r] = (oacc[dt][qt][r] * a0 + xo[dt][qt][r][lane] * a1) * inv;
+          *reinterpret_cast<u32x2*>(ob + 16 * dt + 4 * g) = u32x2{pack2<BF16>(o[0], o[1]),
+                                                                  pack2<BF16>(o[2], o[3])};
+        }
+        if (a.lse && g == 0)
+          a.lse[bh * a.N + qtok] = l > 0.f ? (m * c + __log2f(l)) * 0.69314718055994531f : -INFINITY;
+      }
     }
   }
 }
@@ -433,14 +458,14 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
   const bool list_lds = kmax <= LIST_MAX;
   if (dtype == CAB_BF16) {
     if (list_lds)
-      attn_fwd_kernel<true, true><<<grid, 256, 0, s>>>(a);
+      attn_fwd_kernel<true, true><<<grid, 128, 0, s>>>(a);
     else
-      attn_fwd_kernel<true, false><<<grid, 256, 0, s>>>(a);
+      attn_fwd_kernel<true, false><<<grid, 128, 0, s>>>(a);
   } else {
     if (list_lds)
-      attn_fwd_kernel<false, true><<<grid, 256, 0, s>>>(a);
+      attn_fwd_kernel<false, true><<<grid, 128, 0, s>>>(a);
     else
-      attn_fwd_kernel<false, false><<<grid, 256, 0, s>>>(a);
+      attn_fwd_kernel<false, false><<<grid, 128, 0, s>>>(a);
   }
   return launch_status("cab_block_sparse_attn_fwd");
 }
