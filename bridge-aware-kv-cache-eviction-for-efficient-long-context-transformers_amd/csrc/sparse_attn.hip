@@ -6,19 +6,21 @@
 //     (16 KB per (b, h, key block), zero past N), in the caller's workspace.
 //     One streaming pass; it moves the transposition MFMA needs for P V out
 //     of the attention loop.
-//  2. attn_fwd_kernel: one workgroup of 2 waves per (b, h, query block i).
-//     Wave h (h = 0, 1) owns key half h (keys 32 h .. 32 h + 31) of every kept
-//     key block and all 64 queries of the block. Per block it loads its K
+//  2. attn_fwd_kernel: one workgroup of 4 waves per (b, h, query block i).
+//     Wave (kh, qh) owns key half kh (keys 32 kh .. 32 kh + 31) of every kept
+//     key block and query half qh (32 queries) of the block. Per block it loads its K
 //     half and its packed V^T half straight from memory into registers (each
 //     byte is read by exactly one wave; nothing goes through LDS) and computes
-//       S^T = K_h Q^T    (32 MFMA 16x16x32: A = K rows, B = Q in registers)
+//       S^T = K_kh Q^T    (16 MFMA 16x16x32: A = K rows, B = Q in registers)
 //       online softmax over its 32 keys, fp32, log2 domain
-//       O_h^T += V_h^T P^T (32 MFMA 16x16x32: A = packed V^T, B = P)
-//     The two waves keep separate running maxima, sums and accumulators (a
-//     split of the key dimension), so the loop has no barrier; they are
-//     merged once at the end through LDS.
+//       O^T += V_kh^T P^T (16 MFMA 16x16x32: A = packed V^T, B = P)
+//       row sums = 1 P^T  (2 MFMA: the sums of exactly the bf16 P used above)
+//     The two key halves keep separate running maxima, sums and accumulators
+//     (a split of the key dimension), so the loop has no barrier; they are
+//     merged once at the end through LDS. About 230 registers per lane: two
+//     waves per SIMD, one's softmax overlapping the other's MFMAs.
 // Transposed products keep the query on the lane axis: lane l holds queries
-// 16 qt + l % 16 (qt = 0..3) in S, P and O alike. S^T's accumulator already
+// 32 qh + 16 qt + l % 16 (qt = 0, 1) in S, P and O alike. S^T's accumulator already
 // is the P^T B operand with k-slots {4 g + r, 16 + 4 g + r} (g = lane / 16,
 // r = 0..3), the key order pack_vt_kernel writes V^T in.
 // The loop is software-pipelined: while block p's softmax runs on the vector
@@ -126,22 +128,46 @@ __global__ __launch_bounds__(256) void pack_vt_kernel(PackArgs a) {
   }
 }
 
-// Per-wave register tiles of one key block (this wave's 32-key half).
-struct KTile { u32x4 r[2][4]; };  // K[32 h + 16 tt + l % 16][32 ds + 8 g .. +8]
-struct VTile { u32x4 r[8]; };     // packed V^T slot (dt, s = h, l), dt = 0..7
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Direct-to-LDS staging of one key block by the 4 waves of the workgroup
+// (global_load_lds_dwordx4: each lane supplies its own global address, the
+// 16 bytes land at the wave-uniform LDS base + 16 * lane).
+//  K slot (tt, ds, L) = K[16 tt + L % 16][32 ds + 8 (L / 16) .. +8]: wave w fetches
+//    tt = w (rows past N are clamped to N - 1; their scores are masked);
+//  V^T slots: the packed tile, wave w fetches slot rows 4 w .. 4 w + 3.
+__device__ __forceinline__ void stage_block(const AttnArgs& a, const uint16_t* kb, const u32x4* vtb,
+                                            int64_t j, u32x4* kst, u32x4* vst) {
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  int64_t tk = j * BS + 16 * w + (l & 15);
+  tk = tk < a.N ? tk : a.N - 1;
+  const uint16_t* kp = kb + tk * a.ks[2] + 8 * (l >> 4);
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    __builtin_amdgcn_global_load_lds(kp + 32 * r, (lds_void*)(kst + (w * 4 + r) * 64), 16, 0, 0);
+  const u32x4* vp = vtb + j * TILE_SLOTS + w * 256 + l;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    __builtin_amdgcn_global_load_lds(vp + 64 * r, (lds_void*)(vst + (w * 4 + r) * 64), 16, 0, 0);
+}
 
 template <bool BF16, bool LIST_LDS>
-__global__ __launch_bounds__(128) void attn_fwd_kernel(AttnArgs a) {
-  __shared__ int32_t slist[LIST_MAX];
-  __shared__ float xo[8][4][4][64];  // wave 1's O^T [dt][qt][r][lane] for the merge
-  __shared__ float xm[4][64], xl[4][64];
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
+  // One LDS object: [K stage 0][V^T stage 0][K stage 1][V^T stage 1][list]; the
+  // merge at the end reuses the stages.
+  __shared__ u32x4 smem[4 * TILE_SLOTS + LIST_MAX / 4];
+  auto stage_k = [&](int s) { return smem + 2 * s * TILE_SLOTS; };
+  auto stage_v = [&](int s) { return smem + (2 * s + 1) * TILE_SLOTS; };
+  int32_t* slist = reinterpret_cast<int32_t*>(smem + 4 * TILE_SLOTS);
 
   const int64_t total = a.B * a.H * a.M;
   const int64_t logical = xcd_remap(blockIdx.x, total);
   const int64_t bh = logical / a.M;
   const int64_t i = a.M - 1 - (logical - bh * a.M);  // longest causal rows first
   const int64_t b = bh / a.H, hh = bh - (bh / a.H) * a.H;
-  const int kh = threadIdx.x >> 6;  // key half owned by this wave
+  const int w = threadIdx.x >> 6;
+  const int kh = w & 1;   // key half of every block owned by this wave
+  const int qh = w >> 1;  // query half (queries 32 qh .. 32 qh + 31) owned by this wave
   const int lane = lane_id();
   const int g = lane >> 4, l16 = lane & 15;
 
@@ -154,7 +180,7 @@ __global__ __launch_bounds__(128) void attn_fwd_kernel(AttnArgs a) {
   cnt = cnt < 0 ? 0 : (cnt > a.kmax ? a.kmax : cnt);
   const int32_t* glist = a.kv_idx + row * a.kmax;
   if constexpr (LIST_LDS) {
-    for (int p = threadIdx.x; p < cnt; p += 128) slist[p] = glist[p];
+    for (int p = threadIdx.x; p < cnt; p += 256) slist[p] = glist[p];
     __syncthreads();
   }
   auto entry = [&](int p) -> int64_t {
@@ -166,195 +192,169 @@ __global__ __launch_bounds__(128) void attn_fwd_kernel(AttnArgs a) {
   // An entry outside [0, M) is computed as block 0 with every score masked.
   auto block_of = [&](int64_t j) -> int64_t { return (j >= 0 && j < a.M) ? j : 0; };
 
-  auto load_k = [&](int64_t j, KTile& t) {
+  // Q^T as the B operand: qreg[qt][ds] = Q[32 qh + 16 qt + l % 16][32 ds + 8 g .. +8].
+  u32x4 qreg[2][4];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      int64_t tk = j * BS + 32 * kh + 16 * tt + l16;
-      tk = tk < a.N ? tk : a.N - 1;  // rows past N are masked
-      const uint16_t* kp = kb + tk * a.ks[2] + 8 * g;
-#pragma unroll
-      for (int ds = 0; ds < 4; ++ds) t.r[tt][ds] = *reinterpret_cast<const u32x4*>(kp + 32 * ds);
-    }
-  };
-  auto load_v = [&](int64_t j, VTile& t) {
-    const u32x4* vp = vtb + j * TILE_SLOTS + kh * 64 + lane;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) t.r[dt] = vp[dt * 128];
-  };
-
-  // Q^T as the B operand: qreg[qt][ds] = Q[16 qt + l % 16][32 ds + 8 g .. +8].
-  u32x4 qreg[4][4];
-#pragma unroll
-  for (int qt = 0; qt < 4; ++qt) {
-    const int64_t qtok = i * BS + 16 * qt + l16;
+  for (int qt = 0; qt < 2; ++qt) {
+    const int64_t qtok = i * BS + 32 * qh + 16 * qt + l16;
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds)
       qreg[qt][ds] = qtok < a.N ? *reinterpret_cast<const u32x4*>(qb + qtok * a.qs[2] + 32 * ds + 8 * g)
                                 : u32x4{0u, 0u, 0u, 0u};
   }
+  // All-ones A operand: ones x P^T puts each query's row sum over the block's
+  // keys in every row of the result (the sum of exactly the P that P V uses).
+  const uint32_t one2 = BF16 ? 0x3f803f80u : 0x3c003c00u;
+  const u32x4 ones = {one2, one2, one2, one2};
 
-  f32x4 oacc[8][4];  // O^T[16 dt + 4 g + r][16 qt + l % 16]
+  f32x4 oacc[8][2];  // O^T[16 dt + 4 g + r][32 qh + 16 qt + l % 16]
+  f32x4 lacc[2];     // row sums (all four r equal)
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
+  for (int qt = 0; qt < 2; ++qt) {
+    lacc[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int qt = 0; qt < 4; ++qt) oacc[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const float c = a.scale_log2;
-  float m_run[4], l_run[4];  // per query qt: running max of raw scores, partial row sum
-#pragma unroll
-  for (int qt = 0; qt < 4; ++qt) {
-    m_run[qt] = -INFINITY;
-    l_run[qt] = 0.f;
+    for (int dt = 0; dt < 8; ++dt) oacc[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-
-  // S^T of one block half: sacc[tt][qt][r] = score(key 32 h + 16 tt + 4 g + r, query 16 qt + l % 16).
-  auto scores = [&](const KTile& kt, f32x4 (&sacc)[2][4]) {
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (int qt = 0; qt < 4; ++qt) sacc[tt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ds = 0; ds < 4; ++ds)
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int qt = 0; qt < 4; ++qt)
-          sacc[tt][qt] = mfma16<BF16>(kt.r[tt][ds], qreg[qt][ds], sacc[tt][qt]);
-  };
+  const float c = a.scale_log2;
+  float m_run[2] = {-INFINITY, -INFINITY};  // running max of the raw scores per query
 
   if (cnt > 0) {
-    // Register pipeline: at the top of step p, sc holds S(p), kt holds
-    // K(p + 1) and vt holds V(p). Each buffer is refilled right after the
-    // MFMAs that read it were issued, about one step ahead of its use.
-    KTile kt;
-    VTile vt;
-    f32x4 sc[2][4];
-    load_k(block_of(entry(0)), kt);
-    load_v(block_of(entry(0)), vt);
-    scores(kt, sc);
-    if (cnt > 1) load_k(block_of(entry(1)), kt);
+    // Block 0's staging, then Q ready once (so no wait for Q stays in the loop).
+    stage_block(a, kb, vtb, block_of(entry(0)), stage_k(0), stage_v(0));
+    asm volatile("" ::"v"(qreg[0][0]), "v"(qreg[0][1]), "v"(qreg[0][2]), "v"(qreg[0][3]),
+                 "v"(qreg[1][0]), "v"(qreg[1][1]), "v"(qreg[1][2]), "v"(qreg[1][3]));
 
-    for (int p = 0; p < cnt; ++p) {
+    // Block p lives in LDS stage PAR = p % 2 (compile time, so the compiler
+    // sees the staging of block p + 1 into the other stage cannot alias).
+    auto step = [&](int p, auto par_tag) {
+      constexpr int PAR = decltype(par_tag)::value;
       const int64_t jraw = entry(p);
       const bool valid = jraw >= 0 && jraw < a.M;
       const int64_t j = valid ? jraw : 0;
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's staging of block p landed
+      __builtin_amdgcn_s_barrier();        // ... and every wave's; stage PAR ^ 1 is free
+      if (p + 1 < cnt) stage_block(a, kb, vtb, block_of(entry(p + 1)), stage_k(PAR ^ 1), stage_v(PAR ^ 1));
+      const u32x4* ks = stage_k(PAR);
+      const u32x4* vts = stage_v(PAR);
 
-      // Mask and running max of block p (rare branches first).
+      // S^T of the block half: sc[tt][qt][r] = score(key 32 kh + 16 tt + 4 g + r,
+      // query 32 qh + 16 qt + l % 16).
+      f32x4 sc[2][2];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) sc[tt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          const u32x4 kop = ks[((2 * kh + tt) * 4 + ds) * 64 + lane];
+#pragma unroll
+          for (int qt = 0; qt < 2; ++qt) sc[tt][qt] = mfma16<BF16>(kop, qreg[qt][ds], sc[tt][qt]);
+        }
+
       if (!valid || (a.causal && j >= i) || (j + 1) * BS > a.N) {
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-          for (int qt = 0; qt < 4; ++qt)
+          for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int64_t ktok = j * BS + 32 * kh + 16 * tt + 4 * g + r;
-              const int64_t qtok = i * BS + 16 * qt + l16;
+              const int64_t qtok = i * BS + 32 * qh + 16 * qt + l16;
               if (!valid || ktok >= a.N || (a.causal && ktok > qtok)) sc[tt][qt][r] = -INFINITY;
             }
       }
-      float mx[4];
-      bool any_grow = false;
-      bool grow[4];
+      float mx[2];
+      bool grow[2];
 #pragma unroll
-      for (int qt = 0; qt < 4; ++qt) {
-        float m = fmaxf(fmaxf(fmaxf(sc[0][qt][0], sc[0][qt][1]), fmaxf(sc[0][qt][2], sc[0][qt][3])),
-                        fmaxf(fmaxf(sc[1][qt][0], sc[1][qt][1]), fmaxf(sc[1][qt][2], sc[1][qt][3])));
+      for (int qt = 0; qt < 2; ++qt) {
+        float m = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(sc[0][qt][0], sc[0][qt][1]), sc[0][qt][2]),
+                                  __builtin_fmaxf(__builtin_fmaxf(sc[0][qt][3], sc[1][qt][0]), sc[1][qt][1]));
+        m = __builtin_fmaxf(__builtin_fmaxf(m, sc[1][qt][2]), sc[1][qt][3]);
         m = fmaxf(m, shfl_xor_f32(m, 16));
         m = fmaxf(m, shfl_xor_f32(m, 32));
         mx[qt] = m;
         grow[qt] = m > m_run[qt] && (m_run[qt] == -INFINITY || (m - m_run[qt]) * c > RESCALE_LOG2);
-        any_grow |= grow[qt];
       }
-      if (__builtin_amdgcn_ballot_w64(any_grow)) {
+      if (__builtin_amdgcn_ballot_w64(grow[0] || grow[1])) {
 #pragma unroll
-        for (int qt = 0; qt < 4; ++qt) {
+        for (int qt = 0; qt < 2; ++qt) {
           const float m_new = grow[qt] ? mx[qt] : m_run[qt];
           const float alpha =
               m_run[qt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run[qt] - m_new) * c);
-          l_run[qt] *= alpha;
+          lacc[qt] *= alpha;
 #pragma unroll
           for (int dt = 0; dt < 8; ++dt) oacc[dt][qt] *= alpha;
           m_run[qt] = m_new;
         }
       }
-
-      // Straight-line block: scores of block p + 1 on the matrix cores (on the
-      // last block they read a stale buffer and are discarded) interleaved
-      // with block p's exponentials, then P(p) V(p).
-      f32x4 sn[2][4];
-      scores(kt, sn);
-      if (p + 2 < cnt) load_k(block_of(entry(p + 2)), kt);
-      u32x4 pb[4];
+      u32x4 pb[2];
 #pragma unroll
-      for (int qt = 0; qt < 4; ++qt) {
+      for (int qt = 0; qt < 2; ++qt) {
         const float mc = m_run[qt] == -INFINITY ? 0.f : m_run[qt] * c;
         float pv[2][4];
-        float ps = 0.f;
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
+          for (int r = 0; r < 4; ++r)
             pv[tt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tt][qt][r], c, -mc));
-            ps += pv[tt][r];
-          }
-        l_run[qt] += ps;
         pb[qt][0] = pack2<BF16>(pv[0][0], pv[0][1]);
         pb[qt][1] = pack2<BF16>(pv[0][2], pv[0][3]);
         pb[qt][2] = pack2<BF16>(pv[1][0], pv[1][1]);
         pb[qt][3] = pack2<BF16>(pv[1][2], pv[1][3]);
       }
 #pragma unroll
-      for (int qt = 0; qt < 4; ++qt)
+      for (int dt = 0; dt < 8; ++dt) {
+        const u32x4 vop = vts[(dt * 2 + kh) * 64 + lane];
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) oacc[dt][qt] = mfma16<BF16>(vt.r[dt], pb[qt], oacc[dt][qt]);
-      if (p + 1 < cnt) load_v(block_of(entry(p + 1)), vt);
-      // Interleave: each score MFMA followed by a few softmax instructions.
-#pragma unroll
-      for (int k = 0; k < 32; ++k) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+        for (int qt = 0; qt < 2; ++qt) oacc[dt][qt] = mfma16<BF16>(vop, pb[qt], oacc[dt][qt]);
       }
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int qt = 0; qt < 4; ++qt) sc[tt][qt] = sn[tt][qt];
+      for (int qt = 0; qt < 2; ++qt) lacc[qt] = mfma16<BF16>(ones, pb[qt], lacc[qt]);
+    };
+    for (int p = 0; p < cnt; p += 2) {
+      step(p, std::integral_constant<int, 0>{});
+      if (p + 1 < cnt) step(p + 1, std::integral_constant<int, 1>{});
     }
   }
 
-  // Merge the two key halves: wave 1 hands its maxima, sums and O^T to wave 0.
-#pragma unroll
-  for (int qt = 0; qt < 4; ++qt) {
-    l_run[qt] += shfl_xor_f32(l_run[qt], 16);
-    l_run[qt] += shfl_xor_f32(l_run[qt], 32);
-  }
+  // Merge the two key halves of each query half through LDS (reusing the
+  // staging area: wave (1, qh) hands its maxima, sums and O^T to wave (0, qh)).
+  __syncthreads();
+  float* xo = reinterpret_cast<float*>(smem) + qh * (8 * 2 * 4 * 64 + 2 * 2 * 64);
+  float* xm = xo + 8 * 2 * 4 * 64;
+  float* xl = xm + 2 * 64;
   if (kh == 1) {
 #pragma unroll
-    for (int qt = 0; qt < 4; ++qt) {
-      xm[qt][lane] = m_run[qt];
-      xl[qt][lane] = l_run[qt];
+    for (int qt = 0; qt < 2; ++qt) {
+      xm[qt * 64 + lane] = m_run[qt];
+      xl[qt * 64 + lane] = lacc[qt][0];
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) xo[dt][qt][r][lane] = oacc[dt][qt][r];
+        for (int r = 0; r < 4; ++r) xo[((dt * 2 + qt) * 4 + r) * 64 + lane] = oacc[dt][qt][r];
     }
   }
   __syncthreads();
   if (kh == 0) {
 #pragma unroll
-    for (int qt = 0; qt < 4; ++qt) {
-      const float m1 = xm[qt][lane], l1 = xl[qt][lane];
+    for (int qt = 0; qt < 2; ++qt) {
+      const float m1 = xm[qt * 64 + lane], l1 = xl[qt * 64 + lane];
       const float m = fmaxf(m_run[qt], m1);
       const float a0 = m_run[qt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run[qt] - m) * c);
       const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m1 - m) * c);
-      const float l = l_run[qt] * a0 + l1 * a1;
+      const float l = lacc[qt][0] * a0 + l1 * a1;
       const float inv = l > 0.f ? 1.0f / l : 0.f;
-      const int64_t qtok = i * BS + 16 * qt + l16;
+      const int64_t qtok = i * BS + 32 * qh + 16 * qt + l16;
       if (qtok < a.N) {
         uint16_t* ob = a.o + b * a.os[0] + hh * a.os[1] + qtok * a.os[2];
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
           float o[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o[r] = (oacc[dt][qt][r] * a0 + xo[dt][qt][r][lane] * a1) * inv;
+          for (int r = 0; r < 4; ++r)
+            o[r] = (oacc[dt][qt][r] * a0 + xo[((dt * 2 + qt) * 4 + r) * 64 + lane] * a1) * inv;
           *reinterpret_cast<u32x2*>(ob + 16 * dt + 4 * g) = u32x2{pack2<BF16>(o[0], o[1]),
                                                                   pack2<BF16>(o[2], o[3])};
         }
@@ -458,14 +458,14 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
   const bool list_lds = kmax <= LIST_MAX;
   if (dtype == CAB_BF16) {
     if (list_lds)
-      attn_fwd_kernel<true, true><<<grid, 128, 0, s>>>(a);
+      attn_fwd_kernel<true, true><<<grid, 256, 0, s>>>(a);
     else
-      attn_fwd_kernel<true, false><<<grid, 128, 0, s>>>(a);
+      attn_fwd_kernel<true, false><<<grid, 256, 0, s>>>(a);
   } else {
     if (list_lds)
-      attn_fwd_kernel<false, true><<<grid, 128, 0, s>>>(a);
+      attn_fwd_kernel<false, true><<<grid, 256, 0, s>>>(a);
     else
-      attn_fwd_kernel<false, false><<<grid, 128, 0, s>>>(a);
+      attn_fwd_kernel<false, false><<<grid, 256, 0, s>>>(a);
   }
   return launch_status("cab_block_sparse_attn_fwd");
 }
