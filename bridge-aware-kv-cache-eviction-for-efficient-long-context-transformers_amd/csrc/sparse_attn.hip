@@ -6,28 +6,29 @@
 //     (16 KB per (b, h, key block), zero past N), in the caller's workspace.
 //     One streaming pass; it moves the transposition MFMA needs for P V out
 //     of the attention loop.
-//  2. attn_fwd_kernel: one workgroup of 4 waves per (b, h, query block i).
-//     Wave (kh, qh) owns key half kh (keys 32 kh .. 32 kh + 31) of every kept
-//     key block and query half qh (32 queries) of the block. Per block it loads its K
-//     half and its packed V^T half straight from memory into registers (each
-//     byte is read by exactly one wave; nothing goes through LDS) and computes
+//  2. attn_fwd_kernel: one workgroup of 4 waves per (b, h, query block i),
+//     two workgroups per CU. Wave (kh, qh) owns key half kh (keys 32 kh ..
+//     32 kh + 31) of every kept key block and query half qh (32 queries).
+//     The 4 waves stage each kept key block (K rows and the packed V^T tile,
+//     32 KB) into one of two LDS stages with direct-to-LDS loads
+//     (global_load_lds_dwordx4), one block ahead; per block each wave reads
+//     its K half and V^T half from LDS and computes
 //       S^T = K_kh Q^T    (16 MFMA 16x16x32: A = K rows, B = Q in registers)
 //       online softmax over its 32 keys, fp32, log2 domain
 //       O^T += V_kh^T P^T (16 MFMA 16x16x32: A = packed V^T, B = P)
 //       row sums = 1 P^T  (2 MFMA: the sums of exactly the bf16 P used above)
 //     The two key halves keep separate running maxima, sums and accumulators
-//     (a split of the key dimension), so the loop has no barrier; they are
-//     merged once at the end through LDS. About 230 registers per lane: two
-//     waves per SIMD, one's softmax overlapping the other's MFMAs.
+//     (a split of the key dimension), merged once at the end through LDS.
+//     One barrier per block hands a stage from the waves that read it to
+//     the waves that refill it.
 // Transposed products keep the query on the lane axis: lane l holds queries
 // 32 qh + 16 qt + l % 16 (qt = 0, 1) in S, P and O alike. S^T's accumulator already
 // is the P^T B operand with k-slots {4 g + r, 16 + 4 g + r} (g = lane / 16,
-// r = 0..3), the key order pack_vt_kernel writes V^T in.
-// The loop is software-pipelined: while block p's softmax runs on the vector
-// ALUs, block p + 1's scores run on the matrix cores, and block p + 2's K
-// and block p + 1's V^T are in flight in registers. The accumulator is
-// rescaled only when a query's running maximum grows by more than 2^8 (P
-// stays below 256; the final division by the row sum is unchanged).
+// r = 0..3), the key order pack_vt_kernel writes V^T in. Column maxima use
+// gfx950's lane swaps (v_permlane16/32_swap), not LDS.
+// The accumulator is rescaled only when a query's running maximum grows by
+// more than 2^8 (P stays below 256; the final division by the row sum is
+// unchanged).
 // Workgroups are mapped so that one XCD runs consecutive query blocks of the
 // same heads (their K/V share L2), longest causal rows first.
 //
@@ -54,7 +55,7 @@ struct AttnArgs {
   int64_t qs[3], ks[3], os[3];  // b, h, token strides (elements)
   const int32_t* kv_idx;
   const int32_t* kv_cnt;
-  int64_t B, H, N, M;
+  int32_t BH, H, N, M;  // B * H, heads, tokens, key blocks (all < 2^31)
   int32_t kmax;
   float scale_log2;
   int causal;
@@ -130,26 +131,39 @@ __global__ __launch_bounds__(256) void pack_vt_kernel(PackArgs a) {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Direct-to-LDS staging of one key block by the 4 waves of the workgroup
-// (global_load_lds_dwordx4: each lane supplies its own global address, the
-// 16 bytes land at the wave-uniform LDS base + 16 * lane).
-//  K slot (tt, ds, L) = K[16 tt + L % 16][32 ds + 8 (L / 16) .. +8]: wave w fetches
-//    tt = w (rows past N are clamped to N - 1; their scores are masked);
-//  V^T slots: the packed tile, wave w fetches slot rows 4 w .. 4 w + 3.
-__device__ __forceinline__ void stage_block(const AttnArgs& a, const uint16_t* kb, const u32x4* vtb,
-                                            int64_t j, u32x4* kst, u32x4* vst) {
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  int64_t tk = j * BS + 16 * w + (l & 15);
-  tk = tk < a.N ? tk : a.N - 1;
-  const uint16_t* kp = kb + tk * a.ks[2] + 8 * (l >> 4);
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-    __builtin_amdgcn_global_load_lds(kp + 32 * r, (lds_void*)(kst + (w * 4 + r) * 64), 16, 0, 0);
-  const u32x4* vp = vtb + j * TILE_SLOTS + w * 256 + l;
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-    __builtin_amdgcn_global_load_lds(vp + 64 * r, (lds_void*)(vst + (w * 4 + r) * 64), 16, 0, 0);
+// gfx950 lane swaps between the two halves of two registers (v_permlane32_swap:
+// 32-lane halves; v_permlane16_swap: odd and even 16-lane rows), written as
+// inline asm because the compiler's builtins return the first result twice.
+// The s_nop gives the two wait states a swap needs after a VALU write of
+// its operands.
+__device__ __forceinline__ void lane_swap32(uint32_t& a, uint32_t& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
 }
+__device__ __forceinline__ void lane_swap16(uint32_t& a, uint32_t& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+// Maxima over the four lane groups (lanes c + 16 g, g = 0..3) of two
+// registers at once, without an LDS round trip. In: x0, x1 hold per-lane
+// partial maxima of query column c = lane % 16 for query tiles 0 and 1.
+// Out: each holds its tile's full column maximum in every lane.
+__device__ __forceinline__ void colmax2(float& x0, float& x1) {
+  uint32_t a = __builtin_bit_cast(uint32_t, x0), b = __builtin_bit_cast(uint32_t, x1);
+  lane_swap32(a, b);  // one register holds both tiles' lower halves, the other the upper
+  float y = __builtin_fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+  // y: tile 0 merged over g and g ^ 2 in one 32-lane half, tile 1 in the other.
+  a = b = __builtin_bit_cast(uint32_t, y);
+  lane_swap16(a, b);  // rows g and g ^ 1 side by side
+  y = __builtin_fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+  a = b = __builtin_bit_cast(uint32_t, y);
+  lane_swap32(a, b);  // each half broadcast to all 64 lanes
+  x0 = __builtin_bit_cast(float, a);
+  x1 = __builtin_bit_cast(float, b);
+}
+
+// Running-max sentinel: a finite stand-in for -inf, so that -max * c stays
+// finite and exp2(s * c - max * c) of a masked score (-inf) is exactly 0.
+constexpr float M_EMPTY = -1.0e30f;
 
 template <bool BF16, bool LIST_LDS>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
@@ -160,47 +174,78 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   auto stage_v = [&](int s) { return smem + (2 * s + 1) * TILE_SLOTS; };
   int32_t* slist = reinterpret_cast<int32_t*>(smem + 4 * TILE_SLOTS);
 
-  const int64_t total = a.B * a.H * a.M;
-  const int64_t logical = xcd_remap(blockIdx.x, total);
-  const int64_t bh = logical / a.M;
-  const int64_t i = a.M - 1 - (logical - bh * a.M);  // longest causal rows first
-  const int64_t b = bh / a.H, hh = bh - (bh / a.H) * a.H;
-  const int w = threadIdx.x >> 6;
+  const int M = a.M, N = a.N;
+  const int logical = static_cast<int>(xcd_remap(blockIdx.x, static_cast<int64_t>(a.BH) * M));
+  const int bh = logical / M;
+  const int i = M - 1 - (logical - bh * M);  // longest causal rows first
+  const int b = bh / a.H, hh = bh - (bh / a.H) * a.H;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int kh = w & 1;   // key half of every block owned by this wave
   const int qh = w >> 1;  // query half (queries 32 qh .. 32 qh + 31) owned by this wave
   const int lane = lane_id();
   const int g = lane >> 4, l16 = lane & 15;
 
   const uint16_t* qb = a.q + b * a.qs[0] + hh * a.qs[1];
-  const uint16_t* kb = a.k + b * a.ks[0] + hh * a.ks[1];
-  const u32x4* vtb = reinterpret_cast<const u32x4*>(a.vt) + bh * a.M * TILE_SLOTS;
+  const char* kbytes = reinterpret_cast<const char*>(a.k + b * a.ks[0] + hh * a.ks[1]);
+  const char* vtbytes = reinterpret_cast<const char*>(a.vt) + static_cast<int64_t>(bh) * M * TILE_BYTES;
 
-  const int64_t row = bh * a.M + i;
-  int cnt = a.kv_cnt[row];
+  int cnt = a.kv_cnt[bh * static_cast<int64_t>(M) + i];
   cnt = cnt < 0 ? 0 : (cnt > a.kmax ? a.kmax : cnt);
-  const int32_t* glist = a.kv_idx + row * a.kmax;
+  const int32_t* glist = a.kv_idx + (static_cast<int64_t>(bh) * M + i) * a.kmax;
   if constexpr (LIST_LDS) {
     for (int p = threadIdx.x; p < cnt; p += 256) slist[p] = glist[p];
     __syncthreads();
   }
-  auto entry = [&](int p) -> int64_t {
+  auto entry = [&](int p) -> int {
     if constexpr (LIST_LDS)
-      return slist[p];
+      return __builtin_amdgcn_readfirstlane(slist[p]);
     else
       return glist[p];
   };
-  // An entry outside [0, M) is computed as block 0 with every score masked.
-  auto block_of = [&](int64_t j) -> int64_t { return (j >= 0 && j < a.M) ? j : 0; };
+
+  // Staging of key block j into LDS by the 4 waves (global_load_lds_dwordx4:
+  // each lane gives its own global address, the 16 bytes land at the
+  // wave-uniform LDS base + 16 * lane; the immediate offset moves both).
+  //  K slot (tt, ds, L) = K[16 tt + L % 16][32 ds + 8 (L / 16) .. +8]: wave w
+  //   fetches tt = w, ds = 0..3 (64 bytes apart in the row, 1 KB apart in LDS);
+  //   rows past N are clamped to N - 1 (their scores are masked).
+  //  V^T: wave w fetches slot rows 4 w .. 4 w + 3 of the packed tile (1 KB each).
+  const int krow = 16 * w + l16;
+  const int64_t krow_bytes = a.ks[2] * 2;
+  const int64_t kcol_bytes = 16 * g;
+  const int64_t koff = krow * krow_bytes + kcol_bytes;
+  const int64_t kblk_bytes = BS * krow_bytes;
+  const int voff = w * 4096 + 16 * lane;
+  auto stage = [&](int j, u32x4* kst, u32x4* vst) {
+    const char* kp;
+    if ((j + 1) * BS <= N) {
+      kp = kbytes + j * kblk_bytes + koff;
+    } else {
+      const int tk = j * BS + krow < N ? j * BS + krow : N - 1;
+      kp = kbytes + tk * krow_bytes + kcol_bytes;
+    }
+    char* kl = reinterpret_cast<char*>(kst) + w * 4096;
+    __builtin_amdgcn_global_load_lds(kp, (lds_void*)kl, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(kp, (lds_void*)(kl + 1024 - 64), 16, 64, 0);
+    __builtin_amdgcn_global_load_lds(kp, (lds_void*)(kl + 2048 - 128), 16, 128, 0);
+    __builtin_amdgcn_global_load_lds(kp, (lds_void*)(kl + 3072 - 192), 16, 192, 0);
+    const char* vp = vtbytes + static_cast<int64_t>(j) * TILE_BYTES + voff;
+    char* vl = reinterpret_cast<char*>(vst) + w * 4096;
+    __builtin_amdgcn_global_load_lds(vp, (lds_void*)vl, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(vp, (lds_void*)vl, 16, 1024, 0);
+    __builtin_amdgcn_global_load_lds(vp, (lds_void*)vl, 16, 2048, 0);
+    __builtin_amdgcn_global_load_lds(vp, (lds_void*)vl, 16, 3072, 0);
+  };
 
   // Q^T as the B operand: qreg[qt][ds] = Q[32 qh + 16 qt + l % 16][32 ds + 8 g .. +8].
   u32x4 qreg[2][4];
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
-    const int64_t qtok = i * BS + 32 * qh + 16 * qt + l16;
+    const int qtok = i * BS + 32 * qh + 16 * qt + l16;
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds)
-      qreg[qt][ds] = qtok < a.N ? *reinterpret_cast<const u32x4*>(qb + qtok * a.qs[2] + 32 * ds + 8 * g)
-                                : u32x4{0u, 0u, 0u, 0u};
+      qreg[qt][ds] = qtok < N ? *reinterpret_cast<const u32x4*>(qb + qtok * a.qs[2] + 32 * ds + 8 * g)
+                              : u32x4{0u, 0u, 0u, 0u};
   }
   // All-ones A operand: ones x P^T puts each query's row sum over the block's
   // keys in every row of the result (the sum of exactly the P that P V uses).
@@ -216,11 +261,15 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     for (int dt = 0; dt < 8; ++dt) oacc[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   const float c = a.scale_log2;
-  float m_run[2] = {-INFINITY, -INFINITY};  // running max of the raw scores per query
+  // Running maximum of the raw scores per query, and -max * c.
+  float m_run[2] = {M_EMPTY, M_EMPTY};
+  float nmc[2] = {-M_EMPTY * c, -M_EMPTY * c};
 
   if (cnt > 0) {
-    // Block 0's staging, then Q ready once (so no wait for Q stays in the loop).
-    stage_block(a, kb, vtb, block_of(entry(0)), stage_k(0), stage_v(0));
+    int jraw = entry(0);
+    auto block_of = [&](int j) { return (j >= 0 && j < M) ? j : 0; };
+    stage(block_of(jraw), stage_k(0), stage_v(0));
+    // Q ready once, so that no wait for Q stays in the loop.
     asm volatile("" ::"v"(qreg[0][0]), "v"(qreg[0][1]), "v"(qreg[0][2]), "v"(qreg[0][3]),
                  "v"(qreg[1][0]), "v"(qreg[1][1]), "v"(qreg[1][2]), "v"(qreg[1][3]));
 
@@ -228,14 +277,24 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     // sees the staging of block p + 1 into the other stage cannot alias).
     auto step = [&](int p, auto par_tag) {
       constexpr int PAR = decltype(par_tag)::value;
-      const int64_t jraw = entry(p);
-      const bool valid = jraw >= 0 && jraw < a.M;
-      const int64_t j = valid ? jraw : 0;
+      const bool valid = jraw >= 0 && jraw < M;
+      const int j = valid ? jraw : 0;
       __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's staging of block p landed
       __builtin_amdgcn_s_barrier();        // ... and every wave's; stage PAR ^ 1 is free
-      if (p + 1 < cnt) stage_block(a, kb, vtb, block_of(entry(p + 1)), stage_k(PAR ^ 1), stage_v(PAR ^ 1));
+      int jnext = 0;
+      if (p + 1 < cnt) {
+        jnext = entry(p + 1);
+        stage(block_of(jnext), stage_k(PAR ^ 1), stage_v(PAR ^ 1));
+      }
       const u32x4* ks = stage_k(PAR);
       const u32x4* vts = stage_v(PAR);
+      u32x4 kop[4][2], vop[8];
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) kop[ds][tt] = ks[((2 * kh + tt) * 4 + ds) * 64 + lane];
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) vop[dt] = vts[(dt * 2 + kh) * 64 + lane];
 
       // S^T of the block half: sc[tt][qt][r] = score(key 32 kh + 16 tt + 4 g + r,
       // query 32 qh + 16 qt + l % 16).
@@ -247,71 +306,70 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int ds = 0; ds < 4; ++ds)
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          const u32x4 kop = ks[((2 * kh + tt) * 4 + ds) * 64 + lane];
+        for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-          for (int qt = 0; qt < 2; ++qt) sc[tt][qt] = mfma16<BF16>(kop, qreg[qt][ds], sc[tt][qt]);
-        }
+          for (int qt = 0; qt < 2; ++qt) sc[tt][qt] = mfma16<BF16>(kop[ds][tt], qreg[qt][ds], sc[tt][qt]);
 
-      if (!valid || (a.causal && j >= i) || (j + 1) * BS > a.N) {
+      if (!valid || (a.causal && j >= i) || (j + 1) * BS > N) {
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
           for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const int64_t ktok = j * BS + 32 * kh + 16 * tt + 4 * g + r;
-              const int64_t qtok = i * BS + 32 * qh + 16 * qt + l16;
-              if (!valid || ktok >= a.N || (a.causal && ktok > qtok)) sc[tt][qt][r] = -INFINITY;
+              const int ktok = j * BS + 32 * kh + 16 * tt + 4 * g + r;
+              const int qtok = i * BS + 32 * qh + 16 * qt + l16;
+              if (!valid || ktok >= N || (a.causal && ktok > qtok)) sc[tt][qt][r] = -INFINITY;
             }
       }
       float mx[2];
-      bool grow[2];
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
-        float m = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(sc[0][qt][0], sc[0][qt][1]), sc[0][qt][2]),
-                                  __builtin_fmaxf(__builtin_fmaxf(sc[0][qt][3], sc[1][qt][0]), sc[1][qt][1]));
-        m = __builtin_fmaxf(__builtin_fmaxf(m, sc[1][qt][2]), sc[1][qt][3]);
-        m = fmaxf(m, shfl_xor_f32(m, 16));
-        m = fmaxf(m, shfl_xor_f32(m, 32));
-        mx[qt] = m;
-        grow[qt] = m > m_run[qt] && (m_run[qt] == -INFINITY || (m - m_run[qt]) * c > RESCALE_LOG2);
+        const float m0 = __builtin_fmaxf(__builtin_fmaxf(sc[0][qt][0], sc[0][qt][1]),
+                                         __builtin_fmaxf(sc[0][qt][2], sc[0][qt][3]));
+        const float m1 = __builtin_fmaxf(__builtin_fmaxf(sc[1][qt][0], sc[1][qt][1]),
+                                         __builtin_fmaxf(sc[1][qt][2], sc[1][qt][3]));
+        mx[qt] = __builtin_fmaxf(m0, m1);
       }
-      if (__builtin_amdgcn_ballot_w64(grow[0] || grow[1])) {
+      colmax2(mx[0], mx[1]);
+      // Rescale only when a query's maximum grew by more than 2^RESCALE_LOG2
+      // in exp2 units (always on its first non-empty block).
+      const bool grow0 = __builtin_fmaf(mx[0], c, nmc[0]) > RESCALE_LOG2;
+      const bool grow1 = __builtin_fmaf(mx[1], c, nmc[1]) > RESCALE_LOG2;
+      if (__builtin_amdgcn_ballot_w64(grow0 || grow1)) {
+        const bool grow[2] = {grow0, grow1};
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
           const float m_new = grow[qt] ? mx[qt] : m_run[qt];
-          const float alpha =
-              m_run[qt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run[qt] - m_new) * c);
+          const float alpha = __builtin_amdgcn_exp2f((m_run[qt] - m_new) * c);
           lacc[qt] *= alpha;
 #pragma unroll
           for (int dt = 0; dt < 8; ++dt) oacc[dt][qt] *= alpha;
           m_run[qt] = m_new;
+          nmc[qt] = -m_new * c;
         }
       }
       u32x4 pb[2];
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
-        const float mc = m_run[qt] == -INFINITY ? 0.f : m_run[qt] * c;
         float pv[2][4];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            pv[tt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tt][qt][r], c, -mc));
+            pv[tt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tt][qt][r], c, nmc[qt]));
         pb[qt][0] = pack2<BF16>(pv[0][0], pv[0][1]);
         pb[qt][1] = pack2<BF16>(pv[0][2], pv[0][3]);
         pb[qt][2] = pack2<BF16>(pv[1][0], pv[1][1]);
         pb[qt][3] = pack2<BF16>(pv[1][2], pv[1][3]);
       }
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const u32x4 vop = vts[(dt * 2 + kh) * 64 + lane];
+      for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) oacc[dt][qt] = mfma16<BF16>(vop, pb[qt], oacc[dt][qt]);
-      }
+        for (int qt = 0; qt < 2; ++qt) oacc[dt][qt] = mfma16<BF16>(vop[dt], pb[qt], oacc[dt][qt]);
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) lacc[qt] = mfma16<BF16>(ones, pb[qt], lacc[qt]);
+      jraw = jnext;
     };
     for (int p = 0; p < cnt; p += 2) {
       step(p, std::integral_constant<int, 0>{});
@@ -342,12 +400,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     for (int qt = 0; qt < 2; ++qt) {
       const float m1 = xm[qt * 64 + lane], l1 = xl[qt * 64 + lane];
       const float m = fmaxf(m_run[qt], m1);
-      const float a0 = m_run[qt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run[qt] - m) * c);
-      const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m1 - m) * c);
+      const float a0 = __builtin_amdgcn_exp2f((m_run[qt] - m) * c);
+      const float a1 = __builtin_amdgcn_exp2f((m1 - m) * c);
       const float l = lacc[qt][0] * a0 + l1 * a1;
       const float inv = l > 0.f ? 1.0f / l : 0.f;
-      const int64_t qtok = i * BS + 32 * qh + 16 * qt + l16;
-      if (qtok < a.N) {
+      const int qtok = i * BS + 32 * qh + 16 * qt + l16;
+      if (qtok < N) {
         uint16_t* ob = a.o + b * a.os[0] + hh * a.os[1] + qtok * a.os[2];
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
@@ -359,7 +417,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
                                                                   pack2<BF16>(o[2], o[3])};
         }
         if (a.lse && g == 0)
-          a.lse[bh * a.N + qtok] = l > 0.f ? (m * c + __log2f(l)) * 0.69314718055994531f : -INFINITY;
+          a.lse[static_cast<int64_t>(bh) * N + qtok] =
+              l > 0.f ? (m * c + __log2f(l)) * 0.69314718055994531f : -INFINITY;
       }
     }
   }
@@ -419,8 +478,9 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
   CAB_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, CAB_EWORKSPACE,
               "cab_block_sparse_attn_fwd: workspace not 16-byte aligned");
   const int64_t total = B * H * M;
-  CAB_REQUIRE(total <= INT32_MAX && B * H <= 65535, CAB_ESHAPE,
-              "cab_block_sparse_attn_fwd: problem too large (B*H <= 65535, B*H*M < 2^31)");
+  CAB_REQUIRE(total <= INT32_MAX && B * H <= 65535 && N <= INT32_MAX - BS, CAB_ESHAPE,
+              "cab_block_sparse_attn_fwd: problem too large (B*H <= 65535, B*H*M < 2^31, "
+              "N < 2^31 - 64)");
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   PackArgs p;
@@ -447,10 +507,10 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
   }
   a.kv_idx = kv_idx;
   a.kv_cnt = kv_cnt;
-  a.B = B;
-  a.H = H;
-  a.N = N;
-  a.M = M;
+  a.BH = static_cast<int32_t>(B * H);
+  a.H = static_cast<int32_t>(H);
+  a.N = static_cast<int32_t>(N);
+  a.M = static_cast<int32_t>(M);
   a.kmax = kmax;
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   a.causal = causal ? 1 : 0;

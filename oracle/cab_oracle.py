@@ -14,7 +14,9 @@ in float32), so a gather compares bit-for-bit after widening.
 Pinning of each function (tests/test_oracle.py):
 
 - ``canonical_sqnorm``: exact-arithmetic cases (small integers, where every
-  summation order is exact), a brute-force Python loop in the same order, and
+  summation order is exact), a bound against the exactly rounded sum
+  (``math.fsum``), a hand-derived input whose value differs between the
+  chunked-pairwise order, a plain left-to-right sum and the exact sum, and
   zero-padding invariance for D not a power of two.
 - ``coarsen_max_l2``: brute-force loop on tiny inputs, planted maximum,
   exact ties (lowest index wins), NaN handling, block_size 1 = identity,
@@ -139,9 +141,7 @@ def compute_block_frc(q_coarse, k_coarse, temperature: float = 1.0,
       (kernel_benchmark.py:135-137; CAB_Attention_Colab.ipynb:361; methods.py:332).
     - Normalisation ``minmax``: ``(A - min) / (max - min + 1e-8)`` per (b, h),
       left unchanged when max == min
-      (CAB_Attention_Colab.ipynb:249, cell 11 src l.75-81); ``none``: A;
-      ``softmax``: row softmax over key blocks (named in TODO.md:114, no
-      reference code).
+      (CAB_Attention_Colab.ipynb:249, cell 11 src l.75-81); ``none``: A.
     - Redundancy ``T = Ahat @ Ahat`` (README.md:36, :240; kernel_benchmark.py:143-144).
     - ``additive``: ``F = Ahat - lambda T`` (README.md:37, :236; Colab :367).
       ``multiplicative``: ``F = Ahat / (1 + lambda T / (Ahat + 1e-8))``
@@ -162,10 +162,6 @@ def compute_block_frc(q_coarse, k_coarse, temperature: float = 1.0,
         ahat = np.where(mx > mn, (a - mn) / (mx - mn + 1e-8), a)
     elif normalization == "none":
         ahat = a
-    elif normalization == "softmax":
-        z = a - a.max(axis=-1, keepdims=True)
-        e = np.exp(z)
-        ahat = e / e.sum(axis=-1, keepdims=True)
     else:
         raise ValueError(f"unknown normalization {normalization!r}")
     t = np.matmul(ahat, ahat)

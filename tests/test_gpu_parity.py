@@ -286,6 +286,29 @@ def test_attention_parity(cuda, dt, N, causal, sp):
     np.testing.assert_allclose(np32(lse)[0, 0], want_lse, atol=1e-3, rtol=1e-4)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_wide_dynamic_range(cuda, causal):
+    """Query rows alternate between score scales 100 and 0.01 every 16 tokens
+    (neighbouring lane tiles of one wave), so a running maximum taken from the
+    wrong query overflows exp2 (inf/NaN) or flushes every weight to 0."""
+    from cab_attention.kernels import block_sparse_attention
+    B, H, N, D, bs = 1, 2, 512, 128, 64
+    scale = np.where((np.arange(N) // 16) % 2 == 0, 100.0, 0.01).astype(np.float32)
+    q = (seeded((B, H, N, D), 11, torch.float32) * torch.from_numpy(scale)[:, None]).to(torch.bfloat16)
+    k = seeded((B, H, N, D), 12, torch.bfloat16)
+    v = seeded((B, H, N, D), 13, torch.bfloat16)
+    M = N // bs
+    f = np.random.default_rng(5).standard_normal((B, H, M, M)).astype(np.float32)
+    _, idx, cnt = O.generate_block_mask(f, 0.5, causal=causal)
+    out = block_sparse_attention(q.to(cuda), k.to(cuda), v.to(cuda), torch.from_numpy(idx).to(cuda),
+                                 torch.from_numpy(cnt).to(cuda), bs, causal=causal)
+    want = O.sparse_attention(np32(q), np32(k), np32(v), idx, cnt, bs, causal=causal)
+    got = np32(out)
+    assert np.isfinite(got).all()
+    err = np.abs(got - want).max()
+    assert err <= 2e-2, f"max abs error {err}"
+
+
 def test_attention_empty_rows_and_bad_indices(cuda):
     from cab_attention.kernels import block_sparse_attention
     B, H, N, D, bs = 1, 1, 256, 128, 64
