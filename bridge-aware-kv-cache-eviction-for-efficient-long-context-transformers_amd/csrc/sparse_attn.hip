@@ -131,6 +131,15 @@ __global__ __launch_bounds__(256) void pack_vt_kernel(PackArgs a) {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+// 16-byte direct-to-LDS load per lane: global g + OFF, LDS l + OFF + 16 * lane.
+// OFF is the instruction's immediate, a 13-bit signed field: the compiler
+// wraps larger constants without a diagnostic, so they are refused here.
+template <int OFF>
+__device__ __forceinline__ void dma16(const char* g, char* l) {
+  static_assert(OFF >= 0 && OFF < 4096, "global_load_lds immediate offset must be in [0, 4096)");
+  __builtin_amdgcn_global_load_lds(g, (lds_void*)l, 16, OFF, 0);
+}
+
 // gfx950 lane swaps between the two halves of two registers (v_permlane32_swap:
 // 32-lane halves; v_permlane16_swap: odd and even 16-lane rows), written as
 // inline asm because the compiler's builtins return the first result twice.
@@ -206,36 +215,54 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   // Staging of key block j into LDS by the 4 waves (global_load_lds_dwordx4:
   // each lane gives its own global address, the 16 bytes land at the
   // wave-uniform LDS base + 16 * lane; the immediate offset moves both).
-  //  K slot (tt, ds, L) = K[16 tt + L % 16][32 ds + 8 (L / 16) .. +8]: wave w
-  //   fetches tt = w, ds = 0..3 (64 bytes apart in the row, 1 KB apart in LDS);
-  //   rows past N are clamped to N - 1 (their scores are masked).
+  //  K: row-major, 64 rows x 256 bytes, the 16-byte chunks of row R stored
+  //   XOR-swizzled (chunk c at position c ^ (R % 16)) so that the operand
+  //   reads below are bank-conflict free. Instruction r of wave w fetches the
+  //   four whole rows 16 w + 4 r .. +3 (full 128-byte lines); rows past N
+  //   are clamped to N - 1 (their scores are masked).
   //  V^T: wave w fetches slot rows 4 w .. 4 w + 3 of the packed tile (1 KB each).
-  const int krow = 16 * w + l16;
   const int64_t krow_bytes = a.ks[2] * 2;
-  const int64_t kcol_bytes = 16 * g;
-  const int64_t koff = krow * krow_bytes + kcol_bytes;
   const int64_t kblk_bytes = BS * krow_bytes;
+  const int ksub = lane >> 4;  // row inside the instruction's 4-row group
+  uint32_t koff[4];            // lane byte offsets inside a full key block
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    koff[r] = static_cast<uint32_t>((16 * w + 4 * r + ksub) * krow_bytes +
+                                    16 * (l16 ^ ((4 * r + ksub) & 15)));
   const int voff = w * 4096 + 16 * lane;
   auto stage = [&](int j, u32x4* kst, u32x4* vst) {
-    const char* kp;
-    if ((j + 1) * BS <= N) {
-      kp = kbytes + j * kblk_bytes + koff;
-    } else {
-      const int tk = j * BS + krow < N ? j * BS + krow : N - 1;
-      kp = kbytes + tk * krow_bytes + kcol_bytes;
-    }
     char* kl = reinterpret_cast<char*>(kst) + w * 4096;
-    __builtin_amdgcn_global_load_lds(kp, (lds_void*)kl, 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(kp, (lds_void*)(kl + 1024 - 64), 16, 64, 0);
-    __builtin_amdgcn_global_load_lds(kp, (lds_void*)(kl + 2048 - 128), 16, 128, 0);
-    __builtin_amdgcn_global_load_lds(kp, (lds_void*)(kl + 3072 - 192), 16, 192, 0);
+    if ((j + 1) * BS <= N) {
+      const char* kbj = kbytes + j * kblk_bytes;
+      dma16<0>(kbj + koff[0], kl);
+      dma16<0>(kbj + koff[1], kl + 1024);
+      dma16<0>(kbj + koff[2], kl + 2048);
+      dma16<0>(kbj + koff[3], kl + 3072);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = j * BS + 16 * w + 4 * r + ksub;
+        const int64_t rb = (row < N ? row : N - 1) * krow_bytes;
+        const char* kp = kbytes + rb + 16 * (l16 ^ ((4 * r + ksub) & 15));
+        if (r == 0) dma16<0>(kp, kl);
+        if (r == 1) dma16<0>(kp, kl + 1024);
+        if (r == 2) dma16<0>(kp, kl + 2048);
+        if (r == 3) dma16<0>(kp, kl + 3072);
+      }
+    }
     const char* vp = vtbytes + static_cast<int64_t>(j) * TILE_BYTES + voff;
     char* vl = reinterpret_cast<char*>(vst) + w * 4096;
-    __builtin_amdgcn_global_load_lds(vp, (lds_void*)vl, 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(vp, (lds_void*)vl, 16, 1024, 0);
-    __builtin_amdgcn_global_load_lds(vp, (lds_void*)vl, 16, 2048, 0);
-    __builtin_amdgcn_global_load_lds(vp, (lds_void*)vl, 16, 3072, 0);
+    dma16<0>(vp, vl);
+    dma16<1024>(vp, vl);
+    dma16<2048>(vp, vl);
+    dma16<3072>(vp, vl);
   };
+
+  // K operand (key 32 kh + 16 tt + l % 16, dims 32 ds + 8 g .. +8) inside a
+  // stage: row R = 32 kh + 16 tt + l % 16 (R % 16 = l % 16), chunk 4 ds + g.
+  uint32_t kread[4];
+#pragma unroll
+  for (int ds = 0; ds < 4; ++ds) kread[ds] = 256 * (32 * kh + l16) + 16 * ((4 * ds + g) ^ l16);
 
   // Q^T as the B operand: qreg[qt][ds] = Q[32 qh + 16 qt + l % 16][32 ds + 8 g .. +8].
   u32x4 qreg[2][4];
@@ -286,13 +313,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
         jnext = entry(p + 1);
         stage(block_of(jnext), stage_k(PAR ^ 1), stage_v(PAR ^ 1));
       }
-      const u32x4* ks = stage_k(PAR);
+      const char* ks = reinterpret_cast<const char*>(stage_k(PAR));
       const u32x4* vts = stage_v(PAR);
       u32x4 kop[4][2], vop[8];
 #pragma unroll
       for (int ds = 0; ds < 4; ++ds)
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) kop[ds][tt] = ks[((2 * kh + tt) * 4 + ds) * 64 + lane];
+        for (int tt = 0; tt < 2; ++tt)
+          kop[ds][tt] = *reinterpret_cast<const u32x4*>(ks + kread[ds] + 4096 * tt);
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) vop[dt] = vts[(dt * 2 + kh) * 64 + lane];
 
@@ -478,6 +506,9 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
   CAB_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, CAB_EWORKSPACE,
               "cab_block_sparse_attn_fwd: workspace not 16-byte aligned");
   const int64_t total = B * H * M;
+  CAB_REQUIRE(k_strides[2] <= (int64_t{1} << 24), CAB_ESHAPE,
+              "cab_block_sparse_attn_fwd: k token stride %lld too large (<= 2^24 elements)",
+              (long long)k_strides[2]);
   CAB_REQUIRE(total <= INT32_MAX && B * H <= 65535 && N <= INT32_MAX - BS, CAB_ESHAPE,
               "cab_block_sparse_attn_fwd: problem too large (B*H <= 65535, B*H*M < 2^31, "
               "N < 2^31 - 64)");
