@@ -5,16 +5,20 @@ TFLOP/s, % of roofline".
 
 - ``value``: block-sparse attention throughput at BASELINE config 4
   (CABAttention forward, causal, bf16, B=1 H=32 N=65536 D=128, block_size 64,
-  sparsity 0.95): useful kept-tile TFLOP per second of the executor kernel,
-  with Q/K/V and the predictor's block lists resident in HBM. One step = one
-  executor launch over the whole batch.
+  sparsity 0.95): useful kept-tile TFLOP per second of one executor step
+  (V packing + the attention kernel), with Q/K/V and the predictor's block
+  lists resident in HBM. One step = one ``cab_block_sparse_attn_fwd`` call.
+- ``roofline``: the attention kernel alone (``cab_block_sparse_attn_fwd_packed``
+  on pre-packed V) against the bf16 dense MFMA peak, timed with HIP events on
+  the launch stream; ``traffic`` from the committed rocprofv3 PMC summary.
 - ``predictor``: latency of CoarseCurvaturePredictor.forward (coarsen + FRC +
-  mask, dense bool mask out) at config 3 (B=2 H=8 N=128000 D=128), plus the
-  per-stage times and the config-4 predictor + attention end-to-end time.
-- ``roofline``: the executor against the bf16 dense MFMA peak, from HIP events
-  on the launch stream; ``traffic`` from the committed rocprofv3 PMC summary.
-- ``cpu_baseline``: the float64 numpy oracle on a bounded sample of the same
-  workload, on this host's cores.
+  mask, dense bool mask out) at config 3 (B=2 H=8 N=128000 D=128), per-stage
+  times and the config-4 predictor + attention end-to-end time.
+- ``bridge``: config 5 (structured bridge stress test, B=1 H=8 N=131072,
+  sparsity 0.99): planted bridges kept, mask agreement with the CPU oracle on
+  two heads, predictor + attention latency.
+- ``cpu_baseline``: the float64 numpy oracle on a bounded sample of the
+  config-4 attention workload, on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -86,9 +90,8 @@ def blas_threads() -> int:
     return os.cpu_count() or 1
 
 
-def cpu_attention_baseline(q, k, v, idx, cnt, heads, rows, flops_fn):
-    """Oracle block-sparse attention on a sample of (head, query block) rows."""
-    import numpy as np
+def cpu_attention_baseline(q, k, v, idx, cnt, heads, flops_fn):
+    """Oracle block-sparse attention on every query block of a few heads."""
     from oracle import cab_oracle as O
     hs = list(heads)
     qs = q[:, hs].float().cpu().numpy()
@@ -97,11 +100,9 @@ def cpu_attention_baseline(q, k, v, idx, cnt, heads, rows, flops_fn):
     ii = idx[:, hs].cpu().numpy()
     cc = cnt[:, hs].cpu().numpy()
     t0 = time.perf_counter()
-    O.sparse_attention(qs, ks, vs, ii, cc, 64, causal=True, query_blocks=rows)
+    O.sparse_attention(qs, ks, vs, ii, cc, 64, causal=True)
     dt = time.perf_counter() - t0
-    sel = np.zeros_like(cc, dtype=bool)
-    sel[..., rows] = True
-    flops = flops_fn(ii, cc, sel)
+    flops = flops_fn(ii, cc)
     return flops / dt / 1e12, dt, flops
 
 
@@ -118,13 +119,95 @@ def cpu_predictor_baseline(q, k, block_size, sparsity):
     return time.perf_counter() - t0
 
 
+def bridge_inputs(B, H, N, D, seed, dev, dtype, bs=64, clusters=16, run_blocks=64, noise=0.1,
+                  n_bridges=4, bridge_scale=0.05):
+    """Config 5: clustered keys/queries with planted low-magnitude bridges.
+
+    Per (b, h): ``clusters`` centres ~ N(0, I_D); key block m belongs to run
+    ``m // run_blocks`` and takes centre ``run % clusters``; every token is its
+    centre plus ``noise`` * N(0, 1) (queries and keys drawn separately).
+    ``n_bridges`` (query block i, key block j) pairs from a seeded permutation,
+    with j in a different cluster than i, get ``K[j block] = bridge_scale *
+    Q[i block]``. Returns ``q, k, pairs``.
+    """
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    M = (N + bs - 1) // bs
+    centres = torch.randn((B, H, clusters, D), generator=g, device=dev)
+    cl = (torch.arange(M, device=dev) // run_blocks) % clusters
+    tok = cl.repeat_interleave(bs)[:N]
+    base = centres[:, :, tok]
+    q = base + noise * torch.randn((B, H, N, D), generator=g, device=dev)
+    k = base + noise * torch.randn((B, H, N, D), generator=g, device=dev)
+    del base
+    perm = torch.randperm(M, generator=g, device=dev).tolist()
+    clh = cl.tolist()
+    used, pairs = set(), []
+    for i in perm:
+        if i in used:
+            continue
+        j = next((x for x in perm if x not in used and x != i and clh[x] != clh[i]), None)
+        if j is None:
+            continue
+        pairs.append((i, j))
+        used |= {i, j}
+        if len(pairs) == n_bridges:
+            break
+    for i, j in pairs:
+        k[:, :, j * bs:(j + 1) * bs] = bridge_scale * q[:, :, i * bs:(i + 1) * bs]
+    return q.to(dtype), k.to(dtype), pairs
+
+
+def mask_agreement(gpu_mask, gpu_frc, of, omask, keep, keep_diag=True, causal=False):
+    """Fraction of identical mask entries, and the number of differing entries
+    whose oracle FRC is not within the GPU/oracle score difference of the
+    row's selection threshold (0 means every difference is a near-tie)."""
+    import numpy as np
+    gm = gpu_mask.cpu().numpy()
+    diff = gm != omask
+    gf = gpu_frc.float().cpu().numpy()
+    B, H, M, _ = of.shape
+    far = 0
+    for b, h, i in {(b, h, i) for b, h, i, _ in zip(*np.nonzero(diff))}:
+        ncand = i + 1 if causal else M
+        cand = [j for j in range(ncand) if not (keep_diag and j == i)]
+        need = min(keep, ncand) - (1 if keep_diag else 0)
+        vals = np.sort(of[b, h, i, cand])
+        theta = vals[need - 1] if need > 0 else None
+        delta = 8 * np.abs(gf[b, h, i] - of[b, h, i]).max() + 1e-7 * np.abs(of[b, h, i]).max()
+        for j in np.flatnonzero(diff[b, h, i]):
+            if theta is None or abs(of[b, h, i, j] - theta) > delta:
+                far += 1
+    return float(1.0 - diff.mean()), far
+
+
+def predictor_only(args, dev, bs, D) -> int:
+    """Config-3 predictor timing alone (one JSON line, no headline fields)."""
+    import torch
+    from cab_attention import CoarseCurvaturePredictor
+    B3, H3, N3 = 2, 8, 128000
+    q3 = seeded_gpu((B3, H3, N3, D), 1, torch.bfloat16, dev)
+    k3 = seeded_gpu((B3, H3, N3, D), 2, torch.bfloat16, dev)
+    pred3 = CoarseCurvaturePredictor(block_size=bs, sparsity=0.95, lambda_redundancy=0.5)
+    for _ in range(args.warmup):
+        pred3(q3, k3)
+    ms = time_events(lambda: pred3(q3, k3), args.steps)
+    print(json.dumps({"predictor_config3_ms": round(ms, 4), "steps": args.steps}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--attn-only", action="store_true", help="skip the predictor section")
+    ap.add_argument("--cpu-heads", type=int, default=8,
+                    help="config-4 heads the CPU baseline runs (every query block of each)")
+    ap.add_argument("--attn-only", action="store_true",
+                    help="skip the predictor and bridge sections")
+    ap.add_argument("--predictor-only", action="store_true",
+                    help="only time the config-3 predictor (for per-kernel profiles)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -148,12 +231,15 @@ def main() -> int:
         return 0
 
     from cab_attention import CoarseCurvaturePredictor
-    from cab_attention.kernels import (block_sparse_attention, coarsen_qk_max_l2,
-                                       compute_block_frc, generate_block_index, kept_tile_flops)
+    from cab_attention.kernels import (block_sparse_attention, block_sparse_attention_packed,
+                                       coarsen_qk_max_l2, compute_block_frc,
+                                       generate_block_index, kept_tile_flops, pack_v)
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     bs, D = 64, 128
+    if args.predictor_only:
+        return predictor_only(args, dev, bs, D)
 
     # ---------------- config 4: predictor (causal) + block-sparse attention
     B, H, N, sp = 1, 32, 65536, 0.95
@@ -166,21 +252,35 @@ def main() -> int:
     idx, cnt = pred4.predict_index(q, k)
     torch.cuda.synchronize()
     flops = kept_tile_flops(idx, cnt, bs, D, N, causal=True)
+    tiles = int(cnt.sum().item())
     out = torch.empty_like(q)
-    attn = lambda: block_sparse_attention(q, k, v, idx, cnt, bs, causal=True, out=out)
-    for _ in range(args.warmup):
-        attn()
-    torch.cuda.synchronize()
-    log(f"timing {args.steps} executor steps ({flops / 1e12:.3f} TFLOP useful each)")
-    attn_ms = time_events(attn, args.steps)
-    attn_tflops = flops / (attn_ms * 1e-3) / 1e12
+    # predictor + attention end to end first: it also brings the clocks up
+    # before the timed executor steps
     e2e = lambda: block_sparse_attention(q, k, v, *pred4.predict_index(q, k), bs, causal=True,
                                          out=out)
     e2e()
     e2e_ms = time_events(e2e, max(3, args.steps // 4))
-    log(f"attention {attn_ms:.3f} ms = {attn_tflops:.1f} TFLOP/s; e2e {e2e_ms:.3f} ms")
+    attn = lambda: block_sparse_attention(q, k, v, idx, cnt, bs, causal=True, out=out)
+    for _ in range(args.warmup):
+        attn()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} executor steps ({flops / 1e12:.3f} TFLOP useful, {tiles} tiles)")
+    attn_ms = time_events(attn, args.steps)
+    attn_tflops = flops / (attn_ms * 1e-3) / 1e12
+    # the attention kernel alone, on pre-packed V (roofline)
+    vt = pack_v(v, bs)
+    kern = lambda: block_sparse_attention_packed(q, k, vt, idx, cnt, bs, causal=True, out=out)
+    for _ in range(args.warmup):
+        kern()
+    kern_ms = time_events(kern, args.steps)
+    kern_tflops = flops / (kern_ms * 1e-3) / 1e12
+    pack_ms = time_events(lambda: pack_v(v, bs), args.steps)
+    log(f"step {attn_ms:.3f} ms = {attn_tflops:.1f} TFLOP/s; kernel {kern_ms:.3f} ms = "
+        f"{kern_tflops:.1f} TFLOP/s; pack_v {pack_ms:.3f} ms; e2e {e2e_ms:.3f} ms")
+    del vt
 
     result_pred = None
+    result_bridge = None
     if not args.attn_only:
         # ---------------- config 3: predictor latency at N = 128k
         B3, H3, N3 = 2, 8, 128000
@@ -211,8 +311,12 @@ def main() -> int:
             "stages_ms": {"coarsen": round(st_coarsen, 4), "frc": round(st_frc, 4),
                           "mask": round(st_mask, 4)},
             "coarsen_GBps": round(coarsen_bytes / (st_coarsen * 1e-3) / 1e9, 1),
+            "coarsen_frac_hbm": round(coarsen_bytes / (st_coarsen * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
             "frc_TFLOPs": round((tri_flops + aff_flops) / (st_frc * 1e-3) / 1e12, 1),
+            "frc_frac_mfma": round((tri_flops + aff_flops) / (st_frc * 1e-3) / 1e12
+                                   / PEAK_BF16_TFLOPS, 4),
             "mask_GBps": round(mask_bytes / (st_mask * 1e-3) / 1e9, 1),
+            "mask_frac_hbm": round(mask_bytes / (st_mask * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
             "config4_predictor_plus_attention_ms": round(e2e_ms, 4),
         }
         log(f"predictor {pred_ms:.3f} ms (coarsen {st_coarsen:.3f}, frc {st_frc:.3f}, "
@@ -224,31 +328,65 @@ def main() -> int:
         del q3, k3, qc, kc, f3
         torch.cuda.empty_cache()
 
+        # ---------------- config 5: structured bridge stress test
+        B5, H5, N5, sp5 = 1, 8, 131072, 0.99
+        log("config5 bridge inputs")
+        q5, k5, pairs = bridge_inputs(B5, H5, N5, D, 5, dev, torch.bfloat16)
+        v5 = seeded_gpu((B5, H5, N5, D), 6, torch.bfloat16, dev)
+        pred5 = CoarseCurvaturePredictor(block_size=bs, sparsity=sp5, lambda_redundancy=0.5)
+        out5 = torch.empty_like(q5)
+        run5 = lambda: block_sparse_attention(q5, k5, v5, *pred5.predict_index(q5, k5), bs,
+                                              out=out5)
+        run5()
+        e2e5_ms = time_events(run5, max(3, args.steps // 4))
+        mask5, diag5 = pred5(q5, k5, return_diagnostics=True)
+        kept = [[bool(mask5[0, h, i, j].item()) for (i, j) in pairs] for h in range(H5)]
+        result_bridge = {
+            "config": "config5: B=1 H=8 N=131072 D=128 bs=64 s=0.99 lambda=0.5 bf16; 16 "
+                      "clusters in runs of 64 blocks, noise 0.1, 4 planted bridges "
+                      "K[j] = 0.05 Q[i]",
+            "bridges_qblock_kblock": pairs,
+            "bridges_kept_per_head": [sum(r) for r in kept],
+            "bridges_kept_total": f"{sum(sum(r) for r in kept)}/{len(pairs) * H5}",
+            "predictor_plus_attention_ms": round(e2e5_ms, 4),
+            "effective_sparsity": round(diag5["effective_sparsity"], 5),
+        }
+        if not args.no_cpu:
+            from oracle import cab_oracle as O
+            heads5 = [0, 1]
+            qh = q5[:, heads5].float().cpu().numpy()
+            kh = k5[:, heads5].float().cpu().numpy()
+            qc5, _ = O.coarsen_max_l2(qh, bs)
+            kc5, _ = O.coarsen_max_l2(kh, bs)
+            of5, _, _ = O.compute_block_frc(qc5, kc5, lambda_redundancy=0.5)
+            om5, _, _ = O.generate_block_mask(of5, sp5)
+            agree, far = mask_agreement(mask5[:, heads5], diag5["frc_scores"][:, heads5], of5,
+                                        om5, O.keep_count(om5.shape[-1], sp5))
+            okept = [[bool(om5[0, hh, i, j]) for (i, j) in pairs] for hh in range(len(heads5))]
+            result_bridge["mask_agreement_vs_oracle"] = round(agree, 6)
+            result_bridge["mask_diffs_not_near_threshold"] = far
+            result_bridge["oracle_heads"] = heads5
+            result_bridge["oracle_bridges_kept"] = [sum(r) for r in okept]
+        log(f"bridge: kept {result_bridge['bridges_kept_total']}, e2e {e2e5_ms:.3f} ms")
+        del q5, k5, v5, out5, mask5, diag5
+        torch.cuda.empty_cache()
+
     cpu = None
     if not args.no_cpu:
-        M = N // bs
-        rows = list(range(M - 48, M))  # full-length causal rows
-        heads = [0, 17]
+        heads = list(range(0, H, max(1, H // args.cpu_heads)))[:args.cpu_heads]
 
-        def sample_flops(ii, cc, sel):
-            tiles = 0
-            diag = 0
-            for b in range(ii.shape[0]):
-                for h in range(ii.shape[1]):
-                    for i in np.flatnonzero(sel[b, h]):
-                        js = ii[b, h, i, :cc[b, h, i]]
-                        tiles += len(js)
-                        diag += int((js == i).sum())
-            return (tiles - diag) * 4 * bs * bs * D + diag * 2 * bs * (bs + 1) * D
+        def sample_flops(ii, cc):
+            t = torch.from_numpy(ii)
+            c = torch.from_numpy(cc)
+            return kept_tile_flops(t, c, bs, D, N, causal=True)
 
-        log("cpu baseline: oracle attention sample")
-        tfl, secs, fl = cpu_attention_baseline(q, k, v, idx, cnt, heads, rows, sample_flops)
+        log(f"cpu baseline: oracle attention on heads {heads}")
+        tfl, secs, fl = cpu_attention_baseline(q, k, v, idx, cnt, heads, sample_flops)
         cpu = {"value": round(tfl, 6), "unit": "TFLOP/s", "cores": blas_threads(),
                "kind": "port",
-               "sample": f"float64 numpy oracle, heads {heads} x query blocks {rows[0]}-{rows[-1]} "
-                         f"of config 4 ({fl / 1e9:.1f} GFLOP useful in {secs:.1f} s)"}
+               "sample": f"float64 numpy oracle, every query block of heads {heads} of config 4 "
+                         f"({fl / 1e9:.1f} GFLOP useful in {secs:.1f} s)"}
 
-    achieved = attn_tflops
     traffic = read_traffic()
     line = {
         "metric": METRIC,
@@ -266,12 +404,15 @@ def main() -> int:
         "config": {"workload": "config4: CABAttention causal block-sparse executor, B=1 H=32 "
                                "N=65536 D=128 bs=64 sparsity=0.95, predictor block lists",
                    "B": B, "H": H, "N": N, "D": D, "block_size": bs, "sparsity": sp,
-                   "causal": True, "useful_tflop_per_step": round(flops / 1e12, 4)},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                   "causal": True, "kept_tiles": tiles,
+                   "useful_tflop_per_step": round(flops / 1e12, 4),
+                   "pack_v_ms": round(pack_ms, 4), "attn_kernel_ms": round(kern_ms, 4)},
+        "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(kern_tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic},
         "cpu_baseline": cpu,
         "predictor": result_pred,
+        "bridge": result_bridge,
     }
     print(json.dumps(line), flush=True)
     return 0

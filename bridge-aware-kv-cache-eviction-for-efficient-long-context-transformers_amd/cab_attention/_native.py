@@ -44,6 +44,12 @@ SIGNATURES = {
                                                  _i64, _i64x4, _i64x4, _i64x4, _i64x4, _i32, _ptr,
                                                  _ptr, _i32, _f32, ctypes.c_int, _ptr, _ptr, _ptr,
                                                  ctypes.c_size_t, _ptr]),
+    "cab_block_sparse_attn_pack_v": (ctypes.c_int, [_ptr, ctypes.c_int, _i64, _i64, _i64, _i64,
+                                                    _i64x4, _i32, _ptr, ctypes.c_size_t, _ptr]),
+    "cab_block_sparse_attn_fwd_packed": (ctypes.c_int, [_ptr, _ptr, _ptr, ctypes.c_int, _i64, _i64,
+                                                        _i64, _i64, _i64x4, _i64x4, _i64x4, _i32,
+                                                        _ptr, _ptr, _i32, _f32, ctypes.c_int, _ptr,
+                                                        _ptr, ctypes.c_size_t, _ptr]),
 }
 
 _lock = threading.Lock()

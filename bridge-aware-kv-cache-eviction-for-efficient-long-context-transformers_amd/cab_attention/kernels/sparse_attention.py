@@ -16,6 +16,26 @@ import torch
 from .. import _native as nat
 
 
+def _check_lists(kv_idx, kv_cnt, B, H, M):
+    if kv_idx.dim() != 4 or tuple(kv_idx.shape[:3]) != (B, H, M):
+        raise ValueError(f"kv_idx must be [B, H, M={M}, kmax]; got {tuple(kv_idx.shape)}")
+    if tuple(kv_cnt.shape) != (B, H, M):
+        raise ValueError(f"kv_cnt must be [B, H, M={M}]; got {tuple(kv_cnt.shape)}")
+    if kv_idx.dtype != torch.int32 or kv_cnt.dtype != torch.int32:
+        raise TypeError("kv_idx and kv_cnt must be int32")
+    return kv_idx.contiguous(), kv_cnt.contiguous()
+
+
+def _outputs(q, out, return_lse, dev):
+    B, H, N, D = q.shape
+    if out is None:
+        out = torch.empty((B, H, N, D), dtype=q.dtype, device=dev)
+    elif tuple(out.shape) != (B, H, N, D) or out.dtype != q.dtype:
+        raise ValueError("out must match q's shape and dtype")
+    lse = torch.empty((B, H, N), dtype=torch.float32, device=dev) if return_lse else None
+    return out, lse
+
+
 def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                            kv_idx: torch.Tensor, kv_cnt: torch.Tensor, block_size: int = 64,
                            causal: bool = False, scale: float | None = None,
@@ -41,22 +61,11 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     dt = nat.dtype_code(q)
     B, H, N, D = q.shape
     M = (N + block_size - 1) // block_size
-    if kv_idx.dim() != 4 or tuple(kv_idx.shape[:3]) != (B, H, M):
-        raise ValueError(f"kv_idx must be [B, H, M={M}, kmax]; got {tuple(kv_idx.shape)}")
-    if tuple(kv_cnt.shape) != (B, H, M):
-        raise ValueError(f"kv_cnt must be [B, H, M={M}]; got {tuple(kv_cnt.shape)}")
-    if kv_idx.dtype != torch.int32 or kv_cnt.dtype != torch.int32:
-        raise TypeError("kv_idx and kv_cnt must be int32")
-    kv_idx = kv_idx.contiguous()
-    kv_cnt = kv_cnt.contiguous()
+    kv_idx, kv_cnt = _check_lists(kv_idx, kv_cnt, B, H, M)
     q = nat.aligned_rows(q)
     k = nat.aligned_rows(k)
     v = nat.aligned_rows(v)
-    if out is None:
-        out = torch.empty((B, H, N, D), dtype=q.dtype, device=dev)
-    elif tuple(out.shape) != (B, H, N, D) or out.dtype != q.dtype:
-        raise ValueError("out must match q's shape and dtype")
-    lse = torch.empty((B, H, N), dtype=torch.float32, device=dev) if return_lse else None
+    out, lse = _outputs(q, out, return_lse, dev)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     wbytes = lib.cab_block_sparse_attn_workspace_bytes(B, H, N, D, int(block_size))
@@ -69,6 +78,61 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             int(bool(causal)), out.data_ptr(), nat.ptr(lse), ws.data_ptr(), ws.numel(),
             nat.stream_ptr(dev))
     nat.check("cab_block_sparse_attn_fwd", st)
+    return (out, lse) if return_lse else out
+
+
+def pack_v(v: torch.Tensor, block_size: int = 64) -> torch.Tensor:
+    """V ``[B, H, N, D]`` -> its packed V^T tiles (uint8, 16 KB per (b, h, key
+    block)) for :func:`block_sparse_attention_packed`; reusable while V is
+    unchanged."""
+    if v.dim() != 4:
+        raise ValueError(f"v must be [B, H, N, D]; got {tuple(v.shape)}")
+    dev = nat.require_device(v)
+    lib = nat.load()
+    dt = nat.dtype_code(v)
+    B, H, N, D = v.shape
+    v = nat.aligned_rows(v)
+    wbytes = lib.cab_block_sparse_attn_workspace_bytes(B, H, N, D, int(block_size))
+    vt = torch.empty(max(int(wbytes), 16), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        st = lib.cab_block_sparse_attn_pack_v(v.data_ptr(), dt, B, H, N, D, nat.strides4(v),
+                                              int(block_size), vt.data_ptr(), vt.numel(),
+                                              nat.stream_ptr(dev))
+    nat.check("cab_block_sparse_attn_pack_v", st)
+    return vt
+
+
+def block_sparse_attention_packed(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor,
+                                  kv_idx: torch.Tensor, kv_cnt: torch.Tensor,
+                                  block_size: int = 64, causal: bool = False,
+                                  scale: float | None = None, out: torch.Tensor | None = None,
+                                  return_lse: bool = False):
+    """:func:`block_sparse_attention` with V given as :func:`pack_v`'s tiles."""
+    if q.dim() != 4 or q.shape != k.shape:
+        raise ValueError(f"q, k must share one [B, H, N, D] shape; got {tuple(q.shape)}, "
+                         f"{tuple(k.shape)}")
+    if q.dtype != k.dtype:
+        raise TypeError("q, k dtypes differ")
+    if vt.dtype != torch.uint8 or not vt.is_contiguous():
+        raise TypeError("vt must be the contiguous uint8 tensor pack_v returned")
+    dev = nat.require_device(q, k, vt, kv_idx, kv_cnt)
+    lib = nat.load()
+    dt = nat.dtype_code(q)
+    B, H, N, D = q.shape
+    M = (N + block_size - 1) // block_size
+    kv_idx, kv_cnt = _check_lists(kv_idx, kv_cnt, B, H, M)
+    q = nat.aligned_rows(q)
+    k = nat.aligned_rows(k)
+    out, lse = _outputs(q, out, return_lse, dev)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    with torch.cuda.device(dev):
+        st = lib.cab_block_sparse_attn_fwd_packed(
+            q.data_ptr(), k.data_ptr(), vt.data_ptr(), dt, B, H, N, D, nat.strides4(q),
+            nat.strides4(k), nat.strides4(out), int(block_size), kv_idx.data_ptr(),
+            kv_cnt.data_ptr(), int(kv_idx.shape[-1]), float(scale), int(bool(causal)),
+            out.data_ptr(), nat.ptr(lse), vt.numel(), nat.stream_ptr(dev))
+    nat.check("cab_block_sparse_attn_fwd_packed", st)
     return (out, lse) if return_lse else out
 
 

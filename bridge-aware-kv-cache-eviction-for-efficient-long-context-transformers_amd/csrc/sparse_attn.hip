@@ -457,78 +457,87 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
 
 using namespace cab;
 
-extern "C" size_t cab_block_sparse_attn_workspace_bytes(int64_t B, int64_t H, int64_t N,
-                                                        int64_t D, int32_t block_size) {
-  if (B <= 0 || H <= 0 || N <= 0 || D != HD || block_size != BS) return 0;
-  return static_cast<size_t>(B * H * ceil_div(N, BS)) * TILE_BYTES;
+namespace {
+
+// Shape and scalar checks shared by the three entry points.
+cab_status_t check_common(const char* fn, cab_dtype_t dtype, int64_t B, int64_t H, int64_t N,
+                          int64_t D, int32_t block_size) {
+  CAB_REQUIRE(dtype == CAB_BF16 || dtype == CAB_F16, CAB_EDTYPE,
+              "%s: dtype %d unsupported (bf16 or fp16)", fn, (int)dtype);
+  CAB_REQUIRE(B >= 0 && H >= 0 && N >= 0, CAB_ESHAPE, "%s: negative size", fn);
+  CAB_REQUIRE(D == HD, CAB_ESHAPE, "%s: head dim %lld unsupported (128)", fn, (long long)D);
+  CAB_REQUIRE(block_size == BS, CAB_ESHAPE, "%s: block_size %d unsupported (64)", fn,
+              (int)block_size);
+  const int64_t M = ceil_div(N, BS);
+  CAB_REQUIRE(B * H * M <= INT32_MAX && B * H <= 65535 && N <= INT32_MAX - BS, CAB_ESHAPE,
+              "%s: problem too large (B*H <= 65535, B*H*M < 2^31, N < 2^31 - 64)", fn);
+  return CAB_OK;
 }
 
-extern "C" cab_status_t cab_block_sparse_attn_fwd(
-    const void* q, const void* k, const void* v, cab_dtype_t dtype, int64_t B, int64_t H,
-    int64_t N, int64_t D, const int64_t q_strides[4], const int64_t k_strides[4],
-    const int64_t v_strides[4], const int64_t o_strides[4], int32_t block_size,
-    const int32_t* kv_idx, const int32_t* kv_cnt, int32_t kmax, float scale, int causal,
-    void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
-  clear_error();
-  CAB_REQUIRE(dtype == CAB_BF16 || dtype == CAB_F16, CAB_EDTYPE,
-              "cab_block_sparse_attn_fwd: dtype %d unsupported (bf16 or fp16)", (int)dtype);
-  CAB_REQUIRE(B >= 0 && H >= 0 && N >= 0, CAB_ESHAPE, "cab_block_sparse_attn_fwd: negative size");
-  CAB_REQUIRE(D == HD, CAB_ESHAPE, "cab_block_sparse_attn_fwd: head dim %lld unsupported (128)",
-              (long long)D);
-  CAB_REQUIRE(block_size == BS, CAB_ESHAPE,
-              "cab_block_sparse_attn_fwd: block_size %d unsupported (64)", (int)block_size);
-  CAB_REQUIRE(kmax >= 1, CAB_EINVAL, "cab_block_sparse_attn_fwd: kmax=%d must be >= 1", (int)kmax);
-  CAB_REQUIRE(std::isfinite(scale) && scale > 0.f, CAB_EINVAL,
-              "cab_block_sparse_attn_fwd: scale must be finite and > 0");
-  CAB_REQUIRE(q_strides && k_strides && v_strides && o_strides, CAB_EINVAL,
-              "cab_block_sparse_attn_fwd: null stride array");
-  const int64_t M = ceil_div(N, BS);
-  if (B == 0 || H == 0 || M == 0) return CAB_OK;
-  CAB_REQUIRE(q && k && v && out && kv_idx && kv_cnt, CAB_EINVAL,
-              "cab_block_sparse_attn_fwd: null tensor pointer");
-  const void* ptrs[4] = {q, k, v, out};
-  const int64_t* strides[4] = {q_strides, k_strides, v_strides, o_strides};
-  const char* names[4] = {"q", "k", "v", "out"};
-  for (int t = 0; t < 4; ++t) {
-    CAB_REQUIRE(strides[t][3] == 1, CAB_ESHAPE,
-                "cab_block_sparse_attn_fwd: %s last-dim stride must be 1", names[t]);
-    CAB_REQUIRE(reinterpret_cast<uintptr_t>(ptrs[t]) % 16 == 0, CAB_ESHAPE,
-                "cab_block_sparse_attn_fwd: %s not 16-byte aligned", names[t]);
-    for (int d = 0; d < 3; ++d)
-      CAB_REQUIRE(strides[t][d] >= 0 && (strides[t][d] * 2) % 16 == 0, CAB_ESHAPE,
-                  "cab_block_sparse_attn_fwd: %s stride[%d]=%lld must keep rows 16-byte aligned",
-                  names[t], d, (long long)strides[t][d]);
-  }
-  const size_t need = static_cast<size_t>(B * H * M) * TILE_BYTES;
-  CAB_REQUIRE(workspace != nullptr && workspace_bytes >= need, CAB_EWORKSPACE,
-              "cab_block_sparse_attn_fwd: workspace of %zu bytes given, %zu needed",
-              workspace_bytes, need);
-  CAB_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, CAB_EWORKSPACE,
-              "cab_block_sparse_attn_fwd: workspace not 16-byte aligned");
-  const int64_t total = B * H * M;
-  CAB_REQUIRE(k_strides[2] <= (int64_t{1} << 24), CAB_ESHAPE,
-              "cab_block_sparse_attn_fwd: k token stride %lld too large (<= 2^24 elements)",
-              (long long)k_strides[2]);
-  CAB_REQUIRE(total <= INT32_MAX && B * H <= 65535 && N <= INT32_MAX - BS, CAB_ESHAPE,
-              "cab_block_sparse_attn_fwd: problem too large (B*H <= 65535, B*H*M < 2^31, "
-              "N < 2^31 - 64)");
-  hipStream_t s = static_cast<hipStream_t>(stream);
+cab_status_t check_tensor(const char* fn, const char* name, const void* ptr,
+                          const int64_t* strides) {
+  CAB_REQUIRE(ptr != nullptr, CAB_EINVAL, "%s: null %s", fn, name);
+  CAB_REQUIRE(strides != nullptr, CAB_EINVAL, "%s: null %s strides", fn, name);
+  CAB_REQUIRE(strides[3] == 1, CAB_ESHAPE, "%s: %s last-dim stride must be 1", fn, name);
+  CAB_REQUIRE(reinterpret_cast<uintptr_t>(ptr) % 16 == 0, CAB_ESHAPE,
+              "%s: %s not 16-byte aligned", fn, name);
+  for (int d = 0; d < 3; ++d)
+    CAB_REQUIRE(strides[d] >= 0 && (strides[d] * 2) % 16 == 0, CAB_ESHAPE,
+                "%s: %s stride[%d]=%lld must keep rows 16-byte aligned", fn, name, d,
+                (long long)strides[d]);
+  return CAB_OK;
+}
 
+cab_status_t check_packed(const char* fn, const void* vt, size_t bytes, int64_t B, int64_t H,
+                          int64_t M) {
+  const size_t need = static_cast<size_t>(B * H * M) * TILE_BYTES;
+  CAB_REQUIRE(vt != nullptr && bytes >= need, CAB_EWORKSPACE,
+              "%s: workspace of %zu bytes given, %zu needed", fn, bytes, need);
+  CAB_REQUIRE(reinterpret_cast<uintptr_t>(vt) % 16 == 0, CAB_EWORKSPACE,
+              "%s: workspace not 16-byte aligned", fn);
+  return CAB_OK;
+}
+
+cab_status_t check_attn(const char* fn, const void* q, const void* k, const int64_t* q_strides,
+                        const int64_t* k_strides, const int64_t* o_strides, void* out,
+                        const int32_t* kv_idx, const int32_t* kv_cnt, int32_t kmax, float scale) {
+  CAB_REQUIRE(kmax >= 1, CAB_EINVAL, "%s: kmax=%d must be >= 1", fn, (int)kmax);
+  CAB_REQUIRE(std::isfinite(scale) && scale > 0.f, CAB_EINVAL, "%s: scale must be finite and > 0",
+              fn);
+  CAB_REQUIRE(kv_idx != nullptr && kv_cnt != nullptr, CAB_EINVAL, "%s: null block list", fn);
+  cab_status_t st;
+  if ((st = check_tensor(fn, "q", q, q_strides)) != CAB_OK) return st;
+  if ((st = check_tensor(fn, "k", k, k_strides)) != CAB_OK) return st;
+  if ((st = check_tensor(fn, "out", out, o_strides)) != CAB_OK) return st;
+  CAB_REQUIRE(k_strides[2] <= (int64_t{1} << 24), CAB_ESHAPE,
+              "%s: k token stride %lld too large (<= 2^24 elements)", fn, (long long)k_strides[2]);
+  return CAB_OK;
+}
+
+cab_status_t launch_pack(const char* fn, const void* v, const int64_t* v_strides, int64_t B,
+                         int64_t H, int64_t N, void* vt, hipStream_t s) {
   PackArgs p;
   p.v = static_cast<const uint16_t*>(v);
-  p.vt = static_cast<uint16_t*>(workspace);
+  p.vt = static_cast<uint16_t*>(vt);
   for (int d = 0; d < 3; ++d) p.vs[d] = v_strides[d];
   p.H = H;
   p.N = N;
-  p.M = M;
-  pack_vt_kernel<<<dim3(static_cast<unsigned>(M), static_cast<unsigned>(B * H)), 256, 0, s>>>(p);
-  cab_status_t st = launch_status("cab_block_sparse_attn_fwd/pack_vt");
-  if (st != CAB_OK) return st;
+  p.M = ceil_div(N, BS);
+  pack_vt_kernel<<<dim3(static_cast<unsigned>(p.M), static_cast<unsigned>(B * H)), 256, 0, s>>>(p);
+  return launch_status(fn);
+}
 
+cab_status_t launch_attn(const char* fn, const void* q, const void* k, const void* vt,
+                         cab_dtype_t dtype, int64_t B, int64_t H, int64_t N,
+                         const int64_t* q_strides, const int64_t* k_strides,
+                         const int64_t* o_strides, const int32_t* kv_idx, const int32_t* kv_cnt,
+                         int32_t kmax, float scale, int causal, void* out, float* lse,
+                         hipStream_t s) {
+  const int64_t M = ceil_div(N, BS);
   AttnArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k);
-  a.vt = static_cast<const uint16_t*>(workspace);
+  a.vt = static_cast<const uint16_t*>(vt);
   a.o = static_cast<uint16_t*>(out);
   a.lse = lse;
   for (int d = 0; d < 3; ++d) {
@@ -545,7 +554,7 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
   a.kmax = kmax;
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   a.causal = causal ? 1 : 0;
-  dim3 grid(static_cast<unsigned>(total));
+  const dim3 grid(static_cast<unsigned>(B * H * M));
   const bool list_lds = kmax <= LIST_MAX;
   if (dtype == CAB_BF16) {
     if (list_lds)
@@ -558,5 +567,79 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
     else
       attn_fwd_kernel<false, false><<<grid, 256, 0, s>>>(a);
   }
-  return launch_status("cab_block_sparse_attn_fwd");
+  return launch_status(fn);
+}
+
+}  // namespace
+
+extern "C" size_t cab_block_sparse_attn_workspace_bytes(int64_t B, int64_t H, int64_t N,
+                                                        int64_t D, int32_t block_size) {
+  if (B <= 0 || H <= 0 || N <= 0 || D != HD || block_size != BS) return 0;
+  return static_cast<size_t>(B * H * ceil_div(N, BS)) * TILE_BYTES;
+}
+
+extern "C" cab_status_t cab_block_sparse_attn_pack_v(const void* v, cab_dtype_t dtype, int64_t B,
+                                                     int64_t H, int64_t N, int64_t D,
+                                                     const int64_t v_strides[4],
+                                                     int32_t block_size, void* workspace,
+                                                     size_t workspace_bytes, void* stream) {
+  const char* fn = "cab_block_sparse_attn_pack_v";
+  clear_error();
+  cab_status_t st = check_common(fn, dtype, B, H, N, D, block_size);
+  if (st != CAB_OK) return st;
+  const int64_t M = ceil_div(N, BS);
+  if (B == 0 || H == 0 || M == 0) return CAB_OK;
+  if ((st = check_tensor(fn, "v", v, v_strides)) != CAB_OK) return st;
+  if ((st = check_packed(fn, workspace, workspace_bytes, B, H, M)) != CAB_OK) return st;
+  return launch_pack(fn, v, v_strides, B, H, N, workspace, static_cast<hipStream_t>(stream));
+}
+
+extern "C" cab_status_t cab_block_sparse_attn_fwd_packed(
+    const void* q, const void* k, const void* vt, cab_dtype_t dtype, int64_t B, int64_t H,
+    int64_t N, int64_t D, const int64_t q_strides[4], const int64_t k_strides[4],
+    const int64_t o_strides[4], int32_t block_size, const int32_t* kv_idx,
+    const int32_t* kv_cnt, int32_t kmax, float scale, int causal, void* out, float* lse,
+    size_t vt_bytes, void* stream) {
+  const char* fn = "cab_block_sparse_attn_fwd_packed";
+  clear_error();
+  cab_status_t st = check_common(fn, dtype, B, H, N, D, block_size);
+  if (st != CAB_OK) return st;
+  const int64_t M = ceil_div(N, BS);
+  if (B == 0 || H == 0 || M == 0) return CAB_OK;
+  if ((st = check_attn(fn, q, k, q_strides, k_strides, o_strides, out, kv_idx, kv_cnt, kmax,
+                       scale)) != CAB_OK)
+    return st;
+  if ((st = check_packed(fn, vt, vt_bytes, B, H, M)) != CAB_OK) return st;
+  return launch_attn(fn, q, k, vt, dtype, B, H, N, q_strides, k_strides, o_strides, kv_idx,
+                     kv_cnt, kmax, scale, causal, out, lse, static_cast<hipStream_t>(stream));
+}
+
+extern "C" cab_status_t cab_block_sparse_attn_fwd(
+    const void* q, const void* k, const void* v, cab_dtype_t dtype, int64_t B, int64_t H,
+    int64_t N, int64_t D, const int64_t q_strides[4], const int64_t k_strides[4],
+    const int64_t v_strides[4], const int64_t o_strides[4], int32_t block_size,
+    const int32_t* kv_idx, const int32_t* kv_cnt, int32_t kmax, float scale, int causal,
+    void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "cab_block_sparse_attn_fwd";
+  clear_error();
+  cab_status_t st = check_common(fn, dtype, B, H, N, D, block_size);
+  if (st != CAB_OK) return st;
+  CAB_REQUIRE(kmax >= 1, CAB_EINVAL, "%s: kmax=%d must be >= 1", fn, (int)kmax);
+  CAB_REQUIRE(std::isfinite(scale) && scale > 0.f, CAB_EINVAL, "%s: scale must be finite and > 0",
+              fn);
+  CAB_REQUIRE(q_strides && k_strides && v_strides && o_strides, CAB_EINVAL,
+              "%s: null stride array", fn);
+  const int64_t M = ceil_div(N, BS);
+  if (B == 0 || H == 0 || M == 0) return CAB_OK;
+  if ((st = check_attn(fn, q, k, q_strides, k_strides, o_strides, out, kv_idx, kv_cnt, kmax,
+                       scale)) != CAB_OK)
+    return st;
+  if ((st = check_tensor(fn, "v", v, v_strides)) != CAB_OK) return st;
+  if ((st = check_packed(fn, workspace, workspace_bytes, B, H, M)) != CAB_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if ((st = launch_pack("cab_block_sparse_attn_fwd/pack_v", v, v_strides, B, H, N, workspace, s)) !=
+      CAB_OK)
+    return st;
+  return launch_attn(fn, q, k, workspace, dtype, B, H, N, q_strides, k_strides, o_strides,
+                     kv_idx, kv_cnt, kmax, scale, causal, out, lse, s);
 }

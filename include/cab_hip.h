@@ -162,6 +162,35 @@ cab_status_t cab_block_sparse_attn_fwd(const void* q, const void* k, const void*
                                        int causal, void* out, float* lse, void* workspace,
                                        size_t workspace_bytes, void* stream);
 
+/*
+ * The two halves of cab_block_sparse_attn_fwd, for callers that run several
+ * executor passes over the same V (the packed tiles can be reused while V is
+ * unchanged) or time the attention kernel alone. No counterpart in the
+ * reference: its executor has no V preparation step.
+ *
+ * cab_block_sparse_attn_pack_v: writes V's packed V^T tiles (16 KB per
+ * (b, h, key block), zero past N) into `workspace`
+ * (cab_block_sparse_attn_workspace_bytes() bytes, 16-byte aligned).
+ */
+cab_status_t cab_block_sparse_attn_pack_v(const void* v, cab_dtype_t dtype, int64_t B, int64_t H,
+                                          int64_t N, int64_t D, const int64_t v_strides[4],
+                                          int32_t block_size, void* workspace,
+                                          size_t workspace_bytes, void* stream);
+
+/*
+ * cab_block_sparse_attn_fwd_packed: cab_block_sparse_attn_fwd with V given
+ * as the tiles cab_block_sparse_attn_pack_v wrote (`vt`, `vt_bytes` bytes).
+ * Same arguments, rules and result otherwise.
+ */
+cab_status_t cab_block_sparse_attn_fwd_packed(const void* q, const void* k, const void* vt,
+                                              cab_dtype_t dtype, int64_t B, int64_t H, int64_t N,
+                                              int64_t D, const int64_t q_strides[4],
+                                              const int64_t k_strides[4],
+                                              const int64_t o_strides[4], int32_t block_size,
+                                              const int32_t* kv_idx, const int32_t* kv_cnt,
+                                              int32_t kmax, float scale, int causal, void* out,
+                                              float* lse, size_t vt_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,7 +33,8 @@ def test_header_declares_the_hot_path():
     syms = declared_symbols()
     for name in ("cab_abi_version", "cab_last_error", "cab_coarsen_maxl2",
                  "cab_block_frc_workspace_bytes", "cab_block_frc", "cab_block_topk",
-                 "cab_block_sparse_attn_workspace_bytes", "cab_block_sparse_attn_fwd"):
+                 "cab_block_sparse_attn_workspace_bytes", "cab_block_sparse_attn_fwd",
+                 "cab_block_sparse_attn_pack_v", "cab_block_sparse_attn_fwd_packed"):
         assert name in syms
     assert set(syms) == set(nat.SIGNATURES), "ctypes table and header disagree"
 
@@ -115,6 +116,18 @@ def test_attention_validation(lib):
     assert call(os=_s4(1, 1, 1, 3)) == nat.CAB_ESHAPE
     assert call(wsb=1024) == nat.CAB_EWORKSPACE
     assert call(ws=None) == nat.CAB_EWORKSPACE
+    pack = lambda **kw: lib.cab_block_sparse_attn_pack_v(
+        kw.get("v", FAKE), nat.CAB_BF16, 1, 8, 64, kw.get("D", 128), st, 64, FAKE,
+        kw.get("wsb", 1 << 30), None)
+    assert pack(D=64) == nat.CAB_ESHAPE
+    assert pack(v=None) == nat.CAB_EINVAL
+    assert pack(wsb=100) == nat.CAB_EWORKSPACE
+    packed = lambda **kw: lib.cab_block_sparse_attn_fwd_packed(
+        FAKE, FAKE, kw.get("vt", FAKE), nat.CAB_BF16, 1, 8, 64, 128, st, st, st, 64, FAKE, FAKE,
+        kw.get("kmax", 3), 0.088, 1, FAKE, None, kw.get("vtb", 1 << 30), None)
+    assert packed(kmax=0) == nat.CAB_EINVAL
+    assert packed(vt=None) == nat.CAB_EWORKSPACE
+    assert packed(vtb=8 * 16384 - 1) == nat.CAB_EWORKSPACE
 
 
 def test_python_layer_refuses_cpu_tensors(lib):

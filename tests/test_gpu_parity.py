@@ -309,6 +309,27 @@ def test_attention_wide_dynamic_range(cuda, causal):
     assert err <= 2e-2, f"max abs error {err}"
 
 
+def test_attention_packed_path_matches_fused(cuda):
+    """pack_v + block_sparse_attention_packed give the same bits as the fused
+    entry point, and the packed V can be reused for a second call."""
+    from cab_attention.kernels import (block_sparse_attention, block_sparse_attention_packed,
+                                       pack_v)
+    B, H, N, D, bs = 2, 2, 1000, 128, 64
+    q, k, v = (seeded((B, H, N, D), s, torch.bfloat16).to(cuda) for s in (21, 22, 23))
+    M = (N + bs - 1) // bs
+    f = np.random.default_rng(9).standard_normal((B, H, M, M)).astype(np.float32)
+    _, idx, cnt = O.generate_block_mask(f, 0.6, causal=True)
+    idx, cnt = torch.from_numpy(idx).to(cuda), torch.from_numpy(cnt).to(cuda)
+    ref, ref_lse = block_sparse_attention(q, k, v, idx, cnt, bs, causal=True, return_lse=True)
+    vt = pack_v(v, bs)
+    for _ in range(2):
+        got, lse = block_sparse_attention_packed(q, k, vt, idx, cnt, bs, causal=True,
+                                                 return_lse=True)
+        assert torch.equal(got, ref) and torch.equal(lse, ref_lse)
+    with pytest.raises(ValueError):
+        block_sparse_attention_packed(q, k, vt[:-16], idx, cnt, bs, causal=True)
+
+
 def test_attention_empty_rows_and_bad_indices(cuda):
     from cab_attention.kernels import block_sparse_attention
     B, H, N, D, bs = 1, 1, 256, 128, 64
@@ -373,3 +394,39 @@ def test_attention_config4_sampled(cuda):
         for i in rows:
             err = np.abs(got[0, 0, 64 * i:64 * i + 64] - want[0, 0, 64 * i:64 * i + 64]).max()
             assert err <= 2e-2, f"head {h} block {i}: {err}"
+
+
+# ---------------------------------------------------------------------------
+# Config 5 (structured bridge stress test), reduced size
+# ---------------------------------------------------------------------------
+
+def test_bridge_stress_matches_oracle(cuda):
+    """Clustered Q/K with planted low-magnitude bridges: the GPU predictor's
+    mask agrees with the oracle's (differences only at near-ties) and keeps
+    exactly the bridges the oracle keeps."""
+    import bench
+    from cab_attention import CoarseCurvaturePredictor
+    from cab_attention.kernels import block_sparse_attention
+    B, H, N, D, sp = 1, 2, 16384, 128, 0.95
+    q, k, pairs = bench.bridge_inputs(B, H, N, D, 5, cuda, torch.bfloat16)
+    assert len(pairs) == 4
+    pred = CoarseCurvaturePredictor(block_size=64, sparsity=sp, lambda_redundancy=0.5)
+    mask, diag = pred(q, k, return_diagnostics=True)
+    qc, _ = O.coarsen_max_l2(np32(q), 64)
+    kc, _ = O.coarsen_max_l2(np32(k), 64)
+    of, _, _ = O.compute_block_frc(qc, kc, lambda_redundancy=0.5)
+    om, oidx, ocnt = O.generate_block_mask(of, sp)
+    agree, far = bench.mask_agreement(mask, diag["frc_scores"], of, om, O.keep_count(om.shape[-1], sp))
+    assert far == 0 and agree >= 0.99
+    for h in range(H):
+        for i, j in pairs:
+            assert bool(mask[0, h, i, j]) == bool(om[0, h, i, j])
+    v = seeded((B, H, N, D), 6, torch.bfloat16).to(cuda)
+    idx, cnt = pred.predict_index(q, k)
+    out = block_sparse_attention(q, k, v, idx, cnt, 64)
+    rows = [0, 5, 100, 255]
+    want = O.sparse_attention(np32(q), np32(k), np32(v), idx.cpu().numpy(), cnt.cpu().numpy(), 64,
+                              query_blocks=rows)
+    got = np32(out)
+    for i in rows:
+        assert np.abs(got[..., 64 * i:64 * i + 64, :] - want[..., 64 * i:64 * i + 64, :]).max() <= 2e-2
