@@ -174,6 +174,230 @@ __device__ __forceinline__ void colmax2(float& x0, float& x1) {
 // finite and exp2(s * c - max * c) of a masked score (-inf) is exactly 0.
 constexpr float M_EMPTY = -1.0e30f;
 
+// Online-softmax state of one wave: 32 queries (two tiles of 16, query on
+// the lane axis) against one key half of every kept block.
+struct WaveAcc {
+  u32x4 qreg[2][4];  // Q^T B operand: qreg[qt][ds] = Q[q0 + 16 qt + l % 16][32 ds + 8 g .. +8]
+  f32x4 oacc[8][2];  // O^T[16 dt + 4 g + r][q0 + 16 qt + l % 16]
+  f32x4 lacc[2];     // row sums (all four r equal)
+  float m_run[2];    // running maximum of the raw scores
+  float nmc[2];      // -m_run * c
+};
+
+// A wave's place in its group of four: key half kh, query half qh.
+struct WaveGeo {
+  int kh, qh, lane, g, l16;
+  uint32_t kread[4];  // K operand byte offsets inside a K stage
+};
+
+__device__ __forceinline__ WaveGeo wave_geo(int w4) {
+  WaveGeo ge;
+  ge.kh = w4 & 1;
+  ge.qh = (w4 >> 1) & 1;
+  ge.lane = lane_id();
+  ge.g = ge.lane >> 4;
+  ge.l16 = ge.lane & 15;
+  // K operand (key 32 kh + 16 tt + l % 16, dims 32 ds + 8 g .. +8) inside a
+  // stage: row R = 32 kh + 16 tt + l % 16 (R % 16 = l % 16), chunk 4 ds + g,
+  // stored XOR-swizzled at chunk position (4 ds + g) ^ (R % 16).
+#pragma unroll
+  for (int ds = 0; ds < 4; ++ds)
+    ge.kread[ds] = 256 * (32 * ge.kh + ge.l16) + 16 * ((4 * ds + ge.g) ^ ge.l16);
+  return ge;
+}
+
+// Loads the wave's 32 queries (from token q0; rows at or past N are zero)
+// and clears the accumulators.
+__device__ __forceinline__ void acc_init(WaveAcc& s, const WaveGeo& ge, const uint16_t* qb,
+                                         int64_t qs2, int q0, int N, float c) {
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qtok = q0 + 16 * qt + ge.l16;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds)
+      s.qreg[qt][ds] = (q0 >= 0 && qtok < N)
+                           ? *reinterpret_cast<const u32x4*>(qb + qtok * qs2 + 32 * ds + 8 * ge.g)
+                           : u32x4{0u, 0u, 0u, 0u};
+    s.lacc[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) s.oacc[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    s.m_run[qt] = M_EMPTY;
+    s.nmc[qt] = -M_EMPTY * c;
+  }
+}
+
+// Marks the queries as loaded: later waits in the block loop then never
+// have to cover the Q loads.
+__device__ __forceinline__ void acc_q_ready(WaveAcc& s) {
+  asm volatile("" ::"v"(s.qreg[0][0]), "v"(s.qreg[0][1]), "v"(s.qreg[0][2]), "v"(s.qreg[0][3]),
+               "v"(s.qreg[1][0]), "v"(s.qreg[1][1]), "v"(s.qreg[1][2]), "v"(s.qreg[1][3]));
+}
+
+// One key block j (staged at ks / vts) for the wave's queries of query block i:
+//   S^T = K_kh Q^T (16 MFMA), masks, online softmax (fp32, log2 domain),
+//   O^T += V_kh^T P^T (16 MFMA), row sums = 1 P^T (2 MFMA).
+template <bool BF16>
+__device__ __forceinline__ void acc_block(WaveAcc& s, const WaveGeo& ge, const char* ks,
+                                          const u32x4* vts, int j, int i, bool valid, int N,
+                                          bool causal, float c) {
+  const uint32_t one2 = BF16 ? 0x3f803f80u : 0x3c003c00u;
+  const u32x4 ones = {one2, one2, one2, one2};
+  u32x4 kop[4][2], vop[8];
+#pragma unroll
+  for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+      kop[ds][tt] = *reinterpret_cast<const u32x4*>(ks + ge.kread[ds] + 4096 * tt);
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) vop[dt] = vts[(dt * 2 + ge.kh) * 64 + ge.lane];
+
+  // sc[tt][qt][r] = score(key 32 kh + 16 tt + 4 g + r, query 32 qh + 16 qt + l % 16)
+  f32x4 sc[2][2];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) sc[tt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) sc[tt][qt] = mfma16<BF16>(kop[ds][tt], s.qreg[qt][ds], sc[tt][qt]);
+
+  if (!valid || (causal && j >= i) || (j + 1) * BS > N) {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int ktok = j * BS + 32 * ge.kh + 16 * tt + 4 * ge.g + r;
+          const int qtok = i * BS + 32 * ge.qh + 16 * qt + ge.l16;
+          if (!valid || ktok >= N || (causal && ktok > qtok)) sc[tt][qt][r] = -INFINITY;
+        }
+  }
+  float mx[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const float m0 = __builtin_fmaxf(__builtin_fmaxf(sc[0][qt][0], sc[0][qt][1]),
+                                     __builtin_fmaxf(sc[0][qt][2], sc[0][qt][3]));
+    const float m1 = __builtin_fmaxf(__builtin_fmaxf(sc[1][qt][0], sc[1][qt][1]),
+                                     __builtin_fmaxf(sc[1][qt][2], sc[1][qt][3]));
+    mx[qt] = __builtin_fmaxf(m0, m1);
+  }
+  colmax2(mx[0], mx[1]);
+  // Rescale only when a query's maximum grew by more than 2^RESCALE_LOG2
+  // in exp2 units (always on its first non-empty block).
+  const bool grow0 = __builtin_fmaf(mx[0], c, s.nmc[0]) > RESCALE_LOG2;
+  const bool grow1 = __builtin_fmaf(mx[1], c, s.nmc[1]) > RESCALE_LOG2;
+  if (__builtin_amdgcn_ballot_w64(grow0 || grow1)) {
+    const bool grow[2] = {grow0, grow1};
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const float m_new = grow[qt] ? mx[qt] : s.m_run[qt];
+      const float alpha = __builtin_amdgcn_exp2f((s.m_run[qt] - m_new) * c);
+      s.lacc[qt] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) s.oacc[dt][qt] *= alpha;
+      s.m_run[qt] = m_new;
+      s.nmc[qt] = -m_new * c;
+    }
+  }
+  u32x4 pb[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    float pv[2][4];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        pv[tt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tt][qt][r], c, s.nmc[qt]));
+    pb[qt][0] = pack2<BF16>(pv[0][0], pv[0][1]);
+    pb[qt][1] = pack2<BF16>(pv[0][2], pv[0][3]);
+    pb[qt][2] = pack2<BF16>(pv[1][0], pv[1][1]);
+    pb[qt][3] = pack2<BF16>(pv[1][2], pv[1][3]);
+  }
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) s.oacc[dt][qt] = mfma16<BF16>(vop[dt], pb[qt], s.oacc[dt][qt]);
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) s.lacc[qt] = mfma16<BF16>(ones, pb[qt], s.lacc[qt]);
+}
+
+// Merge of the two key halves of a query half through LDS: the kh = 1 wave
+// exports (acc_export), and after a workgroup barrier the kh = 0 wave
+// combines and writes out, lse (acc_store).
+constexpr int XCHG_FLOATS = 8 * 2 * 4 * 64 + 2 * 2 * 64;  // per query half
+
+__device__ __forceinline__ void acc_export(const WaveAcc& s, const WaveGeo& ge, float* xo) {
+  float* xm = xo + 8 * 2 * 4 * 64;
+  float* xl = xm + 2 * 64;
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    xm[qt * 64 + ge.lane] = s.m_run[qt];
+    xl[qt * 64 + ge.lane] = s.lacc[qt][0];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) xo[((dt * 2 + qt) * 4 + r) * 64 + ge.lane] = s.oacc[dt][qt][r];
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ void acc_store(const WaveAcc& s, const WaveGeo& ge, const float* xo,
+                                          uint16_t* obase, int64_t os2, float* lse_row, int q0,
+                                          int N, float c) {
+  const float* xm = xo + 8 * 2 * 4 * 64;
+  const float* xl = xm + 2 * 64;
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const float m1 = xm[qt * 64 + ge.lane], l1 = xl[qt * 64 + ge.lane];
+    const float m = fmaxf(s.m_run[qt], m1);
+    const float a0 = __builtin_amdgcn_exp2f((s.m_run[qt] - m) * c);
+    const float a1 = __builtin_amdgcn_exp2f((m1 - m) * c);
+    const float l = s.lacc[qt][0] * a0 + l1 * a1;
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    const int qtok = q0 + 16 * qt + ge.l16;
+    if (qtok < N) {
+      uint16_t* ob = obase + qtok * os2;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          o[r] = (s.oacc[dt][qt][r] * a0 + xo[((dt * 2 + qt) * 4 + r) * 64 + ge.lane] * a1) * inv;
+        *reinterpret_cast<u32x2*>(ob + 16 * dt + 4 * ge.g) = u32x2{pack2<BF16>(o[0], o[1]),
+                                                                   pack2<BF16>(o[2], o[3])};
+      }
+      if (lse_row && ge.g == 0)
+        lse_row[qtok] = l > 0.f ? (m * c + __log2f(l)) * 0.69314718055994531f : -INFINITY;
+    }
+  }
+}
+
+// K staging offsets. K lands row-major, 64 rows x 256 bytes, the 16-byte
+// chunks of row R XOR-swizzled (chunk c at position c ^ (R % 16)) so that the
+// operand reads are bank-conflict free; one instruction fetches four whole
+// rows (full 128-byte lines): lane L takes row 4 x + L / 16 (x = the
+// instruction's 4-row group), stored chunk L % 16.
+__device__ __forceinline__ uint32_t k_lane_off(int group4, int lane, int64_t krow_bytes) {
+  const int row = 4 * group4 + (lane >> 4);
+  return static_cast<uint32_t>(row * krow_bytes + 16 * ((lane & 15) ^ (row & 15)));
+}
+
+__device__ __forceinline__ const char* k_lane_ptr_clamped(const char* kbytes, int j, int group4,
+                                                          int lane, int N, int64_t krow_bytes) {
+  const int rr = 4 * group4 + (lane >> 4);
+  const int row = j * BS + rr;
+  const int64_t rb = (row < N ? row : N - 1) * krow_bytes;
+  return kbytes + rb + 16 * ((lane & 15) ^ (rr & 15));
+}
+
+// ---------------------------------------------------------------------------
+// attn_fwd_kernel: one query block per workgroup of 4 waves, two workgroups
+// per CU, two LDS stages.
+// ---------------------------------------------------------------------------
 template <bool BF16, bool LIST_LDS>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   // One LDS object: [K stage 0][V^T stage 0][K stage 1][V^T stage 1][list]; the
@@ -189,10 +413,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   const int i = M - 1 - (logical - bh * M);  // longest causal rows first
   const int b = bh / a.H, hh = bh - (bh / a.H) * a.H;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-  const int kh = w & 1;   // key half of every block owned by this wave
-  const int qh = w >> 1;  // query half (queries 32 qh .. 32 qh + 31) owned by this wave
-  const int lane = lane_id();
-  const int g = lane >> 4, l16 = lane & 15;
+  const WaveGeo ge = wave_geo(w);
+  const float c = a.scale_log2;
 
   const uint16_t* qb = a.q + b * a.qs[0] + hh * a.qs[1];
   const char* kbytes = reinterpret_cast<const char*>(a.k + b * a.ks[0] + hh * a.ks[1]);
@@ -212,24 +434,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
       return glist[p];
   };
 
-  // Staging of key block j into LDS by the 4 waves (global_load_lds_dwordx4:
-  // each lane gives its own global address, the 16 bytes land at the
-  // wave-uniform LDS base + 16 * lane; the immediate offset moves both).
-  //  K: row-major, 64 rows x 256 bytes, the 16-byte chunks of row R stored
-  //   XOR-swizzled (chunk c at position c ^ (R % 16)) so that the operand
-  //   reads below are bank-conflict free. Instruction r of wave w fetches the
-  //   four whole rows 16 w + 4 r .. +3 (full 128-byte lines); rows past N
-  //   are clamped to N - 1 (their scores are masked).
-  //  V^T: wave w fetches slot rows 4 w .. 4 w + 3 of the packed tile (1 KB each).
+  // Staging of key block j by the 4 waves: wave w fetches K rows 16 w .. +15
+  // (4 instructions) and V^T slot rows 4 w .. 4 w + 3 (1 KB each).
   const int64_t krow_bytes = a.ks[2] * 2;
   const int64_t kblk_bytes = BS * krow_bytes;
-  const int ksub = lane >> 4;  // row inside the instruction's 4-row group
-  uint32_t koff[4];            // lane byte offsets inside a full key block
+  uint32_t koff[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-    koff[r] = static_cast<uint32_t>((16 * w + 4 * r + ksub) * krow_bytes +
-                                    16 * (l16 ^ ((4 * r + ksub) & 15)));
-  const int voff = w * 4096 + 16 * lane;
+  for (int r = 0; r < 4; ++r) koff[r] = k_lane_off(4 * w + r, ge.lane, krow_bytes);
+  const int voff = w * 4096 + 16 * ge.lane;
   auto stage = [&](int j, u32x4* kst, u32x4* vst) {
     char* kl = reinterpret_cast<char*>(kst) + w * 4096;
     if ((j + 1) * BS <= N) {
@@ -239,16 +451,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
       dma16<0>(kbj + koff[2], kl + 2048);
       dma16<0>(kbj + koff[3], kl + 3072);
     } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = j * BS + 16 * w + 4 * r + ksub;
-        const int64_t rb = (row < N ? row : N - 1) * krow_bytes;
-        const char* kp = kbytes + rb + 16 * (l16 ^ ((4 * r + ksub) & 15));
-        if (r == 0) dma16<0>(kp, kl);
-        if (r == 1) dma16<0>(kp, kl + 1024);
-        if (r == 2) dma16<0>(kp, kl + 2048);
-        if (r == 3) dma16<0>(kp, kl + 3072);
-      }
+      dma16<0>(k_lane_ptr_clamped(kbytes, j, 4 * w + 0, ge.lane, N, krow_bytes), kl);
+      dma16<0>(k_lane_ptr_clamped(kbytes, j, 4 * w + 1, ge.lane, N, krow_bytes), kl + 1024);
+      dma16<0>(k_lane_ptr_clamped(kbytes, j, 4 * w + 2, ge.lane, N, krow_bytes), kl + 2048);
+      dma16<0>(k_lane_ptr_clamped(kbytes, j, 4 * w + 3, ge.lane, N, krow_bytes), kl + 3072);
     }
     const char* vp = vtbytes + static_cast<int64_t>(j) * TILE_BYTES + voff;
     char* vl = reinterpret_cast<char*>(vst) + w * 4096;
@@ -258,47 +464,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     dma16<3072>(vp, vl);
   };
 
-  // K operand (key 32 kh + 16 tt + l % 16, dims 32 ds + 8 g .. +8) inside a
-  // stage: row R = 32 kh + 16 tt + l % 16 (R % 16 = l % 16), chunk 4 ds + g.
-  uint32_t kread[4];
-#pragma unroll
-  for (int ds = 0; ds < 4; ++ds) kread[ds] = 256 * (32 * kh + l16) + 16 * ((4 * ds + g) ^ l16);
-
-  // Q^T as the B operand: qreg[qt][ds] = Q[32 qh + 16 qt + l % 16][32 ds + 8 g .. +8].
-  u32x4 qreg[2][4];
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const int qtok = i * BS + 32 * qh + 16 * qt + l16;
-#pragma unroll
-    for (int ds = 0; ds < 4; ++ds)
-      qreg[qt][ds] = qtok < N ? *reinterpret_cast<const u32x4*>(qb + qtok * a.qs[2] + 32 * ds + 8 * g)
-                              : u32x4{0u, 0u, 0u, 0u};
-  }
-  // All-ones A operand: ones x P^T puts each query's row sum over the block's
-  // keys in every row of the result (the sum of exactly the P that P V uses).
-  const uint32_t one2 = BF16 ? 0x3f803f80u : 0x3c003c00u;
-  const u32x4 ones = {one2, one2, one2, one2};
-
-  f32x4 oacc[8][2];  // O^T[16 dt + 4 g + r][32 qh + 16 qt + l % 16]
-  f32x4 lacc[2];     // row sums (all four r equal)
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    lacc[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) oacc[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  const float c = a.scale_log2;
-  // Running maximum of the raw scores per query, and -max * c.
-  float m_run[2] = {M_EMPTY, M_EMPTY};
-  float nmc[2] = {-M_EMPTY * c, -M_EMPTY * c};
+  WaveAcc st;
+  acc_init(st, ge, qb, a.qs[2], i * BS + 32 * ge.qh, N, c);
 
   if (cnt > 0) {
     int jraw = entry(0);
     auto block_of = [&](int j) { return (j >= 0 && j < M) ? j : 0; };
     stage(block_of(jraw), stage_k(0), stage_v(0));
-    // Q ready once, so that no wait for Q stays in the loop.
-    asm volatile("" ::"v"(qreg[0][0]), "v"(qreg[0][1]), "v"(qreg[0][2]), "v"(qreg[0][3]),
-                 "v"(qreg[1][0]), "v"(qreg[1][1]), "v"(qreg[1][2]), "v"(qreg[1][3]));
+    acc_q_ready(st);
 
     // Block p lives in LDS stage PAR = p % 2 (compile time, so the compiler
     // sees the staging of block p + 1 into the other stage cannot alias).
@@ -313,90 +486,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
         jnext = entry(p + 1);
         stage(block_of(jnext), stage_k(PAR ^ 1), stage_v(PAR ^ 1));
       }
-      const char* ks = reinterpret_cast<const char*>(stage_k(PAR));
-      const u32x4* vts = stage_v(PAR);
-      u32x4 kop[4][2], vop[8];
-#pragma unroll
-      for (int ds = 0; ds < 4; ++ds)
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-          kop[ds][tt] = *reinterpret_cast<const u32x4*>(ks + kread[ds] + 4096 * tt);
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) vop[dt] = vts[(dt * 2 + kh) * 64 + lane];
-
-      // S^T of the block half: sc[tt][qt][r] = score(key 32 kh + 16 tt + 4 g + r,
-      // query 32 qh + 16 qt + l % 16).
-      f32x4 sc[2][2];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) sc[tt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ds = 0; ds < 4; ++ds)
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-          for (int qt = 0; qt < 2; ++qt) sc[tt][qt] = mfma16<BF16>(kop[ds][tt], qreg[qt][ds], sc[tt][qt]);
-
-      if (!valid || (a.causal && j >= i) || (j + 1) * BS > N) {
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-          for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int ktok = j * BS + 32 * kh + 16 * tt + 4 * g + r;
-              const int qtok = i * BS + 32 * qh + 16 * qt + l16;
-              if (!valid || ktok >= N || (a.causal && ktok > qtok)) sc[tt][qt][r] = -INFINITY;
-            }
-      }
-      float mx[2];
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        const float m0 = __builtin_fmaxf(__builtin_fmaxf(sc[0][qt][0], sc[0][qt][1]),
-                                         __builtin_fmaxf(sc[0][qt][2], sc[0][qt][3]));
-        const float m1 = __builtin_fmaxf(__builtin_fmaxf(sc[1][qt][0], sc[1][qt][1]),
-                                         __builtin_fmaxf(sc[1][qt][2], sc[1][qt][3]));
-        mx[qt] = __builtin_fmaxf(m0, m1);
-      }
-      colmax2(mx[0], mx[1]);
-      // Rescale only when a query's maximum grew by more than 2^RESCALE_LOG2
-      // in exp2 units (always on its first non-empty block).
-      const bool grow0 = __builtin_fmaf(mx[0], c, nmc[0]) > RESCALE_LOG2;
-      const bool grow1 = __builtin_fmaf(mx[1], c, nmc[1]) > RESCALE_LOG2;
-      if (__builtin_amdgcn_ballot_w64(grow0 || grow1)) {
-        const bool grow[2] = {grow0, grow1};
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-          const float m_new = grow[qt] ? mx[qt] : m_run[qt];
-          const float alpha = __builtin_amdgcn_exp2f((m_run[qt] - m_new) * c);
-          lacc[qt] *= alpha;
-#pragma unroll
-          for (int dt = 0; dt < 8; ++dt) oacc[dt][qt] *= alpha;
-          m_run[qt] = m_new;
-          nmc[qt] = -m_new * c;
-        }
-      }
-      u32x4 pb[2];
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        float pv[2][4];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            pv[tt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tt][qt][r], c, nmc[qt]));
-        pb[qt][0] = pack2<BF16>(pv[0][0], pv[0][1]);
-        pb[qt][1] = pack2<BF16>(pv[0][2], pv[0][3]);
-        pb[qt][2] = pack2<BF16>(pv[1][0], pv[1][1]);
-        pb[qt][3] = pack2<BF16>(pv[1][2], pv[1][3]);
-      }
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) oacc[dt][qt] = mfma16<BF16>(vop[dt], pb[qt], oacc[dt][qt]);
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) lacc[qt] = mfma16<BF16>(ones, pb[qt], lacc[qt]);
+      acc_block<BF16>(st, ge, reinterpret_cast<const char*>(stage_k(PAR)), stage_v(PAR), j, i,
+                      valid, N, a.causal, c);
       jraw = jnext;
     };
     for (int p = 0; p < cnt; p += 2) {
@@ -405,51 +496,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
     }
   }
 
-  // Merge the two key halves of each query half through LDS (reusing the
-  // staging area: wave (1, qh) hands its maxima, sums and O^T to wave (0, qh)).
   __syncthreads();
-  float* xo = reinterpret_cast<float*>(smem) + qh * (8 * 2 * 4 * 64 + 2 * 2 * 64);
-  float* xm = xo + 8 * 2 * 4 * 64;
-  float* xl = xm + 2 * 64;
-  if (kh == 1) {
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      xm[qt * 64 + lane] = m_run[qt];
-      xl[qt * 64 + lane] = lacc[qt][0];
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) xo[((dt * 2 + qt) * 4 + r) * 64 + lane] = oacc[dt][qt][r];
-    }
-  }
+  float* xo = reinterpret_cast<float*>(smem) + ge.qh * XCHG_FLOATS;
+  if (ge.kh == 1) acc_export(st, ge, xo);
   __syncthreads();
-  if (kh == 0) {
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      const float m1 = xm[qt * 64 + lane], l1 = xl[qt * 64 + lane];
-      const float m = fmaxf(m_run[qt], m1);
-      const float a0 = __builtin_amdgcn_exp2f((m_run[qt] - m) * c);
-      const float a1 = __builtin_amdgcn_exp2f((m1 - m) * c);
-      const float l = lacc[qt][0] * a0 + l1 * a1;
-      const float inv = l > 0.f ? 1.0f / l : 0.f;
-      const int qtok = i * BS + 32 * qh + 16 * qt + l16;
-      if (qtok < N) {
-        uint16_t* ob = a.o + b * a.os[0] + hh * a.os[1] + qtok * a.os[2];
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          float o[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            o[r] = (oacc[dt][qt][r] * a0 + xo[((dt * 2 + qt) * 4 + r) * 64 + lane] * a1) * inv;
-          *reinterpret_cast<u32x2*>(ob + 16 * dt + 4 * g) = u32x2{pack2<BF16>(o[0], o[1]),
-                                                                  pack2<BF16>(o[2], o[3])};
-        }
-        if (a.lse && g == 0)
-          a.lse[static_cast<int64_t>(bh) * N + qtok] =
-              l > 0.f ? (m * c + __log2f(l)) * 0.69314718055994531f : -INFINITY;
-      }
-    }
-  }
+  if (ge.kh == 0)
+    acc_store<BF16>(st, ge, xo, a.o + b * a.os[0] + hh * a.os[1], a.os[2],
+                    a.lse ? a.lse + static_cast<int64_t>(bh) * N : nullptr, i * BS + 32 * ge.qh,
+                    N, c);
 }
 
 }  // namespace

@@ -258,7 +258,8 @@ ATOL = {"bf16": 2e-2, "fp16": 5e-3}
 
 @pytest.mark.parametrize("dt", ["bf16", "fp16"])
 @pytest.mark.parametrize("N,causal,sp", [(512, False, 0.5), (512, True, 0.5), (500, True, 0.7),
-                                         (1024, False, 0.9), (256, False, 0.0)])
+                                         (1024, False, 0.9), (256, False, 0.0),
+                                         (700, True, 0.5), (130, False, 0.4)])  # odd M
 def test_attention_parity(cuda, dt, N, causal, sp):
     from cab_attention.kernels import block_sparse_attention
     B, H, D, bs = 1, 2, 128, 64
@@ -328,6 +329,31 @@ def test_attention_packed_path_matches_fused(cuda):
         assert torch.equal(got, ref) and torch.equal(lse, ref_lse)
     with pytest.raises(ValueError):
         block_sparse_attention_packed(q, k, vt[:-16], idx, cnt, bs, causal=True)
+
+
+def test_attention_unsorted_and_long_lists(cuda):
+    """Unsorted block lists, and lists too long to be staged in LDS (read
+    from global memory instead), give the oracle's result."""
+    from cab_attention.kernels import block_sparse_attention
+    B, H, N, D, bs = 1, 2, 1000, 128, 64
+    q, k, v = (seeded((B, H, N, D), s, torch.bfloat16) for s in (31, 32, 33))
+    M = (N + bs - 1) // bs
+    f = np.random.default_rng(3).standard_normal((B, H, M, M)).astype(np.float32)
+    _, idx, cnt = O.generate_block_mask(f, 0.5, causal=True)
+    want = O.sparse_attention(np32(q), np32(k), np32(v), idx, cnt, bs, causal=True)
+    rng = np.random.default_rng(4)
+    shuffled = idx.copy()
+    for hh in range(H):
+        for i in range(M):
+            c = cnt[0, hh, i]
+            shuffled[0, hh, i, :c] = rng.permutation(shuffled[0, hh, i, :c])
+    long = np.full((B, H, M, 2100), -1, np.int32)
+    long[..., :idx.shape[-1]] = idx
+    for lists in (shuffled, long):
+        out = block_sparse_attention(q.to(cuda), k.to(cuda), v.to(cuda),
+                                     torch.from_numpy(lists).to(cuda), torch.from_numpy(cnt).to(cuda),
+                                     bs, causal=True)
+        assert np.abs(np32(out) - want).max() <= 2e-2
 
 
 def test_attention_empty_rows_and_bad_indices(cuda):
