@@ -297,6 +297,13 @@ def main() -> int:
         st_coarsen = time_events(lambda: coarsen_qk_max_l2(q3, k3, bs), iters)
         st_frc = time_events(lambda: compute_block_frc(qc, kc, diagnostics=False), iters)
         st_mask = time_events(lambda: generate_block_index(f3, sp, dense=True), iters)
+        # CAB V4 hybrid selection (half of each row by magnitude): the coarse
+        # affinity stands in for the block magnitudes here
+        _, a3, _ = compute_block_frc(qc, kc)
+        st_hybrid = time_events(lambda: generate_block_index(f3, sp, dense=True, select_high=True,
+                                                             magnitude_scores=a3,
+                                                             magnitude_ratio=0.5), iters)
+        del a3
         M3 = (N3 + bs - 1) // bs
         k3keep = pred3.keep_per_row(N3)
         coarsen_bytes = 2 * B3 * H3 * N3 * D * 2 + 2 * B3 * H3 * M3 * (D * 2 + 4)
@@ -317,6 +324,7 @@ def main() -> int:
                                    / PEAK_BF16_TFLOPS, 4),
             "mask_GBps": round(mask_bytes / (st_mask * 1e-3) / 1e9, 1),
             "mask_frac_hbm": round(mask_bytes / (st_mask * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "hybrid_mask_ms": round(st_hybrid, 4),
             "config4_predictor_plus_attention_ms": round(e2e_ms, 4),
         }
         log(f"predictor {pred_ms:.3f} ms (coarsen {st_coarsen:.3f}, frc {st_frc:.3f}, "

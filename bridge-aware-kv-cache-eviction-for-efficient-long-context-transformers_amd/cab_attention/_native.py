@@ -39,6 +39,8 @@ SIGNATURES = {
                                      ctypes.c_size_t, _ptr]),
     "cab_block_topk": (ctypes.c_int, [_ptr, _i64, _i64, _i64, _i32, ctypes.c_int, ctypes.c_int,
                                       ctypes.c_int, _ptr, _ptr, _ptr, _ptr]),
+    "cab_block_topk_hybrid": (ctypes.c_int, [_ptr, _ptr, _i64, _i64, _i64, _i32, _i32, ctypes.c_int,
+                                             ctypes.c_int, ctypes.c_int, _ptr, _ptr, _ptr, _ptr]),
     "cab_block_sparse_attn_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i32]),
     "cab_block_sparse_attn_fwd": (ctypes.c_int, [_ptr, _ptr, _ptr, ctypes.c_int, _i64, _i64, _i64,
                                                  _i64, _i64x4, _i64x4, _i64x4, _i64x4, _i32, _ptr,

@@ -2,12 +2,12 @@
 
 from .coarsening import coarsen_qk_max_l2, coarsen_qk_max_l2_pytorch
 from .frc_kernel import (compute_block_frc, generate_block_index, generate_block_mask,
-                         keep_count, visualize_frc_statistics)
+                         keep_count, magnitude_quota, visualize_frc_statistics)
 from .sparse_attention import (block_sparse_attention, block_sparse_attention_packed,
                                kept_tile_flops, pack_v)
 
 __all__ = [
     "coarsen_qk_max_l2", "coarsen_qk_max_l2_pytorch", "compute_block_frc", "generate_block_mask",
-    "generate_block_index", "keep_count", "visualize_frc_statistics", "block_sparse_attention",
+    "generate_block_index", "keep_count", "magnitude_quota", "visualize_frc_statistics", "block_sparse_attention",
     "block_sparse_attention_packed", "pack_v", "kept_tile_flops",
 ]

@@ -77,11 +77,25 @@ def compute_block_frc(q_coarse: torch.Tensor, k_coarse: torch.Tensor, temperatur
     return frc, aff, tri
 
 
+def magnitude_quota(k: int, magnitude_ratio: float) -> int:
+    """Blocks per row reserved for the magnitude ranking of the hybrid mask:
+    ``int(k * magnitude_ratio)`` in ``[0, k]`` ("reserve X% of budget for
+    top-magnitude blocks", methods.py:404-418)."""
+    if not 0.0 <= float(magnitude_ratio) <= 1.0:
+        raise ValueError(f"magnitude_ratio must be in [0, 1], got {magnitude_ratio}")
+    return min(k, max(0, int(k * float(magnitude_ratio))))
+
+
 def _select(frc: torch.Tensor, sparsity: float, select_high: bool, keep_diagonal: bool,
-            causal: bool, dense: bool):
+            causal: bool, dense: bool, magnitude_scores: torch.Tensor | None = None,
+            magnitude_ratio: float = 0.5):
     if frc.dim() != 4 or frc.shape[-1] != frc.shape[-2]:
         raise ValueError(f"frc must be [B, H, M, M]; got {tuple(frc.shape)}")
-    dev = nat.require_device(frc)
+    if magnitude_scores is not None and tuple(magnitude_scores.shape) != tuple(frc.shape):
+        raise ValueError(f"magnitude_scores must match frc's shape {tuple(frc.shape)}; got "
+                         f"{tuple(magnitude_scores.shape)}")
+    tensors = (frc,) if magnitude_scores is None else (frc, magnitude_scores)
+    dev = nat.require_device(*tensors)
     lib = nat.load()
     B, H, M, _ = frc.shape
     k = keep_count(M, sparsity) if M > 0 else 1
@@ -89,11 +103,20 @@ def _select(frc: torch.Tensor, sparsity: float, select_high: bool, keep_diagonal
     kv_idx = torch.empty((B, H, M, k), dtype=torch.int32, device=dev)
     kv_cnt = torch.empty((B, H, M), dtype=torch.int32, device=dev)
     mask = torch.empty((B, H, M, M), dtype=torch.bool, device=dev) if dense else None
+    flags = (int(bool(select_high)), int(bool(keep_diagonal)), int(bool(causal)))
     with torch.cuda.device(dev):
-        st = lib.cab_block_topk(f.data_ptr(), B, H, M, k, int(bool(select_high)),
-                                int(bool(keep_diagonal)), int(bool(causal)), kv_idx.data_ptr(),
-                                kv_cnt.data_ptr(), nat.ptr(mask), nat.stream_ptr(dev))
-    nat.check("cab_block_topk", st)
+        if magnitude_scores is None:
+            name = "cab_block_topk"
+            st = lib.cab_block_topk(f.data_ptr(), B, H, M, k, *flags, kv_idx.data_ptr(),
+                                    kv_cnt.data_ptr(), nat.ptr(mask), nat.stream_ptr(dev))
+        else:
+            name = "cab_block_topk_hybrid"
+            mg = magnitude_scores.to(torch.float32).contiguous()
+            st = lib.cab_block_topk_hybrid(f.data_ptr(), mg.data_ptr(), B, H, M, k,
+                                           magnitude_quota(k, magnitude_ratio), *flags,
+                                           kv_idx.data_ptr(), kv_cnt.data_ptr(), nat.ptr(mask),
+                                           nat.stream_ptr(dev))
+    nat.check(name, st)
     return kv_idx, kv_cnt, mask
 
 
@@ -107,24 +130,29 @@ def generate_block_mask(frc_scores: torch.Tensor, sparsity: float = 0.95, select
     when causal, candidates ``j <= i``), lowest FRC first (highest with
     ``select_high``, as methods.py:342 passes), ties to the lower block index.
     ``keep_diagonal`` forces block ``i`` in; it counts toward k.
+
+    Hybrid (CAB V4, methods.py:465-473): with ``magnitude_scores``
+    ``[B, H, M, M]`` the first ``int(k * magnitude_ratio)`` of a row's blocks
+    after the diagonal (fewer if the row has fewer) are those with the
+    highest magnitude; FRC order fills the rest.
     """
-    if magnitude_scores is not None:
-        raise NotImplementedError(
-            "hybrid magnitude + FRC selection (magnitude_scores / magnitude_ratio) is not "
-            "implemented by this framework yet")
-    _, _, mask = _select(frc_scores, sparsity, select_high, keep_diagonal, causal, dense=True)
+    _, _, mask = _select(frc_scores, sparsity, select_high, keep_diagonal, causal, dense=True,
+                         magnitude_scores=magnitude_scores, magnitude_ratio=magnitude_ratio)
     return mask
 
 
 def generate_block_index(frc_scores: torch.Tensor, sparsity: float = 0.95,
                          select_high: bool = False, keep_diagonal: bool = True,
-                         causal: bool = False, dense: bool = False):
+                         causal: bool = False, dense: bool = False,
+                         magnitude_scores: torch.Tensor | None = None,
+                         magnitude_ratio: float = 0.5):
     """Compact form of :func:`generate_block_mask` for the sparse executor.
 
     Returns ``(kv_idx int32 [B, H, M, k] ascending with -1 padding,
     kv_cnt int32 [B, H, M], mask or None)``.
     """
-    return _select(frc_scores, sparsity, select_high, keep_diagonal, causal, dense)
+    return _select(frc_scores, sparsity, select_high, keep_diagonal, causal, dense,
+                   magnitude_scores, magnitude_ratio)
 
 
 def visualize_frc_statistics(frc_scores: torch.Tensor, affinity: torch.Tensor,

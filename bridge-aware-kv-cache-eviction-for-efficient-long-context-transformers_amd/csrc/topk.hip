@@ -10,8 +10,12 @@
 // popcount, and writes the compact ascending index list and, optionally, the
 // dense 0/1 row.
 //
-// HBM traffic per row: 4 M bytes read; 4 k + 4 (+ M for the dense mask)
-// bytes written. Bound by HBM bandwidth.
+// Hybrid selection (cab_block_topk_hybrid) first runs the same search on
+// the row's magnitude keys for its magnitude quota, marks those blocks taken,
+// and then searches the FRC keys of the remaining candidates.
+//
+// HBM traffic per row: 4 M bytes read (8 M hybrid); 4 k + 4 (+ M for the
+// dense mask) bytes written. Bound by HBM bandwidth.
 #include "cab_internal.h"
 
 namespace cab {
@@ -19,11 +23,13 @@ namespace {
 
 struct TopkArgs {
   const float* frc;
+  const float* mag;  // hybrid only: magnitude scores, the highest kept first
   int32_t* kv_idx;
   int32_t* kv_cnt;
   uint8_t* dense;
   int64_t rows, M;
   int32_t k;
+  int32_t kmag;      // hybrid only: per-row magnitude quota
   int select_high, keep_diagonal, causal;
 };
 
@@ -37,7 +43,31 @@ __device__ __forceinline__ uint32_t order_key(float f, bool high) {
   return high ? ~u : u;
 }
 
-template <int NCH>
+// theta = the need-th smallest key among the candidates (the largest theta
+// with count(key < theta) < need), by a 32-step bitwise search in which every
+// step counts with one ballot per register; returns in need_eq how many keys
+// equal to theta (the first ones in j order) complete the selection.
+template <int NCH, typename Cand>
+__device__ __forceinline__ uint32_t kth_key(const uint32_t (&key)[NCH], Cand is_cand, int64_t need,
+                                            int64_t& need_eq) {
+  uint32_t theta = 0u;
+  need_eq = 0;
+  if (need <= 0) return theta;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t trial = theta | (1u << b);
+    int64_t cnt = 0;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) cnt += __popcll(ballot64(is_cand(c) && key[c] < trial));
+    if (cnt < need) theta = trial;
+  }
+  int64_t below = 0;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) below += __popcll(ballot64(is_cand(c) && key[c] < theta));
+  need_eq = need - below;
+  return theta;
+}
+
+template <int NCH, bool HYB>
 __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= a.rows) return;  // uniform per wave
@@ -49,6 +79,7 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   const int64_t need = kd ? krow - 1 : krow;
   const float* f = a.frc + row * a.M;
   const bool high = a.select_high != 0;
+  const uint64_t lt_mask = lanemask_lt();
 
   uint32_t key[NCH];
 #pragma unroll
@@ -61,35 +92,52 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
     return j < ncand && !(kd && j == i);
   };
 
-  // theta = need-th smallest candidate key (largest theta with
-  // count(key < theta) < need).
-  uint32_t theta = 0u;
-  int64_t need_eq = 0;
-  if (need > 0) {
-    for (int b = 31; b >= 0; --b) {
-      const uint32_t trial = theta | (1u << b);
-      int64_t cnt = 0;
+  // Hybrid: the need_m candidates of highest magnitude first (bit c of msel
+  // marks register c of this lane as taken).
+  uint64_t msel[(NCH + 63) / 64];
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) cnt += __popcll(ballot64(is_cand(c) && key[c] < trial));
-      if (cnt < need) theta = trial;
+  for (int w = 0; w < (NCH + 63) / 64; ++w) msel[w] = 0;
+  int64_t need_m = 0;
+  if constexpr (HYB) {
+    need_m = min(static_cast<int64_t>(a.kmag), need);
+    const float* mg = a.mag + row * a.M;
+    uint32_t mkey[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int64_t j = 64 * c + lane;
+      mkey[c] = j < a.M ? order_key(mg[j], true) : 0xffffffffu;
     }
-    int64_t below = 0;
+    int64_t meq = 0;
+    const uint32_t mtheta = kth_key(mkey, is_cand, need_m, meq);
+    int64_t eq_seen = 0;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) below += __popcll(ballot64(is_cand(c) && key[c] < theta));
-    need_eq = need - below;
+    for (int c = 0; c < NCH; ++c) {
+      const bool cand = is_cand(c) && need_m > 0;
+      const bool eq = cand && mkey[c] == mtheta;
+      const uint64_t eqb = ballot64(eq);
+      const int64_t eq_rank = eq_seen + __popcll(eqb & lt_mask);
+      if ((cand && mkey[c] < mtheta) || (eq && eq_rank < meq)) msel[c >> 6] |= 1ull << (c & 63);
+      eq_seen += __popcll(eqb);
+    }
   }
+  auto taken = [&](int c) { return ((msel[c >> 6] >> (c & 63)) & 1ull) != 0; };
+  auto is_cand_f = [&](int c) { return is_cand(c) && !taken(c); };
+
+  // FRC order for the rest of the row.
+  const int64_t need_f = need - need_m;
+  int64_t need_eq = 0;
+  const uint32_t theta = kth_key(key, is_cand_f, need_f, need_eq);
 
   int64_t pos = 0, eq_seen = 0;
-  const uint64_t lt_mask = lanemask_lt();
   int32_t* out = a.kv_idx + row * a.k;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int64_t j = 64 * c + lane;
-    const bool cand = is_cand(c);
-    const bool eq = cand && need > 0 && key[c] == theta;
+    const bool cand = is_cand_f(c) && need_f > 0;
+    const bool eq = cand && key[c] == theta;
     const uint64_t eqb = ballot64(eq);
     const int64_t eq_rank = eq_seen + __popcll(eqb & lt_mask);
-    const bool sel = (cand && need > 0 && key[c] < theta) || (eq && eq_rank < need_eq) ||
+    const bool sel = (cand && key[c] < theta) || (eq && eq_rank < need_eq) || taken(c) ||
                      (kd && j == i);
     const uint64_t selb = ballot64(sel);
     if (sel) out[pos + __popcll(selb & lt_mask)] = static_cast<int32_t>(j);
@@ -101,6 +149,57 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   if (lane == 0) a.kv_cnt[row] = static_cast<int32_t>(pos);
 }
 
+template <bool HYB>
+void launch_topk(const TopkArgs& a, dim3 grid, hipStream_t s) {
+  const int64_t nch = ceil_div(a.M, 64);
+  if (nch <= 1) topk_kernel<1, HYB><<<grid, 256, 0, s>>>(a);
+  else if (nch <= 2) topk_kernel<2, HYB><<<grid, 256, 0, s>>>(a);
+  else if (nch <= 4) topk_kernel<4, HYB><<<grid, 256, 0, s>>>(a);
+  else if (nch <= 8) topk_kernel<8, HYB><<<grid, 256, 0, s>>>(a);
+  else if (nch <= 16) topk_kernel<16, HYB><<<grid, 256, 0, s>>>(a);
+  else if (nch <= 32) topk_kernel<32, HYB><<<grid, 256, 0, s>>>(a);
+  else if (nch <= 64) topk_kernel<64, HYB><<<grid, 256, 0, s>>>(a);
+  else topk_kernel<128, HYB><<<grid, 256, 0, s>>>(a);
+}
+
+cab_status_t topk_common(const char* fn, const float* frc, const float* mag, int64_t B, int64_t H,
+                         int64_t M, int32_t k, int32_t kmag, int select_high, int keep_diagonal,
+                         int causal, int32_t* kv_idx, int32_t* kv_cnt, uint8_t* dense_mask,
+                         void* stream, bool hybrid) {
+  clear_error();
+  CAB_REQUIRE(B >= 0 && H >= 0 && M >= 0, CAB_ESHAPE, "%s: negative size", fn);
+  CAB_REQUIRE(M <= 8192, CAB_ESHAPE, "%s: M=%lld exceeds 8192", fn, (long long)M);
+  CAB_REQUIRE(k >= 1, CAB_EINVAL, "%s: k=%d must be >= 1", fn, (int)k);
+  CAB_REQUIRE(M == 0 || k <= M, CAB_EINVAL, "%s: k=%d exceeds M=%lld", fn, (int)k, (long long)M);
+  CAB_REQUIRE(!hybrid || (kmag >= 0 && kmag <= k), CAB_EINVAL,
+              "%s: magnitude quota %d outside [0, k=%d]", fn, (int)kmag, (int)k);
+  const int64_t rows = B * H * M;
+  if (rows == 0) return CAB_OK;
+  CAB_REQUIRE(frc && kv_idx && kv_cnt, CAB_EINVAL, "%s: null tensor pointer", fn);
+  CAB_REQUIRE(!hybrid || mag, CAB_EINVAL, "%s: null magnitude scores", fn);
+  const int64_t blocks = ceil_div(rows, 4);
+  CAB_REQUIRE(blocks <= INT32_MAX, CAB_ESHAPE, "%s: problem too large", fn);
+  TopkArgs a;
+  a.frc = frc;
+  a.mag = mag;
+  a.kv_idx = kv_idx;
+  a.kv_cnt = kv_cnt;
+  a.dense = dense_mask;
+  a.rows = rows;
+  a.M = M;
+  a.k = k;
+  a.kmag = kmag;
+  a.select_high = select_high;
+  a.keep_diagonal = keep_diagonal;
+  a.causal = causal;
+  const dim3 grid(static_cast<unsigned>(blocks));
+  if (hybrid)
+    launch_topk<true>(a, grid, static_cast<hipStream_t>(stream));
+  else
+    launch_topk<false>(a, grid, static_cast<hipStream_t>(stream));
+  return launch_status(fn);
+}
+
 }  // namespace
 }  // namespace cab
 
@@ -110,38 +209,15 @@ extern "C" cab_status_t cab_block_topk(const float* frc, int64_t B, int64_t H, i
                                        int32_t k, int select_high, int keep_diagonal, int causal,
                                        int32_t* kv_idx, int32_t* kv_cnt, uint8_t* dense_mask,
                                        void* stream) {
-  clear_error();
-  CAB_REQUIRE(B >= 0 && H >= 0 && M >= 0, CAB_ESHAPE, "cab_block_topk: negative size");
-  CAB_REQUIRE(M <= 8192, CAB_ESHAPE, "cab_block_topk: M=%lld exceeds 8192", (long long)M);
-  CAB_REQUIRE(k >= 1, CAB_EINVAL, "cab_block_topk: k=%d must be >= 1", (int)k);
-  CAB_REQUIRE(M == 0 || k <= M, CAB_EINVAL, "cab_block_topk: k=%d exceeds M=%lld", (int)k,
-              (long long)M);
-  const int64_t rows = B * H * M;
-  if (rows == 0) return CAB_OK;
-  CAB_REQUIRE(frc && kv_idx && kv_cnt, CAB_EINVAL, "cab_block_topk: null tensor pointer");
-  const int64_t blocks = ceil_div(rows, 4);
-  CAB_REQUIRE(blocks <= INT32_MAX, CAB_ESHAPE, "cab_block_topk: problem too large");
-  TopkArgs a;
-  a.frc = frc;
-  a.kv_idx = kv_idx;
-  a.kv_cnt = kv_cnt;
-  a.dense = dense_mask;
-  a.rows = rows;
-  a.M = M;
-  a.k = k;
-  a.select_high = select_high;
-  a.keep_diagonal = keep_diagonal;
-  a.causal = causal;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  dim3 grid(static_cast<unsigned>(blocks));
-  const int64_t nch = ceil_div(M, 64);
-  if (nch <= 1) topk_kernel<1><<<grid, 256, 0, s>>>(a);
-  else if (nch <= 2) topk_kernel<2><<<grid, 256, 0, s>>>(a);
-  else if (nch <= 4) topk_kernel<4><<<grid, 256, 0, s>>>(a);
-  else if (nch <= 8) topk_kernel<8><<<grid, 256, 0, s>>>(a);
-  else if (nch <= 16) topk_kernel<16><<<grid, 256, 0, s>>>(a);
-  else if (nch <= 32) topk_kernel<32><<<grid, 256, 0, s>>>(a);
-  else if (nch <= 64) topk_kernel<64><<<grid, 256, 0, s>>>(a);
-  else topk_kernel<128><<<grid, 256, 0, s>>>(a);
-  return launch_status("cab_block_topk");
+  return topk_common("cab_block_topk", frc, nullptr, B, H, M, k, 0, select_high, keep_diagonal,
+                     causal, kv_idx, kv_cnt, dense_mask, stream, false);
+}
+
+extern "C" cab_status_t cab_block_topk_hybrid(const float* frc, const float* magnitude, int64_t B,
+                                              int64_t H, int64_t M, int32_t k, int32_t k_mag,
+                                              int select_high, int keep_diagonal, int causal,
+                                              int32_t* kv_idx, int32_t* kv_cnt,
+                                              uint8_t* dense_mask, void* stream) {
+  return topk_common("cab_block_topk_hybrid", frc, magnitude, B, H, M, k, k_mag, select_high,
+                     keep_diagonal, causal, kv_idx, kv_cnt, dense_mask, stream, true);
 }

@@ -128,6 +128,25 @@ cab_status_t cab_block_topk(const float* frc, int64_t B, int64_t H, int64_t M, i
                             void* stream);
 
 /*
+ * Hybrid per-row block selection (CAB V4).
+ * Replaces generate_block_mask(frc, sparsity, select_high, keep_diagonal, causal,
+ * magnitude_scores, magnitude_ratio) of cab_attention/kernels/frc_kernel.py
+ * (absent; contract: experiments/longbench_qa/methods.py:404-418, :465-473;
+ * benchmarks/kernel_benchmark.py:197-205); the caller computes
+ * k_mag = int(k * magnitude_ratio).
+ *
+ * Row i selects as cab_block_topk, except that after the forced diagonal
+ * its first min(k_mag, remaining count) blocks are the candidates with the
+ * highest magnitude (ties to the lower j, -0.0 == +0.0, NaN above +inf); the
+ * rest of its count comes from the remaining candidates in FRC order.
+ * magnitude: contiguous fp32 [B,H,M,M]. 0 <= k_mag <= k.
+ */
+cab_status_t cab_block_topk_hybrid(const float* frc, const float* magnitude, int64_t B, int64_t H,
+                                   int64_t M, int32_t k, int32_t k_mag, int select_high,
+                                   int keep_diagonal, int causal, int32_t* kv_idx, int32_t* kv_cnt,
+                                   uint8_t* dense_mask, void* stream);
+
+/*
  * Workspace bytes cab_block_sparse_attn_fwd needs: one packed V^T tile
  * (16 KB) per (b, h, key block). 0 for unsupported sizes.
  */

@@ -48,6 +48,7 @@ __all__ = [
     "compute_block_frc",
     "order_keys",
     "generate_block_mask",
+    "magnitude_quota",
     "expand_block_mask",
     "effective_sparsity",
     "sparse_attention",
@@ -211,22 +212,46 @@ def order_keys(values: np.ndarray, select_high: bool) -> np.ndarray:
     return key
 
 
+def magnitude_quota(k: int, magnitude_ratio: float) -> int:
+    """Blocks per row reserved for the magnitude ranking in the hybrid mask:
+    ``int(k * magnitude_ratio)`` clamped to ``[0, k]`` (the same integer
+    floor as ``keep_count``). The reference defines the split only in words,
+    "reserve X% of budget for top-magnitude blocks" (methods.py:404-418)."""
+    if not 0.0 <= float(magnitude_ratio) <= 1.0:
+        raise ValueError(f"magnitude_ratio must be in [0, 1], got {magnitude_ratio}")
+    return min(k, max(0, int(k * float(magnitude_ratio))))
+
+
 def generate_block_mask(frc, sparsity: float, select_high: bool = False,
-                        keep_diagonal: bool = True, causal: bool = False):
+                        keep_diagonal: bool = True, causal: bool = False,
+                        magnitude_scores=None, magnitude_ratio: float = 0.5):
     """Per-row block selection (README.md:40-42; methods.py:339-345).
 
     Row i keeps ``k = keep_count(M, sparsity)`` blocks (``min(k, i+1)`` when
     causal, candidates ``j <= i``) with the lowest FRC (highest when
     ``select_high``), ties to the lower j. With ``keep_diagonal`` the block
-    ``j = i`` is always kept and counts toward k. Returns
-    ``(mask bool[B,H,M,M], kv_idx int32[B,H,M,k] ascending, -1 padded,
-    kv_cnt int32[B,H,M])``.
+    ``j = i`` is always kept and counts toward k.
+
+    Hybrid (CAB V4, methods.py:404-418, :465-473): with ``magnitude_scores``
+    the row first keeps ``min(magnitude_quota(k, ratio), need)`` candidates
+    with the highest magnitude (``need`` = the row's count after the forced
+    diagonal), then fills the rest of its count from the remaining candidates
+    in FRC order.
+
+    Returns ``(mask bool[B,H,M,M], kv_idx int32[B,H,M,k] ascending, -1
+    padded, kv_cnt int32[B,H,M])``.
     """
     f = np.asarray(frc)
     b, h, m, m2 = f.shape
     assert m == m2
     k = keep_count(m, sparsity)
     keys = order_keys(f, select_high)
+    kmag = 0
+    if magnitude_scores is not None:
+        mag = np.asarray(magnitude_scores)
+        assert mag.shape == f.shape
+        mkeys = order_keys(mag, True)
+        kmag = magnitude_quota(k, magnitude_ratio)
     mask = np.zeros((b, h, m, m), dtype=bool)
     kv_idx = np.full((b, h, m, k), -1, dtype=np.int32)
     kv_cnt = np.zeros((b, h, m), dtype=np.int32)
@@ -234,20 +259,24 @@ def generate_block_mask(frc, sparsity: float, select_high: bool = False,
         ncand = i + 1 if causal else m
         krow = min(k, ncand)
         cand = np.arange(ncand)
-        rowkeys = keys[:, :, i, :ncand]
-        if keep_diagonal:
-            others = cand[cand != i]
-            order = np.argsort(rowkeys[..., others], axis=-1, kind="stable")
-            chosen = others[order[..., :krow - 1]]
-            diag = np.full((b, h, 1), i, dtype=chosen.dtype)
-            chosen = np.concatenate([diag, chosen], axis=-1)
-        else:
-            order = np.argsort(rowkeys, axis=-1, kind="stable")
-            chosen = order[..., :krow]
-        chosen = np.sort(chosen, axis=-1)
-        kv_idx[:, :, i, :krow] = chosen
-        kv_cnt[:, :, i] = krow
-        np.put_along_axis(mask[:, :, i, :], chosen, True, axis=-1)
+        others = cand[cand != i] if keep_diagonal else cand
+        need = krow - (1 if keep_diagonal else 0)
+        need_m = min(kmag, need)
+        for bb in range(b):
+            for hh in range(h):
+                chosen = [i] if keep_diagonal else []
+                rest = others
+                if need_m > 0:
+                    order = np.argsort(mkeys[bb, hh, i, rest], kind="stable")
+                    pick = rest[order[:need_m]]
+                    chosen += pick.tolist()
+                    rest = np.setdiff1d(rest, pick)
+                order = np.argsort(keys[bb, hh, i, rest], kind="stable")
+                chosen += rest[order[:need - need_m]].tolist()
+                chosen = np.sort(np.asarray(chosen, dtype=np.int64))
+                kv_idx[bb, hh, i, :krow] = chosen
+                kv_cnt[bb, hh, i] = krow
+                mask[bb, hh, i, chosen] = True
     return mask, kv_idx, kv_cnt
 
 

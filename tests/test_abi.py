@@ -34,7 +34,8 @@ def test_header_declares_the_hot_path():
     for name in ("cab_abi_version", "cab_last_error", "cab_coarsen_maxl2",
                  "cab_block_frc_workspace_bytes", "cab_block_frc", "cab_block_topk",
                  "cab_block_sparse_attn_workspace_bytes", "cab_block_sparse_attn_fwd",
-                 "cab_block_sparse_attn_pack_v", "cab_block_sparse_attn_fwd_packed"):
+                 "cab_block_sparse_attn_pack_v", "cab_block_sparse_attn_fwd_packed",
+                 "cab_block_topk_hybrid"):
         assert name in syms
     assert set(syms) == set(nat.SIGNATURES), "ctypes table and header disagree"
 
@@ -98,6 +99,11 @@ def test_topk_validation(lib):
     assert call(k=65) == nat.CAB_EINVAL
     assert call(M=9000, k=3) == nat.CAB_ESHAPE
     assert call(M=0) == nat.CAB_OK
+    hyb = lambda **kw: lib.cab_block_topk_hybrid(FAKE, kw.get("mag", FAKE), 1, 1, 64, 3,
+                                                 kw.get("kmag", 1), 1, 1, 0, FAKE, FAKE, None, None)
+    assert hyb(kmag=4) == nat.CAB_EINVAL
+    assert hyb(kmag=-1) == nat.CAB_EINVAL
+    assert hyb(mag=None) == nat.CAB_EINVAL
 
 
 def test_attention_validation(lib):

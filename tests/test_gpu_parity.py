@@ -186,6 +186,32 @@ def test_topk_bit_exact(cuda, M, flags):
         np.testing.assert_array_equal(mask.cpu().numpy(), omask)
 
 
+@pytest.mark.parametrize("M", [7, 100, 513, 2000])
+@pytest.mark.parametrize("ratio", [0.0, 0.3, 0.5, 1.0])
+@pytest.mark.parametrize("flags", [(True, True, False), (False, True, True), (True, False, True)])
+def test_topk_hybrid_bit_exact(cuda, M, ratio, flags):
+    """CAB V4 hybrid selection (magnitude quota, then FRC) against the oracle."""
+    from cab_attention.kernels import generate_block_index, generate_block_mask
+    select_high, keep_diag, causal = flags
+    g = torch.Generator().manual_seed(M + 7)
+    f = torch.randint(-20, 20, (1, 2, M, M), generator=g).float()     # many exact ties
+    mag = torch.randint(0, 10, (1, 2, M, M), generator=g).float()
+    mag[0, 1] = torch.rand(M, M, generator=g)
+    for sp in (0.95, 0.6):
+        idx, cnt, mask = generate_block_index(f.to(cuda), sp, select_high=select_high,
+                                              keep_diagonal=keep_diag, causal=causal, dense=True,
+                                              magnitude_scores=mag.to(cuda), magnitude_ratio=ratio)
+        omask, oidx, ocnt = O.generate_block_mask(f.numpy(), sp, select_high, keep_diag, causal,
+                                                  magnitude_scores=mag.numpy(),
+                                                  magnitude_ratio=ratio)
+        np.testing.assert_array_equal(cnt.cpu().numpy(), ocnt)
+        np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
+        np.testing.assert_array_equal(mask.cpu().numpy(), omask)
+    m2 = generate_block_mask(f.to(cuda), 0.6, select_high, keep_diag, causal,
+                             magnitude_scores=mag.to(cuda), magnitude_ratio=ratio)
+    assert torch.equal(m2.cpu(), torch.from_numpy(omask))
+
+
 def test_topk_nan_inf(cuda):
     from cab_attention.kernels import generate_block_index
     f = torch.tensor([[[[0.0, float("nan"), -float("inf"), float("inf"), -0.0, 1.0]] * 6]])

@@ -242,6 +242,63 @@ def test_mask_matches_brute_force(select_high, keep_diag, causal):
     assert O.effective_sparsity(mask) == pytest.approx(1 - cnt.sum() / mask.size)
 
 
+def _brute_hybrid(f, mag, k, kmag, select_high, keep_diag, causal):
+    """Python-loop restatement of the hybrid rule, written independently of
+    the oracle: diagonal, then the largest magnitudes, then FRC order."""
+    m = f.shape[0]
+    rows = []
+    for i in range(m):
+        cand = list(range(i + 1 if causal else m))
+        krow = min(k, len(cand))
+        chosen = [i] if keep_diag else []
+        rest = [j for j in cand if not (keep_diag and j == i)]
+        need = krow - len(chosen)
+        nm = min(kmag, need)
+        by_mag = sorted(rest, key=lambda j: (-(0.0 if mag[i, j] == 0 else float(mag[i, j])), j))
+        chosen += by_mag[:nm]
+        rest = [j for j in rest if j not in by_mag[:nm]]
+        sign = -1.0 if select_high else 1.0
+        rest.sort(key=lambda j: (sign * (0.0 if f[i, j] == 0 else float(f[i, j])), j))
+        chosen += rest[:need - nm]
+        rows.append(sorted(chosen))
+    return rows
+
+
+@pytest.mark.parametrize("ratio", [0.0, 0.25, 0.5, 1.0])
+@pytest.mark.parametrize("select_high,keep_diag,causal", [(True, True, False), (False, True, True),
+                                                          (True, False, True), (False, False, False)])
+def test_hybrid_mask_matches_brute_force(ratio, select_high, keep_diag, causal):
+    rng = np.random.default_rng(11)
+    m = 30
+    f = rng.integers(-3, 4, size=(1, 2, m, m)).astype(np.float32)    # many ties
+    mag = rng.integers(0, 5, size=(1, 2, m, m)).astype(np.float32)
+    mask, idx, cnt = O.generate_block_mask(f, 0.7, select_high, keep_diag, causal,
+                                           magnitude_scores=mag, magnitude_ratio=ratio)
+    k = O.keep_count(m, 0.7)
+    kmag = O.magnitude_quota(k, ratio)
+    assert kmag == int(k * ratio)
+    for h in range(2):
+        want = _brute_hybrid(f[0, h], mag[0, h], k, kmag, select_high, keep_diag, causal)
+        for i in range(m):
+            assert idx[0, h, i, :cnt[0, h, i]].tolist() == want[i]
+            assert sorted(np.flatnonzero(mask[0, h, i]).tolist()) == want[i]
+
+
+def test_hybrid_mask_special_cases():
+    rng = np.random.default_rng(12)
+    f = rng.standard_normal((1, 1, 40, 40)).astype(np.float32)
+    mag = rng.standard_normal((1, 1, 40, 40)).astype(np.float32)
+    pure, _, _ = O.generate_block_mask(f, 0.8)
+    ratio0, _, _ = O.generate_block_mask(f, 0.8, magnitude_scores=mag, magnitude_ratio=0.0)
+    np.testing.assert_array_equal(pure, ratio0)               # no magnitude share: pure FRC
+    # ratio 1: every non-diagonal slot by magnitude = pure selection on -|mag| order
+    ratio1, _, _ = O.generate_block_mask(f, 0.8, magnitude_scores=mag, magnitude_ratio=1.0)
+    bymag, _, _ = O.generate_block_mask(mag, 0.8, select_high=True)
+    np.testing.assert_array_equal(ratio1, bymag)
+    with pytest.raises(ValueError):
+        O.magnitude_quota(10, 1.5)
+
+
 def test_mask_nan_and_signed_zero_order():
     f = np.array([[[[0.0, -0.0, np.nan, 1.0, -1.0]] * 5]], np.float32)
     _, idx, cnt = O.generate_block_mask(f, 0.4, keep_diagonal=False)   # k = 3 per row
