@@ -2,9 +2,8 @@
 //
 // One wave64 per FRC row. The row's M scores are read once (coalesced, lane l
 // holds columns j = 64 c + l) and mapped to order-preserving uint32 keys in
-// registers. The k-th smallest key is found by a 32-step bitwise search: each
-// step counts the candidates below a trial threshold with one ballot +
-// popcount per register, so all lanes agree on every decision without LDS.
+// registers. The k-th smallest key is found by a 4-pass radix select (8 bits
+// per pass, a 256-bin LDS histogram per wave, a wave-wide prefix scan).
 // A last pass in ascending j keeps every key below the threshold and the
 // first (in j) keys equal to it, assigns output slots with a prefix
 // popcount, and writes the compact ascending index list and, optionally, the
@@ -44,27 +43,87 @@ __device__ __forceinline__ uint32_t order_key(float f, bool high) {
 }
 
 // theta = the need-th smallest key among the candidates (the largest theta
-// with count(key < theta) < need), by a 32-step bitwise search in which every
-// step counts with one ballot per register; returns in need_eq how many keys
-// equal to theta (the first ones in j order) complete the selection.
+// with count(key < theta) < need), by a radix select over the key's four
+// bytes, most significant first: each pass histograms the next byte of the
+// candidates that still match the chosen prefix in the wave's LDS histogram,
+// and a wave-wide scan picks the bin where the running count reaches need.
+// The histogram keeps HSUB interleaved copies of every bin (lane % HSUB
+// picks one), so that the many keys of a row that share a byte do not all
+// update one LDS word. Returns in need_eq how many keys equal to theta (the
+// first ones in j order) complete the selection.
+constexpr int HSUB = 8;
+// Orders one wave's LDS accesses across its lanes (the histogram is shared
+// by the lanes of a wave; other waves of the workgroup may have exited).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
 template <int NCH, typename Cand>
 __device__ __forceinline__ uint32_t kth_key(const uint32_t (&key)[NCH], Cand is_cand, int64_t need,
-                                            int64_t& need_eq) {
-  uint32_t theta = 0u;
+                                            int64_t& need_eq, uint32_t* hist) {
+  const int lane = lane_id();
+  uint32_t prefix = 0u, pmask = 0u;
+  int64_t rem = need;  // rank still to find among the keys matching the prefix
   need_eq = 0;
-  if (need <= 0) return theta;
-  for (int b = 31; b >= 0; --b) {
-    const uint32_t trial = theta | (1u << b);
-    int64_t cnt = 0;
+  if (need <= 0) return 0u;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) cnt += __popcll(ballot64(is_cand(c) && key[c] < trial));
-    if (cnt < need) theta = trial;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    wave_sync();  // the previous pass's reads are done
+    // Layout: 16-byte slot (q, l) at index 64 q + l holds copies 4 (q % 2) .. +3
+    // of bin 4 l + q / 2, so lane l clears and sums its own four bins with
+    // lane-contiguous (conflict-free) 16-byte accesses.
+    u32x4* slots = reinterpret_cast<u32x4*>(hist);
+#pragma unroll
+    for (int q = 0; q < HSUB; ++q) slots[64 * q + lane] = u32x4{0u, 0u, 0u, 0u};
+    wave_sync();
+    const uint32_t sub = static_cast<uint32_t>(lane % HSUB);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      if (is_cand(c) && (key[c] & pmask) == prefix) {
+        const uint32_t bn = (key[c] >> shift) & 255u;
+        const uint32_t q = 2u * (bn & 3u) + (sub >> 2);
+        atomicAdd(&hist[4u * (64u * q + (bn >> 2)) + (sub & 3u)], 1u);
+      }
+    wave_sync();
+    // Bins 4 lane .. 4 lane + 3: inclusive prefix counts across the wave.
+    uint32_t hv[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int q = 0; q < HSUB; ++q) {
+      const u32x4 x = slots[64 * q + lane];
+      hv[q / 2] += x[0] + x[1] + x[2] + x[3];
+    }
+    const uint32_t mine = hv[0] + hv[1] + hv[2] + hv[3];
+    uint32_t incl = mine;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t up = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += up;
+    }
+    const uint32_t excl = incl - mine;
+    // First lane whose bins reach rank rem; inside it, the first such bin.
+    const uint64_t reach = ballot64(static_cast<int64_t>(incl) >= rem);
+    const int src = __builtin_ctzll(reach);
+    uint32_t run = excl, bin = 0u;
+    bool found = false;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (!found && static_cast<int64_t>(run + hv[q]) >= rem) {
+        found = true;
+        bin = 4u * lane + q;
+      } else if (!found) {
+        run += hv[q];
+      }
+    }
+    const uint32_t sel_bin = __shfl(bin, src, 64);
+    const uint32_t below = __shfl(run, src, 64);
+    rem -= below;
+    prefix |= sel_bin << shift;
+    pmask |= 255u << shift;
   }
-  int64_t below = 0;
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) below += __popcll(ballot64(is_cand(c) && key[c] < theta));
-  need_eq = need - below;
-  return theta;
+  need_eq = rem;  // keys below theta: need - rem; the rest are ties at theta
+  return prefix;
 }
 
 template <int NCH, bool HYB>
@@ -80,16 +139,29 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   const float* f = a.frc + row * a.M;
   const bool high = a.select_high != 0;
   const uint64_t lt_mask = lanemask_lt();
+  __shared__ uint32_t hist_all[4][256 * HSUB];
+  uint32_t* hist = hist_all[threadIdx.x >> 6];
 
+  // Loads are unconditional (the index is clamped) so that all NCH are in
+  // flight together; columns past M get the largest key.
+  const int Mi = static_cast<int>(a.M);
   uint32_t key[NCH];
+  {
+    float v[NCH];
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int64_t j = 64 * c + lane;
-    key[c] = j < a.M ? order_key(f[j], high) : 0xffffffffu;
+    for (int c = 0; c < NCH; ++c) {
+      const int j = 64 * c + lane;
+      v[c] = f[j < Mi ? j : Mi - 1];
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) asm volatile("" ::"v"(v[c]));  // keeps the loads unconditional
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) key[c] = 64 * c + lane < Mi ? order_key(v[c], high) : 0xffffffffu;
   }
+  const int ncand_i = static_cast<int>(ncand), i_i = static_cast<int>(i);
   auto is_cand = [&](int c) {
-    const int64_t j = 64 * c + lane;
-    return j < ncand && !(kd && j == i);
+    const int j = 64 * c + lane;
+    return j < ncand_i && !(kd && j == i_i);
   };
 
   // Hybrid: the need_m candidates of highest magnitude first (bit c of msel
@@ -102,13 +174,20 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
     need_m = min(static_cast<int64_t>(a.kmag), need);
     const float* mg = a.mag + row * a.M;
     uint32_t mkey[NCH];
+    {
+      float v[NCH];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const int64_t j = 64 * c + lane;
-      mkey[c] = j < a.M ? order_key(mg[j], true) : 0xffffffffu;
+      for (int c = 0; c < NCH; ++c) {
+        const int j = 64 * c + lane;
+        v[c] = mg[j < Mi ? j : Mi - 1];
+      }
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) asm volatile("" ::"v"(v[c]));
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) mkey[c] = 64 * c + lane < Mi ? order_key(v[c], true) : 0xffffffffu;
     }
     int64_t meq = 0;
-    const uint32_t mtheta = kth_key(mkey, is_cand, need_m, meq);
+    const uint32_t mtheta = kth_key(mkey, is_cand, need_m, meq, hist);
     int64_t eq_seen = 0;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
@@ -126,7 +205,7 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   // FRC order for the rest of the row.
   const int64_t need_f = need - need_m;
   int64_t need_eq = 0;
-  const uint32_t theta = kth_key(key, is_cand_f, need_f, need_eq);
+  const uint32_t theta = kth_key(key, is_cand_f, need_f, need_eq, hist);
 
   int64_t pos = 0, eq_seen = 0;
   int32_t* out = a.kv_idx + row * a.k;
