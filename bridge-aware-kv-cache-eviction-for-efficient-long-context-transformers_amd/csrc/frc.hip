@@ -275,7 +275,9 @@ struct TriArgs {
 
 // LDS operand tile in MFMA order: slot (kk, sub, lane) of 16 bytes holds the
 // 8 consecutive k values lane needs for a 32x32x16 MFMA, so every operand
-// read is one contiguous 1 KB wave access.
+// read is one 1 KB wave access. Inside each 64-slot group the slot of lane L
+// is stored at position L ^ (4 (2 kk + L / 32)): the four threads that load
+// one row's 64 bytes then write four different LDS bank groups.
 constexpr int SLOTS = (TK / 16) * (TT / 32) * 64;  // 512 slots = 8 KB per plane
 
 __device__ __forceinline__ void tri_load(const uint16_t* plane, int64_t row0, int64_t k0, int64_t Mp,
@@ -294,7 +296,7 @@ __device__ __forceinline__ void tri_store(u32x4* lds, const u32x4 (&reg)[2]) {
     const int cid = threadIdx.x + 256 * q;
     const int row = cid >> 2, kc = cid & 3;
     const int kk = kc >> 1, hf = kc & 1, sub = row >> 5;
-    lds[(kk * (TT / 32) + sub) * 64 + (row & 31) + 32 * hf] = reg[q];
+    lds[(kk * (TT / 32) + sub) * 64 + (((row & 31) + 32 * hf) ^ (4 * (2 * kk + hf)))] = reg[q];
   }
 }
 
@@ -332,26 +334,35 @@ __global__ __launch_bounds__(256) void triangle_kernel(TriArgs a) {
 #pragma unroll
     for (int y = 0; y < 2; ++y) acc[x][y] = f32x16{};
 
-  u32x4 reg[4][2];
-#pragma unroll
-  for (int p = 0; p < 4; ++p) tri_load(planes[p], rows[p], 0, a.Mp, reg[p]);
+  // Operand k-slices travel global -> registers -> LDS; the registers of
+  // slice kt + 2 are loaded while slice kt is multiplied (two register
+  // buffers, two LDS stages), so a load has two slices of MFMA work to land.
+  u32x4 reg[2][4][2];
   const int nk = static_cast<int>(a.Mp / TK);
-  for (int kt = 0; kt < nk; ++kt) {
-    const int st = kt & 1;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) tri_store(lds[st][p], reg[p]);
+  for (int p = 0; p < 4; ++p) tri_load(planes[p], rows[p], 0, a.Mp, reg[0][p]);
+  if (nk > 1) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) tri_load(planes[p], rows[p], TK, a.Mp, reg[1][p]);
+  }
+  auto slice = [&](int kt, auto buf_tag) {
+    constexpr int st = decltype(buf_tag)::value;  // slice kt uses register buffer and LDS stage kt % 2
+#pragma unroll
+    for (int p = 0; p < 4; ++p) tri_store(lds[st][p], reg[st][p]);
     __syncthreads();
-    if (kt + 1 < nk) {
+    if (kt + 2 < nk) {
 #pragma unroll
-      for (int p = 0; p < 4; ++p) tri_load(planes[p], rows[p], static_cast<int64_t>(kt + 1) * TK, a.Mp, reg[p]);
+      for (int p = 0; p < 4; ++p)
+        tri_load(planes[p], rows[p], static_cast<int64_t>(kt + 2) * TK, a.Mp, reg[st][p]);
     }
 #pragma unroll
     for (int kk = 0; kk < TK / 16; ++kk) {
       bf16x8 ah[2], al[2], bh8[2], bl[2];
+      const int lsw = lane ^ (4 * (2 * kk + (lane >> 5)));
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const int sa = (kk * (TT / 32) + 2 * wi + s) * 64 + lane;
-        const int sb = (kk * (TT / 32) + 2 * wj + s) * 64 + lane;
+        const int sa = (kk * (TT / 32) + 2 * wi + s) * 64 + lsw;
+        const int sb = (kk * (TT / 32) + 2 * wj + s) * 64 + lsw;
         ah[s] = __builtin_bit_cast(bf16x8, lds[st][0][sa]);
         al[s] = __builtin_bit_cast(bf16x8, lds[st][1][sa]);
         bh8[s] = __builtin_bit_cast(bf16x8, lds[st][2][sb]);
@@ -366,6 +377,10 @@ __global__ __launch_bounds__(256) void triangle_kernel(TriArgs a) {
           acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[x], bh8[y], acc[x][y], 0, 0, 0);
         }
     }
+  };
+  for (int kt = 0; kt < nk; kt += 2) {
+    slice(kt, std::integral_constant<int, 0>{});
+    if (kt + 1 < nk) slice(kt + 1, std::integral_constant<int, 1>{});
   }
 
   // Epilogue: F = combine(Ahat, T) for the wave's 64x64 block.
