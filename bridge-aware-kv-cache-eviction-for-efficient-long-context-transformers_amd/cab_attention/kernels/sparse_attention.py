@@ -43,7 +43,8 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     """``out[t] = softmax_s(q_t . k_s * scale) v_s`` over the key blocks
     ``kv_idx[b, h, i, :kv_cnt[b, h, i]]`` of the query block i holding t.
 
-    q, k, v: ``[B, H, N, D]`` bf16 or fp16 (D = 128, block_size = 64); causal
+    q, k, v: ``[B, H, N, D]`` bf16, fp16 or fp32 (D = 128, block_size = 64;
+    fp32 runs on split bf16 hi + lo operands, three MFMA products each); causal
     drops keys s > t; a query with no key gets 0; ``scale`` (> 0) defaults to
     ``1/sqrt(D)``. Index entries outside ``[0, M)`` are skipped. ``out`` may be
     a preallocated ``[B, H, N, D]`` view (any strides with a contiguous last
@@ -68,7 +69,7 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     out, lse = _outputs(q, out, return_lse, dev)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    wbytes = lib.cab_block_sparse_attn_workspace_bytes(B, H, N, D, int(block_size))
+    wbytes = lib.cab_block_sparse_attn_workspace_bytes(dt, B, H, N, D, int(block_size))
     ws = torch.empty(max(int(wbytes), 16), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         st = lib.cab_block_sparse_attn_fwd(
@@ -84,7 +85,7 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 def pack_v(v: torch.Tensor, block_size: int = 64) -> torch.Tensor:
     """V ``[B, H, N, D]`` -> its packed V^T tiles (uint8, 16 KB per (b, h, key
     block)) for :func:`block_sparse_attention_packed`; reusable while V is
-    unchanged."""
+    unchanged. bf16 / fp16 only."""
     if v.dim() != 4:
         raise ValueError(f"v must be [B, H, N, D]; got {tuple(v.shape)}")
     dev = nat.require_device(v)
@@ -92,7 +93,7 @@ def pack_v(v: torch.Tensor, block_size: int = 64) -> torch.Tensor:
     dt = nat.dtype_code(v)
     B, H, N, D = v.shape
     v = nat.aligned_rows(v)
-    wbytes = lib.cab_block_sparse_attn_workspace_bytes(B, H, N, D, int(block_size))
+    wbytes = lib.cab_block_sparse_attn_workspace_bytes(dt, B, H, N, D, int(block_size))
     vt = torch.empty(max(int(wbytes), 16), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         st = lib.cab_block_sparse_attn_pack_v(v.data_ptr(), dt, B, H, N, D, nat.strides4(v),

@@ -32,6 +32,14 @@
 // Workgroups are mapped so that one XCD runs consecutive query blocks of the
 // same heads (their K/V share L2), longest causal rows first.
 //
+// fp32 inputs run the same kernel on bf16 MFMA with every operand split in
+// two, x = hi + lo (hi = bf16(x), lo = bf16(x - hi), RNE), and three products
+// per MFMA site: a b ~ a_hi b_hi + a_lo b_hi + a_hi b_lo (the dropped
+// a_lo b_lo and the rounding of lo leave a relative error near 2^-16 per
+// product). pack_split_kernel writes each key block's K and V^T halves as
+// one 64 KB image (the exact LDS layout of a stage); the attention kernel
+// then runs one workgroup per CU with 64 KB stages and writes fp32 output.
+//
 // Algorithmic work per kept tile: 4 * 64 * 64 * 128 flops (2 * 64 * 65 * 128
 // on a causal diagonal tile). Bound: MFMA.
 #include "cab_internal.h"
@@ -45,12 +53,19 @@ constexpr int TILE_SLOTS = 1024;             // 16-byte slots per packed V^T til
 constexpr size_t TILE_BYTES = TILE_SLOTS * 16;
 constexpr float RESCALE_LOG2 = 8.0f;         // lazy rescale threshold (2^8)
 constexpr int LIST_MAX = 2048;               // kv lists up to this length are staged in LDS
+// fp32 block image: [K hi rows][K lo rows][V^T hi tile][V^T lo tile], 16 KB each.
+constexpr size_t SPLIT_BLOCK_BYTES = 4 * TILE_BYTES;
+
+// Bytes of packed data per (b, h, key block) for an input dtype.
+constexpr size_t block_bytes(cab_dtype_t dt) {
+  return dt == CAB_F32 ? SPLIT_BLOCK_BYTES : TILE_BYTES;
+}
 
 struct AttnArgs {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* vt;  // packed V^T tiles [B*H][M][TILE_SLOTS] x 16 bytes
-  uint16_t* o;
+  const void* q;       // bf16 / fp16 / fp32 [B, H, N, D]
+  const uint16_t* k;   // bf16 / fp16 K (unused for fp32: K is in the block images)
+  const uint16_t* vt;  // per (b, h, key block): V^T tile (16 KB) or fp32 block image (64 KB)
+  void* o;             // same dtype as q
   float* lse;
   int64_t qs[3], ks[3], os[3];  // b, h, token strides (elements)
   const int32_t* kv_idx;
@@ -89,11 +104,51 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   }
 }
 
+// fp32 -> bf16 pair split of two values: {hi, lo} with hi = bf16(x) and
+// lo = bf16(x - hi), both round-to-nearest-even (x - hi is exact in fp32).
+__device__ __forceinline__ u32x2 split2(float x0, float x1) {
+  const uint32_t hi = pack2<true>(x0, x1);
+  const float h0 = __builtin_bit_cast(float, hi << 16);
+  const float h1 = __builtin_bit_cast(float, hi & 0xffff0000u);
+  return u32x2{hi, pack2<true>(x0 - h0, x1 - h1)};
+}
+
+// Eight consecutive fp32 values (x0, x1) -> bf16x8 hi and lo operands.
+__device__ __forceinline__ void split8(const f32x4& x0, const f32x4& x1, u32x4& hi, u32x4& lo) {
+  const u32x2 a = split2(x0[0], x0[1]), b = split2(x0[2], x0[3]);
+  const u32x2 e = split2(x1[0], x1[1]), f = split2(x1[2], x1[3]);
+  hi = u32x4{a[0], b[0], e[0], f[0]};
+  lo = u32x4{a[1], b[1], e[1], f[1]};
+}
+
+typedef uint16_t VRows[HD + 8];  // one block of V rows in LDS, padded
+
 // V^T tile slot (dt, s, L) (index (2 dt + s) * 64 + L) holds, for d = 16 dt + L % 16
 // and g = L / 16, the 8 values V[32 s + 4 g + r][d] (r = 0..3) followed by
 // V[32 s + 16 + 4 g + r][d] (r = 0..3).
+__device__ __forceinline__ u32x4 vt_slot(const VRows* vs, int slot) {
+  const int row = slot >> 6, L = slot & 63;
+  const int dt = row >> 1, s = row & 1, g = L >> 4;
+  const int d = 16 * dt + (L & 15);
+  const int k0 = 32 * s + 4 * g;
+  u32x4 x;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    x[2 * p + 0] = static_cast<uint32_t>(vs[k0 + 16 * p + 0][d]) |
+                   (static_cast<uint32_t>(vs[k0 + 16 * p + 1][d]) << 16);
+    x[2 * p + 1] = static_cast<uint32_t>(vs[k0 + 16 * p + 2][d]) |
+                   (static_cast<uint32_t>(vs[k0 + 16 * p + 3][d]) << 16);
+  }
+  return x;
+}
+
+__device__ __forceinline__ void vrows_put(VRows* vs, int key, int c, const u32x4& x) {
+  *reinterpret_cast<u32x2*>(&vs[key][8 * c]) = u32x2{x[0], x[1]};
+  *reinterpret_cast<u32x2*>(&vs[key][8 * c + 4]) = u32x2{x[2], x[3]};
+}
+
 __global__ __launch_bounds__(256) void pack_vt_kernel(PackArgs a) {
-  __shared__ uint16_t vs[BS][HD + 8];  // padded rows
+  __shared__ VRows vs[BS];
   const int64_t bh = blockIdx.y, j = blockIdx.x;
   const int64_t b = bh / a.H, h = bh - (bh / a.H) * a.H;
   const uint16_t* vb = a.v + b * a.vs[0] + h * a.vs[1];
@@ -105,27 +160,62 @@ __global__ __launch_bounds__(256) void pack_vt_kernel(PackArgs a) {
     const int64_t t = j * BS + key;
     const u32x4 x = t < a.N ? *reinterpret_cast<const u32x4*>(vb + t * a.vs[2] + 8 * c)
                             : u32x4{0u, 0u, 0u, 0u};
-    *reinterpret_cast<u32x2*>(&vs[key][8 * c]) = u32x2{x[0], x[1]};
-    *reinterpret_cast<u32x2*>(&vs[key][8 * c + 4]) = u32x2{x[2], x[3]};
+    vrows_put(vs, key, c, x);
   }
   __syncthreads();
   u32x4* out = reinterpret_cast<u32x4*>(a.vt) + (bh * a.M + j) * TILE_SLOTS;
 #pragma unroll
+  for (int r = 0; r < 4; ++r) out[tid + 256 * r] = vt_slot(vs, tid + 256 * r);
+}
+
+struct SplitPackArgs {
+  const float* k;
+  const float* v;
+  uint16_t* img;  // [B*H][M] block images of SPLIT_BLOCK_BYTES
+  int64_t ks[3], vs[3];
+  int64_t H, N, M;
+};
+
+// fp32 K and V of key block j -> its 64 KB block image (zero past N):
+//   K hi / K lo: 64 rows x 256 bytes, the 16-byte chunks of row R stored at
+//     position c ^ (R % 16) (the LDS layout the K operand reads expect);
+//   V^T hi / V^T lo: pack_vt_kernel's tile layout.
+__global__ __launch_bounds__(256) void pack_split_kernel(SplitPackArgs a) {
+  __shared__ VRows vh[BS], vl[BS];
+  const int64_t bh = blockIdx.y, j = blockIdx.x;
+  const int64_t b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const float* kb = a.k + b * a.ks[0] + h * a.ks[1];
+  const float* vb = a.v + b * a.vs[0] + h * a.vs[1];
+  const int tid = threadIdx.x;
+  u32x4* out = reinterpret_cast<u32x4*>(a.img) + (bh * a.M + j) * (4 * TILE_SLOTS);
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int cid = tid + 256 * r;  // 1024 chunks of 8 values
+    const int key = cid >> 4, c = cid & 15;
+    const int64_t t = j * BS + key;
+    const bool in = t < a.N;
+    const float* kp = kb + t * a.ks[2] + 8 * c;
+    const float* vp = vb + t * a.vs[2] + 8 * c;
+    const f32x4 k0 = in ? *reinterpret_cast<const f32x4*>(kp) : zero;
+    const f32x4 k1 = in ? *reinterpret_cast<const f32x4*>(kp + 4) : zero;
+    const f32x4 v0 = in ? *reinterpret_cast<const f32x4*>(vp) : zero;
+    const f32x4 v1 = in ? *reinterpret_cast<const f32x4*>(vp + 4) : zero;
+    u32x4 hi, lo;
+    split8(k0, k1, hi, lo);
+    const int pos = 16 * key + (c ^ (key & 15));
+    out[pos] = hi;
+    out[TILE_SLOTS + pos] = lo;
+    split8(v0, v1, hi, lo);
+    vrows_put(vh, key, c, hi);
+    vrows_put(vl, key, c, lo);
+  }
+  __syncthreads();
+#pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int slot = tid + 256 * r;
-    const int row = slot >> 6, L = slot & 63;
-    const int dt = row >> 1, s = row & 1, g = L >> 4;
-    const int d = 16 * dt + (L & 15);
-    const int k0 = 32 * s + 4 * g;
-    u32x4 x;
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      x[2 * p + 0] = static_cast<uint32_t>(vs[k0 + 16 * p + 0][d]) |
-                     (static_cast<uint32_t>(vs[k0 + 16 * p + 1][d]) << 16);
-      x[2 * p + 1] = static_cast<uint32_t>(vs[k0 + 16 * p + 2][d]) |
-                     (static_cast<uint32_t>(vs[k0 + 16 * p + 3][d]) << 16);
-    }
-    out[slot] = x;
+    out[2 * TILE_SLOTS + slot] = vt_slot(vh, slot);
+    out[3 * TILE_SLOTS + slot] = vt_slot(vl, slot);
   }
 }
 
@@ -178,6 +268,7 @@ constexpr float M_EMPTY = -1.0e30f;
 // the lane axis) against one key half of every kept block.
 struct WaveAcc {
   u32x4 qreg[2][4];  // Q^T B operand: qreg[qt][ds] = Q[q0 + 16 qt + l % 16][32 ds + 8 g .. +8]
+  u32x4 qlo[2][4];   // fp32 inputs: the lo halves of qreg (unused otherwise)
   f32x4 oacc[8][2];  // O^T[16 dt + 4 g + r][q0 + 16 qt + l % 16]
   f32x4 lacc[2];     // row sums (all four r equal)
   float m_run[2];    // running maximum of the raw scores
@@ -206,18 +297,28 @@ __device__ __forceinline__ WaveGeo wave_geo(int w4) {
   return ge;
 }
 
-// Loads the wave's 32 queries (from token q0; rows at or past N are zero)
-// and clears the accumulators.
-__device__ __forceinline__ void acc_init(WaveAcc& s, const WaveGeo& ge, const uint16_t* qb,
+// Loads the wave's 32 queries (from token q0; rows at or past N are zero;
+// fp32 queries split into qreg / qlo) and clears the accumulators.
+template <cab_dtype_t DT>
+__device__ __forceinline__ void acc_init(WaveAcc& s, const WaveGeo& ge, const void* qv,
                                          int64_t qs2, int q0, int N, float c) {
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     const int qtok = q0 + 16 * qt + ge.l16;
+    const bool in = q0 >= 0 && qtok < N;
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds)
-      s.qreg[qt][ds] = (q0 >= 0 && qtok < N)
-                           ? *reinterpret_cast<const u32x4*>(qb + qtok * qs2 + 32 * ds + 8 * ge.g)
-                           : u32x4{0u, 0u, 0u, 0u};
+    for (int ds = 0; ds < 4; ++ds) {
+      if constexpr (DT == CAB_F32) {
+        const float* qp = static_cast<const float*>(qv) + qtok * qs2 + 32 * ds + 8 * ge.g;
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        const f32x4 x0 = in ? *reinterpret_cast<const f32x4*>(qp) : zero;
+        const f32x4 x1 = in ? *reinterpret_cast<const f32x4*>(qp + 4) : zero;
+        split8(x0, x1, s.qreg[qt][ds], s.qlo[qt][ds]);
+      } else {
+        const uint16_t* qp = static_cast<const uint16_t*>(qv) + qtok * qs2 + 32 * ds + 8 * ge.g;
+        s.qreg[qt][ds] = in ? *reinterpret_cast<const u32x4*>(qp) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
     s.lacc[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) s.oacc[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -228,28 +329,43 @@ __device__ __forceinline__ void acc_init(WaveAcc& s, const WaveGeo& ge, const ui
 
 // Marks the queries as loaded: later waits in the block loop then never
 // have to cover the Q loads.
+template <cab_dtype_t DT>
 __device__ __forceinline__ void acc_q_ready(WaveAcc& s) {
   asm volatile("" ::"v"(s.qreg[0][0]), "v"(s.qreg[0][1]), "v"(s.qreg[0][2]), "v"(s.qreg[0][3]),
                "v"(s.qreg[1][0]), "v"(s.qreg[1][1]), "v"(s.qreg[1][2]), "v"(s.qreg[1][3]));
+  if constexpr (DT == CAB_F32)
+    asm volatile("" ::"v"(s.qlo[0][0]), "v"(s.qlo[0][1]), "v"(s.qlo[0][2]), "v"(s.qlo[0][3]),
+                 "v"(s.qlo[1][0]), "v"(s.qlo[1][1]), "v"(s.qlo[1][2]), "v"(s.qlo[1][3]));
 }
 
 // One key block j (staged at ks / vts) for the wave's queries of query block i:
 //   S^T = K_kh Q^T (16 MFMA), masks, online softmax (fp32, log2 domain),
 //   O^T += V_kh^T P^T (16 MFMA), row sums = 1 P^T (2 MFMA).
-template <bool BF16>
+// fp32 (split operands, the lo halves 16 KB past the hi ones in LDS):
+// 48 + 48 + 4 MFMA.
+template <cab_dtype_t DT>
 __device__ __forceinline__ void acc_block(WaveAcc& s, const WaveGeo& ge, const char* ks,
                                           const u32x4* vts, int j, int i, bool valid, int N,
                                           bool causal, float c) {
+  constexpr bool BF16 = DT != CAB_F16;
+  constexpr bool SPLIT = DT == CAB_F32;
   const uint32_t one2 = BF16 ? 0x3f803f80u : 0x3c003c00u;
   const u32x4 ones = {one2, one2, one2, one2};
   u32x4 kop[4][2], vop[8];
+  u32x4 klo[4][2], vlo[8];  // SPLIT only
 #pragma unroll
   for (int ds = 0; ds < 4; ++ds)
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+    for (int tt = 0; tt < 2; ++tt) {
       kop[ds][tt] = *reinterpret_cast<const u32x4*>(ks + ge.kread[ds] + 4096 * tt);
+      if constexpr (SPLIT)
+        klo[ds][tt] = *reinterpret_cast<const u32x4*>(ks + TILE_BYTES + ge.kread[ds] + 4096 * tt);
+    }
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) vop[dt] = vts[(dt * 2 + ge.kh) * 64 + ge.lane];
+  for (int dt = 0; dt < 8; ++dt) {
+    vop[dt] = vts[(dt * 2 + ge.kh) * 64 + ge.lane];
+    if constexpr (SPLIT) vlo[dt] = vts[TILE_SLOTS + (dt * 2 + ge.kh) * 64 + ge.lane];
+  }
 
   // sc[tt][qt][r] = score(key 32 kh + 16 tt + 4 g + r, query 32 qh + 16 qt + l % 16)
   f32x4 sc[2][2];
@@ -262,7 +378,13 @@ __device__ __forceinline__ void acc_block(WaveAcc& s, const WaveGeo& ge, const c
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) sc[tt][qt] = mfma16<BF16>(kop[ds][tt], s.qreg[qt][ds], sc[tt][qt]);
+      for (int qt = 0; qt < 2; ++qt) {
+        if constexpr (SPLIT) {
+          sc[tt][qt] = mfma16<true>(klo[ds][tt], s.qreg[qt][ds], sc[tt][qt]);
+          sc[tt][qt] = mfma16<true>(kop[ds][tt], s.qlo[qt][ds], sc[tt][qt]);
+        }
+        sc[tt][qt] = mfma16<BF16>(kop[ds][tt], s.qreg[qt][ds], sc[tt][qt]);
+      }
 
   if (!valid || (causal && j >= i) || (j + 1) * BS > N) {
 #pragma unroll
@@ -303,7 +425,7 @@ __device__ __forceinline__ void acc_block(WaveAcc& s, const WaveGeo& ge, const c
       s.nmc[qt] = -m_new * c;
     }
   }
-  u32x4 pb[2];
+  u32x4 pb[2], pl[2];  // pl: SPLIT only
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     float pv[2][4];
@@ -312,17 +434,32 @@ __device__ __forceinline__ void acc_block(WaveAcc& s, const WaveGeo& ge, const c
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         pv[tt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tt][qt][r], c, s.nmc[qt]));
-    pb[qt][0] = pack2<BF16>(pv[0][0], pv[0][1]);
-    pb[qt][1] = pack2<BF16>(pv[0][2], pv[0][3]);
-    pb[qt][2] = pack2<BF16>(pv[1][0], pv[1][1]);
-    pb[qt][3] = pack2<BF16>(pv[1][2], pv[1][3]);
+    if constexpr (SPLIT) {
+      const f32x4 p0 = {pv[0][0], pv[0][1], pv[0][2], pv[0][3]};
+      const f32x4 p1 = {pv[1][0], pv[1][1], pv[1][2], pv[1][3]};
+      split8(p0, p1, pb[qt], pl[qt]);
+    } else {
+      pb[qt][0] = pack2<BF16>(pv[0][0], pv[0][1]);
+      pb[qt][1] = pack2<BF16>(pv[0][2], pv[0][3]);
+      pb[qt][2] = pack2<BF16>(pv[1][0], pv[1][1]);
+      pb[qt][3] = pack2<BF16>(pv[1][2], pv[1][3]);
+    }
   }
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) s.oacc[dt][qt] = mfma16<BF16>(vop[dt], pb[qt], s.oacc[dt][qt]);
+    for (int qt = 0; qt < 2; ++qt) {
+      if constexpr (SPLIT) {
+        s.oacc[dt][qt] = mfma16<true>(vlo[dt], pb[qt], s.oacc[dt][qt]);
+        s.oacc[dt][qt] = mfma16<true>(vop[dt], pl[qt], s.oacc[dt][qt]);
+      }
+      s.oacc[dt][qt] = mfma16<BF16>(vop[dt], pb[qt], s.oacc[dt][qt]);
+    }
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) s.lacc[qt] = mfma16<BF16>(ones, pb[qt], s.lacc[qt]);
+  for (int qt = 0; qt < 2; ++qt) {
+    if constexpr (SPLIT) s.lacc[qt] = mfma16<true>(ones, pl[qt], s.lacc[qt]);
+    s.lacc[qt] = mfma16<BF16>(ones, pb[qt], s.lacc[qt]);
+  }
 }
 
 // Merge of the two key halves of a query half through LDS: the kh = 1 wave
@@ -344,10 +481,11 @@ __device__ __forceinline__ void acc_export(const WaveAcc& s, const WaveGeo& ge, 
   }
 }
 
-template <bool BF16>
+template <cab_dtype_t DT>
 __device__ __forceinline__ void acc_store(const WaveAcc& s, const WaveGeo& ge, const float* xo,
-                                          uint16_t* obase, int64_t os2, float* lse_row, int q0,
+                                          void* obase, int64_t os2, float* lse_row, int q0,
                                           int N, float c) {
+  constexpr bool BF16 = DT != CAB_F16;
   const float* xm = xo + 8 * 2 * 4 * 64;
   const float* xl = xm + 2 * 64;
 #pragma unroll
@@ -360,15 +498,20 @@ __device__ __forceinline__ void acc_store(const WaveAcc& s, const WaveGeo& ge, c
     const float inv = l > 0.f ? 1.0f / l : 0.f;
     const int qtok = q0 + 16 * qt + ge.l16;
     if (qtok < N) {
-      uint16_t* ob = obase + qtok * os2;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         float o[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           o[r] = (s.oacc[dt][qt][r] * a0 + xo[((dt * 2 + qt) * 4 + r) * 64 + ge.lane] * a1) * inv;
-        *reinterpret_cast<u32x2*>(ob + 16 * dt + 4 * ge.g) = u32x2{pack2<BF16>(o[0], o[1]),
-                                                                   pack2<BF16>(o[2], o[3])};
+        if constexpr (DT == CAB_F32) {
+          float* ob = static_cast<float*>(obase) + qtok * os2;
+          *reinterpret_cast<f32x4*>(ob + 16 * dt + 4 * ge.g) = f32x4{o[0], o[1], o[2], o[3]};
+        } else {
+          uint16_t* ob = static_cast<uint16_t*>(obase) + qtok * os2;
+          *reinterpret_cast<u32x2*>(ob + 16 * dt + 4 * ge.g) = u32x2{pack2<BF16>(o[0], o[1]),
+                                                                     pack2<BF16>(o[2], o[3])};
+        }
       }
       if (lse_row && ge.g == 0)
         lse_row[qtok] = l > 0.f ? (m * c + __log2f(l)) * 0.69314718055994531f : -INFINITY;
@@ -395,17 +538,21 @@ __device__ __forceinline__ const char* k_lane_ptr_clamped(const char* kbytes, in
 }
 
 // ---------------------------------------------------------------------------
-// attn_fwd_kernel: one query block per workgroup of 4 waves, two workgroups
-// per CU, two LDS stages.
+// attn_fwd_kernel: one query block per workgroup of 4 waves, two LDS stages;
+// two workgroups per CU (bf16 / fp16: 32 KB stages) or one (fp32: 64 KB
+// stages of split operands).
 // ---------------------------------------------------------------------------
-template <bool BF16, bool LIST_LDS>
-__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
-  // One LDS object: [K stage 0][V^T stage 0][K stage 1][V^T stage 1][list]; the
-  // merge at the end reuses the stages.
-  __shared__ u32x4 smem[4 * TILE_SLOTS + LIST_MAX / 4];
-  auto stage_k = [&](int s) { return smem + 2 * s * TILE_SLOTS; };
-  auto stage_v = [&](int s) { return smem + (2 * s + 1) * TILE_SLOTS; };
-  int32_t* slist = reinterpret_cast<int32_t*>(smem + 4 * TILE_SLOTS);
+template <cab_dtype_t DT, bool LIST_LDS>
+__global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(AttnArgs a) {
+  constexpr bool SPLIT = DT == CAB_F32;
+  constexpr int STAGE_SLOTS = (SPLIT ? 4 : 2) * TILE_SLOTS;
+  constexpr int64_t BLOCK_BYTES = static_cast<int64_t>(block_bytes(DT));
+  // One LDS object: [stage 0][stage 1][list], a stage being [K][V^T] or
+  // [K hi][K lo][V^T hi][V^T lo]; the merge at the end reuses the stages.
+  __shared__ u32x4 smem[2 * STAGE_SLOTS + LIST_MAX / 4];
+  auto stage_k = [&](int s) { return smem + s * STAGE_SLOTS; };
+  auto stage_v = [&](int s) { return smem + s * STAGE_SLOTS + STAGE_SLOTS / 2; };
+  int32_t* slist = reinterpret_cast<int32_t*>(smem + 2 * STAGE_SLOTS);
 
   const int M = a.M, N = a.N;
   const int logical = static_cast<int>(xcd_remap(blockIdx.x, static_cast<int64_t>(a.BH) * M));
@@ -416,9 +563,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   const WaveGeo ge = wave_geo(w);
   const float c = a.scale_log2;
 
-  const uint16_t* qb = a.q + b * a.qs[0] + hh * a.qs[1];
-  const char* kbytes = reinterpret_cast<const char*>(a.k + b * a.ks[0] + hh * a.ks[1]);
-  const char* vtbytes = reinterpret_cast<const char*>(a.vt) + static_cast<int64_t>(bh) * M * TILE_BYTES;
+  const void* qb = SPLIT ? static_cast<const void*>(static_cast<const float*>(a.q) + b * a.qs[0] +
+                                                      hh * a.qs[1])
+                         : static_cast<const void*>(static_cast<const uint16_t*>(a.q) +
+                                                    b * a.qs[0] + hh * a.qs[1]);
+  const char* kbytes = SPLIT ? nullptr
+                             : reinterpret_cast<const char*>(a.k + b * a.ks[0] + hh * a.ks[1]);
+  const char* vtbytes = reinterpret_cast<const char*>(a.vt) + static_cast<int64_t>(bh) * M * BLOCK_BYTES;
 
   int cnt = a.kv_cnt[bh * static_cast<int64_t>(M) + i];
   cnt = cnt < 0 ? 0 : (cnt > a.kmax ? a.kmax : cnt);
@@ -435,7 +586,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   };
 
   // Staging of key block j by the 4 waves: wave w fetches K rows 16 w .. +15
-  // (4 instructions) and V^T slot rows 4 w .. 4 w + 3 (1 KB each).
+  // (4 instructions) and V^T slot rows 4 w .. 4 w + 3 (1 KB each). fp32: the
+  // block image is a copy of the stage; wave w copies its 16 KB quarter w.
   const int64_t krow_bytes = a.ks[2] * 2;
   const int64_t kblk_bytes = BS * krow_bytes;
   uint32_t koff[4];
@@ -443,6 +595,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   for (int r = 0; r < 4; ++r) koff[r] = k_lane_off(4 * w + r, ge.lane, krow_bytes);
   const int voff = w * 4096 + 16 * ge.lane;
   auto stage = [&](int j, u32x4* kst, u32x4* vst) {
+    if constexpr (SPLIT) {
+      const char* gp = vtbytes + j * BLOCK_BYTES + w * TILE_BYTES + 16 * ge.lane;
+      char* lp = reinterpret_cast<char*>(kst) + w * TILE_BYTES;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        dma16<0>(gp + 4096 * r, lp + 4096 * r);
+        dma16<1024>(gp + 4096 * r, lp + 4096 * r);
+        dma16<2048>(gp + 4096 * r, lp + 4096 * r);
+        dma16<3072>(gp + 4096 * r, lp + 4096 * r);
+      }
+      return;
+    }
     char* kl = reinterpret_cast<char*>(kst) + w * 4096;
     if ((j + 1) * BS <= N) {
       const char* kbj = kbytes + j * kblk_bytes;
@@ -465,13 +629,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   };
 
   WaveAcc st;
-  acc_init(st, ge, qb, a.qs[2], i * BS + 32 * ge.qh, N, c);
+  acc_init<DT>(st, ge, qb, a.qs[2], i * BS + 32 * ge.qh, N, c);
 
   if (cnt > 0) {
     int jraw = entry(0);
     auto block_of = [&](int j) { return (j >= 0 && j < M) ? j : 0; };
     stage(block_of(jraw), stage_k(0), stage_v(0));
-    acc_q_ready(st);
+    acc_q_ready<DT>(st);
 
     // Block p lives in LDS stage PAR = p % 2 (compile time, so the compiler
     // sees the staging of block p + 1 into the other stage cannot alias).
@@ -486,8 +650,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
         jnext = entry(p + 1);
         stage(block_of(jnext), stage_k(PAR ^ 1), stage_v(PAR ^ 1));
       }
-      acc_block<BF16>(st, ge, reinterpret_cast<const char*>(stage_k(PAR)), stage_v(PAR), j, i,
-                      valid, N, a.causal, c);
+      acc_block<DT>(st, ge, reinterpret_cast<const char*>(stage_k(PAR)), stage_v(PAR), j, i,
+                    valid, N, a.causal, c);
       jraw = jnext;
     };
     for (int p = 0; p < cnt; p += 2) {
@@ -500,8 +664,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnArgs a) {
   float* xo = reinterpret_cast<float*>(smem) + ge.qh * XCHG_FLOATS;
   if (ge.kh == 1) acc_export(st, ge, xo);
   __syncthreads();
+  void* ob = SPLIT ? static_cast<void*>(static_cast<float*>(a.o) + b * a.os[0] + hh * a.os[1])
+                   : static_cast<void*>(static_cast<uint16_t*>(a.o) + b * a.os[0] + hh * a.os[1]);
   if (ge.kh == 0)
-    acc_store<BF16>(st, ge, xo, a.o + b * a.os[0] + hh * a.os[1], a.os[2],
+    acc_store<DT>(st, ge, xo, ob, a.os[2],
                     a.lse ? a.lse + static_cast<int64_t>(bh) * N : nullptr, i * BS + 32 * ge.qh,
                     N, c);
 }
@@ -513,11 +679,17 @@ using namespace cab;
 
 namespace {
 
-// Shape and scalar checks shared by the three entry points.
+// Shape and scalar checks shared by the three entry points. fp32 is accepted
+// by cab_block_sparse_attn_fwd only (its packed form holds K as well as V).
 cab_status_t check_common(const char* fn, cab_dtype_t dtype, int64_t B, int64_t H, int64_t N,
-                          int64_t D, int32_t block_size) {
-  CAB_REQUIRE(dtype == CAB_BF16 || dtype == CAB_F16, CAB_EDTYPE,
-              "%s: dtype %d unsupported (bf16 or fp16)", fn, (int)dtype);
+                          int64_t D, int32_t block_size, bool allow_f32) {
+  if (allow_f32)
+    CAB_REQUIRE(dtype == CAB_BF16 || dtype == CAB_F16 || dtype == CAB_F32, CAB_EDTYPE,
+                "%s: dtype %d unsupported (bf16, fp16 or fp32)", fn, (int)dtype);
+  else
+    CAB_REQUIRE(dtype == CAB_BF16 || dtype == CAB_F16, CAB_EDTYPE,
+                "%s: dtype %d unsupported (bf16 or fp16; fp32 runs through "
+                "cab_block_sparse_attn_fwd)", fn, (int)dtype);
   CAB_REQUIRE(B >= 0 && H >= 0 && N >= 0, CAB_ESHAPE, "%s: negative size", fn);
   CAB_REQUIRE(D == HD, CAB_ESHAPE, "%s: head dim %lld unsupported (128)", fn, (long long)D);
   CAB_REQUIRE(block_size == BS, CAB_ESHAPE, "%s: block_size %d unsupported (64)", fn,
@@ -529,22 +701,22 @@ cab_status_t check_common(const char* fn, cab_dtype_t dtype, int64_t B, int64_t 
 }
 
 cab_status_t check_tensor(const char* fn, const char* name, const void* ptr,
-                          const int64_t* strides) {
+                          const int64_t* strides, int64_t esize) {
   CAB_REQUIRE(ptr != nullptr, CAB_EINVAL, "%s: null %s", fn, name);
   CAB_REQUIRE(strides != nullptr, CAB_EINVAL, "%s: null %s strides", fn, name);
   CAB_REQUIRE(strides[3] == 1, CAB_ESHAPE, "%s: %s last-dim stride must be 1", fn, name);
   CAB_REQUIRE(reinterpret_cast<uintptr_t>(ptr) % 16 == 0, CAB_ESHAPE,
               "%s: %s not 16-byte aligned", fn, name);
   for (int d = 0; d < 3; ++d)
-    CAB_REQUIRE(strides[d] >= 0 && (strides[d] * 2) % 16 == 0, CAB_ESHAPE,
+    CAB_REQUIRE(strides[d] >= 0 && (strides[d] * esize) % 16 == 0, CAB_ESHAPE,
                 "%s: %s stride[%d]=%lld must keep rows 16-byte aligned", fn, name, d,
                 (long long)strides[d]);
   return CAB_OK;
 }
 
 cab_status_t check_packed(const char* fn, const void* vt, size_t bytes, int64_t B, int64_t H,
-                          int64_t M) {
-  const size_t need = static_cast<size_t>(B * H * M) * TILE_BYTES;
+                          int64_t M, cab_dtype_t dtype) {
+  const size_t need = static_cast<size_t>(B * H * M) * block_bytes(dtype);
   CAB_REQUIRE(vt != nullptr && bytes >= need, CAB_EWORKSPACE,
               "%s: workspace of %zu bytes given, %zu needed", fn, bytes, need);
   CAB_REQUIRE(reinterpret_cast<uintptr_t>(vt) % 16 == 0, CAB_EWORKSPACE,
@@ -554,15 +726,16 @@ cab_status_t check_packed(const char* fn, const void* vt, size_t bytes, int64_t 
 
 cab_status_t check_attn(const char* fn, const void* q, const void* k, const int64_t* q_strides,
                         const int64_t* k_strides, const int64_t* o_strides, void* out,
-                        const int32_t* kv_idx, const int32_t* kv_cnt, int32_t kmax, float scale) {
+                        const int32_t* kv_idx, const int32_t* kv_cnt, int32_t kmax, float scale,
+                        int64_t esize) {
   CAB_REQUIRE(kmax >= 1, CAB_EINVAL, "%s: kmax=%d must be >= 1", fn, (int)kmax);
   CAB_REQUIRE(std::isfinite(scale) && scale > 0.f, CAB_EINVAL, "%s: scale must be finite and > 0",
               fn);
   CAB_REQUIRE(kv_idx != nullptr && kv_cnt != nullptr, CAB_EINVAL, "%s: null block list", fn);
   cab_status_t st;
-  if ((st = check_tensor(fn, "q", q, q_strides)) != CAB_OK) return st;
-  if ((st = check_tensor(fn, "k", k, k_strides)) != CAB_OK) return st;
-  if ((st = check_tensor(fn, "out", out, o_strides)) != CAB_OK) return st;
+  if ((st = check_tensor(fn, "q", q, q_strides, esize)) != CAB_OK) return st;
+  if ((st = check_tensor(fn, "k", k, k_strides, esize)) != CAB_OK) return st;
+  if ((st = check_tensor(fn, "out", out, o_strides, esize)) != CAB_OK) return st;
   CAB_REQUIRE(k_strides[2] <= (int64_t{1} << 24), CAB_ESHAPE,
               "%s: k token stride %lld too large (<= 2^24 elements)", fn, (long long)k_strides[2]);
   return CAB_OK;
@@ -581,6 +754,33 @@ cab_status_t launch_pack(const char* fn, const void* v, const int64_t* v_strides
   return launch_status(fn);
 }
 
+cab_status_t launch_pack_split(const char* fn, const void* k, const int64_t* k_strides,
+                               const void* v, const int64_t* v_strides, int64_t B, int64_t H,
+                               int64_t N, void* img, hipStream_t s) {
+  SplitPackArgs p;
+  p.k = static_cast<const float*>(k);
+  p.v = static_cast<const float*>(v);
+  p.img = static_cast<uint16_t*>(img);
+  for (int d = 0; d < 3; ++d) {
+    p.ks[d] = k_strides[d];
+    p.vs[d] = v_strides[d];
+  }
+  p.H = H;
+  p.N = N;
+  p.M = ceil_div(N, BS);
+  pack_split_kernel<<<dim3(static_cast<unsigned>(p.M), static_cast<unsigned>(B * H)), 256, 0, s>>>(
+      p);
+  return launch_status(fn);
+}
+
+template <cab_dtype_t DT>
+void launch_attn_kernel(bool list_lds, dim3 grid, hipStream_t s, const AttnArgs& a) {
+  if (list_lds)
+    attn_fwd_kernel<DT, true><<<grid, 256, 0, s>>>(a);
+  else
+    attn_fwd_kernel<DT, false><<<grid, 256, 0, s>>>(a);
+}
+
 cab_status_t launch_attn(const char* fn, const void* q, const void* k, const void* vt,
                          cab_dtype_t dtype, int64_t B, int64_t H, int64_t N,
                          const int64_t* q_strides, const int64_t* k_strides,
@@ -589,10 +789,10 @@ cab_status_t launch_attn(const char* fn, const void* q, const void* k, const voi
                          hipStream_t s) {
   const int64_t M = ceil_div(N, BS);
   AttnArgs a;
-  a.q = static_cast<const uint16_t*>(q);
+  a.q = q;
   a.k = static_cast<const uint16_t*>(k);
   a.vt = static_cast<const uint16_t*>(vt);
-  a.o = static_cast<uint16_t*>(out);
+  a.o = out;
   a.lse = lse;
   for (int d = 0; d < 3; ++d) {
     a.qs[d] = q_strides[d];
@@ -610,26 +810,22 @@ cab_status_t launch_attn(const char* fn, const void* q, const void* k, const voi
   a.causal = causal ? 1 : 0;
   const dim3 grid(static_cast<unsigned>(B * H * M));
   const bool list_lds = kmax <= LIST_MAX;
-  if (dtype == CAB_BF16) {
-    if (list_lds)
-      attn_fwd_kernel<true, true><<<grid, 256, 0, s>>>(a);
-    else
-      attn_fwd_kernel<true, false><<<grid, 256, 0, s>>>(a);
-  } else {
-    if (list_lds)
-      attn_fwd_kernel<false, true><<<grid, 256, 0, s>>>(a);
-    else
-      attn_fwd_kernel<false, false><<<grid, 256, 0, s>>>(a);
-  }
+  if (dtype == CAB_BF16)
+    launch_attn_kernel<CAB_BF16>(list_lds, grid, s, a);
+  else if (dtype == CAB_F16)
+    launch_attn_kernel<CAB_F16>(list_lds, grid, s, a);
+  else
+    launch_attn_kernel<CAB_F32>(list_lds, grid, s, a);
   return launch_status(fn);
 }
 
 }  // namespace
 
-extern "C" size_t cab_block_sparse_attn_workspace_bytes(int64_t B, int64_t H, int64_t N,
-                                                        int64_t D, int32_t block_size) {
+extern "C" size_t cab_block_sparse_attn_workspace_bytes(cab_dtype_t dtype, int64_t B, int64_t H,
+                                                        int64_t N, int64_t D, int32_t block_size) {
+  if (dtype != CAB_BF16 && dtype != CAB_F16 && dtype != CAB_F32) return 0;
   if (B <= 0 || H <= 0 || N <= 0 || D != HD || block_size != BS) return 0;
-  return static_cast<size_t>(B * H * ceil_div(N, BS)) * TILE_BYTES;
+  return static_cast<size_t>(B * H * ceil_div(N, BS)) * block_bytes(dtype);
 }
 
 extern "C" cab_status_t cab_block_sparse_attn_pack_v(const void* v, cab_dtype_t dtype, int64_t B,
@@ -639,12 +835,12 @@ extern "C" cab_status_t cab_block_sparse_attn_pack_v(const void* v, cab_dtype_t 
                                                      size_t workspace_bytes, void* stream) {
   const char* fn = "cab_block_sparse_attn_pack_v";
   clear_error();
-  cab_status_t st = check_common(fn, dtype, B, H, N, D, block_size);
+  cab_status_t st = check_common(fn, dtype, B, H, N, D, block_size, false);
   if (st != CAB_OK) return st;
   const int64_t M = ceil_div(N, BS);
   if (B == 0 || H == 0 || M == 0) return CAB_OK;
-  if ((st = check_tensor(fn, "v", v, v_strides)) != CAB_OK) return st;
-  if ((st = check_packed(fn, workspace, workspace_bytes, B, H, M)) != CAB_OK) return st;
+  if ((st = check_tensor(fn, "v", v, v_strides, 2)) != CAB_OK) return st;
+  if ((st = check_packed(fn, workspace, workspace_bytes, B, H, M, dtype)) != CAB_OK) return st;
   return launch_pack(fn, v, v_strides, B, H, N, workspace, static_cast<hipStream_t>(stream));
 }
 
@@ -656,14 +852,14 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd_packed(
     size_t vt_bytes, void* stream) {
   const char* fn = "cab_block_sparse_attn_fwd_packed";
   clear_error();
-  cab_status_t st = check_common(fn, dtype, B, H, N, D, block_size);
+  cab_status_t st = check_common(fn, dtype, B, H, N, D, block_size, false);
   if (st != CAB_OK) return st;
   const int64_t M = ceil_div(N, BS);
   if (B == 0 || H == 0 || M == 0) return CAB_OK;
   if ((st = check_attn(fn, q, k, q_strides, k_strides, o_strides, out, kv_idx, kv_cnt, kmax,
-                       scale)) != CAB_OK)
+                       scale, 2)) != CAB_OK)
     return st;
-  if ((st = check_packed(fn, vt, vt_bytes, B, H, M)) != CAB_OK) return st;
+  if ((st = check_packed(fn, vt, vt_bytes, B, H, M, dtype)) != CAB_OK) return st;
   return launch_attn(fn, q, k, vt, dtype, B, H, N, q_strides, k_strides, o_strides, kv_idx,
                      kv_cnt, kmax, scale, causal, out, lse, static_cast<hipStream_t>(stream));
 }
@@ -676,7 +872,7 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
     void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "cab_block_sparse_attn_fwd";
   clear_error();
-  cab_status_t st = check_common(fn, dtype, B, H, N, D, block_size);
+  cab_status_t st = check_common(fn, dtype, B, H, N, D, block_size, true);
   if (st != CAB_OK) return st;
   CAB_REQUIRE(kmax >= 1, CAB_EINVAL, "%s: kmax=%d must be >= 1", fn, (int)kmax);
   CAB_REQUIRE(std::isfinite(scale) && scale > 0.f, CAB_EINVAL, "%s: scale must be finite and > 0",
@@ -685,15 +881,19 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
               "%s: null stride array", fn);
   const int64_t M = ceil_div(N, BS);
   if (B == 0 || H == 0 || M == 0) return CAB_OK;
+  const int64_t esize = dtype == CAB_F32 ? 4 : 2;
   if ((st = check_attn(fn, q, k, q_strides, k_strides, o_strides, out, kv_idx, kv_cnt, kmax,
-                       scale)) != CAB_OK)
+                       scale, esize)) != CAB_OK)
     return st;
-  if ((st = check_tensor(fn, "v", v, v_strides)) != CAB_OK) return st;
-  if ((st = check_packed(fn, workspace, workspace_bytes, B, H, M)) != CAB_OK) return st;
+  if ((st = check_tensor(fn, "v", v, v_strides, esize)) != CAB_OK) return st;
+  if ((st = check_packed(fn, workspace, workspace_bytes, B, H, M, dtype)) != CAB_OK) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if ((st = launch_pack("cab_block_sparse_attn_fwd/pack_v", v, v_strides, B, H, N, workspace, s)) !=
-      CAB_OK)
-    return st;
+  if (dtype == CAB_F32)
+    st = launch_pack_split("cab_block_sparse_attn_fwd/pack_split", k, k_strides, v, v_strides, B,
+                           H, N, workspace, s);
+  else
+    st = launch_pack("cab_block_sparse_attn_fwd/pack_v", v, v_strides, B, H, N, workspace, s);
+  if (st != CAB_OK) return st;
   return launch_attn(fn, q, k, workspace, dtype, B, H, N, q_strides, k_strides, o_strides,
                      kv_idx, kv_cnt, kmax, scale, causal, out, lse, s);
 }

@@ -49,7 +49,7 @@ enum { CAB_NORM_NONE = 0, CAB_NORM_MINMAX = 1 };
 /* FRC combination (experiments/longbench_qa/config.py:465; test.ipynb:111-145). */
 enum { CAB_FRC_ADDITIVE = 0, CAB_FRC_MULTIPLICATIVE = 1, CAB_FRC_AUGMENTED = 2 };
 
-#define CAB_ABI_VERSION 1
+#define CAB_ABI_VERSION 2
 
 int cab_abi_version(void);
 const char* cab_last_error(void);
@@ -147,11 +147,12 @@ cab_status_t cab_block_topk_hybrid(const float* frc, const float* magnitude, int
                                    uint8_t* dense_mask, void* stream);
 
 /*
- * Workspace bytes cab_block_sparse_attn_fwd needs: one packed V^T tile
- * (16 KB) per (b, h, key block). 0 for unsupported sizes.
+ * Workspace bytes cab_block_sparse_attn_fwd needs for `dtype`: per (b, h,
+ * key block) one packed V^T tile (16 KB, bf16 / fp16) or one split K and
+ * V^T image (64 KB, fp32). 0 for unsupported sizes or dtypes.
  */
-size_t cab_block_sparse_attn_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D,
-                                             int32_t block_size);
+size_t cab_block_sparse_attn_workspace_bytes(cab_dtype_t dtype, int64_t B, int64_t H, int64_t N,
+                                             int64_t D, int32_t block_size);
 
 /*
  * Block-sparse attention forward.
@@ -163,13 +164,17 @@ size_t cab_block_sparse_attn_workspace_bytes(int64_t B, int64_t H, int64_t N, in
  * For query block i: out[t] = softmax_s(q_t . k_s * scale) v_s over the tokens
  * s of the key blocks kv_idx[b,h,i,0:kv_cnt[b,h,i]] (entries outside [0, M)
  * are skipped, kv_cnt is clamped to [0, kmax]); when causal, keys s > t are
- * dropped; a query with no key gets 0. fp32 online softmax, bf16/fp16 MFMA.
- * q, k, v: [B,H,N,D] (strides), out: [B,H,N,D] (strides), dtype bf16 or fp16.
+ * dropped; a query with no key gets 0. fp32 online softmax, bf16/fp16 MFMA
+ * (fp32 inputs: each operand split into a bf16 hi + lo pair, three MFMA
+ * products per product, fp32 output; relative error near 2^-16 per product).
+ * q, k, v: [B,H,N,D] (strides), out: [B,H,N,D] (strides), dtype bf16, fp16
+ * or fp32.
  * block_size == 64, D == 128, scale > 0. kv_idx: contiguous int32
  * [B,H,M,kmax], kv_cnt: contiguous int32 [B,H,M]. lse: fp32 [B,H,N]
  * natural-log log-sum-exp of the scaled scores (-inf for a query with no
- * key), or NULL. workspace: cab_block_sparse_attn_workspace_bytes() bytes,
- * 16-byte aligned, overwritten (V is repacked there first).
+ * key), or NULL. workspace: cab_block_sparse_attn_workspace_bytes(dtype, ...)
+ * bytes, 16-byte aligned, overwritten (V, and for fp32 K, is repacked there
+ * first).
  */
 cab_status_t cab_block_sparse_attn_fwd(const void* q, const void* k, const void* v,
                                        cab_dtype_t dtype, int64_t B, int64_t H,
@@ -190,6 +195,7 @@ cab_status_t cab_block_sparse_attn_fwd(const void* q, const void* k, const void*
  * cab_block_sparse_attn_pack_v: writes V's packed V^T tiles (16 KB per
  * (b, h, key block), zero past N) into `workspace`
  * (cab_block_sparse_attn_workspace_bytes() bytes, 16-byte aligned).
+ * bf16 / fp16 only (CAB_EDTYPE for fp32, whose packed form also holds K).
  */
 cab_status_t cab_block_sparse_attn_pack_v(const void* v, cab_dtype_t dtype, int64_t B, int64_t H,
                                           int64_t N, int64_t D, const int64_t v_strides[4],

@@ -107,14 +107,23 @@ def test_topk_validation(lib):
 
 
 def test_attention_validation(lib):
-    assert lib.cab_block_sparse_attn_workspace_bytes(1, 8, 65, 128, 64) == 8 * 2 * 16384
-    assert lib.cab_block_sparse_attn_workspace_bytes(1, 8, 64, 64, 64) == 0
+    ws = lib.cab_block_sparse_attn_workspace_bytes
+    assert ws(nat.CAB_BF16, 1, 8, 65, 128, 64) == 8 * 2 * 16384
+    assert ws(nat.CAB_F16, 1, 8, 65, 128, 64) == 8 * 2 * 16384
+    assert ws(nat.CAB_F32, 1, 8, 65, 128, 64) == 8 * 2 * 65536  # split K and V^T images
+    assert ws(nat.CAB_BF16, 1, 8, 64, 64, 64) == 0
+    assert ws(7, 1, 8, 64, 128, 64) == 0
     st = _s4(8 * 64 * 128, 64 * 128, 128, 1)
     call = lambda **kw: lib.cab_block_sparse_attn_fwd(
         FAKE, FAKE, FAKE, kw.get("dt", nat.CAB_BF16), 1, 8, 64, kw.get("D", 128), st, st, st,
         kw.get("os", st), kw.get("bs", 64), FAKE, FAKE, kw.get("kmax", 3), kw.get("scale", 0.088),
         1, FAKE, None, kw.get("ws", FAKE), kw.get("wsb", 1 << 30), None)
     assert call(dt=nat.CAB_F32 + 9) == nat.CAB_EDTYPE
+    # fp32: rows must stay 16-byte aligned at 4 bytes per element and the
+    # workspace must hold the 64 KB split images
+    st2 = _s4(8 * 64 * 130, 64 * 130, 130, 1)  # 260-byte bf16 rows (ok), 520-byte fp32 rows (not)
+    assert call(dt=nat.CAB_F32, os=st2) == nat.CAB_ESHAPE
+    assert call(dt=nat.CAB_F32, wsb=8 * 65536 - 1) == nat.CAB_EWORKSPACE
     assert call(D=96) == nat.CAB_ESHAPE
     assert call(bs=48) == nat.CAB_ESHAPE
     assert call(kmax=0) == nat.CAB_EINVAL
@@ -128,12 +137,17 @@ def test_attention_validation(lib):
     assert pack(D=64) == nat.CAB_ESHAPE
     assert pack(v=None) == nat.CAB_EINVAL
     assert pack(wsb=100) == nat.CAB_EWORKSPACE
+    assert lib.cab_block_sparse_attn_pack_v(FAKE, nat.CAB_F32, 1, 8, 64, 128, st, 64, FAKE,
+                                            1 << 30, None) == nat.CAB_EDTYPE
     packed = lambda **kw: lib.cab_block_sparse_attn_fwd_packed(
         FAKE, FAKE, kw.get("vt", FAKE), nat.CAB_BF16, 1, 8, 64, 128, st, st, st, 64, FAKE, FAKE,
         kw.get("kmax", 3), 0.088, 1, FAKE, None, kw.get("vtb", 1 << 30), None)
     assert packed(kmax=0) == nat.CAB_EINVAL
     assert packed(vt=None) == nat.CAB_EWORKSPACE
     assert packed(vtb=8 * 16384 - 1) == nat.CAB_EWORKSPACE
+    assert lib.cab_block_sparse_attn_fwd_packed(
+        FAKE, FAKE, FAKE, nat.CAB_F32, 1, 8, 64, 128, st, st, st, 64, FAKE, FAKE, 3, 0.088, 1,
+        FAKE, None, 1 << 30, None) == nat.CAB_EDTYPE
 
 
 def test_python_layer_refuses_cpu_tensors(lib):
