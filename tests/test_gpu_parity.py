@@ -404,6 +404,51 @@ def test_attention_empty_rows_and_bad_indices(cuda, dt):
     assert np.abs(got - want).max() <= ATOL[dt]
 
 
+def _hand_lists(M, causal, kmax=6):
+    """Hand-made lists: neighbouring rows that share blocks and rows that
+    share none, an unsorted row, a repeated block, an empty row, and a
+    ragged last row."""
+    rows = [[0], [0, 1], [1, 2, 0], [3, 0, 2, 1], [4, 4, 1], [5, 1, 3], [], [7, 6, 0], [8, 2]]
+    if not causal:
+        rows = [r + [M - 1 - (i % 3)] if r else r for i, r in enumerate(rows)]
+    idx = np.full((1, 1, M, kmax), -1, np.int32)
+    cnt = np.zeros((1, 1, M), np.int32)
+    for i in range(M):
+        r = rows[i % len(rows)]
+        r = [j % M for j in r] if causal is False else [min(j, i) for j in r]
+        idx[0, 0, i, :len(r)] = r
+        cnt[0, 0, i] = len(r)
+    return idx, cnt
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dt", ["bf16", "fp16", "fp32"])
+def test_attention_hand_made_lists(cuda, dt, causal):
+    """Hand-made lists on one head and predictor-style lists on another,
+    against the oracle. A repeated block counts twice, as in the oracle."""
+    from cab_attention.kernels import block_sparse_attention
+    B, H, N, D, bs = 1, 2, 64 * 9 - 20, 128, 64  # M = 9, ragged last block
+    M = 9
+    q, k, v = (seeded((B, H, N, D), s, DTYPES[dt]) for s in (41, 42, 43))
+    idx0, cnt0 = _hand_lists(M, causal)
+    f = np.random.default_rng(17).standard_normal((B, 1, M, M)).astype(np.float32)
+    _, idx1, cnt1 = O.generate_block_mask(f, 0.4, causal=causal)
+    kmax = max(idx0.shape[-1], idx1.shape[-1])
+    idx = np.full((B, H, M, kmax), -1, np.int32)
+    idx[:, :1, :, :idx0.shape[-1]] = idx0
+    idx[:, 1:, :, :idx1.shape[-1]] = idx1
+    cnt = np.concatenate([cnt0, cnt1], axis=1)
+    out, lse = block_sparse_attention(q.to(cuda), k.to(cuda), v.to(cuda), torch.from_numpy(idx).to(cuda),
+                                      torch.from_numpy(cnt).to(cuda), bs, causal=causal, return_lse=True)
+    want = O.sparse_attention(np32(q), np32(k), np32(v), idx, cnt, bs, causal=causal)
+    got = np32(out)
+    assert np.isfinite(got).all()
+    err = np.abs(got - want).max()
+    assert err <= ATOL[dt], f"max abs error {err}"
+    assert np.all(got[0, 0, 6 * bs:7 * bs] == 0)  # the empty row
+    assert np.all(np.isneginf(np32(lse)[0, 0, 6 * bs:7 * bs]))
+
+
 @pytest.mark.parametrize("dt", ["bf16", "fp32"])
 def test_attention_strided_output_and_module(cuda, dt):
     """CABAttention: qkv views in, [B, N, H, D] output buffer, oracle on the
