@@ -70,7 +70,10 @@ struct AttnArgs {
   int64_t qs[3], ks[3], os[3];  // b, h, token strides (elements)
   const int32_t* kv_idx;
   const int32_t* kv_cnt;
-  int32_t BH, H, N, M;  // B * H, heads, tokens, key blocks (all < 2^31)
+  int32_t BH, H, N, M;  // B * H, query heads, query tokens, query blocks (all < 2^31)
+  int32_t Nk, Mk;       // key tokens, key blocks
+  int32_t group;        // query heads per K / V head
+  int32_t qoff;         // causal: query token t sees keys <= t + qoff
   int32_t kmax;
   float scale_log2;
   int causal;
@@ -338,15 +341,23 @@ __device__ __forceinline__ void acc_q_ready(WaveAcc& s) {
                  "v"(s.qlo[1][0]), "v"(s.qlo[1][1]), "v"(s.qlo[1][2]), "v"(s.qlo[1][3]));
 }
 
+// Whether key block j needs per-key masks for query block i: an invalid
+// list entry, keys past Nk, or (causal) a key after some query of the block.
+__device__ __forceinline__ bool block_needs_mask(int j, int i, bool valid, int Nk, bool causal,
+                                                 int qoff) {
+  return !valid || (j + 1) * BS > Nk || (causal && j * BS + BS - 1 > i * BS + qoff);
+}
+
 // One key block j (staged at ks / vts) for the wave's queries of query block i:
 //   S^T = K_kh Q^T (16 MFMA), masks, online softmax (fp32, log2 domain),
 //   O^T += V_kh^T P^T (16 MFMA), row sums = 1 P^T (2 MFMA).
 // fp32 (split operands, the lo halves 16 KB past the hi ones in LDS):
-// 48 + 48 + 4 MFMA.
+// 48 + 48 + 4 MFMA. Keys at or past Nk and (causal) keys after t + qoff for
+// query t are dropped.
 template <cab_dtype_t DT>
 __device__ __forceinline__ void acc_block(WaveAcc& s, const WaveGeo& ge, const char* ks,
-                                          const u32x4* vts, int j, int i, bool valid, int N,
-                                          bool causal, float c) {
+                                          const u32x4* vts, int j, int i, bool valid, int Nk,
+                                          bool causal, int qoff, float c) {
   constexpr bool BF16 = DT != CAB_F16;
   constexpr bool SPLIT = DT == CAB_F32;
   const uint32_t one2 = BF16 ? 0x3f803f80u : 0x3c003c00u;
@@ -386,7 +397,7 @@ __device__ __forceinline__ void acc_block(WaveAcc& s, const WaveGeo& ge, const c
         sc[tt][qt] = mfma16<BF16>(kop[ds][tt], s.qreg[qt][ds], sc[tt][qt]);
       }
 
-  if (!valid || (causal && j >= i) || (j + 1) * BS > N) {
+  if (block_needs_mask(j, i, valid, Nk, causal, qoff)) {
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -395,7 +406,7 @@ __device__ __forceinline__ void acc_block(WaveAcc& s, const WaveGeo& ge, const c
         for (int r = 0; r < 4; ++r) {
           const int ktok = j * BS + 32 * ge.kh + 16 * tt + 4 * ge.g + r;
           const int qtok = i * BS + 32 * ge.qh + 16 * qt + ge.l16;
-          if (!valid || ktok >= N || (causal && ktok > qtok)) sc[tt][qt][r] = -INFINITY;
+          if (!valid || ktok >= Nk || (causal && ktok > qtok + qoff)) sc[tt][qt][r] = -INFINITY;
         }
   }
   float mx[2];
@@ -542,7 +553,12 @@ __device__ __forceinline__ const char* k_lane_ptr_clamped(const char* kbytes, in
 // two workgroups per CU (bf16 / fp16: 32 KB stages) or one (fp32: 64 KB
 // stages of split operands).
 // ---------------------------------------------------------------------------
-template <cab_dtype_t DT, bool LIST_LDS>
+// Key-block lists of a query block: the caller's kv_idx staged in LDS, read
+// from global memory (lists longer than LIST_MAX), or dense (every key block
+// up to the causal limit, in order).
+constexpr int LIST_LDS = 0, LIST_GLOBAL = 1, LIST_DENSE = 2;
+
+template <cab_dtype_t DT, int LIST>
 __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(AttnArgs a) {
   constexpr bool SPLIT = DT == CAB_F32;
   constexpr int STAGE_SLOTS = (SPLIT ? 4 : 2) * TILE_SLOTS;
@@ -554,11 +570,13 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
   auto stage_v = [&](int s) { return smem + s * STAGE_SLOTS + STAGE_SLOTS / 2; };
   int32_t* slist = reinterpret_cast<int32_t*>(smem + 2 * STAGE_SLOTS);
 
-  const int M = a.M, N = a.N;
+  const int M = a.M, N = a.N, Mk = a.Mk, Nk = a.Nk;
   const int logical = static_cast<int>(xcd_remap(blockIdx.x, static_cast<int64_t>(a.BH) * M));
   const int bh = logical / M;
   const int i = M - 1 - (logical - bh * M);  // longest causal rows first
   const int b = bh / a.H, hh = bh - (bh / a.H) * a.H;
+  const int hk = hh / a.group;                        // K / V head
+  const int64_t bhk = static_cast<int64_t>(b) * (a.H / a.group) + hk;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const WaveGeo ge = wave_geo(w);
   const float c = a.scale_log2;
@@ -568,21 +586,31 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
                          : static_cast<const void*>(static_cast<const uint16_t*>(a.q) +
                                                     b * a.qs[0] + hh * a.qs[1]);
   const char* kbytes = SPLIT ? nullptr
-                             : reinterpret_cast<const char*>(a.k + b * a.ks[0] + hh * a.ks[1]);
-  const char* vtbytes = reinterpret_cast<const char*>(a.vt) + static_cast<int64_t>(bh) * M * BLOCK_BYTES;
+                             : reinterpret_cast<const char*>(a.k + b * a.ks[0] + hk * a.ks[1]);
+  const char* vtbytes = reinterpret_cast<const char*>(a.vt) + bhk * Mk * BLOCK_BYTES;
 
-  int cnt = a.kv_cnt[bh * static_cast<int64_t>(M) + i];
-  cnt = cnt < 0 ? 0 : (cnt > a.kmax ? a.kmax : cnt);
-  const int32_t* glist = a.kv_idx + (static_cast<int64_t>(bh) * M + i) * a.kmax;
-  if constexpr (LIST_LDS) {
+  int cnt;
+  const int32_t* glist = nullptr;
+  if constexpr (LIST == LIST_DENSE) {
+    // Key blocks 0 .. the last one holding a key some query of block i sees.
+    const int last = i * BS + BS - 1 + a.qoff;
+    cnt = !a.causal ? Mk : (last < 0 ? 0 : (last / BS + 1 < Mk ? last / BS + 1 : Mk));
+  } else {
+    cnt = a.kv_cnt[bh * static_cast<int64_t>(M) + i];
+    cnt = cnt < 0 ? 0 : (cnt > a.kmax ? a.kmax : cnt);
+    glist = a.kv_idx + (static_cast<int64_t>(bh) * M + i) * a.kmax;
+  }
+  if constexpr (LIST == LIST_LDS) {
     for (int p = threadIdx.x; p < cnt; p += 256) slist[p] = glist[p];
     __syncthreads();
   }
   auto entry = [&](int p) -> int {
-    if constexpr (LIST_LDS)
+    if constexpr (LIST == LIST_LDS)
       return __builtin_amdgcn_readfirstlane(slist[p]);
-    else
+    else if constexpr (LIST == LIST_GLOBAL)
       return glist[p];
+    else
+      return p;
   };
 
   // Staging of key block j by the 4 waves: wave w fetches K rows 16 w .. +15
@@ -608,17 +636,17 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
       return;
     }
     char* kl = reinterpret_cast<char*>(kst) + w * 4096;
-    if ((j + 1) * BS <= N) {
+    if ((j + 1) * BS <= Nk) {
       const char* kbj = kbytes + j * kblk_bytes;
       dma16<0>(kbj + koff[0], kl);
       dma16<0>(kbj + koff[1], kl + 1024);
       dma16<0>(kbj + koff[2], kl + 2048);
       dma16<0>(kbj + koff[3], kl + 3072);
     } else {
-      dma16<0>(k_lane_ptr_clamped(kbytes, j, 4 * w + 0, ge.lane, N, krow_bytes), kl);
-      dma16<0>(k_lane_ptr_clamped(kbytes, j, 4 * w + 1, ge.lane, N, krow_bytes), kl + 1024);
-      dma16<0>(k_lane_ptr_clamped(kbytes, j, 4 * w + 2, ge.lane, N, krow_bytes), kl + 2048);
-      dma16<0>(k_lane_ptr_clamped(kbytes, j, 4 * w + 3, ge.lane, N, krow_bytes), kl + 3072);
+      dma16<0>(k_lane_ptr_clamped(kbytes, j, 4 * w + 0, ge.lane, Nk, krow_bytes), kl);
+      dma16<0>(k_lane_ptr_clamped(kbytes, j, 4 * w + 1, ge.lane, Nk, krow_bytes), kl + 1024);
+      dma16<0>(k_lane_ptr_clamped(kbytes, j, 4 * w + 2, ge.lane, Nk, krow_bytes), kl + 2048);
+      dma16<0>(k_lane_ptr_clamped(kbytes, j, 4 * w + 3, ge.lane, Nk, krow_bytes), kl + 3072);
     }
     const char* vp = vtbytes + static_cast<int64_t>(j) * TILE_BYTES + voff;
     char* vl = reinterpret_cast<char*>(vst) + w * 4096;
@@ -633,7 +661,7 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
 
   if (cnt > 0) {
     int jraw = entry(0);
-    auto block_of = [&](int j) { return (j >= 0 && j < M) ? j : 0; };
+    auto block_of = [&](int j) { return (j >= 0 && j < Mk) ? j : 0; };
     stage(block_of(jraw), stage_k(0), stage_v(0));
     acc_q_ready<DT>(st);
 
@@ -641,7 +669,7 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
     // sees the staging of block p + 1 into the other stage cannot alias).
     auto step = [&](int p, auto par_tag) {
       constexpr int PAR = decltype(par_tag)::value;
-      const bool valid = jraw >= 0 && jraw < M;
+      const bool valid = jraw >= 0 && jraw < Mk;
       const int j = valid ? jraw : 0;
       __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's staging of block p landed
       __builtin_amdgcn_s_barrier();        // ... and every wave's; stage PAR ^ 1 is free
@@ -651,7 +679,7 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
         stage(block_of(jnext), stage_k(PAR ^ 1), stage_v(PAR ^ 1));
       }
       acc_block<DT>(st, ge, reinterpret_cast<const char*>(stage_k(PAR)), stage_v(PAR), j, i,
-                    valid, N, a.causal, c);
+                    valid, Nk, a.causal, a.qoff, c);
       jraw = jnext;
     };
     for (int p = 0; p < cnt; p += 2) {
@@ -670,6 +698,136 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
     acc_store<DT>(st, ge, xo, ob, a.os[2],
                     a.lse ? a.lse + static_cast<int64_t>(bh) * N : nullptr, i * BS + 32 * ge.qh,
                     N, c);
+}
+
+// ---------------------------------------------------------------------------
+// key_score_kernel: per-key attention totals (cab_attn_key_scores).
+// score[k] = sum over queries t of softmax_t(k) = exp(s_tk - lse_t), with
+// the natural-log lse of attn_fwd_kernel's rows. One workgroup of 4 waves per
+// (b, h, key block j); every wave holds the block's 64 keys as the B operand
+// of S = Q K^T (K^T tiles in 16 registers x 4) and walks 16-query tiles
+// (wave w: tiles w, w + 4, ... of those that see block j), reading Q and the
+// lse straight from global memory one tile ahead. Per tile:
+//   S (16 queries x 64 keys) = 16 MFMA 16x16x32,
+//   P = exp2(S c - lse log2 e) (fp32, masked entries 0),
+//   column sums over the tile's queries, kept per lane.
+// The lane and wave partial sums are added once at the end (fixed order,
+// no atomics) and written to, or added into, score[b, h, keys of block j].
+// ---------------------------------------------------------------------------
+struct KeyScoreArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const float* lse;  // [B, H, Nq] contiguous
+  float* score;      // score[b * ss0 + h * ss1 + token]
+  int64_t qs[3], ks[3], ss[2];
+  int32_t BH, H, group, Nq, Nk, Mk, qoff, causal, accumulate;
+  float scale_log2;
+};
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void key_score_kernel(KeyScoreArgs a) {
+  __shared__ float red[4][4][64];
+  const int Mk = a.Mk;
+  const int logical = static_cast<int>(xcd_remap(blockIdx.x, static_cast<int64_t>(a.BH) * Mk));
+  const int bh = logical / Mk;
+  const int j = logical - bh * Mk;  // causal: block 0 sees the most queries, first
+  const int b = bh / a.H, hh = bh - (bh / a.H) * a.H;
+  const int hk = hh / a.group;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int lane = lane_id(), l16 = lane & 15, g = lane >> 4;
+  const float c = a.scale_log2;
+  constexpr float LOG2E = 1.4426950408889634f;
+
+  const uint16_t* qb = a.q + b * a.qs[0] + hh * a.qs[1];
+  const uint16_t* kb = a.k + b * a.ks[0] + hk * a.ks[1];
+  const float* lb = a.lse + static_cast<int64_t>(bh) * a.Nq;
+
+  // K^T operand: kop[kt][ds] = K[16 kt + l16][32 ds + 8 g .. +8] (zero past Nk).
+  u32x4 kop[4][4];
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt) {
+    const int key = j * BS + 16 * kt + l16;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds)
+      kop[kt][ds] = key < a.Nk ? *reinterpret_cast<const u32x4*>(kb + key * a.ks[2] + 32 * ds + 8 * g)
+                               : u32x4{0u, 0u, 0u, 0u};
+  }
+
+  // Query tiles that see block j: queries t with t + qoff >= its first key.
+  const int t_first = a.causal ? j * BS - a.qoff : 0;
+  const int tile0 = t_first <= 0 ? 0 : t_first / 16;
+  const int ntiles = (a.Nq + 15) / 16;
+
+  auto load_tile = [&](int tile, u32x4 (&qop)[4], float (&l2)[4]) {
+    const int q = 16 * tile + l16;
+    const int qc = q < a.Nq ? q : a.Nq - 1;  // clamped, masked below
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds)
+      qop[ds] = *reinterpret_cast<const u32x4*>(qb + qc * a.qs[2] + 32 * ds + 8 * g);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * tile + 4 * g + r;
+      l2[r] = lb[t < a.Nq ? t : a.Nq - 1] * LOG2E;
+    }
+  };
+
+  float colsum[4] = {0.f, 0.f, 0.f, 0.f};
+  int tile = tile0 + w;
+  if (tile < ntiles) {
+    u32x4 qop[4];
+    float l2[4];
+    load_tile(tile, qop, l2);
+    for (; tile < ntiles; tile += 4) {
+      u32x4 qn[4];
+      float ln[4];
+      const int next = tile + 4 < ntiles ? tile + 4 : tile;
+      load_tile(next, qn, ln);  // one tile ahead (a repeat of this tile at the end)
+      f32x4 sc[4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        sc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ds = 0; ds < 4; ++ds) sc[kt] = mfma16<BF16>(qop[ds], kop[kt][ds], sc[kt]);
+      }
+      // sc[kt][r]: query 16 tile + 4 g + r, key j BS + 16 kt + l16.
+      const int t0 = 16 * tile + 4 * g;
+      const bool edge = 16 * tile + 15 >= a.Nq || (j + 1) * BS > a.Nk ||
+                        (a.causal && j * BS + BS - 1 > 16 * tile + a.qoff);
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const int key = j * BS + 16 * kt + l16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][r], c, -l2[r]));
+          if (edge) {
+            const int t = t0 + r;
+            if (t >= a.Nq || key >= a.Nk || (a.causal && key > t + a.qoff)) p = 0.f;
+          }
+          colsum[kt] += p;
+        }
+      }
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds) qop[ds] = qn[ds];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) l2[r] = ln[r];
+    }
+  }
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt) red[w][kt][lane] = colsum[kt];
+  __syncthreads();
+  if (w == 0) {
+    const int kt = lane >> 4, cix = lane & 15;
+    float sum = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww)
+#pragma unroll
+      for (int gg = 0; gg < 4; ++gg) sum += red[ww][kt][16 * gg + cix];
+    const int key = j * BS + lane;
+    if (key < a.Nk) {
+      float* dst = a.score + b * a.ss[0] + hh * a.ss[1] + key;
+      *dst = a.accumulate ? *dst + sum : sum;
+    }
+  }
 }
 
 }  // namespace
@@ -774,20 +932,29 @@ cab_status_t launch_pack_split(const char* fn, const void* k, const int64_t* k_s
 }
 
 template <cab_dtype_t DT>
-void launch_attn_kernel(bool list_lds, dim3 grid, hipStream_t s, const AttnArgs& a) {
-  if (list_lds)
-    attn_fwd_kernel<DT, true><<<grid, 256, 0, s>>>(a);
+void launch_attn_kernel(int list, dim3 grid, hipStream_t s, const AttnArgs& a) {
+  if (list == LIST_LDS)
+    attn_fwd_kernel<DT, LIST_LDS><<<grid, 256, 0, s>>>(a);
+  else if (list == LIST_GLOBAL)
+    attn_fwd_kernel<DT, LIST_GLOBAL><<<grid, 256, 0, s>>>(a);
   else
-    attn_fwd_kernel<DT, false><<<grid, 256, 0, s>>>(a);
+    attn_fwd_kernel<DT, LIST_DENSE><<<grid, 256, 0, s>>>(a);
 }
 
+// Problem geometry of one executor call: query heads H over Hkv K / V heads,
+// Nq query and Nk key tokens, the causal offset and the list mode.
+struct AttnGeom {
+  int64_t B, H, Hkv, Nq, Nk;
+  int64_t qoff;
+  int list;
+};
+
 cab_status_t launch_attn(const char* fn, const void* q, const void* k, const void* vt,
-                         cab_dtype_t dtype, int64_t B, int64_t H, int64_t N,
-                         const int64_t* q_strides, const int64_t* k_strides,
-                         const int64_t* o_strides, const int32_t* kv_idx, const int32_t* kv_cnt,
-                         int32_t kmax, float scale, int causal, void* out, float* lse,
-                         hipStream_t s) {
-  const int64_t M = ceil_div(N, BS);
+                         cab_dtype_t dtype, const AttnGeom& g, const int64_t* q_strides,
+                         const int64_t* k_strides, const int64_t* o_strides,
+                         const int32_t* kv_idx, const int32_t* kv_cnt, int32_t kmax, float scale,
+                         int causal, void* out, float* lse, hipStream_t s) {
+  const int64_t M = ceil_div(g.Nq, BS);
   AttnArgs a;
   a.q = q;
   a.k = static_cast<const uint16_t*>(k);
@@ -801,22 +968,30 @@ cab_status_t launch_attn(const char* fn, const void* q, const void* k, const voi
   }
   a.kv_idx = kv_idx;
   a.kv_cnt = kv_cnt;
-  a.BH = static_cast<int32_t>(B * H);
-  a.H = static_cast<int32_t>(H);
-  a.N = static_cast<int32_t>(N);
+  a.BH = static_cast<int32_t>(g.B * g.H);
+  a.H = static_cast<int32_t>(g.H);
+  a.N = static_cast<int32_t>(g.Nq);
   a.M = static_cast<int32_t>(M);
+  a.Nk = static_cast<int32_t>(g.Nk);
+  a.Mk = static_cast<int32_t>(ceil_div(g.Nk, BS));
+  a.group = static_cast<int32_t>(g.H / g.Hkv);
+  a.qoff = static_cast<int32_t>(g.qoff);
   a.kmax = kmax;
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   a.causal = causal ? 1 : 0;
-  const dim3 grid(static_cast<unsigned>(B * H * M));
-  const bool list_lds = kmax <= LIST_MAX;
+  const dim3 grid(static_cast<unsigned>(g.B * g.H * M));
   if (dtype == CAB_BF16)
-    launch_attn_kernel<CAB_BF16>(list_lds, grid, s, a);
+    launch_attn_kernel<CAB_BF16>(g.list, grid, s, a);
   else if (dtype == CAB_F16)
-    launch_attn_kernel<CAB_F16>(list_lds, grid, s, a);
+    launch_attn_kernel<CAB_F16>(g.list, grid, s, a);
   else
-    launch_attn_kernel<CAB_F32>(list_lds, grid, s, a);
+    launch_attn_kernel<CAB_F32>(g.list, grid, s, a);
   return launch_status(fn);
+}
+
+// The sparse entry points: one K / V head per query head, Nq = Nk = N.
+AttnGeom sparse_geom(int64_t B, int64_t H, int64_t N, int32_t kmax) {
+  return AttnGeom{B, H, H, N, N, 0, kmax <= LIST_MAX ? LIST_LDS : LIST_GLOBAL};
 }
 
 }  // namespace
@@ -860,8 +1035,9 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd_packed(
                        scale, 2)) != CAB_OK)
     return st;
   if ((st = check_packed(fn, vt, vt_bytes, B, H, M, dtype)) != CAB_OK) return st;
-  return launch_attn(fn, q, k, vt, dtype, B, H, N, q_strides, k_strides, o_strides, kv_idx,
-                     kv_cnt, kmax, scale, causal, out, lse, static_cast<hipStream_t>(stream));
+  return launch_attn(fn, q, k, vt, dtype, sparse_geom(B, H, N, kmax), q_strides, k_strides,
+                     o_strides, kv_idx, kv_cnt, kmax, scale, causal, out, lse,
+                     static_cast<hipStream_t>(stream));
 }
 
 extern "C" cab_status_t cab_block_sparse_attn_fwd(
@@ -894,6 +1070,144 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
   else
     st = launch_pack("cab_block_sparse_attn_fwd/pack_v", v, v_strides, B, H, N, workspace, s);
   if (st != CAB_OK) return st;
-  return launch_attn(fn, q, k, workspace, dtype, B, H, N, q_strides, k_strides, o_strides,
-                     kv_idx, kv_cnt, kmax, scale, causal, out, lse, s);
+  return launch_attn(fn, q, k, workspace, dtype, sparse_geom(B, H, N, kmax), q_strides, k_strides,
+                     o_strides, kv_idx, kv_cnt, kmax, scale, causal, out, lse, s);
+}
+
+// ---------------------------------------------------------------------------
+// Dense attention with per-key scores (the eviction path's fused kernel).
+// ---------------------------------------------------------------------------
+
+namespace {
+
+// Shape checks of the dense entry points: H query heads over H_kv K / V
+// heads (H % H_kv == 0), N_q queries, N_k keys, D = 128.
+cab_status_t check_dense(const char* fn, cab_dtype_t dtype, bool allow_f32, int64_t B, int64_t H,
+                         int64_t H_kv, int64_t N_q, int64_t N_k, int64_t D) {
+  if (allow_f32)
+    CAB_REQUIRE(dtype == CAB_BF16 || dtype == CAB_F16 || dtype == CAB_F32, CAB_EDTYPE,
+                "%s: dtype %d unsupported (bf16, fp16 or fp32)", fn, (int)dtype);
+  else
+    CAB_REQUIRE(dtype == CAB_BF16 || dtype == CAB_F16, CAB_EDTYPE,
+                "%s: dtype %d unsupported (bf16 or fp16)", fn, (int)dtype);
+  CAB_REQUIRE(B >= 0 && H >= 0 && H_kv >= 0 && N_q >= 0 && N_k >= 0, CAB_ESHAPE,
+              "%s: negative size", fn);
+  CAB_REQUIRE(D == HD, CAB_ESHAPE, "%s: head dim %lld unsupported (128)", fn, (long long)D);
+  CAB_REQUIRE(H_kv > 0 ? H % H_kv == 0 : H == 0, CAB_ESHAPE,
+              "%s: %lld query heads are not a multiple of %lld K/V heads", fn, (long long)H,
+              (long long)H_kv);
+  CAB_REQUIRE(B * H * ceil_div(N_q, BS) <= INT32_MAX && B * H * ceil_div(N_k, BS) <= INT32_MAX &&
+                  N_q <= INT32_MAX - BS && N_k <= INT32_MAX - BS,
+              CAB_ESHAPE, "%s: problem too large (B*H*blocks < 2^31, N < 2^31 - 64)", fn);
+  return CAB_OK;
+}
+
+}  // namespace
+
+extern "C" size_t cab_flash_attn_workspace_bytes(cab_dtype_t dtype, int64_t B, int64_t H_kv,
+                                                 int64_t N_k, int64_t D) {
+  if (dtype != CAB_BF16 && dtype != CAB_F16 && dtype != CAB_F32) return 0;
+  if (B <= 0 || H_kv <= 0 || N_k <= 0 || D != HD) return 0;
+  return static_cast<size_t>(B * H_kv * ceil_div(N_k, BS)) * block_bytes(dtype);
+}
+
+extern "C" cab_status_t cab_flash_attn_fwd(
+    const void* q, const void* k, const void* v, cab_dtype_t dtype, int64_t B, int64_t H,
+    int64_t H_kv, int64_t N_q, int64_t N_k, int64_t D, const int64_t q_strides[4],
+    const int64_t k_strides[4], const int64_t v_strides[4], const int64_t o_strides[4],
+    float scale, int causal, void* out, float* lse, void* workspace, size_t workspace_bytes,
+    void* stream) {
+  const char* fn = "cab_flash_attn_fwd";
+  clear_error();
+  cab_status_t st = check_dense(fn, dtype, true, B, H, H_kv, N_q, N_k, D);
+  if (st != CAB_OK) return st;
+  CAB_REQUIRE(std::isfinite(scale) && scale > 0.f, CAB_EINVAL, "%s: scale must be finite and > 0",
+              fn);
+  CAB_REQUIRE(q_strides && k_strides && v_strides && o_strides, CAB_EINVAL,
+              "%s: null stride array", fn);
+  if (B == 0 || H == 0 || N_q == 0) return CAB_OK;
+  const int64_t esize = dtype == CAB_F32 ? 4 : 2;
+  if ((st = check_tensor(fn, "q", q, q_strides, esize)) != CAB_OK) return st;
+  if ((st = check_tensor(fn, "out", out, o_strides, esize)) != CAB_OK) return st;
+  CAB_REQUIRE(lse == nullptr || reinterpret_cast<uintptr_t>(lse) % 4 == 0, CAB_ESHAPE,
+              "%s: lse not 4-byte aligned", fn);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (N_k == 0 || H_kv == 0) {
+    // No keys: every row attends to nothing (output 0, lse -inf); K, V and
+    // the workspace are not read (q stands in for their addresses).
+    const AttnGeom g{B, H, H_kv > 0 ? H_kv : H, N_q, 0, -N_q, LIST_DENSE};
+    return launch_attn(fn, q, q, q, dtype, g, q_strides, q_strides, o_strides, nullptr, nullptr,
+                       1, scale, causal, out, lse, s);
+  }
+  if ((st = check_tensor(fn, "k", k, k_strides, esize)) != CAB_OK) return st;
+  if ((st = check_tensor(fn, "v", v, v_strides, esize)) != CAB_OK) return st;
+  CAB_REQUIRE(k_strides[2] <= (int64_t{1} << 24), CAB_ESHAPE,
+              "%s: k token stride %lld too large (<= 2^24 elements)", fn, (long long)k_strides[2]);
+  const int64_t Mk = ceil_div(N_k, BS);
+  const size_t need = static_cast<size_t>(B * H_kv * Mk) * block_bytes(dtype);
+  CAB_REQUIRE(workspace != nullptr && workspace_bytes >= need, CAB_EWORKSPACE,
+              "%s: workspace of %zu bytes given, %zu needed", fn, workspace_bytes, need);
+  CAB_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, CAB_EWORKSPACE,
+              "%s: workspace not 16-byte aligned", fn);
+  if (dtype == CAB_F32)
+    st = launch_pack_split("cab_flash_attn_fwd/pack_split", k, k_strides, v, v_strides, B, H_kv,
+                           N_k, workspace, s);
+  else
+    st = launch_pack("cab_flash_attn_fwd/pack_v", v, v_strides, B, H_kv, N_k, workspace, s);
+  if (st != CAB_OK) return st;
+  const AttnGeom g{B, H, H_kv, N_q, N_k, N_k - N_q, LIST_DENSE};
+  return launch_attn(fn, q, k, workspace, dtype, g, q_strides, k_strides, o_strides, nullptr,
+                     nullptr, 1, scale, causal, out, lse, s);
+}
+
+extern "C" cab_status_t cab_attn_key_scores(
+    const void* q, const void* k, const float* lse, cab_dtype_t dtype, int64_t B, int64_t H,
+    int64_t H_kv, int64_t N_q, int64_t N_k, int64_t D, const int64_t q_strides[4],
+    const int64_t k_strides[4], float scale, int causal, float* scores,
+    const int64_t score_strides[3], int accumulate, void* stream) {
+  const char* fn = "cab_attn_key_scores";
+  clear_error();
+  cab_status_t st = check_dense(fn, dtype, false, B, H, H_kv, N_q, N_k, D);
+  if (st != CAB_OK) return st;
+  CAB_REQUIRE(std::isfinite(scale) && scale > 0.f, CAB_EINVAL, "%s: scale must be finite and > 0",
+              fn);
+  CAB_REQUIRE(q_strides && k_strides && score_strides, CAB_EINVAL, "%s: null stride array", fn);
+  if (B == 0 || H == 0 || N_k == 0) return CAB_OK;
+  CAB_REQUIRE(scores != nullptr, CAB_EINVAL, "%s: null scores", fn);
+  CAB_REQUIRE(score_strides[2] == 1 && score_strides[0] >= 0 && score_strides[1] >= 0,
+              CAB_ESHAPE, "%s: scores must have a contiguous token dim", fn);
+  if (N_q > 0) {
+    if ((st = check_tensor(fn, "q", q, q_strides, 2)) != CAB_OK) return st;
+    CAB_REQUIRE(lse != nullptr && reinterpret_cast<uintptr_t>(lse) % 4 == 0, CAB_EINVAL,
+                "%s: lse must be the fp32 [B, H, N_q] rows cab_flash_attn_fwd wrote", fn);
+  }
+  if ((st = check_tensor(fn, "k", k, k_strides, 2)) != CAB_OK) return st;
+  KeyScoreArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.lse = lse;
+  a.score = scores;
+  for (int d = 0; d < 3; ++d) {
+    a.qs[d] = q_strides[d];
+    a.ks[d] = k_strides[d];
+  }
+  a.ss[0] = score_strides[0];
+  a.ss[1] = score_strides[1];
+  a.BH = static_cast<int32_t>(B * H);
+  a.H = static_cast<int32_t>(H);
+  a.group = static_cast<int32_t>(H / H_kv);
+  a.Nq = static_cast<int32_t>(N_q);
+  a.Nk = static_cast<int32_t>(N_k);
+  a.Mk = static_cast<int32_t>(ceil_div(N_k, BS));
+  a.qoff = static_cast<int32_t>(N_k - N_q);
+  a.causal = causal ? 1 : 0;
+  a.accumulate = accumulate ? 1 : 0;
+  a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
+  const dim3 grid(static_cast<unsigned>(B * H * a.Mk));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == CAB_BF16)
+    key_score_kernel<true><<<grid, 256, 0, s>>>(a);
+  else
+    key_score_kernel<false><<<grid, 256, 0, s>>>(a);
+  return launch_status(fn);
 }

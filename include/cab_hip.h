@@ -49,7 +49,7 @@ enum { CAB_NORM_NONE = 0, CAB_NORM_MINMAX = 1 };
 /* FRC combination (experiments/longbench_qa/config.py:465; test.ipynb:111-145). */
 enum { CAB_FRC_ADDITIVE = 0, CAB_FRC_MULTIPLICATIVE = 1, CAB_FRC_AUGMENTED = 2 };
 
-#define CAB_ABI_VERSION 2
+#define CAB_ABI_VERSION 3
 
 int cab_abi_version(void);
 const char* cab_last_error(void);
@@ -215,6 +215,51 @@ cab_status_t cab_block_sparse_attn_fwd_packed(const void* q, const void* k, cons
                                               const int32_t* kv_idx, const int32_t* kv_cnt,
                                               int32_t kmax, float scale, int causal, void* out,
                                               float* lse, size_t vt_bytes, void* stream);
+
+/*
+ * Dense attention with per-key attention totals, for KV-cache eviction.
+ * Replaces _flash_attention_fwd_kernel / flash_attention_with_cumulative_scores
+ * of cab_attention/kernels/flash_attention_accumulate.py:23-169, :172-261
+ * (callers: :384-445 in the HF attention patch, read back by
+ * experiments/longbench_qa/runner.py:493-538), as two calls:
+ *
+ * cab_flash_attn_fwd: out[t] = softmax_s(q_t . k_s * scale) v_s over every key
+ * s (when causal, s <= t + N_k - N_q: the queries are the last N_q positions
+ * of the key sequence); lse[t] = the natural-log log-sum-exp of the scaled
+ * scores (-inf for a query that sees no key), or lse = NULL. H query heads
+ * share H_kv K / V heads (query head h reads K / V head h / (H / H_kv)).
+ * q, out: [B,H,N_q,D]; k, v: [B,H_kv,N_k,D] (strides); lse: contiguous fp32
+ * [B,H,N_q]. D == 128; bf16, fp16 or fp32 (fp32: split bf16 MFMA as in
+ * cab_block_sparse_attn_fwd). workspace: cab_flash_attn_workspace_bytes()
+ * bytes, 16-byte aligned, overwritten.
+ *
+ * cab_attn_key_scores: score[b,h,s] (+)= sum over queries t of
+ * exp(q_t . k_s * scale - lse[b,h,t]), i.e. the total softmax probability
+ * key s receives from the N_q queries (same masking), with the lse rows of
+ * cab_flash_attn_fwd on the same q, k. Written when accumulate == 0, added
+ * to the existing values otherwise (the reference's running total across
+ * calls). scores: fp32 [B,H,N_k] with strides {b, h, 1}. bf16 or fp16.
+ * Each key's total is summed in a fixed order (no atomics): the result is
+ * deterministic. The reference's kernel adds exp(s - running maximum)
+ * instead, a value that depends on its tiling; this is the quantity its
+ * eager fallback sums (runner.py:680-685).
+ */
+size_t cab_flash_attn_workspace_bytes(cab_dtype_t dtype, int64_t B, int64_t H_kv, int64_t N_k,
+                                      int64_t D);
+
+cab_status_t cab_flash_attn_fwd(const void* q, const void* k, const void* v, cab_dtype_t dtype,
+                                int64_t B, int64_t H, int64_t H_kv, int64_t N_q, int64_t N_k,
+                                int64_t D, const int64_t q_strides[4], const int64_t k_strides[4],
+                                const int64_t v_strides[4], const int64_t o_strides[4],
+                                float scale, int causal, void* out, float* lse, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
+cab_status_t cab_attn_key_scores(const void* q, const void* k, const float* lse,
+                                 cab_dtype_t dtype, int64_t B, int64_t H, int64_t H_kv,
+                                 int64_t N_q, int64_t N_k, int64_t D, const int64_t q_strides[4],
+                                 const int64_t k_strides[4], float scale, int causal,
+                                 float* scores, const int64_t score_strides[3], int accumulate,
+                                 void* stream);
 
 #ifdef __cplusplus
 }

@@ -32,6 +32,11 @@ Pinning of each function (tests/test_oracle.py):
   form (CAB_Attention_Colab.ipynb:376-382), all-kept equals dense softmax
   attention, constant scores give the mean of the kept V rows.
 - ``estimate_flops``: closed forms.
+- ``dense_attention_scores``: uniform scores (closed forms for the output,
+  the log-sum-exp and the harmonic causal key totals), key totals summing
+  to the number of queries that see a key, agreement with
+  ``dense_masked_attention`` and with torch's float64 softmax / SDPA, and
+  grouped K / V equal to repeated heads.
 """
 
 from __future__ import annotations
@@ -41,6 +46,7 @@ import math
 import numpy as np
 
 __all__ = [
+    "dense_attention_scores",
     "canonical_sqnorm",
     "coarsen_max_l2",
     "num_blocks",
@@ -378,3 +384,53 @@ def estimate_flops(n: int, d: int, block_size: int = 64) -> dict:
     a = 2 * m * m * d
     t = 2 * m * m * m
     return {"M": m, "coarsening": c, "matmul": a, "triangles": t, "total": c + a + t}
+
+
+def dense_attention_scores(q, k, v, scale=None, causal: bool = False):
+    """Dense attention with per-key attention totals, in float64.
+
+    The computation of flash_attention_with_cumulative_scores
+    (cab_attention/kernels/flash_attention_accumulate.py:23-169, :172-261):
+    ``out_t = sum_s softmax_s(q_t . k_s * scale) v_s`` over the N_k keys, and
+    per key the attention it receives, ``score_s = sum_t softmax_t(s)`` --
+    the normalised probabilities the reference's eager path sums
+    (experiments/longbench_qa/runner.py:680-685), not the kernel's
+    running-maximum exponentials (:145-156). ``causal`` lets query t see keys
+    ``s <= t + N_k - N_q`` (the queries are the last N_q positions; the
+    reference leaves its causal line commented out, :107). q: ``[B,H,N_q,D]``,
+    k, v: ``[B,H_kv,N_k,D]`` with H_kv dividing H (head h uses K/V head
+    ``h // (H // H_kv)``, the reference's repeat_kv, :470-481).
+
+    Returns (out ``[B,H,N_q,D]``, lse ``[B,H,N_q]`` natural log, -inf for a
+    query seeing no key, scores ``[B,H,N_k]``); a query seeing no key gets 0.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    b, h, nq, d = q.shape
+    hkv, nk = k.shape[1], k.shape[2]
+    if h % hkv:
+        raise ValueError("query heads must be a multiple of K/V heads")
+    group = h // hkv
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    out = np.zeros((b, h, nq, d))
+    lse = np.full((b, h, nq), -np.inf)
+    scores = np.zeros((b, h, nk))
+    allowed = np.ones((nq, nk), bool)
+    if causal:
+        allowed = np.arange(nk)[None, :] <= np.arange(nq)[:, None] + (nk - nq)
+    for bb in range(b):
+        for hh in range(h):
+            kk, vv = k[bb, hh // group], v[bb, hh // group]
+            s = np.where(allowed, (q[bb, hh] @ kk.T) * scale, -np.inf)
+            mx = s.max(axis=1, keepdims=True)
+            seen = np.isfinite(mx[:, 0])
+            e = np.exp(np.where(seen[:, None], s - np.where(seen[:, None], mx, 0.0), -np.inf))
+            den = e.sum(axis=1, keepdims=True)
+            p = np.divide(e, den, out=np.zeros_like(e), where=den > 0)
+            out[bb, hh] = p @ vv
+            lse[bb, hh] = np.where(seen, mx[:, 0] + np.log(np.where(seen, den[:, 0], 1.0)), -np.inf)
+            scores[bb, hh] = p.sum(axis=0)
+    return out, lse, scores
+

@@ -35,7 +35,8 @@ def test_header_declares_the_hot_path():
                  "cab_block_frc_workspace_bytes", "cab_block_frc", "cab_block_topk",
                  "cab_block_sparse_attn_workspace_bytes", "cab_block_sparse_attn_fwd",
                  "cab_block_sparse_attn_pack_v", "cab_block_sparse_attn_fwd_packed",
-                 "cab_block_topk_hybrid"):
+                 "cab_block_topk_hybrid", "cab_flash_attn_workspace_bytes",
+                 "cab_flash_attn_fwd", "cab_attn_key_scores"):
         assert name in syms
     assert set(syms) == set(nat.SIGNATURES), "ctypes table and header disagree"
 
@@ -191,3 +192,32 @@ def test_module_contract_on_host():
         CABAttention(dim=500, num_heads=8)
     with pytest.raises(ValueError):
         CoarseCurvaturePredictor(sparsity=1.5)
+
+
+def test_dense_attention_validation(lib):
+    """cab_flash_attn_fwd / cab_attn_key_scores refuse bad shapes, dtypes,
+    head groupings, scales and workspaces before any launch."""
+    ws = lib.cab_flash_attn_workspace_bytes
+    assert ws(nat.CAB_BF16, 1, 2, 65, 128) == 2 * 2 * 16384
+    assert ws(nat.CAB_F32, 1, 2, 65, 128) == 2 * 2 * 65536
+    assert ws(nat.CAB_BF16, 1, 2, 65, 64) == 0
+    st = _s4(8 * 64 * 128, 64 * 128, 128, 1)
+    fwd = lambda **kw: lib.cab_flash_attn_fwd(
+        FAKE, FAKE, FAKE, kw.get("dt", nat.CAB_BF16), 1, kw.get("H", 8), kw.get("Hkv", 2), 64, 64,
+        kw.get("D", 128), st, st, st, kw.get("os", st), kw.get("scale", 0.088), 1, FAKE, None,
+        kw.get("ws", FAKE), kw.get("wsb", 1 << 30), None)
+    assert fwd(dt=9) == nat.CAB_EDTYPE
+    assert fwd(D=64) == nat.CAB_ESHAPE
+    assert fwd(H=8, Hkv=3) == nat.CAB_ESHAPE
+    assert fwd(scale=0.0) == nat.CAB_EINVAL
+    assert fwd(os=_s4(1, 1, 1, 3)) == nat.CAB_ESHAPE
+    assert fwd(wsb=2 * 16384 - 1) == nat.CAB_EWORKSPACE
+    assert fwd(ws=None) == nat.CAB_EWORKSPACE
+    ss = _s4(8 * 64, 64, 1, 0)
+    sc = lambda **kw: lib.cab_attn_key_scores(
+        FAKE, FAKE, kw.get("lse", FAKE), kw.get("dt", nat.CAB_BF16), 1, 8, 2, 64, 64, 128, st, st,
+        0.088, 1, kw.get("scores", FAKE), kw.get("ss", ss), 0, None)
+    assert sc(dt=nat.CAB_F32) == nat.CAB_EDTYPE
+    assert sc(lse=None) == nat.CAB_EINVAL
+    assert sc(scores=None) == nat.CAB_EINVAL
+    assert sc(ss=_s4(8 * 64, 64, 2, 0)) == nat.CAB_ESHAPE

@@ -6,6 +6,7 @@ import math
 
 import numpy as np
 import pytest
+import torch
 
 from conftest import GOLDEN
 from oracle import cab_oracle as O
@@ -373,3 +374,79 @@ def test_estimate_flops_closed_form():
     assert e["triangles"] == 2 * 2048 ** 3
     assert e["matmul"] == 2 * 2048 ** 2 * 128
     assert e["total"] == e["coarsening"] + e["matmul"] + e["triangles"]
+
+
+# ---------------------------------------------------------------------------
+# dense_attention_scores (dense attention with per-key attention totals)
+# ---------------------------------------------------------------------------
+
+def test_dense_scores_uniform_closed_forms():
+    """q = 0: every visible key gets the same weight. Non-causal: out = mean
+    of V, lse = log(N_k), score = N_q / N_k. Causal (queries are the last N_q
+    positions): query t sees t + off + 1 keys, so key s receives
+    sum_{t : t + off >= s} 1 / (t + off + 1)."""
+    rng = np.random.default_rng(0)
+    nq, nk, d = 5, 9, 8
+    q = np.zeros((1, 1, nq, d))
+    k = rng.standard_normal((1, 1, nk, d))
+    v = rng.standard_normal((1, 1, nk, d))
+    out, lse, sc = O.dense_attention_scores(q, k, v)
+    np.testing.assert_allclose(out[0, 0], np.broadcast_to(v[0, 0].mean(0), (nq, d)), atol=1e-12)
+    np.testing.assert_allclose(lse[0, 0], np.log(nk), atol=1e-12)
+    np.testing.assert_allclose(sc[0, 0], nq / nk, atol=1e-12)
+    out, lse, sc = O.dense_attention_scores(q, k, v, causal=True)
+    off = nk - nq
+    for t in range(nq):
+        np.testing.assert_allclose(out[0, 0, t], v[0, 0, :t + off + 1].mean(0), atol=1e-12)
+        assert lse[0, 0, t] == pytest.approx(math.log(t + off + 1))
+    want = [sum(1.0 / (t + off + 1) for t in range(nq) if t + off >= s) for s in range(nk)]
+    np.testing.assert_allclose(sc[0, 0], want, atol=1e-12)
+
+
+def test_dense_scores_invariants_and_manual_form():
+    """Each query's probabilities sum to 1, so the key totals sum to the
+    number of queries that see a key; the output equals the manual masked
+    softmax (dense_masked_attention) on the same mask; more queries than keys
+    leave the first rows with no key (output 0, lse -inf)."""
+    rng = np.random.default_rng(1)
+    for nq, nk, causal in [(7, 7, False), (7, 7, True), (3, 11, True), (12, 5, True)]:
+        q, k, v = (rng.standard_normal((2, 2, n, 16)) for n in (nq, nk, nk))
+        out, lse, sc = O.dense_attention_scores(q, k, v, causal=causal)
+        seen = (np.arange(nq) + nk - nq >= 0) if causal else np.ones(nq, bool)
+        np.testing.assert_allclose(sc.sum(-1), seen.sum(), atol=1e-9)
+        mask = np.ones((2, 2, nq, nk), bool)
+        if causal:
+            mask &= np.arange(nk)[None, :] <= np.arange(nq)[:, None] + (nk - nq)
+        np.testing.assert_allclose(out, O.dense_masked_attention(q, k, v, mask), atol=1e-12)
+        assert np.all(out[:, :, ~seen] == 0) and np.all(np.isneginf(lse[:, :, ~seen]))
+
+
+def test_dense_scores_match_torch_float64():
+    """An independent float64 computation with torch: softmax of the masked
+    scaled scores (column sums = key totals, logsumexp = lse) and
+    scaled_dot_product_attention with a boolean mask for the output."""
+    rng = np.random.default_rng(2)
+    nq, nk, d = 6, 10, 32
+    q, k, v = (torch.from_numpy(rng.standard_normal((1, 2, n, d))) for n in (nq, nk, nk))
+    mask = torch.arange(nk)[None, :] <= torch.arange(nq)[:, None] + (nk - nq)
+    s = (q @ k.transpose(-1, -2)) / math.sqrt(d)
+    s = s.masked_fill(~mask, float("-inf"))
+    p = torch.softmax(s, dim=-1)
+    ref_out = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+    out, lse, sc = O.dense_attention_scores(q.numpy(), k.numpy(), v.numpy(), causal=True)
+    np.testing.assert_allclose(out, ref_out.numpy(), atol=1e-12)
+    np.testing.assert_allclose(sc, p.sum(-2).numpy(), atol=1e-12)
+    np.testing.assert_allclose(lse, torch.logsumexp(s, -1).numpy(), atol=1e-12)
+
+
+def test_dense_scores_grouped_heads_equal_repeated_heads():
+    """K / V with H_kv heads give the same result as K / V with every head
+    repeated H / H_kv times (head h uses K/V head h // (H / H_kv))."""
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((1, 6, 5, 8))
+    k = rng.standard_normal((1, 2, 9, 8))
+    v = rng.standard_normal((1, 2, 9, 8))
+    got = O.dense_attention_scores(q, k, v, causal=True)
+    want = O.dense_attention_scores(q, np.repeat(k, 3, axis=1), np.repeat(v, 3, axis=1), causal=True)
+    for a, b in zip(got, want):
+        np.testing.assert_array_equal(a, b)
