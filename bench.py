@@ -43,6 +43,7 @@ for _p in (str(ROOT), str(PKG)):
 METRIC = "predictor ms @N=128k + block-sparse attn TFLOP/s, % of roofline"
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+PEAK_FP32_TFLOPS = 157.3    # MI355X dense fp32 MFMA
 TRAFFIC_FILE = ROOT / "profiles" / "attn_fwd_config4_traffic.md"
 
 
@@ -281,7 +282,55 @@ def main() -> int:
 
     result_pred = None
     result_bridge = None
+    result_fp32 = None
+    result_evict = None
     if not args.attn_only:
+        # ---------------- config 4 in fp32 (split bf16 operands, fp32 output)
+        q32, k32, v32 = (t.float() for t in (q, k, v))
+        out32 = torch.empty_like(q32)
+        run32 = lambda: block_sparse_attention(q32, k32, v32, idx, cnt, bs, causal=True, out=out32)
+        run32()
+        fp32_ms = time_events(run32, max(3, args.steps // 4))
+        result_fp32 = {
+            "config": "config4 inputs in fp32 (same lists); split bf16 hi+lo operands, three "
+                      "MFMA products per product, fp32 output; step = pack K/V + attention",
+            "ms": round(fp32_ms, 4),
+            "TFLOPs": round(flops / (fp32_ms * 1e-3) / 1e12, 1),
+            "frac_of_fp32_mfma_peak": round(flops / (fp32_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 3),
+        }
+        log(f"fp32 executor {fp32_ms:.3f} ms = {result_fp32['TFLOPs']} TFLOP/s")
+        del q32, k32, v32, out32
+        torch.cuda.empty_cache()
+
+        # ---------------- eviction path: dense attention + per-key totals
+        from cab_attention.kernels import flash_attention, key_scores
+        Be, He, Hkve, Ne = 1, 32, 8, 16384
+        qe = seeded_gpu((Be, He, Ne, D), 7, torch.bfloat16, dev)
+        ke = seeded_gpu((Be, Hkve, Ne, D), 8, torch.bfloat16, dev)
+        ve = seeded_gpu((Be, Hkve, Ne, D), 9, torch.bfloat16, dev)
+        oute, lsee = flash_attention(qe, ke, ve, causal=True, return_lse=True)
+        sce = key_scores(qe, ke, lsee, causal=True)
+        fwd_ms = time_events(lambda: flash_attention(qe, ke, ve, causal=True, out=oute),
+                             max(3, args.steps // 4))
+        sc_ms = time_events(lambda: key_scores(qe, ke, lsee, causal=True, scores=sce),
+                            max(3, args.steps // 4))
+        pairs_e = Be * He * Ne * (Ne + 1) // 2
+        fwd_fl, sc_fl = 4 * D * pairs_e, 2 * D * pairs_e
+        result_evict = {
+            "config": "flash_attention_with_cumulative_scores: B=1 H=32 H_kv=8 N_q=N_k=16384 "
+                      "D=128 causal bf16 (dense attention + per-key softmax totals)",
+            "attention_ms": round(fwd_ms, 4),
+            "attention_TFLOPs": round(fwd_fl / (fwd_ms * 1e-3) / 1e12, 1),
+            "attention_frac_mfma": round(fwd_fl / (fwd_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "key_scores_ms": round(sc_ms, 4),
+            "key_scores_TFLOPs": round(sc_fl / (sc_ms * 1e-3) / 1e12, 1),
+            "key_scores_frac_mfma": round(sc_fl / (sc_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "total_ms": round(fwd_ms + sc_ms, 4),
+        }
+        log(f"eviction path: attention {fwd_ms:.3f} ms, key scores {sc_ms:.3f} ms")
+        del qe, ke, ve, oute, lsee, sce
+        torch.cuda.empty_cache()
+
         # ---------------- config 3: predictor latency at N = 128k
         B3, H3, N3 = 2, 8, 128000
         q3 = seeded_gpu((B3, H3, N3, D), 1, torch.bfloat16, dev)
@@ -421,6 +470,8 @@ def main() -> int:
         "cpu_baseline": cpu,
         "predictor": result_pred,
         "bridge": result_bridge,
+        "fp32_executor": result_fp32,
+        "eviction_path": result_evict,
     }
     print(json.dumps(line), flush=True)
     return 0
