@@ -197,6 +197,40 @@ def predictor_only(args, dev, bs, D) -> int:
     return 0
 
 
+def eviction_path(args, dev, D):
+    """Dense attention + per-key softmax totals (flash_attention_with_cumulative_scores)
+    at B=1 H=32 H_kv=8 N=16384 causal bf16."""
+    import torch
+    from cab_attention.kernels import flash_attention, key_scores
+    Be, He, Hkve, Ne = 1, 32, 8, 16384
+    qe = seeded_gpu((Be, He, Ne, D), 7, torch.bfloat16, dev)
+    ke = seeded_gpu((Be, Hkve, Ne, D), 8, torch.bfloat16, dev)
+    ve = seeded_gpu((Be, Hkve, Ne, D), 9, torch.bfloat16, dev)
+    oute, lsee = flash_attention(qe, ke, ve, causal=True, return_lse=True)
+    sce = key_scores(qe, ke, lsee, causal=True)
+    fwd_ms = time_events(lambda: flash_attention(qe, ke, ve, causal=True, out=oute),
+                         max(3, args.steps // 4))
+    sc_ms = time_events(lambda: key_scores(qe, ke, lsee, causal=True, scores=sce),
+                        max(3, args.steps // 4))
+    pairs_e = Be * He * Ne * (Ne + 1) // 2
+    fwd_fl, sc_fl = 4 * D * pairs_e, 2 * D * pairs_e
+    result_evict = {
+        "config": "flash_attention_with_cumulative_scores: B=1 H=32 H_kv=8 N_q=N_k=16384 "
+                  "D=128 causal bf16 (dense attention + per-key softmax totals)",
+        "attention_ms": round(fwd_ms, 4),
+        "attention_TFLOPs": round(fwd_fl / (fwd_ms * 1e-3) / 1e12, 1),
+        "attention_frac_mfma": round(fwd_fl / (fwd_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "key_scores_ms": round(sc_ms, 4),
+        "key_scores_TFLOPs": round(sc_fl / (sc_ms * 1e-3) / 1e12, 1),
+        "key_scores_frac_mfma": round(sc_fl / (sc_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "total_ms": round(fwd_ms + sc_ms, 4),
+    }
+    log(f"eviction path: attention {fwd_ms:.3f} ms, key scores {sc_ms:.3f} ms")
+    del qe, ke, ve, oute, lsee, sce
+    torch.cuda.empty_cache()
+    return result_evict
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -209,6 +243,8 @@ def main() -> int:
                     help="skip the predictor and bridge sections")
     ap.add_argument("--predictor-only", action="store_true",
                     help="only time the config-3 predictor (for per-kernel profiles)")
+    ap.add_argument("--eviction-only", action="store_true",
+                    help="only time the eviction path (dense attention + key totals; profiles)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -241,6 +277,9 @@ def main() -> int:
     bs, D = 64, 128
     if args.predictor_only:
         return predictor_only(args, dev, bs, D)
+    if args.eviction_only:
+        print(json.dumps({"eviction_path": eviction_path(args, dev, D)}), flush=True)
+        return 0
 
     # ---------------- config 4: predictor (causal) + block-sparse attention
     B, H, N, sp = 1, 32, 65536, 0.95
@@ -302,34 +341,7 @@ def main() -> int:
         del q32, k32, v32, out32
         torch.cuda.empty_cache()
 
-        # ---------------- eviction path: dense attention + per-key totals
-        from cab_attention.kernels import flash_attention, key_scores
-        Be, He, Hkve, Ne = 1, 32, 8, 16384
-        qe = seeded_gpu((Be, He, Ne, D), 7, torch.bfloat16, dev)
-        ke = seeded_gpu((Be, Hkve, Ne, D), 8, torch.bfloat16, dev)
-        ve = seeded_gpu((Be, Hkve, Ne, D), 9, torch.bfloat16, dev)
-        oute, lsee = flash_attention(qe, ke, ve, causal=True, return_lse=True)
-        sce = key_scores(qe, ke, lsee, causal=True)
-        fwd_ms = time_events(lambda: flash_attention(qe, ke, ve, causal=True, out=oute),
-                             max(3, args.steps // 4))
-        sc_ms = time_events(lambda: key_scores(qe, ke, lsee, causal=True, scores=sce),
-                            max(3, args.steps // 4))
-        pairs_e = Be * He * Ne * (Ne + 1) // 2
-        fwd_fl, sc_fl = 4 * D * pairs_e, 2 * D * pairs_e
-        result_evict = {
-            "config": "flash_attention_with_cumulative_scores: B=1 H=32 H_kv=8 N_q=N_k=16384 "
-                      "D=128 causal bf16 (dense attention + per-key softmax totals)",
-            "attention_ms": round(fwd_ms, 4),
-            "attention_TFLOPs": round(fwd_fl / (fwd_ms * 1e-3) / 1e12, 1),
-            "attention_frac_mfma": round(fwd_fl / (fwd_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-            "key_scores_ms": round(sc_ms, 4),
-            "key_scores_TFLOPs": round(sc_fl / (sc_ms * 1e-3) / 1e12, 1),
-            "key_scores_frac_mfma": round(sc_fl / (sc_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-            "total_ms": round(fwd_ms + sc_ms, 4),
-        }
-        log(f"eviction path: attention {fwd_ms:.3f} ms, key scores {sc_ms:.3f} ms")
-        del qe, ke, ve, oute, lsee, sce
-        torch.cuda.empty_cache()
+        result_evict = eviction_path(args, dev, D)
 
         # ---------------- config 3: predictor latency at N = 128k
         B3, H3, N3 = 2, 8, 128000
