@@ -49,7 +49,7 @@ enum { CAB_NORM_NONE = 0, CAB_NORM_MINMAX = 1 };
 /* FRC combination (experiments/longbench_qa/config.py:465; test.ipynb:111-145). */
 enum { CAB_FRC_ADDITIVE = 0, CAB_FRC_MULTIPLICATIVE = 1, CAB_FRC_AUGMENTED = 2 };
 
-#define CAB_ABI_VERSION 3
+#define CAB_ABI_VERSION 4
 
 int cab_abi_version(void);
 const char* cab_last_error(void);
@@ -260,6 +260,64 @@ cab_status_t cab_attn_key_scores(const void* q, const void* k, const float* lse,
                                  const int64_t k_strides[4], float scale, int causal,
                                  float* scores, const int64_t score_strides[3], int accumulate,
                                  void* stream);
+
+/*
+ * KV-cache eviction: which cache positions to keep, and the pruned cache.
+ *
+ * cab_evict_select replaces the selection of
+ * ThreeComponentEvictionPolicy.select_indices (cab_attention/eviction/policy.py:39-200)
+ * and h2o_select_indices (cab_attention/eviction/h2o.py:15-94), called by
+ * CABCache._evict / H2OCache._evict (cache/cab_cache.py:177-226). Over
+ * cache_len positions (<= 2^20), with score[i] = importance_scores[i] for
+ * i < n_scores and 0 beyond (the reference's zero padding), it keeps:
+ *   1. the local window, the last local_budget positions;
+ *   2. importance: the min(importance_budget, remaining) remaining positions
+ *      with the highest score (a tie goes to the lower position; NaN ranks
+ *      above +inf; -0 == +0) -- or, with no scores and importance_fallback,
+ *      the importance_budget positions just before the local window;
+ *   3. bridges, min(bridge_budget, remaining) of the remaining positions by
+ *      bridge_mode: 1 nearest |score - m| with m the lower median of the
+ *      remaining scores (NaN if any is NaN; ties to the lower position),
+ *      2 highest bridge_scores[i] (falls back to 1, or to 3 without scores,
+ *      when step 2 kept nothing), 3 the remaining positions of rank
+ *      [remaining / 3, min(remaining, remaining / 3 + budget)) in position
+ *      order; 0 none.
+ * A kept position is never selected again. Outputs: keep_indices (int64,
+ * ascending, up to cache_len entries), counts = {local, importance, bridge,
+ * total} (int32) and, if not NULL, category[i] = 0 evicted, 1 local,
+ * 2 importance, 3 bridge (uint8, cache_len entries). One workgroup; all
+ * device buffers.
+ */
+cab_status_t cab_evict_select(const float* importance_scores, int64_t n_scores,
+                              const float* bridge_scores, int64_t cache_len,
+                              int32_t local_budget, int32_t importance_budget,
+                              int32_t bridge_budget, int importance_fallback, int bridge_mode,
+                              int64_t* keep_indices, int32_t* counts, uint8_t* category,
+                              void* stream);
+
+/*
+ * Bridge scores of the policy's attention-matrix mode (policy.py:118-138):
+ * with imp = {i : category[i] == 2} (cab_evict_select's output),
+ * bridge_scores[j] = (sum_{i in imp} A[i, j]) * (sum_{i in imp} A[j, i]).
+ * attention: fp32 [cache_len, cache_len], row stride row_stride (elements).
+ * Sums run in increasing i.
+ */
+cab_status_t cab_evict_connectivity(const float* attention, int64_t cache_len, int64_t row_stride,
+                                    const uint8_t* category, float* bridge_scores, void* stream);
+
+/*
+ * Prunes a cache: for each of n_tensors tensors (every layer's K and V),
+ * dst[t][b, h, r, :] = src[t][b, h, keep_indices[r], :] for r < n_keep (rows
+ * of row_bytes bytes; an index outside [0, n_src) gives a zero row).
+ * Replaces the per-layer `cache[:, :, keep_indices, :]` of cab_cache.py:204-208
+ * and h2o_cache.py with one launch per 32 tensors. src / dst: host arrays of
+ * device pointers (16-byte aligned); strides in bytes {b, h, row}, multiples
+ * of 16; keep_indices: int64 device array. dst must not overlap src.
+ */
+cab_status_t cab_kv_gather(const void* const* src, void* const* dst, int32_t n_tensors, int64_t B,
+                           int64_t H, int64_t n_src, int64_t row_bytes,
+                           const int64_t src_strides[3], const int64_t dst_strides[3],
+                           const int64_t* keep_indices, int64_t n_keep, void* stream);
 
 #ifdef __cplusplus
 }

@@ -37,6 +37,14 @@ Pinning of each function (tests/test_oracle.py):
   to the number of queries that see a key, agreement with
   ``dense_masked_attention`` and with torch's float64 softmax / SDPA, and
   grouped K / V equal to repeated heads.
+- ``evict_select``: on tie-free scores, torch.topk / torch.median applied as
+  the reference policies do (policy.py:71-160, h2o.py:45-80); with ties and
+  NaN, the ordering invariants (every kept score ranks at or above every
+  evicted candidate, equal scores kept in position order); the budget
+  arithmetic; the positional and fallback branches.
+- ``evict_connectivity``: explicit sums over the importance rows and
+  columns against numpy's fancy-indexed reductions.
+- ``kv_gather``: identity and reversal permutations, out-of-range rows.
 """
 
 from __future__ import annotations
@@ -46,6 +54,9 @@ import math
 import numpy as np
 
 __all__ = [
+    "evict_select",
+    "evict_connectivity",
+    "kv_gather",
     "dense_attention_scores",
     "canonical_sqnorm",
     "coarsen_max_l2",
@@ -433,4 +444,114 @@ def dense_attention_scores(q, k, v, scale=None, causal: bool = False):
             lse[bb, hh] = np.where(seen, mx[:, 0] + np.log(np.where(seen, den[:, 0], 1.0)), -np.inf)
             scores[bb, hh] = p.sum(axis=0)
     return out, lse, scores
+
+
+def _asc_keys(x) -> np.ndarray:
+    """uint32 keys whose ascending order is the float order with -0 == +0
+    and NaN above +inf (the selection order of cab_evict_select)."""
+    x = np.asarray(x, dtype=np.float32)
+    u = x.view(np.uint32).copy()
+    u[x == 0] = 0
+    u[np.isnan(x)] = 0x7FC00000
+    neg = (u & 0x80000000) != 0
+    return np.where(neg, ~u, u | 0x80000000).astype(np.uint32)
+
+
+def evict_select(scores, cache_len: int, local: int, imp: int, bridge: int,
+                 fallback: bool, mode: int, bridge_scores=None):
+    """The positions a KV cache keeps: local window, importance, bridges.
+
+    Restates ThreeComponentEvictionPolicy.select_indices
+    (cab_attention/eviction/policy.py:39-200) and h2o_select_indices
+    (eviction/h2o.py:15-94) with cab_evict_select's tie rule (torch.topk's
+    order is unspecified): among equal keys the lower position wins, NaN
+    ranks above +inf, -0 equals +0, and a kept position is never chosen
+    again. ``scores`` is zero-padded / truncated to cache_len (policy.py:76-88).
+    ``mode``: 0 no bridges, 1 nearest the lower median of the remaining
+    scores (NaN if one is NaN; policy.py:140-162), 2 highest bridge_scores
+    (policy.py:118-138; falls back to 1, or 3 without scores, when no
+    importance position was kept), 3 the remaining positions of rank
+    [remaining // 3, +budget) (policy.py:164-174). ``fallback``: with no
+    scores, the ``imp`` positions before the local window (policy.py:104-108).
+
+    Returns (kept positions ascending int64, (local, importance, bridge)
+    counts, category uint8: 0 evicted, 1 local, 2 importance, 3 bridge).
+    """
+    n = cache_len
+    s = np.zeros(n, np.float32)
+    if scores is not None:
+        sc = np.asarray(scores, dtype=np.float32).reshape(-1)
+        m = min(sc.size, n)
+        s[:m] = sc[:m]
+    kept = np.zeros(n, bool)
+    cat = np.zeros(n, np.uint8)
+    kept[n - local:] = True
+    cat[n - local:] = 1
+
+    def take_smallest(keys, need, c):
+        cand = np.flatnonzero(~kept)
+        order = cand[np.lexsort((cand, keys[cand]))]
+        sel = order[:need]
+        kept[sel] = True
+        cat[sel] = c
+
+    n_imp = 0
+    if scores is not None:
+        n_imp = min(imp, n - local)
+        if n_imp > 0:
+            take_smallest(~_asc_keys(s), n_imp, 2)
+    elif fallback and imp > 0:
+        s0 = max(0, n - local - imp)
+        kept[s0:n - local] = True
+        cat[s0:n - local] = 2
+        n_imp = n - local - s0
+    free1 = n - local - n_imp
+    if mode == 2 and n_imp == 0:
+        mode = 1 if scores is not None else 3
+    if mode == 1 and scores is None:
+        mode = 3
+    n_br = min(bridge, free1) if (bridge > 0 and free1 > 0 and mode != 0) else 0
+    if n_br > 0:
+        if mode == 1:
+            valid = s[~kept]
+            if np.isnan(valid).any():
+                med = np.float32(np.nan)
+            else:
+                med = np.sort(valid)[(free1 - 1) // 2]
+            dist = np.abs((s - np.float32(med)).astype(np.float32))
+            take_smallest(_asc_keys(dist), n_br, 3)
+        elif mode == 2:
+            take_smallest(~_asc_keys(np.asarray(bridge_scores, np.float32).reshape(-1)[:n]), n_br, 3)
+        else:
+            cand = np.flatnonzero(~kept)
+            sel = cand[free1 // 3:free1 // 3 + n_br]  # a slice: cut at the end
+            n_br = sel.size
+            kept[sel] = True
+            cat[sel] = 3
+    return np.flatnonzero(kept).astype(np.int64), (local, n_imp, n_br), cat
+
+
+def evict_connectivity(attention, category) -> np.ndarray:
+    """Bridge scores of the attention-matrix mode (policy.py:118-138):
+    (sum over importance rows of A) * (sum over importance columns of A), in
+    float64, with importance = category == 2."""
+    a = np.asarray(attention, dtype=np.float64)
+    imp = np.flatnonzero(np.asarray(category) == 2)
+    from_ = np.zeros(a.shape[1])
+    to = np.zeros(a.shape[0])
+    for i in imp:
+        from_ += a[i, :]
+        to += a[:, i]
+    return from_ * to
+
+
+def kv_gather(x, keep) -> np.ndarray:
+    """``x[:, :, keep, :]`` with out-of-range positions giving zero rows
+    (cab_cache.py:204-208)."""
+    x = np.asarray(x)
+    keep = np.asarray(keep, dtype=np.int64)
+    out = np.zeros(x.shape[:2] + (keep.size,) + x.shape[3:], x.dtype)
+    ok = (keep >= 0) & (keep < x.shape[2])
+    out[:, :, ok] = x[:, :, keep[ok]]
+    return out
 

@@ -36,7 +36,8 @@ def test_header_declares_the_hot_path():
                  "cab_block_sparse_attn_workspace_bytes", "cab_block_sparse_attn_fwd",
                  "cab_block_sparse_attn_pack_v", "cab_block_sparse_attn_fwd_packed",
                  "cab_block_topk_hybrid", "cab_flash_attn_workspace_bytes",
-                 "cab_flash_attn_fwd", "cab_attn_key_scores"):
+                 "cab_flash_attn_fwd", "cab_attn_key_scores", "cab_evict_select",
+                 "cab_evict_connectivity", "cab_kv_gather"):
         assert name in syms
     assert set(syms) == set(nat.SIGNATURES), "ctypes table and header disagree"
 
@@ -221,3 +222,27 @@ def test_dense_attention_validation(lib):
     assert sc(lse=None) == nat.CAB_EINVAL
     assert sc(scores=None) == nat.CAB_EINVAL
     assert sc(ss=_s4(8 * 64, 64, 2, 0)) == nat.CAB_ESHAPE
+
+
+def test_eviction_validation(lib):
+    sel = lambda **kw: lib.cab_evict_select(
+        kw.get("scores", FAKE), kw.get("ns", 10), None, kw.get("n", 10), kw.get("local", 2),
+        kw.get("imp", 3), kw.get("br", 2), 1, kw.get("mode", 1), kw.get("keep", FAKE), FAKE, None,
+        None)
+    assert sel(n=(1 << 20) + 1) == nat.CAB_ESHAPE
+    assert sel(local=11) == nat.CAB_EINVAL
+    assert sel(imp=-1) == nat.CAB_EINVAL
+    assert sel(mode=4) == nat.CAB_EINVAL
+    assert sel(mode=2) == nat.CAB_EINVAL  # no bridge scores
+    assert sel(scores=None) == nat.CAB_EINVAL
+    assert sel(keep=None) == nat.CAB_EINVAL
+    assert lib.cab_evict_connectivity(FAKE, 10, 9, FAKE, FAKE, None) == nat.CAB_ESHAPE
+    assert lib.cab_evict_connectivity(None, 10, 10, FAKE, FAKE, None) == nat.CAB_EINVAL
+    ptrs = (ctypes.c_void_p * 1)(FAKE)
+    nulls = (ctypes.c_void_p * 1)(None)
+    st = _s4(1 << 20, 1 << 16, 256, 0)
+    g = lambda **kw: lib.cab_kv_gather(kw.get("src", ptrs), ptrs, 1, 1, 2, 100,
+                                       kw.get("rb", 256), kw.get("ss", st), st, FAKE, 10, None)
+    assert g(rb=100) == nat.CAB_ESHAPE
+    assert g(ss=_s4(1 << 20, 1 << 16, 8, 0)) == nat.CAB_ESHAPE
+    assert g(src=nulls) == nat.CAB_EINVAL

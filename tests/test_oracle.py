@@ -450,3 +450,115 @@ def test_dense_scores_grouped_heads_equal_repeated_heads():
     want = O.dense_attention_scores(q, np.repeat(k, 3, axis=1), np.repeat(v, 3, axis=1), causal=True)
     for a, b in zip(got, want):
         np.testing.assert_array_equal(a, b)
+
+
+# ---------------------------------------------------------------------------
+# evict_select / evict_connectivity / kv_gather (KV-cache eviction)
+# ---------------------------------------------------------------------------
+
+def _masked_topk(scores, exclude, k):
+    """torch.topk over scores with the excluded positions at -inf, the way
+    the reference policies select (policy.py:91-102, h2o.py:70-80)."""
+    t = torch.from_numpy(np.asarray(scores, np.float32)).clone()
+    t[torch.from_numpy(exclude)] = -float("inf")
+    return set(torch.topk(t, k, largest=True).indices.tolist())
+
+
+def test_evict_select_matches_torch_on_tie_free_scores():
+    """Tie-free scores: importance = torch.topk of the scores outside the
+    local window; bridges = torch.topk of -|s - torch.median(remaining)|;
+    the counts follow the budgets."""
+    rng = np.random.default_rng(0)
+    for n, local, imp, br in [(1000, 30, 50, 20), (257, 0, 100, 100), (64, 64, 10, 5), (10, 3, 20, 20)]:
+        s = (rng.standard_normal(n) * 3).astype(np.float32)  # distinct values and distances
+        keep, cnt, cat = O.evict_select(s, n, local, imp, br, True, 1)
+        loc = np.zeros(n, bool)
+        loc[n - local:] = True
+        n_imp = min(imp, n - local)
+        assert cnt == (local, n_imp, min(br, n - local - n_imp))
+        if n_imp:
+            assert set(np.flatnonzero(cat == 2)) == _masked_topk(s, loc, n_imp)
+        sel = cat > 0
+        if cnt[2]:
+            med = torch.median(torch.from_numpy(s[~(loc | (cat == 2))])).item()
+            want = _masked_topk(-np.abs(s - np.float32(med)), loc | (cat == 2), cnt[2])
+            assert set(np.flatnonzero(cat == 3)) == want
+        assert np.array_equal(keep, np.flatnonzero(sel))
+        assert np.all(cat[n - local:] == 1)
+
+
+def test_evict_select_ties_nan_and_order_invariants():
+    """With many equal scores, NaN, +-inf and -0: every kept importance
+    position ranks at or above every evicted candidate (NaN highest), and
+    among equal scores at the boundary the lower positions are kept; -0 and
+    +0 tie."""
+    rng = np.random.default_rng(1)
+    n = 500
+    s = rng.integers(0, 5, n).astype(np.float32)
+    s[[3, 77]] = np.nan
+    s[[10, 11]] = np.inf
+    s[[20, 21]] = -np.inf
+    s[30], s[31] = -0.0, 0.0
+    keep, (loc, n_imp, _), cat = O.evict_select(s, n, 40, 100, 0, True, 0)
+    rank = np.where(np.isnan(s), np.inf, s)  # NaN ranks with (above) +inf
+    imp_pos = np.flatnonzero(cat == 2)
+    rest = np.flatnonzero(cat == 0)
+    assert {3, 77} <= set(imp_pos) and {10, 11} <= set(imp_pos)
+    thr = rank[imp_pos].min()
+    assert np.all(rank[rest] <= thr)
+    eq_kept = imp_pos[rank[imp_pos] == thr]
+    eq_evicted = rest[rank[rest] == thr]
+    assert eq_kept.size == 0 or eq_evicted.size == 0 or eq_kept.max() < eq_evicted.min()
+    _, _, cat0 = O.evict_select(np.array([1, -0.0, 0.0, 2], np.float32), 4, 0, 2, 0, True, 0)
+    assert list(np.flatnonzero(cat0 == 2)) == [0, 3]
+    _, _, cat1 = O.evict_select(np.array([1, -0.0, 0.0, 2, -1], np.float32), 5, 0, 3, 0, True, 0)
+    assert list(np.flatnonzero(cat1 == 2)) == [0, 1, 3]  # -0 == +0: the lower position
+
+
+def test_evict_select_branches_and_padding():
+    """No scores: fallback keeps the positions before the local window, and
+    bridges fall back to the middle third of the rest; scores shorter than
+    the cache are zero-padded, longer ones truncated; a NaN among the
+    remaining scores makes the median NaN (every distance NaN: bridges in
+    position order); H2O-style calls (no fallback) keep nothing without
+    scores."""
+    keep, cnt, cat = O.evict_select(None, 30, 5, 7, 6, True, 1)
+    assert cnt == (5, 7, 6)
+    assert list(np.flatnonzero(cat == 2)) == list(range(18, 25))
+    assert list(np.flatnonzero(cat == 3)) == list(range(6, 12))  # 18 free: ranks 6..11
+    _, cnt, _ = O.evict_select(None, 30, 5, 7, 0, False, 0)
+    assert cnt == (5, 0, 0)
+    s = np.array([5, 1, 9], np.float32)
+    _, _, cat = O.evict_select(s, 6, 0, 4, 0, True, 0)
+    assert list(np.flatnonzero(cat == 2)) == [0, 1, 2, 3]  # 9, 5, 1, then the first padded 0
+    _, _, cat = O.evict_select(np.arange(10, dtype=np.float32), 4, 0, 2, 0, True, 0)
+    assert list(np.flatnonzero(cat == 2)) == [2, 3]
+    s = np.array([0, 1, 2, np.nan, 4, 5, 6, 7], np.float32)
+    _, cnt, cat = O.evict_select(s, 8, 2, 0, 3, True, 1)
+    assert list(np.flatnonzero(cat == 3)) == [0, 1, 2]
+    s = np.array([0, 10, 20, 30, 40, 50, 60, 70, 80], np.float32)
+    _, cnt, cat = O.evict_select(s, 9, 0, 0, 2, True, 1)  # lower median 40: nearest 40, then 30
+    assert list(np.flatnonzero(cat == 3)) == [3, 4]
+
+
+def test_evict_connectivity_and_gather():
+    rng = np.random.default_rng(2)
+    a = rng.random((9, 9))
+    cat = np.array([0, 2, 0, 2, 1, 0, 2, 0, 3], np.uint8)
+    imp = [1, 3, 6]
+    want = a[imp, :].sum(0) * a[:, imp].sum(1)
+    np.testing.assert_allclose(O.evict_connectivity(a, cat), want, rtol=1e-15)
+    x = rng.standard_normal((2, 3, 7, 4)).astype(np.float32)
+    assert np.array_equal(O.kv_gather(x, np.arange(7)), x)
+    assert np.array_equal(O.kv_gather(x, np.arange(6, -1, -1)), x[:, :, ::-1])
+    g = O.kv_gather(x, np.array([1, 9, -1, 0]))
+    assert np.array_equal(g[:, :, 0], x[:, :, 1]) and np.all(g[:, :, 1:3] == 0)
+
+
+def test_evict_select_positional_bridges_are_a_truncated_slice():
+    """The positional branch is remaining[len // 3 : len // 3 + budget]
+    (policy.py:167-172): a budget above len - len // 3 keeps fewer bridges."""
+    keep, cnt, cat = O.evict_select(None, 100, 5, 33, 100, True, 3)
+    assert cnt == (5, 33, 62 - 62 // 3)
+    assert list(np.flatnonzero(cat == 3)) == list(range(20, 62))
+    assert keep.size == 5 + 33 + 42
