@@ -226,9 +226,57 @@ def eviction_path(args, dev, D):
         "total_ms": round(fwd_ms + sc_ms, 4),
     }
     log(f"eviction path: attention {fwd_ms:.3f} ms, key scores {sc_ms:.3f} ms")
+    result_evict.update(eviction_prune(args, dev, sce.sum(dim=(0, 1)), ke))
     del qe, ke, ve, oute, lsee, sce
     torch.cuda.empty_cache()
     return result_evict
+
+
+def eviction_prune(args, dev, importance, k_layer):
+    """Position selection (cab_evict_select: local 30% / importance 50% /
+    median bridges 20% of a keep budget of 20%) on the key totals of the
+    dense pass, at N = 16384 and at the largest cache (2^20 positions), then
+    the one-launch prune of 32 layers' K and V ([1, 8, 16384, 128] bf16) to
+    the kept positions (cab_kv_gather), priced as HBM bytes moved."""
+    import torch
+    from cab_attention.eviction._select import BRIDGE_MEDIAN, select_positions
+    from cab_attention.cache.prune import gather_positions
+    iters = max(5, args.steps)
+
+    def budgets(n):
+        keep = n // 5
+        local, bridge = int(keep * 0.3), int(keep * 0.2)
+        return local, keep - local - bridge, bridge
+
+    n = importance.numel()
+    sel = lambda sc, m: select_positions(m, sc, *budgets(m), False, BRIDGE_MEDIAN, dev)
+    keep, cnt, _, _ = sel(importance, n)
+    sel_ms = time_events(lambda: sel(importance, n), iters)
+    big = 1 << 20
+    big_scores = seeded_gpu((big,), 17, torch.float32, dev)
+    sel(big_scores, big)
+    sel_big_ms = time_events(lambda: sel(big_scores, big), iters)
+    layers = 32
+    tensors = [k_layer + i for i in range(2 * layers)]  # distinct K / V buffers
+    gather_positions(tensors, keep)
+    g_ms = time_events(lambda: gather_positions(tensors, keep), iters)
+    B, H, _, D = k_layer.shape
+    moved = 2 * len(tensors) * B * H * keep.numel() * D * k_layer.element_size()
+    gbs = moved / (g_ms * 1e-3) / 1e9
+    log(f"eviction prune: select {sel_ms * 1e3:.1f} us (N={n}), {sel_big_ms * 1e3:.1f} us "
+        f"(N={big}); gather {g_ms * 1e3:.1f} us = {gbs:.0f} GB/s")
+    del tensors, big_scores
+    return {
+        "select_config": f"cab_evict_select: keep {keep.numel()} of {n} (local/importance/"
+                         f"bridge = {cnt}), median bridges, fp32 scores",
+        "select_us": round(sel_ms * 1e3, 2),
+        "select_us_at_2e20_positions": round(sel_big_ms * 1e3, 2),
+        "gather_config": f"cab_kv_gather: {2 * layers} tensors [{B}, {H}, {n}, {D}] bf16 -> "
+                         f"{keep.numel()} positions",
+        "gather_us": round(g_ms * 1e3, 2),
+        "gather_GBs": round(gbs, 1),
+        "gather_frac_hbm": round(gbs / 8000.0, 4),
+    }
 
 
 def main() -> int:

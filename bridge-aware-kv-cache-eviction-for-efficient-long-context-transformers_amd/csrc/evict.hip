@@ -2,9 +2,10 @@
 // matrix bridge scores (cab_evict_connectivity) and the multi-layer K/V
 // gather that prunes a cache to the kept positions (cab_kv_gather).
 //
-// evict_select_kernel: one workgroup of 1024 threads per call. The kept set
-// lives in an LDS bitmap (one bit per cache position, up to 2^20 positions).
-// Each component is a k-smallest selection over the positions not yet kept:
+// evict_select_kernel: one workgroup of 1024 threads (16 waves) per call. The
+// kept set lives in an LDS bitmap (one bit per cache position, up to 2^20
+// positions). Each component is a k-smallest selection over the positions
+// not yet kept:
 //   local window:  the last `local` positions;
 //   importance:    the highest scores (position > score: the lower position
 //                  wins a tie; NaN ranks above +inf, -0 equals +0);
@@ -12,13 +13,19 @@
 //                  lower median of the remaining scores, the highest given
 //                  bridge scores, or the middle third of the remaining
 //                  positions in order.
-// A selection is a 4-pass radix select over order-preserving uint32 keys
-// (8 bits per pass, a 256-bin LDS histogram, coalesced reads of the scores),
-// then a marking pass: every key below the threshold, and the keys equal to
-// it in position order (thread-contiguous chunks and a block-wide prefix
-// scan) until the count is met. The kept positions are written in ascending
-// order by a last scan over the bitmap. Work: a few passes over 4 bytes per
-// position, L2-resident.
+// Every pass over the positions gives wave w the contiguous segment
+// [w * seg, (w + 1) * seg) (seg a multiple of 256) and walks it 256
+// positions per step, lane l on positions 4l..4l+3 (one 16-byte load, four
+// steps in flight). Ranks in position order come from ballots: a lane's
+// offset is the mbcnt of the ballots of its count's bits, a wave's offset
+// the sum of the earlier waves' totals.
+// A selection is a radix select over order-preserving uint32 keys in three
+// passes of 11, 11 and 10 bits (a 2048-bin LDS histogram; the lanes of a
+// wave that share a bin add once), then a marking pass: every key below the
+// threshold, and the keys equal to it in position order until the count is
+// met (one more pass only when some but not all of them are taken). The
+// kept positions are written in ascending order from the bitmap. Work: four
+// to five passes over 4 bytes per position and selection, L2-resident.
 //
 // kv_gather_kernel: out[t] = in[keep[t]] for the rows of up to 32 tensors
 // per launch (every layer's K and V), 16 bytes per thread; HBM-bound.
@@ -28,9 +35,12 @@ namespace cab {
 namespace {
 
 constexpr int SEL_THREADS = 1024;
+constexpr int SEL_WAVES = SEL_THREADS / 64;
 constexpr int SEL_MAX_LEN = 1 << 20;  // cache positions (the LDS bitmap: 128 KB)
+constexpr int SEL_BINS = 2048;        // radix histogram (11 bits)
+constexpr uint32_t NAN_KEY = 0xffc00000u;
 
-// Ascending float order as uint32: -0 == +0, NaN above +inf.
+// Ascending float order as uint32: -0 == +0, NaN (any) above +inf.
 __device__ __forceinline__ uint32_t asc_key(float f) {
   uint32_t u = __float_as_uint(f);
   if (f == 0.f) u = 0u;
@@ -56,113 +66,307 @@ struct SelArgs {
 
 struct SelShared {
   uint32_t bits[SEL_MAX_LEN / 32];
-  uint32_t hist[256];
-  int32_t scan[SEL_THREADS];
+  uint32_t hist[SEL_BINS];
+  int32_t wave_tot[SEL_WAVES];
   int32_t misc[4];
 };
 
-// Exclusive prefix sum of v over the workgroup; *total gets the sum.
-__device__ int block_scan(int v, SelShared& sh, int* total) {
-  const int t = threadIdx.x;
-  sh.scan[t] = v;
-  __syncthreads();
-  for (int off = 1; off < SEL_THREADS; off <<= 1) {
-    const int x = t >= off ? sh.scan[t - off] : 0;
-    __syncthreads();
-    sh.scan[t] += x;
-    __syncthreads();
+// Keys of the positions: KEY_DESC ~asc(x) (highest first), KEY_DIST
+// asc(|x - med|), KEY_ASC asc(x), KEY_NONE no scores read (positional).
+enum { KEY_DESC = 0, KEY_DIST = 1, KEY_ASC = 2, KEY_NONE = 3 };
+
+struct KeySrc {
+  const float* p;  // scores; positions >= n_valid read as 0
+  int n_valid;
+  float med;
+};
+
+template <int KIND>
+__device__ __forceinline__ uint32_t key_of(float x, float med) {
+  if (KIND == KEY_DESC) return ~asc_key(x);
+  if (KIND == KEY_DIST) return asc_key(fabsf(x - med));
+  return asc_key(x);
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// Set bits of m in the lanes below this one.
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
+}
+
+// Sum of v (0 <= v < 2^BITS) over the lanes below this one, and over the wave.
+template <int BITS>
+__device__ __forceinline__ void lane_offsets(int v, int* below, int* total) {
+  int b = 0, t = 0;
+#pragma unroll
+  for (int i = 0; i < BITS; ++i) {
+    const uint64_t m = __ballot((v >> i) & 1);
+    b += lanes_below(m) << i;
+    t += __popcll(m) << i;
   }
-  const int incl = sh.scan[t];
-  *total = sh.scan[SEL_THREADS - 1];
+  *below = b;
+  *total = t;
+}
+
+// hist[bin] += 1 for the active lanes; lanes sharing the wave's commonest
+// bins add once (same-address LDS atomics serialise).
+__device__ __forceinline__ void hist_add(uint32_t* hist, bool act, uint32_t bin) {
+  uint64_t todo = __ballot(act);
+  for (int it = 0; it < 2 && todo; ++it) {
+    const int leader = __builtin_ctzll(todo);
+    const uint32_t lb = __builtin_amdgcn_readlane(bin, leader);
+    const uint64_t peers = __ballot(act && bin == lb) & todo;
+    if (lane_id() == leader) atomicAdd(&hist[lb], static_cast<uint32_t>(__popcll(peers)));
+    todo &= ~peers;
+  }
+  if ((todo >> lane_id()) & 1ull) atomicAdd(&hist[bin], 1u);
+}
+
+// This wave's segment of [0, n), in positions (multiples of 256).
+__device__ __forceinline__ void wave_segment(int n, int* beg, int* end) {
+  const int seg = ((n + SEL_WAVES - 1) / SEL_WAVES + 255) & ~255;
+  const int w = threadIdx.x >> 6;
+  *beg = w * seg < n ? w * seg : n;
+  *end = *beg + seg < n ? *beg + seg : n;
+}
+
+// Exclusive prefix of the waves' totals for this wave, and the grand total.
+__device__ __forceinline__ int wave_start(SelShared& sh, int mine, int* total) {
+  if (lane_id() == 0) sh.wave_tot[threadIdx.x >> 6] = mine;
   __syncthreads();
-  return incl - v;
+  int s = 0, t = 0;
+  for (int w = 0; w < SEL_WAVES; ++w) {
+    const int v = sh.wave_tot[w];
+    if (w < static_cast<int>(threadIdx.x >> 6)) s += v;
+    t += v;
+  }
+  __syncthreads();
+  *total = t;
+  return s;
 }
 
-__device__ __forceinline__ bool kept(const SelShared& sh, int i) {
-  return (sh.bits[i >> 5] >> (i & 31)) & 1u;
+__device__ __forceinline__ float4 load4(const KeySrc s, int p, int end) {
+  if (p + 3 < s.n_valid && (reinterpret_cast<uintptr_t>(s.p) & 15u) == 0)
+    return *reinterpret_cast<const float4*>(s.p + p);
+  float x[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) x[e] = (p + e < end && p + e < s.n_valid) ? s.p[p + e] : 0.f;
+  return make_float4(x[0], x[1], x[2], x[3]);
 }
 
-// Positions in thread-contiguous chunks (for position-ordered passes).
-__device__ __forceinline__ void my_chunk(int n, int* lo, int* hi) {
-  const int c = (n + SEL_THREADS - 1) / SEL_THREADS;
-  *lo = threadIdx.x * c < n ? threadIdx.x * c : n;
-  *hi = *lo + c < n ? *lo + c : n;
-}
-
-// Keeps the `need` candidates (positions not yet kept) with the smallest
-// keys; equal keys go to the lower position. 1 <= need <= #candidates.
-template <class Key>
-__device__ void select_smallest(int n, int need, Key key, SelShared& sh, uint8_t* category,
-                                uint8_t cat) {
-  uint32_t prefix = 0, mask = 0;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    if (threadIdx.x < 256) sh.hist[threadIdx.x] = 0u;
-    __syncthreads();
-    for (int i = threadIdx.x; i < n; i += SEL_THREADS) {
-      if (kept(sh, i)) continue;
-      const uint32_t k = key(i);
-      if ((k & mask) == prefix) atomicAdd(&sh.hist[(k >> shift) & 255u], 1u);
+// Walks this wave's segment in position order, 256 positions per step with
+// the next four steps' loads in flight: f(p, cand, key) per step, called by
+// every lane of the wave (ballots inside are wave-wide). cand bit e =
+// position p + e exists and is not kept. The loop stays rolled: one
+// workgroup runs this code, so its size matters more than loop overhead.
+template <int KIND, class F>
+__device__ __forceinline__ void walk(int n, const SelShared& sh, const KeySrc s, F f) {
+  int beg, end;
+  wave_segment(n, &beg, &end);
+  const int lane4 = 4 * lane_id();
+  const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 x1 = zero, x2 = zero, x3 = zero, x4 = zero;
+  if (KIND != KEY_NONE) {
+    if (beg + lane4 < end) x1 = load4(s, beg + lane4, end);
+    if (beg + 256 + lane4 < end) x2 = load4(s, beg + 256 + lane4, end);
+    if (beg + 512 + lane4 < end) x3 = load4(s, beg + 512 + lane4, end);
+    if (beg + 768 + lane4 < end) x4 = load4(s, beg + 768 + lane4, end);
+  }
+#pragma unroll 1
+  for (int base = beg; base < end; base += 256) {
+    const int p = base + lane4;
+    const float4 x = x1;
+    x1 = x2;
+    x2 = x3;
+    x3 = x4;
+    if (KIND != KEY_NONE && p + 1024 < end) x4 = load4(s, p + 1024, end);
+    uint32_t cand = 0u;
+    if (p < end) {
+      cand = ~(sh.bits[p >> 5] >> (p & 31)) & 0xfu;
+      if (end - p < 4) cand &= (1u << (end - p)) - 1u;
     }
+    u32x4 k = {0u, 0u, 0u, 0u};
+    if (KIND != KEY_NONE) {
+      k[0] = key_of<KIND>(x.x, s.med);
+      k[1] = key_of<KIND>(x.y, s.med);
+      k[2] = key_of<KIND>(x.z, s.med);
+      k[3] = key_of<KIND>(x.w, s.med);
+    }
+    f(p, cand, k);
+  }
+}
+
+__device__ __forceinline__ void mark(SelShared& sh, int p, uint32_t m, uint8_t* category,
+                                     uint8_t cat) {
+  if (!m) return;
+  atomicOr(&sh.bits[p >> 5], m << (p & 31));
+  if (category)
+    for (int e = 0; e < 4; ++e)
+      if ((m >> e) & 1u) category[p + e] = cat;
+}
+
+// Inclusive prefix sum of v over the lanes of the wave.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(v, off);
+    if (lane >= off) v += y;
+  }
+  return v;
+}
+
+struct Threshold {
+  uint32_t key;  // the need-th smallest candidate key
+  int need_eq;   // how many candidates with this key complete the selection
+  int eq;        // candidates with this key
+  int nan;       // candidates with a NaN score (KEY_ASC only)
+};
+
+// Radix select of the need-th smallest candidate key, 1 <= need <= #candidates.
+template <int KIND>
+__device__ __forceinline__ Threshold radix_select(int n, int need, const KeySrc s, SelShared& sh) {
+  uint32_t prefix = 0u, mask = 0u;
+  Threshold th = {0u, 0, 0, 0};
+  if (threadIdx.x == 0) sh.misc[3] = 0;
+  for (int pass = 0; pass < 3; ++pass) {
+    const int shift = pass == 0 ? 21 : pass == 1 ? 10 : 0;  // bits 31..21, 20..10, 9..0
+    const int nb = pass == 2 ? 1024 : 2048;
+    for (int b = threadIdx.x; b < nb; b += SEL_THREADS) sh.hist[b] = 0u;
     __syncthreads();
-    if (threadIdx.x == 0) {
-      int run = 0, bin = 0;
-      for (; bin < 255; ++bin) {
-        if (run + static_cast<int>(sh.hist[bin]) >= need) break;
-        run += static_cast<int>(sh.hist[bin]);
+    walk<KIND>(n, sh, s, [&](int, uint32_t cand, u32x4 k) {
+      int nan = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool act = ((cand >> e) & 1u) && (k[e] & mask) == prefix;
+        hist_add(sh.hist, act, (k[e] >> shift) & static_cast<uint32_t>(nb - 1));
+        if (KIND == KEY_ASC && pass == 0) nan += (act && k[e] == NAN_KEY) ? 1 : 0;
       }
-      sh.misc[0] = bin;
-      sh.misc[1] = run;
+      if (KIND == KEY_ASC && pass == 0 && nan) atomicAdd(&sh.misc[3], nan);
+    });
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      // wave 0: lane l sums bins [l * per, (l + 1) * per); the first lane
+      // whose inclusive sum reaches need owns the threshold bin, which a
+      // second scan over the owner's bins (one per lane) finds
+      const int per = nb / 64, lane = threadIdx.x;
+      int sum = 0;
+      for (int b = 0; b < per; ++b) sum += static_cast<int>(sh.hist[lane * per + b]);
+      const int incl = wave_incl_scan(sum);
+      const uint64_t hit = __ballot(incl >= need);
+      const int owner = hit ? __builtin_ctzll(hit) : 63;
+      const int run0 = __builtin_amdgcn_readlane(incl - sum, owner);
+      const int h = lane < per ? static_cast<int>(sh.hist[owner * per + lane]) : 0;
+      const int incl2 = run0 + wave_incl_scan(h);
+      const uint64_t hit2 = __ballot(lane < per && incl2 >= need);
+      const int j = hit2 ? __builtin_ctzll(hit2) : per - 1;
+      if (lane == j) {
+        sh.misc[0] = owner * per + j;
+        sh.misc[1] = incl2 - h;
+        sh.misc[2] = h;
+      }
     }
     __syncthreads();
     prefix |= static_cast<uint32_t>(sh.misc[0]) << shift;
-    mask |= 255u << shift;
+    mask |= static_cast<uint32_t>(nb - 1) << shift;
     need -= sh.misc[1];
+    th.eq = sh.misc[2];
+    th.nan = sh.misc[3];
     __syncthreads();
   }
-  // need = how many keys equal to the threshold complete the selection.
-  int lo, hi;
-  my_chunk(n, &lo, &hi);
-  int eq = 0;
-  for (int i = lo; i < hi; ++i)
-    if (!kept(sh, i) && key(i) == prefix) ++eq;
-  int total;
-  int take = need - block_scan(eq, sh, &total);
-  // Every thread has counted before any bit of this selection is set.
-  for (int i = lo; i < hi; ++i) {
-    if (kept(sh, i)) continue;
-    const uint32_t k = key(i);
-    bool sel = k < prefix;
-    if (!sel && k == prefix && take > 0) {
-      sel = true;
-      --take;
+  th.key = prefix;
+  th.need_eq = need;
+  return th;
+}
+
+// Sum of v over the wave (every lane gets it).
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// Marks, in position order, the candidates with q set (the 4-bit masks a
+// walk produces) whose rank among them lies in [first, first + count);
+// `start` is the number of such candidates in the earlier waves' segments.
+template <int KIND, class Q>
+__device__ __forceinline__ void mark_ranked(int n, const KeySrc s, SelShared& sh, int start, int first, int count,
+                            Q q_of, uint8_t* category, uint8_t cat) {
+  int carry = start;
+  walk<KIND>(n, sh, s, [&](int p, uint32_t cand, u32x4 k) {
+    const uint32_t q = q_of(cand, k);
+    int below, tot;
+    lane_offsets<3>(__popc(q), &below, &tot);
+    if (carry < first + count && carry + tot > first) {
+      uint32_t m = 0u;
+      int r = carry + below;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (!((q >> e) & 1u)) continue;
+        if (r >= first && r < first + count) m |= 1u << e;
+        ++r;
+      }
+      mark(sh, p, m, category, cat);
     }
-    if (sel) {
-      atomicOr(&sh.bits[i >> 5], 1u << (i & 31));
-      if (category) category[i] = cat;
-    }
-  }
+    carry += tot;
+  });
   __syncthreads();
 }
 
-// Keeps the not-yet-kept positions of rank [first, first + count) among them,
-// in position order.
-__device__ void select_ranks(int n, int first, int count, SelShared& sh, uint8_t* category,
-                             uint8_t cat) {
-  int lo, hi;
-  my_chunk(n, &lo, &hi);
-  int c = 0;
-  for (int i = lo; i < hi; ++i) c += kept(sh, i) ? 0 : 1;
-  int total;
-  int r = block_scan(c, sh, &total);
-  for (int i = lo; i < hi; ++i) {
-    if (kept(sh, i)) continue;
-    if (r >= first && r < first + count) {
-      atomicOr(&sh.bits[i >> 5], 1u << (i & 31));
-      if (category) category[i] = cat;
+// Keeps the `need` candidates with the smallest keys; equal keys go to the
+// lower position. 1 <= need <= #candidates.
+template <int KIND>
+__device__ __forceinline__ void select_smallest(int n, int need, const KeySrc s, SelShared& sh,
+                                uint8_t* category, uint8_t cat) {
+  const Threshold th = radix_select<KIND>(n, need, s, sh);
+  const bool all_eq = th.need_eq == th.eq;
+  int eq_mine = 0;
+  walk<KIND>(n, sh, s, [&](int p, uint32_t cand, u32x4 k) {
+    uint32_t m = 0u, q = 0u;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (!((cand >> e) & 1u)) continue;
+      if (k[e] < th.key) m |= 1u << e;
+      if (k[e] == th.key) q |= 1u << e;
     }
-    ++r;
+    if (all_eq)
+      m |= q;
+    else
+      eq_mine += __popc(q);
+    mark(sh, p, m, category, cat);
+  });
+  if (all_eq) {
+    __syncthreads();
+    return;
   }
-  __syncthreads();
+  // Ties: the first need_eq equal keys in position order. The walk above
+  // marked only keys below the threshold, so the equal keys are still
+  // candidates.
+  int total;
+  const int start = wave_start(sh, wave_sum(eq_mine), &total);
+  const uint32_t key = th.key;
+  mark_ranked<KIND>(n, s, sh, start, 0, th.need_eq, [key](uint32_t cand, u32x4 k) {
+    uint32_t q = 0u;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (((cand >> e) & 1u) && k[e] == key) q |= 1u << e;
+    return q;
+  }, category, cat);
+}
+
+// Keeps the candidates of rank [first, first + count) among them, in
+// position order.
+__device__ __forceinline__ void select_ranks(int n, int first, int count, SelShared& sh, uint8_t* category,
+                             uint8_t cat) {
+  const KeySrc none = {nullptr, 0, 0.f};
+  int mine = 0;
+  walk<KEY_NONE>(n, sh, none, [&](int, uint32_t cand, u32x4) { mine += __popc(cand); });
+  int total;
+  const int start = wave_start(sh, wave_sum(mine), &total);
+  mark_ranked<KEY_NONE>(n, none, sh, start, first, count,
+                        [](uint32_t cand, u32x4) { return cand; }, category, cat);
 }
 
 __global__ __launch_bounds__(SEL_THREADS) void evict_select_kernel(SelArgs a) {
@@ -171,29 +375,25 @@ __global__ __launch_bounds__(SEL_THREADS) void evict_select_kernel(SelArgs a) {
   const int words = (n + 31) >> 5;
   const int l0 = n - a.local;  // first local position
   for (int w = tid; w < words; w += SEL_THREADS) {
-    // local window bits, positions >= l0 (and < n)
-    uint32_t m = 0u;
+    // local window bits: positions in [l0, n)
     const int b0 = w * 32;
-    if (b0 + 32 <= l0) {
-      m = 0u;
-    } else {
+    uint32_t m = 0u;
+    if (b0 + 32 > l0)
       for (int j = 0; j < 32; ++j)
         if (b0 + j >= l0 && b0 + j < n) m |= 1u << j;
-    }
     sh.bits[w] = m;
   }
   if (a.category)
     for (int i = l0 + tid; i < n; i += SEL_THREADS) a.category[i] = 1;
   __syncthreads();
-  auto score = [&](int i) -> float { return i < a.n_scores ? a.scores[i] : 0.f; };
+  const KeySrc imp_src = {a.scores, a.n_scores, 0.f};
   const int free0 = n - a.local;  // positions not in the local window
 
   // importance
   int n_imp = 0;
   if (a.scores) {
     n_imp = a.imp < free0 ? a.imp : free0;
-    if (n_imp > 0)
-      select_smallest(n, n_imp, [&](int i) { return ~asc_key(score(i)); }, sh, a.category, 2);
+    if (n_imp > 0) select_smallest<KEY_DESC>(n, n_imp, imp_src, sh, a.category, 2);
   } else if (a.imp_fallback && a.imp > 0) {
     const int s0 = n - a.local - a.imp > 0 ? n - a.local - a.imp : 0;
     n_imp = l0 - s0;
@@ -213,50 +413,15 @@ __global__ __launch_bounds__(SEL_THREADS) void evict_select_kernel(SelArgs a) {
   if (a.bridge_budget > 0 && free1 > 0 && mode != 0) {
     n_br = a.bridge_budget < free1 ? a.bridge_budget : free1;
     if (mode == 1) {
-      // lower median of the remaining scores (NaN if any of them is NaN)
-      if (tid == 0) sh.misc[2] = 0;
-      __syncthreads();
-      for (int i = tid; i < n; i += SEL_THREADS)
-        if (!kept(sh, i) && isnan(score(i))) sh.misc[2] = 1;
-      __syncthreads();
-      const bool has_nan = sh.misc[2] != 0;
-      __syncthreads();
-      float med = __uint_as_float(0x7fc00000u);
-      if (!has_nan) {
-        // the ((free1 - 1) / 2 + 1)-th smallest remaining score: a radix
-        // select that marks nothing (its result is read back below)
-        uint32_t prefix = 0, mask = 0;
-        int need = (free1 - 1) / 2 + 1;
-        for (int shift = 24; shift >= 0; shift -= 8) {
-          if (tid < 256) sh.hist[tid] = 0u;
-          __syncthreads();
-          for (int i = tid; i < n; i += SEL_THREADS) {
-            if (kept(sh, i)) continue;
-            const uint32_t k = asc_key(score(i));
-            if ((k & mask) == prefix) atomicAdd(&sh.hist[(k >> shift) & 255u], 1u);
-          }
-          __syncthreads();
-          if (tid == 0) {
-            int run = 0, bin = 0;
-            for (; bin < 255; ++bin) {
-              if (run + static_cast<int>(sh.hist[bin]) >= need) break;
-              run += static_cast<int>(sh.hist[bin]);
-            }
-            sh.misc[0] = bin;
-            sh.misc[1] = run;
-          }
-          __syncthreads();
-          prefix |= static_cast<uint32_t>(sh.misc[0]) << shift;
-          mask |= 255u << shift;
-          need -= sh.misc[1];
-          __syncthreads();
-        }
-        med = key_float(prefix);
-      }
-      select_smallest(n, n_br, [&](int i) { return asc_key(fabsf(score(i) - med)); }, sh,
-                      a.category, 3);
+      // lower median of the remaining scores (NaN if any of them is NaN):
+      // the ((free1 - 1) / 2 + 1)-th smallest
+      const Threshold th = radix_select<KEY_ASC>(n, (free1 - 1) / 2 + 1, imp_src, sh);
+      const float med = th.nan ? __uint_as_float(0x7fc00000u) : key_float(th.key);
+      const KeySrc dist = {a.scores, a.n_scores, med};
+      select_smallest<KEY_DIST>(n, n_br, dist, sh, a.category, 3);
     } else if (mode == 2) {
-      select_smallest(n, n_br, [&](int i) { return ~asc_key(a.bridge[i]); }, sh, a.category, 3);
+      const KeySrc given = {a.bridge, n, 0.f};
+      select_smallest<KEY_DESC>(n, n_br, given, sh, a.category, 3);
     } else {
       // remaining[free1 / 3 : free1 / 3 + budget], cut at the end
       if (n_br > free1 - free1 / 3) n_br = free1 - free1 / 3;
@@ -264,18 +429,32 @@ __global__ __launch_bounds__(SEL_THREADS) void evict_select_kernel(SelArgs a) {
     }
   }
 
-  // kept positions, ascending
-  int lo, hi;
-  my_chunk(n, &lo, &hi);
-  int c = 0;
-  for (int i = lo; i < hi; ++i) c += kept(sh, i) ? 1 : 0;
+  // kept positions, ascending: wave segments of whole words, one word per
+  // lane and step, ranks from the ballots of the popcounts' bits
+  const int wseg = ((words + SEL_WAVES - 1) / SEL_WAVES + 63) & ~63;
+  const int wb = (tid >> 6) * wseg < words ? (tid >> 6) * wseg : words;
+  const int we = wb + wseg < words ? wb + wseg : words;
+  const int lane = lane_id();
+  int mine = 0;
+  for (int w0 = wb; w0 < we; w0 += 64) {
+    const int w = w0 + lane;
+    mine += w < we ? __popc(sh.bits[w]) : 0;
+  }
   int total;
-  int pos = block_scan(c, sh, &total);
-  for (int i = lo; i < hi; ++i) {
-    if (kept(sh, i))
-      a.keep[pos++] = i;
-    else if (a.category)
-      a.category[i] = 0;
+  int pos = wave_start(sh, wave_sum(mine), &total);
+  for (int w0 = wb; w0 < we; w0 += 64) {
+    const int w = w0 + lane;
+    const uint32_t bits = w < we ? sh.bits[w] : 0u;
+    int below, tot;
+    lane_offsets<6>(__popc(bits), &below, &tot);
+    int64_t* out = a.keep + pos + below;
+    for (uint32_t m = bits; m; m &= m - 1) *out++ = w * 32 + __builtin_ctz(m);
+    if (a.category && w < we) {
+      const int hi = w * 32 + 32 < n ? w * 32 + 32 : n;
+      for (int i = w * 32; i < hi; ++i)
+        if (!((bits >> (i & 31)) & 1u)) a.category[i] = 0;
+    }
+    pos += tot;
   }
   if (tid == 0) {
     a.counts[0] = a.local;
