@@ -1,5 +1,5 @@
 """CAB KV cache: three-component eviction (reference:
-``cab_attention/cache/cab_cache.py`` :20-270). Same configuration, update /
+``cab_attention/cache/cab_cache.py`` :20-267). Same configuration, update /
 evict control flow and statistics; the selection runs in ``cab_evict_select``
 and the pruning of every layer in ``cab_kv_gather``."""
 

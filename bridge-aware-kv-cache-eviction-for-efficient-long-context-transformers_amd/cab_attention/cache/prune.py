@@ -1,6 +1,6 @@
 """One-launch pruning of every layer's K and V to the kept positions
 (``cab_kv_gather``), replacing the reference caches' per-layer
-``cache[:, :, keep_indices, :]`` (cab_cache.py:204-208, h2o_cache.py:140-144)."""
+``cache[:, :, keep_indices, :]`` (cab_cache.py:207-210, h2o_cache.py:146-149)."""
 
 from __future__ import annotations
 

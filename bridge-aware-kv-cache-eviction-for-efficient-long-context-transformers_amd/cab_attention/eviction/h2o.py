@@ -1,7 +1,7 @@
 """H2O (heavy-hitter) selection: local window + highest cumulative attention.
 
 Same function, arguments and return values as the reference's
-``cab_attention/eviction/h2o.py`` (:15-94); the selection runs in the HIP
+``cab_attention/eviction/h2o.py`` (:16-94); the selection runs in the HIP
 kernel ``cab_evict_select`` (ties to the lower position, NaN above +inf).
 """
 

@@ -2,7 +2,7 @@
 cumulative attention) and bridges.
 
 Same classes, arguments and return values as the reference's
-``cab_attention/eviction/policy.py`` (:16-200); the selection runs in one
+``cab_attention/eviction/policy.py`` (:17-225); the selection runs in one
 HIP kernel (``cab_evict_select``). Decisions where the reference leaves the
 result to ``torch.topk``'s unspecified tie order: equal scores go to the
 lower position, NaN ranks above +inf, and a position already kept is never
@@ -22,7 +22,7 @@ from ._select import (BRIDGE_MEDIAN, BRIDGE_NONE, BRIDGE_POSITIONAL, BRIDGE_SCOR
 
 @dataclass
 class EvictionConfig:
-    """Budget split of the kept positions (policy.py:16-27)."""
+    """Budget split of the kept positions (policy.py:17-27)."""
     local_ratio: float = 0.3
     bridge_ratio: float = 0.2
     importance_ratio: float = 0.5
@@ -35,7 +35,7 @@ class EvictionConfig:
 
 class ThreeComponentEvictionPolicy:
     """Keeps the local window, the most attended positions, and bridge
-    positions (policy.py:30-200)."""
+    positions (policy.py:29-225)."""
 
     def __init__(self, config: EvictionConfig):
         self.config = config

@@ -1,5 +1,5 @@
 """Cumulative-attention (H2O) importance tracking (reference:
-``cab_attention/scoring/importance.py`` :15-185). The running totals are
+``cab_attention/scoring/importance.py`` :17-133). The running totals are
 torch bookkeeping; the top-k runs in ``cab_evict_select``."""
 
 from __future__ import annotations

@@ -265,8 +265,8 @@ cab_status_t cab_attn_key_scores(const void* q, const void* k, const float* lse,
  * KV-cache eviction: which cache positions to keep, and the pruned cache.
  *
  * cab_evict_select replaces the selection of
- * ThreeComponentEvictionPolicy.select_indices (cab_attention/eviction/policy.py:39-200)
- * and h2o_select_indices (cab_attention/eviction/h2o.py:15-94), called by
+ * ThreeComponentEvictionPolicy.select_indices (cab_attention/eviction/policy.py:40-225)
+ * and h2o_select_indices (cab_attention/eviction/h2o.py:16-94), called by
  * CABCache._evict / H2OCache._evict (cache/cab_cache.py:177-226). Over
  * cache_len positions (<= 2^20), with score[i] = importance_scores[i] for
  * i < n_scores and 0 beyond (the reference's zero padding), it keeps:
@@ -296,7 +296,7 @@ cab_status_t cab_evict_select(const float* importance_scores, int64_t n_scores,
                               void* stream);
 
 /*
- * Bridge scores of the policy's attention-matrix mode (policy.py:118-138):
+ * Bridge scores of the policy's attention-matrix mode (policy.py:122-131):
  * with imp = {i : category[i] == 2} (cab_evict_select's output),
  * bridge_scores[j] = (sum_{i in imp} A[i, j]) * (sum_{i in imp} A[j, i]).
  * attention: fp32 [cache_len, cache_len], row stride row_stride (elements).
@@ -309,7 +309,7 @@ cab_status_t cab_evict_connectivity(const float* attention, int64_t cache_len, i
  * Prunes a cache: for each of n_tensors tensors (every layer's K and V),
  * dst[t][b, h, r, :] = src[t][b, h, keep_indices[r], :] for r < n_keep (rows
  * of row_bytes bytes; an index outside [0, n_src) gives a zero row).
- * Replaces the per-layer `cache[:, :, keep_indices, :]` of cab_cache.py:204-208
+ * Replaces the per-layer `cache[:, :, keep_indices, :]` of cab_cache.py:207-210
  * and h2o_cache.py with one launch per 32 tensors. src / dst: host arrays of
  * device pointers (16-byte aligned); strides in bytes {b, h, row}, multiples
  * of 16; keep_indices: int64 device array. dst must not overlap src.

@@ -38,7 +38,7 @@ Pinning of each function (tests/test_oracle.py):
   ``dense_masked_attention`` and with torch's float64 softmax / SDPA, and
   grouped K / V equal to repeated heads.
 - ``evict_select``: on tie-free scores, torch.topk / torch.median applied as
-  the reference policies do (policy.py:71-160, h2o.py:45-80); with ties and
+  the reference policies do (policy.py:96-170, h2o.py:71-77); with ties and
   NaN, the ordering invariants (every kept score ranks at or above every
   evicted candidate, equal scores kept in position order); the budget
   arithmetic; the positional and fallback branches.
@@ -462,17 +462,17 @@ def evict_select(scores, cache_len: int, local: int, imp: int, bridge: int,
     """The positions a KV cache keeps: local window, importance, bridges.
 
     Restates ThreeComponentEvictionPolicy.select_indices
-    (cab_attention/eviction/policy.py:39-200) and h2o_select_indices
-    (eviction/h2o.py:15-94) with cab_evict_select's tie rule (torch.topk's
+    (cab_attention/eviction/policy.py:40-225) and h2o_select_indices
+    (eviction/h2o.py:16-94) with cab_evict_select's tie rule (torch.topk's
     order is unspecified): among equal keys the lower position wins, NaN
     ranks above +inf, -0 equals +0, and a kept position is never chosen
-    again. ``scores`` is zero-padded / truncated to cache_len (policy.py:76-88).
+    again. ``scores`` is zero-padded / truncated to cache_len (policy.py:84-95, h2o.py:58-69).
     ``mode``: 0 no bridges, 1 nearest the lower median of the remaining
-    scores (NaN if one is NaN; policy.py:140-162), 2 highest bridge_scores
-    (policy.py:118-138; falls back to 1, or 3 without scores, when no
+    scores (NaN if one is NaN; policy.py:143-170), 2 highest bridge_scores
+    (policy.py:122-141; falls back to 1, or 3 without scores, when no
     importance position was kept), 3 the remaining positions of rank
-    [remaining // 3, +budget) (policy.py:164-174). ``fallback``: with no
-    scores, the ``imp`` positions before the local window (policy.py:104-108).
+    [remaining // 3, +budget) (policy.py:172-184). ``fallback``: with no
+    scores, the ``imp`` positions before the local window (policy.py:111-115).
 
     Returns (kept positions ascending int64, (local, importance, bridge)
     counts, category uint8: 0 evicted, 1 local, 2 importance, 3 bridge).
@@ -532,7 +532,7 @@ def evict_select(scores, cache_len: int, local: int, imp: int, bridge: int,
 
 
 def evict_connectivity(attention, category) -> np.ndarray:
-    """Bridge scores of the attention-matrix mode (policy.py:118-138):
+    """Bridge scores of the attention-matrix mode (policy.py:122-131):
     (sum over importance rows of A) * (sum over importance columns of A), in
     float64, with importance = category == 2."""
     a = np.asarray(attention, dtype=np.float64)
@@ -547,7 +547,7 @@ def evict_connectivity(attention, category) -> np.ndarray:
 
 def kv_gather(x, keep) -> np.ndarray:
     """``x[:, :, keep, :]`` with out-of-range positions giving zero rows
-    (cab_cache.py:204-208)."""
+    (cab_cache.py:207-210)."""
     x = np.asarray(x)
     keep = np.asarray(keep, dtype=np.int64)
     out = np.zeros(x.shape[:2] + (keep.size,) + x.shape[3:], x.dtype)

@@ -458,7 +458,7 @@ def test_dense_scores_grouped_heads_equal_repeated_heads():
 
 def _masked_topk(scores, exclude, k):
     """torch.topk over scores with the excluded positions at -inf, the way
-    the reference policies select (policy.py:91-102, h2o.py:70-80)."""
+    the reference policies select (policy.py:96-110, h2o.py:71-77)."""
     t = torch.from_numpy(np.asarray(scores, np.float32)).clone()
     t[torch.from_numpy(exclude)] = -float("inf")
     return set(torch.topk(t, k, largest=True).indices.tolist())
@@ -557,7 +557,7 @@ def test_evict_connectivity_and_gather():
 
 def test_evict_select_positional_bridges_are_a_truncated_slice():
     """The positional branch is remaining[len // 3 : len // 3 + budget]
-    (policy.py:167-172): a budget above len - len // 3 keeps fewer bridges."""
+    (policy.py:172-184): a budget above len - len // 3 keeps fewer bridges."""
     keep, cnt, cat = O.evict_select(None, 100, 5, 33, 100, True, 3)
     assert cnt == (5, 33, 62 - 62 // 3)
     assert list(np.flatnonzero(cat == 3)) == list(range(20, 62))
