@@ -14,7 +14,7 @@ import threading
 import torch
 
 LIB_PATH = pathlib.Path(__file__).resolve().with_name("libcab_hip.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 CAB_OK, CAB_EINVAL, CAB_EDTYPE, CAB_ESHAPE, CAB_EWORKSPACE, CAB_EHIP = range(6)
 CAB_F32, CAB_F16, CAB_BF16 = 0, 1, 2
@@ -65,6 +65,13 @@ SIGNATURES = {
     "cab_evict_connectivity": (ctypes.c_int, [_ptr, _i64, _i64, _ptr, _ptr, _ptr]),
     "cab_kv_gather": (ctypes.c_int, [ctypes.POINTER(_ptr), ctypes.POINTER(_ptr), _i32, _i64, _i64,
                                      _i64, _i64, _i64x4, _i64x4, _ptr, _i64, _ptr]),
+    "cab_token_frc": (ctypes.c_int, [_ptr, ctypes.c_int, _i64, _i64, _ptr, _ptr, _ptr, _ptr]),
+    "cab_attention_symmetrize": (ctypes.c_int, [_ptr, ctypes.c_int, _i64, _i64, _i64, _i64, _i64x4,
+                                                _ptr, _i64, _ptr]),
+    "cab_token_frc_keys_workspace_bytes": (ctypes.c_size_t, [_i64, _i64]),
+    "cab_token_frc_from_keys": (ctypes.c_int, [_ptr, ctypes.c_int, _i64, _i64, _i64, _i64, _i64x4,
+                                               _ptr, _ptr, _ptr, _ptr, _ptr, ctypes.c_size_t,
+                                               _ptr]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,512 @@
+// Token-level Forman-Ricci curvature (cab_token_frc, cab_token_frc_from_keys)
+// and the aggregated key-key attention matrix (cab_attention_symmetrize).
+//
+// For a weighted directed graph A [n, n]:
+//   S_i = sum_j A_ij                              (node strength)
+//   T_i = sum_j sum_k A_ij A_jk = sum_j A_ij S_j  (2-hop weight)
+//   F_i = 4 S_i - 2 S_i + 3 T_i                   (node weight taken = S)
+// T is A times the vector S, so the curvature is two HBM-bound passes over
+// A (token_row_kernel<PASS 0>: row sums; <PASS 1>: row dots with S).
+//
+// From cached keys [B, H, N, D]:
+//   x_n = mean_{b,h} keys[b,h,n,:],  kn_n = x_n / max(|x_n|, 1e-12),
+//   r_i = sum_j relu(kn_i . kn_j),   A_ij = relu(kn_i . kn_j) / (r_i + 1e-8).
+// A is never stored: S_i = r_i / (r_i + 1e-8) and
+// T_i = (sum_j relu(kn_i . kn_j) S_j) / (r_i + 1e-8). keys_prep_kernel
+// writes kn as bf16 hi/lo planes in MFMA operand order; gram_kernel<PASS>
+// computes 32x32 tiles of kn kn^T on MFMA (hi*hi + hi*lo + lo*hi, fp32
+// accumulate) and folds each tile into per-row sums of relu(g) * w_j
+// (w = 1, then w = S); gram_finalize_kernel adds the column-split partials
+// in a fixed order. Algorithmic work: 2 N^2 D flops per Gram pass.
+#include "cab_internal.h"
+
+namespace cab {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Matrix form
+// ---------------------------------------------------------------------------
+
+template <typename T>
+__device__ __forceinline__ float ld_elem(const T* p);
+template <>
+__device__ __forceinline__ float ld_elem<float>(const float* p) { return *p; }
+template <>
+__device__ __forceinline__ float ld_elem<bf16_t>(const bf16_t* p) { return bf16_to_f32(p->bits); }
+template <>
+__device__ __forceinline__ float ld_elem<f16_t>(const f16_t* p) { return f16_to_f32(p->bits); }
+
+// 16 bytes of elements as floats (4 fp32 or 8 16-bit values).
+template <typename T>
+__device__ __forceinline__ void ld_vec(const T* p, float* x) {
+  const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+  if constexpr (std::is_same<T, float>::value) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = __uint_as_float(v[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t lo = static_cast<uint16_t>(v[e] & 0xffffu), hi = static_cast<uint16_t>(v[e] >> 16);
+      if constexpr (std::is_same<T, bf16_t>::value) {
+        x[2 * e] = bf16_to_f32(lo);
+        x[2 * e + 1] = bf16_to_f32(hi);
+      } else {
+        x[2 * e] = f16_to_f32(lo);
+        x[2 * e + 1] = f16_to_f32(hi);
+      }
+    }
+  }
+}
+
+struct RowArgs {
+  const void* a;
+  int64_t n, lda;  // elements
+  float* s;        // strengths: written by pass 0, read by pass 1
+  float* t;        // triangles (pass 1) or null
+  float* f;        // curvature (pass 1)
+};
+
+// One wave per row; each lane sums a fixed, strided subset of the row and a
+// butterfly adds the lanes, so the result does not depend on timing.
+template <typename T, int PASS, bool VEC>
+__global__ __launch_bounds__(256) void token_row_kernel(RowArgs a) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (i >= a.n) return;  // whole wave
+  const int lane = lane_id();
+  const T* row = static_cast<const T*>(a.a) + i * a.lda;
+  float acc = 0.f;
+  int64_t j_tail = 0;
+  if constexpr (VEC) {
+    constexpr int V = 16 / sizeof(T);
+    const int64_t nv = a.n / V * V;
+#pragma unroll 4
+    for (int64_t j = static_cast<int64_t>(lane) * V; j < nv; j += 64 * V) {
+      float x[V];
+      ld_vec<T>(row + j, x);
+      float part = 0.f;
+      if constexpr (PASS == 0) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) part += x[e];
+      } else {
+        float w[V];
+#pragma unroll
+        for (int q = 0; q < V / 4; ++q) {
+          const f32x4 sv = *reinterpret_cast<const f32x4*>(a.s + j + 4 * q);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[4 * q + e] = sv[e];
+        }
+#pragma unroll
+        for (int e = 0; e < V; ++e) part = fmaf(x[e], w[e], part);
+      }
+      acc += part;
+    }
+    j_tail = nv;
+  }
+  for (int64_t j = j_tail + lane; j < a.n; j += 64) {
+    const float x = ld_elem<T>(row + j);
+    acc += PASS == 0 ? x : x * a.s[j];
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) acc += shfl_xor_f32(acc, off);
+  if (lane == 0) {
+    if constexpr (PASS == 0) {
+      a.s[i] = acc;
+    } else {
+      const float s = a.s[i];
+      if (a.t) a.t[i] = acc;
+      a.f[i] = 4.f * s - 2.f * s + 3.f * acc;
+    }
+  }
+}
+
+struct SymArgs {
+  const void* a;
+  int64_t bh, H, nq, nk, n;
+  int64_t st[4];
+  float* out;
+  int64_t ldo;
+  int64_t tiles;  // tiles per dim (32 x 32)
+};
+
+// out[x][y] = (agg[y][x] + agg[x][y]) / 2, agg = mean over (b, h), with a
+// size-1 query or key dim broadcast. A workgroup owns the tile pair
+// (I, J), (J, I) for I <= J: every input element is read once.
+template <typename T>
+__global__ __launch_bounds__(256) void symmetrize_kernel(SymArgs a) {
+  const int64_t I = blockIdx.y, J = blockIdx.x;
+  if (I > J) return;
+  __shared__ float t1[32][33], t2[32][33];
+  const int r = threadIdx.x >> 3, c0 = (threadIdx.x & 7) * 4;
+  float s1[4] = {0.f, 0.f, 0.f, 0.f}, s2[4] = {0.f, 0.f, 0.f, 0.f};
+  const T* base = static_cast<const T*>(a.a);
+  const int64_t x1 = I * 32 + r, x2 = J * 32 + r;
+  for (int64_t bh = 0; bh < a.bh; ++bh) {
+    const int64_t b = bh / a.H, h = bh - (bh / a.H) * a.H;
+    const T* m = base + b * a.st[0] + h * a.st[1];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t y1 = J * 32 + c0 + q, y2 = I * 32 + c0 + q;
+      if (x1 < a.n && y1 < a.n)
+        s1[q] += ld_elem<T>(m + (a.nq == 1 ? 0 : x1) * a.st[2] + (a.nk == 1 ? 0 : y1) * a.st[3]);
+      if (x2 < a.n && y2 < a.n)
+        s2[q] += ld_elem<T>(m + (a.nq == 1 ? 0 : x2) * a.st[2] + (a.nk == 1 ? 0 : y2) * a.st[3]);
+    }
+  }
+  const float cnt = static_cast<float>(a.bh);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    t1[r][c0 + q] = s1[q] / cnt;  // agg[I*32 + r][J*32 + c]
+    t2[r][c0 + q] = s2[q] / cnt;  // agg[J*32 + r][I*32 + c]
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int c = c0 + q;
+    const int64_t y1 = J * 32 + c, y2 = I * 32 + c;
+    if (x1 < a.n && y1 < a.n) a.out[x1 * a.ldo + y1] = (t2[c][r] + t1[r][c]) / 2.f;
+    if (I != J && x2 < a.n && y2 < a.n) a.out[x2 * a.ldo + y2] = (t1[c][r] + t2[r][c]) / 2.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Key form
+// ---------------------------------------------------------------------------
+
+constexpr int GRAM_ROWS = 128;  // rows per workgroup (4 waves x 32)
+
+// Operand planes: for row tile t (32 rows) and k-step s (16 dims), lane
+// L = (row % 32) + 32 * h holds dims 16 s + 8 h .. + 7 as one 16-byte value
+// at index (t * dk + s) * 64 + L. This is the operand order of
+// mfma_f32_32x32x16_bf16 for A (rows) and B (columns) alike.
+struct KeyLayout {
+  int64_t Np, dk, cs, col_tiles;  // padded rows, k-steps, column splits, col tiles per split
+  size_t off_hi, off_lo, off_r, off_s, off_part, total;
+};
+
+KeyLayout key_layout(int64_t N, int64_t D) {
+  KeyLayout L;
+  L.Np = round_up(N > 0 ? N : 1, GRAM_ROWS);
+  L.dk = D <= 64 ? 4 : D <= 128 ? 8 : 16;
+  const int64_t row_blocks = L.Np / GRAM_ROWS, tiles = L.Np / 32;
+  L.cs = ceil_div(512, row_blocks);
+  if (L.cs > tiles) L.cs = tiles;
+  L.col_tiles = ceil_div(tiles, L.cs);
+  L.cs = ceil_div(tiles, L.col_tiles);
+  const size_t plane = static_cast<size_t>(L.Np) * L.dk * 16 * 2;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += static_cast<size_t>(round_up(static_cast<int64_t>(bytes), 256));
+    return at;
+  };
+  L.off_hi = take(plane);
+  L.off_lo = take(plane);
+  L.off_r = take(static_cast<size_t>(L.Np) * 4);
+  L.off_s = take(static_cast<size_t>(L.Np) * 4);
+  L.off_part = take(static_cast<size_t>(L.cs) * L.Np * 4);
+  L.total = o;
+  return L;
+}
+
+struct PrepArgs {
+  const void* k;
+  int64_t H, bh, N, D, Np, dk;
+  int64_t st[4];
+  u32x4* hi;
+  u32x4* lo;
+};
+
+// One wave per position: lane l (l < 32) owns dims 8 (l % 32) .. + 7, and
+// the two lane halves sum the even and odd (b, h) slices.
+template <typename T>
+__global__ __launch_bounds__(256) void keys_prep_kernel(PrepArgs a) {
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (n >= a.Np) return;
+  const int lane = lane_id(), g = lane & 31, par = lane >> 5;
+  float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (n < a.N) {
+    const T* base = static_cast<const T*>(a.k);
+    for (int64_t bh = par; bh < a.bh; bh += 2) {
+      const int64_t b = bh / a.H, h = bh - (bh / a.H) * a.H;
+      const T* p = base + b * a.st[0] + h * a.st[1] + n * a.st[2];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int64_t d = 8 * g + e;
+        if (d < a.D) x[e] += ld_elem<T>(p + d * a.st[3]);
+      }
+    }
+  }
+  const float cnt = static_cast<float>(a.bh);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    x[e] += __shfl_xor(x[e], 32, 64);
+    x[e] = x[e] / cnt;
+    ss = fmaf(x[e], x[e], ss);
+  }
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1) ss += shfl_xor_f32(ss, off);
+  const float den = fmaxf(sqrtf(ss), 1e-12f);
+  if (par == 0 && g < 2 * a.dk) {
+    u32x4 h4, l4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float v0 = x[2 * q] / den, v1 = x[2 * q + 1] / den;
+      const uint16_t h0 = f32_to_bf16(v0), h1 = f32_to_bf16(v1);
+      const uint16_t l0 = f32_to_bf16(v0 - bf16_to_f32(h0)), l1 = f32_to_bf16(v1 - bf16_to_f32(h1));
+      h4[q] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+      l4[q] = static_cast<uint32_t>(l0) | (static_cast<uint32_t>(l1) << 16);
+    }
+    const int64_t s = g >> 1, hh = g & 1;
+    const int64_t idx = ((n >> 5) * a.dk + s) * 64 + (n & 31) + 32 * hh;
+    a.hi[idx] = h4;
+    a.lo[idx] = l4;
+  }
+}
+
+struct GramArgs {
+  const u32x4* hi;
+  const u32x4* lo;
+  const float* w;  // pass 1: S (zero past N)
+  float* part;     // [cs][Np]
+  int64_t Np, tiles, col_tiles;
+};
+
+// Wave w of workgroup (x, y) owns row tile 4x + w and walks column tiles
+// [y col_tiles, (y + 1) col_tiles): each 32x32 tile of kn kn^T is folded
+// into 16 per-lane row partials (lane l: column l % 32, rows
+// 8 (e / 4) + 4 (l / 32) + e % 4), added over the lanes at the end.
+template <int DK, int PASS>
+__global__ __launch_bounds__(256, DK <= 8 ? 2 : 1) void gram_kernel(GramArgs a) {
+  const int lane = lane_id();
+  const int64_t rt = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  u32x4 ah[DK], al[DK];
+#pragma unroll
+  for (int s = 0; s < DK; ++s) {
+    ah[s] = a.hi[(rt * DK + s) * 64 + lane];
+    al[s] = a.lo[(rt * DK + s) * 64 + lane];
+  }
+  float p[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) p[e] = 0.f;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.y) * a.col_tiles;
+  const int64_t c1 = c0 + a.col_tiles < a.tiles ? c0 + a.col_tiles : a.tiles;
+  for (int64_t ct = c0; ct < c1; ++ct) {
+    u32x4 bh[DK], bl[DK];
+#pragma unroll
+    for (int s = 0; s < DK; ++s) {
+      bh[s] = a.hi[(ct * DK + s) * 64 + lane];
+      bl[s] = a.lo[(ct * DK + s) * 64 + lane];
+    }
+    const float wc = PASS == 0 ? 1.f : a.w[ct * 32 + (lane & 31)];
+    f32x16 acc = {};
+#pragma unroll
+    for (int s = 0; s < DK; ++s) {
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, al[s]),
+                                                    __builtin_bit_cast(bf16x8, bh[s]), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ah[s]),
+                                                    __builtin_bit_cast(bf16x8, bl[s]), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ah[s]),
+                                                    __builtin_bit_cast(bf16x8, bh[s]), acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) p[e] = fmaf(fmaxf(acc[e], 0.f), wc, p[e]);
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) p[e] += shfl_xor_f32(p[e], off);
+  }
+  if ((lane & 31) == 0) {
+    const int half = lane >> 5;
+    float* out = a.part + static_cast<int64_t>(blockIdx.y) * a.Np + rt * 32;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) out[8 * (e >> 2) + 4 * half + (e & 3)] = p[e];
+  }
+}
+
+struct FinArgs {
+  const float* part;  // [cs][Np]
+  int64_t cs, Np, N;
+  float* r;           // workspace row sums
+  float* s;           // workspace strengths (zero past N)
+  float* out_s;       // optional outputs
+  float* out_t;
+  float* out_r;
+  float* out_f;
+};
+
+template <int PASS>
+__global__ __launch_bounds__(256) void gram_finalize_kernel(FinArgs a) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= a.Np) return;
+  float sum = 0.f;
+  for (int64_t c = 0; c < a.cs; ++c) sum += a.part[c * a.Np + i];
+  if constexpr (PASS == 0) {
+    const float s = i < a.N ? sum / (sum + 1e-8f) : 0.f;
+    a.r[i] = sum;
+    a.s[i] = s;
+    if (i < a.N) {
+      if (a.out_r) a.out_r[i] = sum;
+      if (a.out_s) a.out_s[i] = s;
+    }
+  } else {
+    if (i >= a.N) return;
+    const float t = sum / (a.r[i] + 1e-8f);
+    const float s = a.s[i];
+    if (a.out_t) a.out_t[i] = t;
+    a.out_f[i] = 4.f * s - 2.f * s + 3.f * t;
+  }
+}
+
+template <typename T>
+cab_status_t launch_rows(const void* A, int64_t n, int64_t lda, float* s, float* t, float* f,
+                         hipStream_t st, const char* fn) {
+  RowArgs a{A, n, lda, s, t, f};
+  const bool vec = reinterpret_cast<uintptr_t>(A) % 16 == 0 &&
+                   (lda * static_cast<int64_t>(sizeof(T))) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(s) % 16 == 0;
+  const unsigned grid = static_cast<unsigned>(ceil_div(n, 4));
+  if (vec) {
+    token_row_kernel<T, 0, true><<<grid, 256, 0, st>>>(a);
+  } else {
+    token_row_kernel<T, 0, false><<<grid, 256, 0, st>>>(a);
+  }
+  cab_status_t r = launch_status(fn);
+  if (r != CAB_OK) return r;
+  if (vec) {
+    token_row_kernel<T, 1, true><<<grid, 256, 0, st>>>(a);
+  } else {
+    token_row_kernel<T, 1, false><<<grid, 256, 0, st>>>(a);
+  }
+  return launch_status(fn);
+}
+
+template <int DK, int PASS>
+void launch_gram(const GramArgs& g, const KeyLayout& L, hipStream_t st) {
+  gram_kernel<DK, PASS><<<dim3(static_cast<unsigned>(L.Np / GRAM_ROWS), static_cast<unsigned>(L.cs)),
+                          256, 0, st>>>(g);
+}
+
+}  // namespace
+}  // namespace cab
+
+using namespace cab;
+
+extern "C" cab_status_t cab_token_frc(const void* attention, cab_dtype_t dtype, int64_t n,
+                                      int64_t row_stride, float* strengths, float* triangles,
+                                      float* frc, void* stream) {
+  const char* fn = "cab_token_frc";
+  clear_error();
+  CAB_REQUIRE(valid_dtype(dtype), CAB_EDTYPE, "%s: unknown dtype %d", fn, static_cast<int>(dtype));
+  CAB_REQUIRE(n >= 0 && ceil_div(n, 4) <= INT32_MAX, CAB_ESHAPE, "%s: bad n %lld", fn,
+              static_cast<long long>(n));
+  if (n == 0) return CAB_OK;
+  CAB_REQUIRE(attention && strengths && frc, CAB_EINVAL, "%s: null attention / strengths / frc", fn);
+  CAB_REQUIRE(row_stride >= n, CAB_ESHAPE, "%s: row_stride %lld below n %lld", fn,
+              static_cast<long long>(row_stride), static_cast<long long>(n));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case CAB_F32: return launch_rows<float>(attention, n, row_stride, strengths, triangles, frc, st, fn);
+    case CAB_BF16: return launch_rows<bf16_t>(attention, n, row_stride, strengths, triangles, frc, st, fn);
+    default: return launch_rows<f16_t>(attention, n, row_stride, strengths, triangles, frc, st, fn);
+  }
+}
+
+extern "C" cab_status_t cab_attention_symmetrize(const void* attention, cab_dtype_t dtype, int64_t B,
+                                                 int64_t H, int64_t N_q, int64_t N_k,
+                                                 const int64_t strides[4], float* out,
+                                                 int64_t out_stride, void* stream) {
+  const char* fn = "cab_attention_symmetrize";
+  clear_error();
+  CAB_REQUIRE(valid_dtype(dtype), CAB_EDTYPE, "%s: unknown dtype %d", fn, static_cast<int>(dtype));
+  CAB_REQUIRE(B >= 1 && H >= 1 && N_q >= 1 && N_k >= 1, CAB_ESHAPE, "%s: empty input", fn);
+  CAB_REQUIRE(N_q == N_k || N_q == 1 || N_k == 1, CAB_ESHAPE,
+              "%s: (agg^T + agg) needs N_q == N_k or a size-1 dim (got %lld, %lld)", fn,
+              static_cast<long long>(N_q), static_cast<long long>(N_k));
+  const int64_t n = N_q > N_k ? N_q : N_k;
+  CAB_REQUIRE(attention && out && strides, CAB_EINVAL, "%s: null argument", fn);
+  CAB_REQUIRE(out_stride >= n, CAB_ESHAPE, "%s: out_stride below n", fn);
+  for (int d = 0; d < 4; ++d) CAB_REQUIRE(strides[d] >= 0, CAB_ESHAPE, "%s: negative stride", fn);
+  const int64_t tiles = ceil_div(n, 32);
+  CAB_REQUIRE(tiles <= 65535, CAB_ESHAPE, "%s: n %lld too large", fn, static_cast<long long>(n));
+  SymArgs a{attention, B * H, H, N_q, N_k, n, {strides[0], strides[1], strides[2], strides[3]},
+            out, out_stride, tiles};
+  const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(tiles));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case CAB_F32: symmetrize_kernel<float><<<grid, 256, 0, st>>>(a); break;
+    case CAB_BF16: symmetrize_kernel<bf16_t><<<grid, 256, 0, st>>>(a); break;
+    default: symmetrize_kernel<f16_t><<<grid, 256, 0, st>>>(a); break;
+  }
+  return launch_status(fn);
+}
+
+extern "C" size_t cab_token_frc_keys_workspace_bytes(int64_t N, int64_t D) {
+  if (N < 0 || D < 1 || D > 256) return 0;
+  return key_layout(N, D).total;
+}
+
+extern "C" cab_status_t cab_token_frc_from_keys(const void* keys, cab_dtype_t dtype, int64_t B,
+                                                int64_t H, int64_t N, int64_t D,
+                                                const int64_t strides[4], float* strengths,
+                                                float* triangles, float* row_sums, float* frc,
+                                                void* workspace, size_t workspace_bytes,
+                                                void* stream) {
+  const char* fn = "cab_token_frc_from_keys";
+  clear_error();
+  CAB_REQUIRE(valid_dtype(dtype), CAB_EDTYPE, "%s: unknown dtype %d", fn, static_cast<int>(dtype));
+  CAB_REQUIRE(B >= 1 && H >= 1 && N >= 0 && D >= 1, CAB_ESHAPE, "%s: bad shape", fn);
+  CAB_REQUIRE(D <= 256, CAB_ESHAPE, "%s: D %lld above 256", fn, static_cast<long long>(D));
+  if (N == 0) return CAB_OK;
+  CAB_REQUIRE(keys && frc && strides && workspace, CAB_EINVAL, "%s: null argument", fn);
+  for (int d = 0; d < 4; ++d) CAB_REQUIRE(strides[d] >= 0, CAB_ESHAPE, "%s: negative stride", fn);
+  const KeyLayout L = key_layout(N, D);
+  CAB_REQUIRE(workspace_bytes >= L.total, CAB_EWORKSPACE, "%s: workspace %zu < %zu bytes", fn,
+              workspace_bytes, L.total);
+  CAB_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, CAB_EWORKSPACE,
+              "%s: workspace not 256-byte aligned", fn);
+  CAB_REQUIRE(L.Np / 4 <= INT32_MAX && L.Np / GRAM_ROWS <= INT32_MAX, CAB_ESHAPE, "%s: N too large",
+              fn);
+  char* ws = static_cast<char*>(workspace);
+  u32x4* hi = reinterpret_cast<u32x4*>(ws + L.off_hi);
+  u32x4* lo = reinterpret_cast<u32x4*>(ws + L.off_lo);
+  float* r = reinterpret_cast<float*>(ws + L.off_r);
+  float* s = reinterpret_cast<float*>(ws + L.off_s);
+  float* part = reinterpret_cast<float*>(ws + L.off_part);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+
+  PrepArgs pa{keys, H, B * H, N, D, L.Np, L.dk, {strides[0], strides[1], strides[2], strides[3]},
+              hi, lo};
+  const unsigned pgrid = static_cast<unsigned>(L.Np / 4);
+  switch (dtype) {
+    case CAB_F32: keys_prep_kernel<float><<<pgrid, 256, 0, st>>>(pa); break;
+    case CAB_BF16: keys_prep_kernel<bf16_t><<<pgrid, 256, 0, st>>>(pa); break;
+    default: keys_prep_kernel<f16_t><<<pgrid, 256, 0, st>>>(pa); break;
+  }
+  cab_status_t rc = launch_status(fn);
+  if (rc != CAB_OK) return rc;
+
+  GramArgs g{hi, lo, s, part, L.Np, L.Np / 32, L.col_tiles};
+  FinArgs f{part, L.cs, L.Np, N, r, s, strengths, triangles, row_sums, frc};
+  const unsigned fgrid = static_cast<unsigned>(ceil_div(L.Np, 256));
+  for (int pass = 0; pass < 2; ++pass) {
+    if (L.dk == 4) {
+      pass == 0 ? launch_gram<4, 0>(g, L, st) : launch_gram<4, 1>(g, L, st);
+    } else if (L.dk == 8) {
+      pass == 0 ? launch_gram<8, 0>(g, L, st) : launch_gram<8, 1>(g, L, st);
+    } else {
+      pass == 0 ? launch_gram<16, 0>(g, L, st) : launch_gram<16, 1>(g, L, st);
+    }
+    rc = launch_status(fn);
+    if (rc != CAB_OK) return rc;
+    if (pass == 0) {
+      gram_finalize_kernel<0><<<fgrid, 256, 0, st>>>(f);
+    } else {
+      gram_finalize_kernel<1><<<fgrid, 256, 0, st>>>(f);
+    }
+    rc = launch_status(fn);
+    if (rc != CAB_OK) return rc;
+  }
+  return CAB_OK;
+}

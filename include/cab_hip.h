@@ -49,7 +49,7 @@ enum { CAB_NORM_NONE = 0, CAB_NORM_MINMAX = 1 };
 /* FRC combination (experiments/longbench_qa/config.py:465; test.ipynb:111-145). */
 enum { CAB_FRC_ADDITIVE = 0, CAB_FRC_MULTIPLICATIVE = 1, CAB_FRC_AUGMENTED = 2 };
 
-#define CAB_ABI_VERSION 4
+#define CAB_ABI_VERSION 5
 
 int cab_abi_version(void);
 const char* cab_last_error(void);
@@ -318,6 +318,52 @@ cab_status_t cab_kv_gather(const void* const* src, void* const* dst, int32_t n_t
                            int64_t H, int64_t n_src, int64_t row_bytes,
                            const int64_t src_strides[3], const int64_t dst_strides[3],
                            const int64_t* keep_indices, int64_t n_keep, void* stream);
+
+/*
+ * Token-level Forman-Ricci curvature of a weighted directed graph A [n, n]
+ * (compute_frc / compute_frc_triton / compute_frc_pytorch,
+ * cab_attention/kernels/frc_triton.py:21-314):
+ *   strengths[i] = S_i = sum_j A[i, j],
+ *   triangles[i] = T_i = sum_j sum_k A[i, j] A[j, k] = sum_j A[i, j] S_j,
+ *   frc[i]       = 4 S_i - 2 S_i + 3 T_i   (node weight taken equal to S).
+ * attention: [n, n] of dtype, row stride row_stride (elements). Two passes
+ * over A, fp32 accumulation in a fixed order. strengths and frc are
+ * required (strengths feeds the second pass), triangles may be NULL; fp32
+ * device arrays of n entries.
+ */
+cab_status_t cab_token_frc(const void* attention, cab_dtype_t dtype, int64_t n, int64_t row_stride,
+                           float* strengths, float* triangles, float* frc, void* stream);
+
+/*
+ * The key-key matrix of FRCTracker.compute_from_attention for a 4-D input
+ * (cab_attention/scoring/frc.py:110-121): with agg = mean over (b, h) of
+ * attention [B, H, N_q, N_k] (element strides), out = (agg^T + agg) / 2 under
+ * broadcasting, so N_q == N_k, or N_q == 1, or N_k == 1; out is fp32
+ * [n, n], n = max(N_q, N_k), row stride out_stride.
+ */
+cab_status_t cab_attention_symmetrize(const void* attention, cab_dtype_t dtype, int64_t B,
+                                      int64_t H, int64_t N_q, int64_t N_k,
+                                      const int64_t strides[4], float* out, int64_t out_stride,
+                                      void* stream);
+
+/*
+ * FRCTracker.compute_from_keys (cab_attention/scoring/frc.py:36-95) without
+ * the [N, N] matrix: with x_n = mean over (b, h) of keys[b, h, n, :],
+ * kn_n = x_n / max(|x_n|, 1e-12), r_i = sum_j relu(kn_i . kn_j) and
+ * A[i, j] = relu(kn_i . kn_j) / (r_i + 1e-8), writes the token curvature of
+ * A as cab_token_frc defines it: S_i = r_i / (r_i + 1e-8),
+ * T_i = (sum_j relu(kn_i . kn_j) S_j) / (r_i + 1e-8). The Gram products run
+ * on MFMA (bf16 hi/lo split of kn, fp32 accumulate). keys: [B, H, N, D] of
+ * dtype (element strides), D <= 256. frc is required; strengths,
+ * triangles and row_sums (r) may be NULL; fp32 arrays of N entries. The
+ * workspace is cab_token_frc_keys_workspace_bytes(N, D) bytes.
+ */
+size_t cab_token_frc_keys_workspace_bytes(int64_t N, int64_t D);
+cab_status_t cab_token_frc_from_keys(const void* keys, cab_dtype_t dtype, int64_t B, int64_t H,
+                                     int64_t N, int64_t D, const int64_t strides[4],
+                                     float* strengths, float* triangles, float* row_sums,
+                                     float* frc, void* workspace, size_t workspace_bytes,
+                                     void* stream);
 
 #ifdef __cplusplus
 }

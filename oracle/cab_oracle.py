@@ -45,6 +45,15 @@ Pinning of each function (tests/test_oracle.py):
 - ``evict_connectivity``: explicit sums over the importance rows and
   columns against numpy's fancy-indexed reductions.
 - ``kv_gather``: identity and reversal permutations, out-of-range rows.
+- ``token_frc``: the reference Triton kernel's literal triple loop
+  (sum_j sum_k A_ij A_jk, frc_triton.py:90-119) on small graphs, closed
+  forms (identity, all-ones, rank-1 uv^T), permutation equivariance.
+- ``frc_from_keys``: torch float64 through the reference's own call
+  sequence (mean, F.normalize, mm, relu, row normalisation, compute_frc),
+  and closed forms (orthonormal keys: G = I; parallel keys: G = all-ones;
+  antipodal keys: relu removes the -1; zero keys give 0).
+- ``symmetrize_attention``: torch broadcasting of (agg.T + agg) / 2 for
+  N_q == N_kv and the size-1 cases, and an explicit (x, y) loop.
 """
 
 from __future__ import annotations
@@ -54,6 +63,9 @@ import math
 import numpy as np
 
 __all__ = [
+    "token_frc",
+    "frc_from_keys",
+    "symmetrize_attention",
     "evict_select",
     "evict_connectivity",
     "kv_gather",
@@ -555,3 +567,40 @@ def kv_gather(x, keep) -> np.ndarray:
     out[:, :, ok] = x[:, :, keep[ok]]
     return out
 
+
+
+def token_frc(attention):
+    """Token-level Forman-Ricci curvature of a weighted directed graph
+    (compute_frc_pytorch, cab_attention/kernels/frc_triton.py:269-293):
+    S = A.sum(1), T = (A @ A).sum(1), F = 4 S - 2 S + 3 T (node weight
+    taken equal to S, :155-160). Returns (S, T, F) in float64."""
+    a = np.asarray(attention, np.float64)
+    s = a.sum(axis=1)
+    t = (a @ a).sum(axis=1)
+    return s, t, 4.0 * s - 2.0 * s + 3.0 * t
+
+
+def frc_from_keys(keys):
+    """FRCTracker.compute_from_keys without its update interval
+    (cab_attention/scoring/frc.py:68-89): x = keys.mean((0, 1)),
+    kn = x / max(|x|, 1e-12) (F.normalize), G = kn kn^T, A = relu(G) row-
+    normalised by (row sum + 1e-8), then token_frc(A). Returns a dict with
+    strengths, triangles, frc and row_sums (sum_j relu(G_ij))."""
+    x = np.asarray(keys, np.float64).mean(axis=(0, 1))
+    kn = x / np.maximum(np.linalg.norm(x, axis=-1, keepdims=True), 1e-12)
+    g = np.maximum(kn @ kn.T, 0.0)
+    r = g.sum(axis=1)
+    a = g / (r[:, None] + 1e-8)
+    s, t, f = token_frc(a)
+    return {"strengths": s, "triangles": t, "frc": f, "row_sums": r}
+
+
+def symmetrize_attention(attention):
+    """The key-key matrix of FRCTracker.compute_from_attention for a 4-D
+    input (scoring/frc.py:110-121): agg = mean over (b, h), then
+    (agg.T + agg) / 2 under numpy (= torch) broadcasting, cut to
+    [:n, :n] with n = min of its shape."""
+    agg = np.asarray(attention, np.float64).mean(axis=(0, 1))
+    sym = (agg.T + agg) / 2.0
+    n = min(sym.shape)
+    return sym[:n, :n]

@@ -37,7 +37,9 @@ def test_header_declares_the_hot_path():
                  "cab_block_sparse_attn_pack_v", "cab_block_sparse_attn_fwd_packed",
                  "cab_block_topk_hybrid", "cab_flash_attn_workspace_bytes",
                  "cab_flash_attn_fwd", "cab_attn_key_scores", "cab_evict_select",
-                 "cab_evict_connectivity", "cab_kv_gather"):
+                 "cab_evict_connectivity", "cab_kv_gather", "cab_token_frc",
+                 "cab_attention_symmetrize", "cab_token_frc_keys_workspace_bytes",
+                 "cab_token_frc_from_keys"):
         assert name in syms
     assert set(syms) == set(nat.SIGNATURES), "ctypes table and header disagree"
 
@@ -246,3 +248,34 @@ def test_eviction_validation(lib):
     assert g(rb=100) == nat.CAB_ESHAPE
     assert g(ss=_s4(1 << 20, 1 << 16, 8, 0)) == nat.CAB_ESHAPE
     assert g(src=nulls) == nat.CAB_EINVAL
+
+
+def test_token_frc_validation(lib):
+    """Argument checks of the token-FRC entry points (nothing is launched)."""
+    tf = lambda **kw: lib.cab_token_frc(kw.get("a", FAKE), kw.get("dt", nat.CAB_F32),
+                                        kw.get("n", 10), kw.get("lda", 10), kw.get("s", FAKE),
+                                        None, kw.get("f", FAKE), None)
+    assert tf(dt=9) == nat.CAB_EDTYPE
+    assert tf(n=-1) == nat.CAB_ESHAPE
+    assert tf(lda=9) == nat.CAB_ESHAPE
+    assert tf(s=None) == nat.CAB_EINVAL
+    assert tf(f=None) == nat.CAB_EINVAL
+    assert tf(a=None, n=0) == nat.CAB_OK  # empty graph: nothing to do
+    st = _s4(600, 100, 10, 1)
+    sym = lambda **kw: lib.cab_attention_symmetrize(FAKE, nat.CAB_BF16, 2, 3, kw.get("nq", 10),
+                                                    kw.get("nk", 10), st, kw.get("out", FAKE),
+                                                    kw.get("ldo", 10), None)
+    assert sym(nq=4, nk=10) == nat.CAB_ESHAPE
+    assert sym(ldo=9) == nat.CAB_ESHAPE
+    assert sym(out=None) == nat.CAB_EINVAL
+    ws = lib.cab_token_frc_keys_workspace_bytes(1000, 128)
+    assert ws > 0 and lib.cab_token_frc_keys_workspace_bytes(1000, 257) == 0
+    assert lib.cab_token_frc_keys_workspace_bytes(2000, 128) > ws
+    ks = _s4(8 * 1000 * 128, 1000 * 128, 128, 1)
+    fk = lambda **kw: lib.cab_token_frc_from_keys(
+        FAKE, nat.CAB_BF16, 1, 8, 1000, kw.get("D", 128), ks, None, None, None, kw.get("f", FAKE),
+        kw.get("ws", FAKE), kw.get("wsb", ws), None)
+    assert fk(D=300) == nat.CAB_ESHAPE
+    assert fk(f=None) == nat.CAB_EINVAL
+    assert fk(wsb=ws - 1) == nat.CAB_EWORKSPACE
+    assert fk(ws=FAKE + 16) == nat.CAB_EWORKSPACE

@@ -562,3 +562,103 @@ def test_evict_select_positional_bridges_are_a_truncated_slice():
     assert cnt == (5, 33, 62 - 62 // 3)
     assert list(np.flatnonzero(cat == 3)) == list(range(20, 62))
     assert keep.size == 5 + 33 + 42
+
+
+def test_token_frc_matches_the_triangle_loop_and_closed_forms():
+    """S and T against the reference Triton kernels' literal loops
+    (frc_triton.py:47-62, :98-119), and closed forms: A = I gives (1, 1, 5);
+    the all-ones graph gives S = n, T = n^2; a rank-1 graph u v^T gives
+    S = u sum(v) and T = u (v . u) sum(v). Relabelling the nodes permutes
+    the result."""
+    rng = np.random.default_rng(11)
+    a = rng.random((7, 7))
+    s, t, f = O.token_frc(a)
+    n = a.shape[0]
+    s_loop = [sum(a[i, j] for j in range(n)) for i in range(n)]
+    t_loop = [sum(a[i, j] * a[j, k] for j in range(n) for k in range(n)) for i in range(n)]
+    np.testing.assert_allclose(s, s_loop, rtol=1e-13)
+    np.testing.assert_allclose(t, t_loop, rtol=1e-13)
+    np.testing.assert_allclose(f, 2 * np.asarray(s_loop) + 3 * np.asarray(t_loop), rtol=1e-13)
+    s, t, f = O.token_frc(np.eye(5))
+    assert np.all(s == 1) and np.all(t == 1) and np.all(f == 5)
+    s, t, f = O.token_frc(np.ones((6, 6)))
+    assert np.all(s == 6) and np.all(t == 36) and np.all(f == 2 * 6 + 3 * 36)
+    u, v = rng.random(9), rng.random(9)
+    s, t, _ = O.token_frc(np.outer(u, v))
+    np.testing.assert_allclose(s, u * v.sum(), rtol=1e-13)
+    np.testing.assert_allclose(t, u * (v @ u) * v.sum(), rtol=1e-13)
+    p = rng.permutation(7)
+    for x, y in zip(O.token_frc(a[p][:, p]), O.token_frc(a)):
+        np.testing.assert_allclose(x, y[p], rtol=1e-13)
+
+
+def _frc_from_keys_torch(keys):
+    """The reference's call sequence (scoring/frc.py:73-89 with
+    compute_frc_pytorch, frc_triton.py:279-293) in torch float64."""
+    import torch.nn.functional as F
+    k = torch.from_numpy(np.asarray(keys, np.float64))
+    kn = F.normalize(k.mean(dim=(0, 1)), dim=-1)
+    att = F.relu(torch.mm(kn, kn.t()))
+    att = att / (att.sum(dim=1, keepdim=True) + 1e-8)
+    s = att.sum(dim=1)
+    t = torch.matmul(att, att).sum(dim=1)
+    return s.numpy(), t.numpy(), (4.0 * s - 2.0 * s + 3.0 * t).numpy()
+
+
+def test_frc_from_keys_matches_torch_and_closed_forms():
+    """Against torch float64 through the reference's own steps; then closed
+    forms. Orthonormal (or antipodal: relu drops the -1) keys give G = I, so
+    sigma = 1 / (1 + 1e-8), S = sigma, T = sigma^2; parallel keys give the
+    all-ones G: S = n / (n + 1e-8), T = S^2; a zero key scores 0. The mean
+    runs over batch and heads."""
+    rng = np.random.default_rng(12)
+    keys = rng.standard_normal((2, 3, 40, 16))
+    got = O.frc_from_keys(keys)
+    for x, y in zip((got["strengths"], got["triangles"], got["frc"]), _frc_from_keys_torch(keys)):
+        np.testing.assert_allclose(x, y, rtol=1e-12)
+    sig = 1.0 / (1.0 + 1e-8)
+    eye = np.zeros((1, 1, 5, 8))
+    eye[0, 0, np.arange(5), np.arange(5)] = rng.random(5) + 0.5
+    r = O.frc_from_keys(eye)
+    np.testing.assert_allclose(r["row_sums"], 1.0, rtol=1e-14)
+    np.testing.assert_allclose(r["strengths"], sig, rtol=1e-14)
+    np.testing.assert_allclose(r["triangles"], sig * sig, rtol=1e-14)
+    anti = np.zeros((1, 1, 2, 4))
+    anti[0, 0, 0, 0], anti[0, 0, 1, 0] = 2.0, -3.0
+    np.testing.assert_allclose(O.frc_from_keys(anti)["frc"], 2 * sig + 3 * sig * sig, rtol=1e-14)
+    u = rng.standard_normal(8)
+    par = (rng.random(6)[:, None] + 0.1) * u[None, :]
+    r = O.frc_from_keys(par[None, None])
+    sp = 6 / (6 + 1e-8)
+    np.testing.assert_allclose(r["row_sums"], 6.0, rtol=1e-14)
+    np.testing.assert_allclose(r["strengths"], sp, rtol=1e-14)
+    np.testing.assert_allclose(r["triangles"], sp * sp, rtol=1e-14)
+    z = rng.standard_normal((1, 2, 4, 8))
+    z[:, :, 2] = 0.0
+    r = O.frc_from_keys(z)
+    assert r["frc"][2] == 0.0 and r["strengths"][2] == 0.0 and np.all(r["frc"][[0, 1, 3]] > 0)
+    base = rng.standard_normal((5, 8))
+    delta = rng.standard_normal((2, 2, 5, 8))
+    delta -= delta.mean(axis=(0, 1), keepdims=True)
+    np.testing.assert_allclose(O.frc_from_keys(base[None, None] + delta)["frc"],
+                               O.frc_from_keys(base[None, None])["frc"], rtol=1e-12)
+
+
+def test_symmetrize_attention_broadcasting():
+    """(agg.T + agg) / 2 of the (b, h)-mean: an explicit element loop for
+    N_q == N_kv, and torch's broadcasting for a single query (a decode step:
+    (a_x + a_y) / 2) or a single key."""
+    rng = np.random.default_rng(13)
+    att = rng.random((2, 3, 6, 6))
+    got = O.symmetrize_attention(att)
+    m = att.mean(axis=(0, 1))
+    want = np.array([[(m[y, x] + m[x, y]) / 2 for y in range(6)] for x in range(6)])
+    np.testing.assert_allclose(got, want, rtol=1e-15)
+    one_q = rng.random((2, 2, 1, 7))
+    a = one_q.mean(axis=(0, 1))[0]
+    np.testing.assert_allclose(O.symmetrize_attention(one_q), (a[:, None] + a[None, :]) / 2, rtol=1e-15)
+    t = torch.from_numpy(one_q).mean(dim=(0, 1))
+    np.testing.assert_allclose(O.symmetrize_attention(one_q), ((t.T + t) / 2.0).numpy(), rtol=1e-15)
+    one_k = rng.random((1, 2, 5, 1))
+    b = one_k.mean(axis=(0, 1))[:, 0]
+    np.testing.assert_allclose(O.symmetrize_attention(one_k), (b[:, None] + b[None, :]) / 2, rtol=1e-15)
