@@ -19,6 +19,10 @@ TFLOP/s, % of roofline".
   two heads, predictor + attention latency.
 - ``cpu_baseline``: the float64 numpy oracle on a bounded sample of the
   config-4 attention workload, on this host's cores.
+- ``fp32_executor``, ``eviction_path``, ``token_frc``: config 4 with fp32
+  inputs; dense attention + per-key totals, eviction selection and the
+  multi-layer K/V prune (the KV-eviction path); token-level FRC of an
+  attention graph and of cached keys.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -279,6 +283,43 @@ def eviction_prune(args, dev, importance, k_layer):
     }
 
 
+def token_frc_section(args, dev):
+    """Token-level FRC: compute_frc on a [16384, 16384] fp32 attention graph
+    (two HBM passes, priced as 2 * 4 N^2 bytes) and
+    FRCTracker.compute_from_keys on keys [1, 8, 16384, 128] bf16 (two MFMA
+    Gram passes, priced as 2 * 2 N^2 D useful flops; the hi/lo split's
+    extra products are not counted)."""
+    import torch
+    from cab_attention.kernels import frc_from_keys, token_frc
+    iters = max(3, args.steps // 2)
+    n = 16384
+    a = torch.rand((n, n), generator=torch.Generator(device=dev).manual_seed(31), device=dev)
+    a = a / a.sum(dim=1, keepdim=True)
+    token_frc(a)
+    m_ms = time_events(lambda: token_frc(a), iters)
+    m_bytes = 2 * 4 * n * n
+    del a
+    torch.cuda.empty_cache()
+    keys = seeded_gpu((1, 8, n, 128), 32, torch.bfloat16, dev)
+    frc_from_keys(keys)
+    k_ms = time_events(lambda: frc_from_keys(keys), iters)
+    k_flops = 2 * 2 * n * n * 128
+    del keys
+    torch.cuda.empty_cache()
+    log(f"token FRC: matrix {m_ms:.3f} ms ({m_bytes / (m_ms * 1e-3) / 1e9:.0f} GB/s), "
+        f"keys {k_ms:.3f} ms ({k_flops / (k_ms * 1e-3) / 1e12:.0f} TFLOP/s)")
+    return {
+        "matrix_config": f"compute_frc: fp32 attention [{n}, {n}] (rows sum to 1)",
+        "matrix_ms": round(m_ms, 4),
+        "matrix_GBs": round(m_bytes / (m_ms * 1e-3) / 1e9, 1),
+        "matrix_frac_hbm": round(m_bytes / (m_ms * 1e-3) / 8e12, 4),
+        "keys_config": f"FRCTracker.compute_from_keys: keys [1, 8, {n}, 128] bf16",
+        "keys_ms": round(k_ms, 4),
+        "keys_TFLOPs": round(k_flops / (k_ms * 1e-3) / 1e12, 1),
+        "keys_frac_mfma": round(k_flops / (k_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -293,6 +334,8 @@ def main() -> int:
                     help="only time the config-3 predictor (for per-kernel profiles)")
     ap.add_argument("--eviction-only", action="store_true",
                     help="only time the eviction path (dense attention + key totals; profiles)")
+    ap.add_argument("--token-frc-only", action="store_true",
+                    help="only time token-level FRC (matrix and keys forms; profiles)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -325,6 +368,9 @@ def main() -> int:
     bs, D = 64, 128
     if args.predictor_only:
         return predictor_only(args, dev, bs, D)
+    if args.token_frc_only:
+        print(json.dumps({"token_frc": token_frc_section(args, dev)}), flush=True)
+        return 0
     if args.eviction_only:
         print(json.dumps({"eviction_path": eviction_path(args, dev, D)}), flush=True)
         return 0
@@ -390,6 +436,7 @@ def main() -> int:
         torch.cuda.empty_cache()
 
         result_evict = eviction_path(args, dev, D)
+        result_tfrc = token_frc_section(args, dev)
 
         # ---------------- config 3: predictor latency at N = 128k
         B3, H3, N3 = 2, 8, 128000
@@ -532,6 +579,7 @@ def main() -> int:
         "bridge": result_bridge,
         "fp32_executor": result_fp32,
         "eviction_path": result_evict,
+        "token_frc": result_tfrc,
     }
     print(json.dumps(line), flush=True)
     return 0
