@@ -21,6 +21,7 @@ namespace {
 
 constexpr int AT = 64;    // affinity tile
 constexpr int TT = 128;   // triangle tile
+constexpr int TT_WIDE = 256;  // wide triangle tile (large M)
 constexpr int TK = 32;    // triangle k-step
 
 struct FrcLayout {
@@ -278,25 +279,31 @@ struct TriArgs {
 // read is one 1 KB wave access. Inside each 64-slot group the slot of lane L
 // is stored at position L ^ (4 (2 kk + L / 32)): the four threads that load
 // one row's 64 bytes then write four different LDS bank groups.
-constexpr int SLOTS = (TK / 16) * (TT / 32) * 64;  // 512 slots = 8 KB per plane
+template <int TILE>
+constexpr int tri_slots() { return (TK / 16) * (TILE / 32) * 64; }
 
+// Thread t moves chunks t and t + THREADS of a plane's TILE x TK slice
+// (TILE rows of 4 x 16 bytes): 2 chunks per thread when THREADS = 2 TILE.
+template <int TILE, int THREADS>
 __device__ __forceinline__ void tri_load(const uint16_t* plane, int64_t row0, int64_t k0, int64_t Mp,
                                          u32x4 (&reg)[2]) {
+  static_assert(THREADS * 2 == TILE * 4, "two 16-byte chunks per thread and plane");
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    const int cid = threadIdx.x + 256 * q;
+    const int cid = threadIdx.x + THREADS * q;
     const int row = cid >> 2, kc = cid & 3;
     reg[q] = *reinterpret_cast<const u32x4*>(plane + (row0 + row) * Mp + k0 + 8 * kc);
   }
 }
 
+template <int TILE, int THREADS>
 __device__ __forceinline__ void tri_store(u32x4* lds, const u32x4 (&reg)[2]) {
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    const int cid = threadIdx.x + 256 * q;
+    const int cid = threadIdx.x + THREADS * q;
     const int row = cid >> 2, kc = cid & 3;
     const int kk = kc >> 1, hf = kc & 1, sub = row >> 5;
-    lds[(kk * (TT / 32) + sub) * 64 + (((row & 31) + 32 * hf) ^ (4 * (2 * kk + hf)))] = reg[q];
+    lds[(kk * (TILE / 32) + sub) * 64 + (((row & 31) + 32 * hf) ^ (4 * (2 * kk + hf)))] = reg[q];
   }
 }
 
@@ -315,8 +322,18 @@ __device__ __forceinline__ float frc_combine(int formula, float ahat, float t, f
   return f;
 }
 
-__global__ __launch_bounds__(256) void triangle_kernel(TriArgs a) {
-  __shared__ u32x4 lds[2][4][SLOTS];  // [stage][Ahi, Alo, Bhi, Blo][slot] = 64 KB
+// T tile of TILE x TILE per workgroup of WI x WJ waves; wave (wi, wj) owns
+// rows wi TILE / WI .. and columns wj TILE / WJ .. as XS x YS MFMA tiles.
+// NBUF register buffers carry operand slices global -> registers -> LDS
+// (two LDS stages): with NBUF = 2 a slice's loads have two slices of MFMA
+// work to land, with NBUF = 1 one slice (for the wide tile, whose
+// accumulators leave room for one buffer only).
+template <int TILE, int WI, int WJ, int NBUF>
+__global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
+  constexpr int THREADS = WI * WJ * 64;
+  constexpr int XS = TILE / WI / 32, YS = TILE / WJ / 32;
+  constexpr int SLOTS = tri_slots<TILE>();
+  __shared__ u32x4 lds[2][4][SLOTS];  // [stage][Ahi, Alo, Bhi, Blo][slot]
   const int64_t total = a.BH * a.nt * a.nt;
   const int64_t logical = xcd_remap(blockIdx.x, total);
   const int64_t bh = logical / (a.nt * a.nt);
@@ -324,78 +341,117 @@ __global__ __launch_bounds__(256) void triangle_kernel(TriArgs a) {
   const int64_t ti = rem / a.nt, tj = rem - (rem / a.nt) * a.nt;
   const size_t pbase = static_cast<size_t>(bh) * a.Mp * a.Mp;
   const uint16_t* planes[4] = {a.xhi + pbase, a.xlo + pbase, a.xthi + pbase, a.xtlo + pbase};
-  const int64_t rows[4] = {ti * TT, ti * TT, tj * TT, tj * TT};
+  const int64_t rows[4] = {ti * TILE, ti * TILE, tj * TILE, tj * TILE};
 
   const int w = threadIdx.x >> 6, lane = lane_id();
-  const int wi = w >> 1, wj = w & 1;
-  f32x16 acc[2][2];
+  const int wi = w / WJ, wj = w - (w / WJ) * WJ;
+  f32x16 acc[XS][YS];
 #pragma unroll
-  for (int x = 0; x < 2; ++x)
+  for (int x = 0; x < XS; ++x)
 #pragma unroll
-    for (int y = 0; y < 2; ++y) acc[x][y] = f32x16{};
+    for (int y = 0; y < YS; ++y) acc[x][y] = f32x16{};
 
-  // Operand k-slices travel global -> registers -> LDS; the registers of
-  // slice kt + 2 are loaded while slice kt is multiplied (two register
-  // buffers, two LDS stages), so a load has two slices of MFMA work to land.
-  u32x4 reg[2][4][2];
   const int nk = static_cast<int>(a.Mp / TK);
-#pragma unroll
-  for (int p = 0; p < 4; ++p) tri_load(planes[p], rows[p], 0, a.Mp, reg[0][p]);
-  if (nk > 1) {
-#pragma unroll
-    for (int p = 0; p < 4; ++p) tri_load(planes[p], rows[p], TK, a.Mp, reg[1][p]);
-  }
-  auto slice = [&](int kt, auto buf_tag) {
-    constexpr int st = decltype(buf_tag)::value;  // slice kt uses register buffer and LDS stage kt % 2
-#pragma unroll
-    for (int p = 0; p < 4; ++p) tri_store(lds[st][p], reg[st][p]);
-    __syncthreads();
-    if (kt + 2 < nk) {
-#pragma unroll
-      for (int p = 0; p < 4; ++p)
-        tri_load(planes[p], rows[p], static_cast<int64_t>(kt + 2) * TK, a.Mp, reg[st][p]);
-    }
+  auto compute = [&](auto st_tag) {
+    constexpr int st = decltype(st_tag)::value;
 #pragma unroll
     for (int kk = 0; kk < TK / 16; ++kk) {
-      bf16x8 ah[2], al[2], bh8[2], bl[2];
+      bf16x8 bh8[YS], bl[YS];
       const int lsw = lane ^ (4 * (2 * kk + (lane >> 5)));
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const int sa = (kk * (TT / 32) + 2 * wi + s) * 64 + lsw;
-        const int sb = (kk * (TT / 32) + 2 * wj + s) * 64 + lsw;
-        ah[s] = __builtin_bit_cast(bf16x8, lds[st][0][sa]);
-        al[s] = __builtin_bit_cast(bf16x8, lds[st][1][sa]);
-        bh8[s] = __builtin_bit_cast(bf16x8, lds[st][2][sb]);
-        bl[s] = __builtin_bit_cast(bf16x8, lds[st][3][sb]);
+      for (int y = 0; y < YS; ++y) {
+        const int sb = (kk * (TILE / 32) + YS * wj + y) * 64 + lsw;
+        bh8[y] = __builtin_bit_cast(bf16x8, lds[st][2][sb]);
+        bl[y] = __builtin_bit_cast(bf16x8, lds[st][3][sb]);
       }
+      // A operands one 32-row strip at a time (fewer live registers).
 #pragma unroll
-      for (int x = 0; x < 2; ++x)
+      for (int x = 0; x < XS; ++x) {
+        const int sa = (kk * (TILE / 32) + XS * wi + x) * 64 + lsw;
+        const bf16x8 ah = __builtin_bit_cast(bf16x8, lds[st][0][sa]);
+        const bf16x8 al = __builtin_bit_cast(bf16x8, lds[st][1][sa]);
 #pragma unroll
-        for (int y = 0; y < 2; ++y) {
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[x], bh8[y], acc[x][y], 0, 0, 0);
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[x], bl[y], acc[x][y], 0, 0, 0);
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[x], bh8[y], acc[x][y], 0, 0, 0);
+        for (int y = 0; y < YS; ++y) {
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh8[y], acc[x][y], 0, 0, 0);
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl[y], acc[x][y], 0, 0, 0);
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh8[y], acc[x][y], 0, 0, 0);
         }
+      }
     }
   };
-  for (int kt = 0; kt < nk; kt += 2) {
-    slice(kt, std::integral_constant<int, 0>{});
-    if (kt + 1 < nk) slice(kt + 1, std::integral_constant<int, 1>{});
+
+  if constexpr (NBUF == 2) {
+    // The registers of slice kt + 2 are loaded while slice kt is multiplied.
+    u32x4 reg[2][4][2];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) tri_load<TILE, THREADS>(planes[p], rows[p], 0, a.Mp, reg[0][p]);
+    if (nk > 1) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) tri_load<TILE, THREADS>(planes[p], rows[p], TK, a.Mp, reg[1][p]);
+    }
+    auto slice = [&](int kt, auto buf_tag) {
+      constexpr int st = decltype(buf_tag)::value;  // register buffer and LDS stage kt % 2
+#pragma unroll
+      for (int p = 0; p < 4; ++p) tri_store<TILE, THREADS>(lds[st][p], reg[st][p]);
+      __syncthreads();
+      if (kt + 2 < nk) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+          tri_load<TILE, THREADS>(planes[p], rows[p], static_cast<int64_t>(kt + 2) * TK, a.Mp,
+                                  reg[st][p]);
+      }
+      compute(buf_tag);
+    };
+    for (int kt = 0; kt < nk; kt += 2) {
+      slice(kt, std::integral_constant<int, 0>{});
+      if (kt + 1 < nk) slice(kt + 1, std::integral_constant<int, 1>{});
+    }
+  } else {
+    // One register buffer: slice kt + 1 is stored to the other LDS stage
+    // after slice kt is multiplied, then slice kt + 2 is loaded.
+    u32x4 reg[4][2];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) tri_load<TILE, THREADS>(planes[p], rows[p], 0, a.Mp, reg[p]);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) tri_store<TILE, THREADS>(lds[0][p], reg[p]);
+    if (nk > 1) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) tri_load<TILE, THREADS>(planes[p], rows[p], TK, a.Mp, reg[p]);
+    }
+    __syncthreads();
+    auto slice = [&](int kt, auto st_tag) {
+      constexpr int st = decltype(st_tag)::value;  // LDS stage of slice kt
+      compute(st_tag);
+      if (kt + 1 < nk) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) tri_store<TILE, THREADS>(lds[st ^ 1][p], reg[p]);
+      }
+      if (kt + 2 < nk) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+          tri_load<TILE, THREADS>(planes[p], rows[p], static_cast<int64_t>(kt + 2) * TK, a.Mp, reg[p]);
+      }
+      __syncthreads();
+    };
+    for (int kt = 0; kt < nk; kt += 2) {
+      slice(kt, std::integral_constant<int, 0>{});
+      if (kt + 1 < nk) slice(kt + 1, std::integral_constant<int, 1>{});
+    }
   }
 
-  // Epilogue: F = combine(Ahat, T) for the wave's 64x64 block.
+  // Epilogue: F = combine(Ahat, T) for the wave's block.
   const int half = lane >> 5;
   const size_t obase = static_cast<size_t>(bh) * a.M * a.M;
 #pragma unroll
-  for (int y = 0; y < 2; ++y) {
-    const int64_t j = tj * TT + wj * 64 + y * 32 + (lane & 31);
+  for (int y = 0; y < YS; ++y) {
+    const int64_t j = tj * TILE + wj * (TILE / WJ) + y * 32 + (lane & 31);
     if (j >= a.M) continue;
     const float sj = a.formula == CAB_FRC_AUGMENTED ? a.rowsum[bh * a.Mp + j] : 0.f;
 #pragma unroll
-    for (int x = 0; x < 2; ++x) {
+    for (int x = 0; x < XS; ++x) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int64_t i = ti * TT + wi * 64 + x * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+        const int64_t i = ti * TILE + wi * (TILE / WI) + x * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
         if (i >= a.M) continue;
         const float t = acc[x][y][e];
         const float ahat = bf16_to_f32(a.xhi[pbase + i * a.Mp + j]) + bf16_to_f32(a.xlo[pbase + i * a.Mp + j]);
@@ -519,12 +575,18 @@ extern "C" cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_
   t.tri = triangles;
   t.M = M;
   t.Mp = L.Mp;
-  t.nt = L.Mp / TT;
   t.BH = BH;
   t.lambda = lambda_redundancy;
   t.formula = formula;
+  // The 256-wide tile stages half the bytes per flop; it is used when Mp
+  // allows it and its tiles still give every CU work.
+  const bool wide = L.Mp % TT_WIDE == 0 && BH * (L.Mp / TT_WIDE) * (L.Mp / TT_WIDE) >= 256;
+  t.nt = L.Mp / (wide ? TT_WIDE : TT);
   const int64_t blocks = BH * t.nt * t.nt;
   CAB_REQUIRE(blocks <= INT32_MAX, CAB_ESHAPE, "cab_block_frc: problem too large");
-  triangle_kernel<<<static_cast<unsigned>(blocks), 256, 0, s>>>(t);
+  if (wide)
+    triangle_kernel<TT_WIDE, 2, 4, 1><<<static_cast<unsigned>(blocks), 512, 0, s>>>(t);
+  else
+    triangle_kernel<TT, 2, 2, 2><<<static_cast<unsigned>(blocks), 256, 0, s>>>(t);
   return launch_status("cab_block_frc/triangles");
 }

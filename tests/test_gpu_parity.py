@@ -130,6 +130,24 @@ def test_frc_parity(cuda, dt, M, formula, normalization):
         assert_frc_close(f, of, oa, ot, lam)
 
 
+@pytest.mark.parametrize("H,M,formula", [(4, 2000, "additive"), (16, 1000, "multiplicative")])
+def test_frc_parity_wide_tile(cuda, H, M, formula):
+    """Shapes that select the 256-wide triangle tile (B H (Mp / 256)^2 >= 256
+    workgroups): M = 2000 fills its 2048 padding exactly up to the last
+    tile, M = 1000 leaves a ragged 24-row margin in its 1024 padding."""
+    from cab_attention.kernels import compute_block_frc
+    B, D, lam = 1, 128, 0.5
+    qc = seeded((B, H, M, D), 15, torch.bfloat16, scale=3.0)
+    kc = seeded((B, H, M, D), 16, torch.bfloat16, scale=3.0)
+    f, a, t = compute_block_frc(qc.to(cuda), kc.to(cuda), lambda_redundancy=lam, formula=formula)
+    of, oa, ot = O.compute_block_frc(np32(qc), np32(kc), lambda_redundancy=lam, formula=formula)
+    np.testing.assert_allclose(np32(t), ot, rtol=1e-4, atol=1e-4 * np.abs(ot).max())
+    if formula == "multiplicative":
+        np.testing.assert_allclose(np32(f), of, rtol=1e-3, atol=1e-5)
+    else:
+        assert_frc_close(f, of, oa, ot, lam)
+
+
 def test_frc_no_diagnostics_matches(cuda):
     from cab_attention.kernels import compute_block_frc
     qc = seeded((2, 2, 300, 128), 13, torch.bfloat16).to(cuda)
