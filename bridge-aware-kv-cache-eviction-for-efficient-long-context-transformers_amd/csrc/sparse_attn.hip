@@ -704,15 +704,18 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
 // key_score_kernel: per-key attention totals (cab_attn_key_scores).
 // score[k] = sum over queries t of softmax_t(k) = exp(s_tk - lse_t), with
 // the natural-log lse of attn_fwd_kernel's rows. One workgroup of 4 waves per
-// (b, h, key block j); every wave holds the block's 64 keys as the B operand
-// of S = Q K^T (K^T tiles in 16 registers x 4) and walks 16-query tiles
-// (wave w: tiles w, w + 4, ... of those that see block j), reading Q and the
-// lse straight from global memory one tile ahead. Per tile:
+// (b, h, group of 4 key blocks); wave w holds block 4 g + w's 64 keys as the
+// B operand of S = Q K^T (K^T tiles in 16 registers x 4). The four waves walk
+// the same 16-query tiles: each tile's Q (4 KB, MFMA operand order) and lse
+// (16 floats, one copy per wave) are staged once per workgroup into a ring
+// of 4 LDS stages by global_load_lds, three tiles ahead, so the texture path
+// carries a quarter of the bytes per MFMA of one wave per key block. Per
+// tile and wave:
 //   S (16 queries x 64 keys) = 16 MFMA 16x16x32,
 //   P = exp2(S c - lse log2 e) (fp32, masked entries 0),
 //   column sums over the tile's queries, kept per lane.
-// The lane and wave partial sums are added once at the end (fixed order,
-// no atomics) and written to, or added into, score[b, h, keys of block j].
+// The lane partials are added once at the end in a fixed order (no
+// atomics) and written to, or added into, score[b, h, keys of the block].
 // ---------------------------------------------------------------------------
 struct KeyScoreArgs {
   const uint16_t* q;
@@ -720,21 +723,24 @@ struct KeyScoreArgs {
   const float* lse;  // [B, H, Nq] contiguous
   float* score;      // score[b * ss0 + h * ss1 + token]
   int64_t qs[3], ks[3], ss[2];
-  int32_t BH, H, group, Nq, Nk, Mk, qoff, causal, accumulate;
+  int32_t BH, H, group, Nq, Nk, Mk, Mkg, qoff, causal, accumulate;
   float scale_log2;
 };
 
+constexpr int KS_STAGES = 4;
+constexpr int KS_STAGE_BYTES = 4096 + 4 * 256;  // Q tile, then one 64-float lse copy per wave
+
 template <bool BF16>
 __global__ __launch_bounds__(256) void key_score_kernel(KeyScoreArgs a) {
-  __shared__ float red[4][4][64];
-  const int Mk = a.Mk;
-  const int logical = static_cast<int>(xcd_remap(blockIdx.x, static_cast<int64_t>(a.BH) * Mk));
-  const int bh = logical / Mk;
-  const int j = logical - bh * Mk;  // causal: block 0 sees the most queries, first
+  __shared__ __attribute__((aligned(16))) char ring[KS_STAGES * KS_STAGE_BYTES];
+  const int logical = static_cast<int>(xcd_remap(blockIdx.x, static_cast<int64_t>(a.BH) * a.Mkg));
+  const int bh = logical / a.Mkg;
+  const int jg = logical - bh * a.Mkg;  // causal: group 0 sees the most queries, first
   const int b = bh / a.H, hh = bh - (bh / a.H) * a.H;
   const int hk = hh / a.group;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int lane = lane_id(), l16 = lane & 15, g = lane >> 4;
+  const int j = 4 * jg + w;  // this wave's key block (none when j >= Mk)
   const float c = a.scale_log2;
   constexpr float LOG2E = 1.4426950408889634f;
 
@@ -753,80 +759,96 @@ __global__ __launch_bounds__(256) void key_score_kernel(KeyScoreArgs a) {
                                : u32x4{0u, 0u, 0u, 0u};
   }
 
-  // Query tiles that see block j: queries t with t + qoff >= its first key.
-  const int t_first = a.causal ? j * BS - a.qoff : 0;
-  const int tile0 = t_first <= 0 ? 0 : t_first / 16;
+  // Query tiles that see the group's first block, and this wave's first.
+  auto first_tile = [&](int blk) {
+    const int t_first = a.causal ? blk * BS - a.qoff : 0;
+    return t_first <= 0 ? 0 : t_first / 16;
+  };
+  const int tile0 = first_tile(4 * jg);
+  const int my0 = first_tile(j);
   const int ntiles = (a.Nq + 15) / 16;
+  const int nt = ntiles > tile0 ? ntiles - tile0 : 0;
 
-  auto load_tile = [&](int tile, u32x4 (&qop)[4], float (&l2)[4]) {
-    const int q = 16 * tile + l16;
+  // Staging of tile tile0 + it: wave w moves Q dims 32 w .. 32 w + 31 of the
+  // tile's 16 queries (lane L: query L % 16, dims 32 w + 8 (L / 16) .. + 7,
+  // landing at 16 L: the A operand of MFMA k-step w) and its own lse copy.
+  auto issue = [&](int it) {
+    char* st = ring + (it % KS_STAGES) * KS_STAGE_BYTES;
+    const int q = 16 * (tile0 + it) + l16;
     const int qc = q < a.Nq ? q : a.Nq - 1;  // clamped, masked below
-#pragma unroll
-    for (int ds = 0; ds < 4; ++ds)
-      qop[ds] = *reinterpret_cast<const u32x4*>(qb + qc * a.qs[2] + 32 * ds + 8 * g);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = 16 * tile + 4 * g + r;
-      l2[r] = lb[t < a.Nq ? t : a.Nq - 1] * LOG2E;
-    }
+    __builtin_amdgcn_global_load_lds(qb + qc * a.qs[2] + 32 * w + 8 * g,
+                                     (lds_void*)(st + 1024 * w), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(lb + qc, (lds_void*)(st + 4096 + 256 * w), 4, 0, 0);
   };
 
   float colsum[4] = {0.f, 0.f, 0.f, 0.f};
-  int tile = tile0 + w;
-  if (tile < ntiles) {
+  const bool has_keys = j < a.Mk;
+  for (int it = 0; it < KS_STAGES - 1 && it < nt; ++it) issue(it);
+  // Tile it lives in stage it % 4, a compile-time constant below, so the
+  // compiler sees the staging of tile it + 3 cannot alias this tile's reads.
+  auto step = [&](int it, auto stage_tag) {
+    constexpr int S = decltype(stage_tag)::value;
+    const int ahead = nt - 1 - it;  // tiles it + 1, it + 2 may be in flight (2 loads each)
+    if (ahead >= 2)
+      __builtin_amdgcn_s_waitcnt(0x0f74);  // vmcnt(4)
+    else if (ahead == 1)
+      __builtin_amdgcn_s_waitcnt(0x0f72);  // vmcnt(2)
+    else
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    __builtin_amdgcn_s_barrier();  // every wave's part of tile it landed; stage (S + 3) % 4 is free
+    if (it + KS_STAGES - 1 < nt) issue(it + KS_STAGES - 1);
+    const int tile = tile0 + it;
+    if (!has_keys || tile < my0) return;
+    const char* st = ring + S * KS_STAGE_BYTES;
     u32x4 qop[4];
-    float l2[4];
-    load_tile(tile, qop, l2);
-    for (; tile < ntiles; tile += 4) {
-      u32x4 qn[4];
-      float ln[4];
-      const int next = tile + 4 < ntiles ? tile + 4 : tile;
-      load_tile(next, qn, ln);  // one tile ahead (a repeat of this tile at the end)
-      f32x4 sc[4];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        sc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ds = 0; ds < 4; ++ds) qop[ds] = reinterpret_cast<const u32x4*>(st + 1024 * ds)[lane];
+    const f32x4 lv = reinterpret_cast<const f32x4*>(st + 4096 + 256 * w)[g];
+    f32x4 sc[4];
 #pragma unroll
-        for (int ds = 0; ds < 4; ++ds) sc[kt] = mfma16<BF16>(qop[ds], kop[kt][ds], sc[kt]);
-      }
-      // sc[kt][r]: query 16 tile + 4 g + r, key j BS + 16 kt + l16.
-      const int t0 = 16 * tile + 4 * g;
-      const bool edge = 16 * tile + 15 >= a.Nq || (j + 1) * BS > a.Nk ||
-                        (a.causal && j * BS + BS - 1 > 16 * tile + a.qoff);
+    for (int kt = 0; kt < 4; ++kt) {
+      sc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        const int key = j * BS + 16 * kt + l16;
+      for (int ds = 0; ds < 4; ++ds) sc[kt] = mfma16<BF16>(qop[ds], kop[kt][ds], sc[kt]);
+    }
+    // sc[kt][r]: query 16 tile + 4 g + r, key j BS + 16 kt + l16.
+    const int t0 = 16 * tile + 4 * g;
+    const bool edge = 16 * tile + 15 >= a.Nq || (j + 1) * BS > a.Nk ||
+                      (a.causal && j * BS + BS - 1 > 16 * tile + a.qoff);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][r], c, -l2[r]));
-          if (edge) {
-            const int t = t0 + r;
-            if (t >= a.Nq || key >= a.Nk || (a.causal && key > t + a.qoff)) p = 0.f;
-          }
-          colsum[kt] += p;
+    for (int kt = 0; kt < 4; ++kt) {
+      const int key = j * BS + 16 * kt + l16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][r], c, -lv[r] * LOG2E));
+        if (edge) {
+          const int t = t0 + r;
+          if (t >= a.Nq || key >= a.Nk || (a.causal && key > t + a.qoff)) p = 0.f;
         }
+        colsum[kt] += p;
       }
-#pragma unroll
-      for (int ds = 0; ds < 4; ++ds) qop[ds] = qn[ds];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) l2[r] = ln[r];
     }
+  };
+  for (int it = 0; it < nt; it += KS_STAGES) {
+    step(it, std::integral_constant<int, 0>{});
+    if (it + 1 < nt) step(it + 1, std::integral_constant<int, 1>{});
+    if (it + 2 < nt) step(it + 2, std::integral_constant<int, 2>{});
+    if (it + 3 < nt) step(it + 3, std::integral_constant<int, 3>{});
   }
+  // Key 16 kt + l16: add the four query-lane groups (lanes l16 + 16 g) in a
+  // fixed order; lane l writes key l of the block.
+  float mine = 0.f;
 #pragma unroll
-  for (int kt = 0; kt < 4; ++kt) red[w][kt][lane] = colsum[kt];
-  __syncthreads();
-  if (w == 0) {
-    const int kt = lane >> 4, cix = lane & 15;
-    float sum = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < 4; ++ww)
-#pragma unroll
-      for (int gg = 0; gg < 4; ++gg) sum += red[ww][kt][16 * gg + cix];
-    const int key = j * BS + lane;
-    if (key < a.Nk) {
-      float* dst = a.score + b * a.ss[0] + hh * a.ss[1] + key;
-      *dst = a.accumulate ? *dst + sum : sum;
-    }
+  for (int kt = 0; kt < 4; ++kt) {
+    float sum = colsum[kt];
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    if (g == kt) mine = sum;
+  }
+  const int key = j * BS + lane;
+  if (has_keys && key < a.Nk) {
+    float* dst = a.score + b * a.ss[0] + hh * a.ss[1] + key;
+    *dst = a.accumulate ? *dst + mine : mine;
   }
 }
 
@@ -1199,11 +1221,12 @@ extern "C" cab_status_t cab_attn_key_scores(
   a.Nq = static_cast<int32_t>(N_q);
   a.Nk = static_cast<int32_t>(N_k);
   a.Mk = static_cast<int32_t>(ceil_div(N_k, BS));
+  a.Mkg = static_cast<int32_t>(ceil_div(a.Mk, 4));
   a.qoff = static_cast<int32_t>(N_k - N_q);
   a.causal = causal ? 1 : 0;
   a.accumulate = accumulate ? 1 : 0;
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
-  const dim3 grid(static_cast<unsigned>(B * H * a.Mk));
+  const dim3 grid(static_cast<unsigned>(B * H * a.Mkg));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == CAB_BF16)
     key_score_kernel<true><<<grid, 256, 0, s>>>(a);
