@@ -706,7 +706,7 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
 // the natural-log lse of attn_fwd_kernel's rows. One workgroup of 4 waves per
 // (b, h, group of 4 key blocks); wave w holds block 4 g + w's 64 keys as the
 // B operand of S = Q K^T (K^T tiles in 16 registers x 4). The four waves walk
-// the same 16-query tiles: each tile's Q (4 KB, MFMA operand order) and lse
+// the same 16-query tiles, last to first: each tile's Q (4 KB, MFMA operand order) and lse
 // (16 floats, one copy per wave) are staged once per workgroup into a ring
 // of 4 LDS stages by global_load_lds, three tiles ahead, so the texture path
 // carries a quarter of the bytes per MFMA of one wave per key block. Per
@@ -769,12 +769,15 @@ __global__ __launch_bounds__(256) void key_score_kernel(KeyScoreArgs a) {
   const int ntiles = (a.Nq + 15) / 16;
   const int nt = ntiles > tile0 ? ntiles - tile0 : 0;
 
-  // Staging of tile tile0 + it: wave w moves Q dims 32 w .. 32 w + 31 of the
+  // Tiles are walked from the last one down, so the workgroups of a head,
+  // which start together, read the same tiles at about the same time (L2).
+  auto tile_of = [&](int it) { return ntiles - 1 - it; };
+  // Staging of tile tile_of(it): wave w moves Q dims 32 w .. 32 w + 31 of the
   // tile's 16 queries (lane L: query L % 16, dims 32 w + 8 (L / 16) .. + 7,
   // landing at 16 L: the A operand of MFMA k-step w) and its own lse copy.
   auto issue = [&](int it) {
     char* st = ring + (it % KS_STAGES) * KS_STAGE_BYTES;
-    const int q = 16 * (tile0 + it) + l16;
+    const int q = 16 * tile_of(it) + l16;
     const int qc = q < a.Nq ? q : a.Nq - 1;  // clamped, masked below
     __builtin_amdgcn_global_load_lds(qb + qc * a.qs[2] + 32 * w + 8 * g,
                                      (lds_void*)(st + 1024 * w), 16, 0, 0);
@@ -797,13 +800,16 @@ __global__ __launch_bounds__(256) void key_score_kernel(KeyScoreArgs a) {
       __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
     __builtin_amdgcn_s_barrier();  // every wave's part of tile it landed; stage (S + 3) % 4 is free
     if (it + KS_STAGES - 1 < nt) issue(it + KS_STAGES - 1);
-    const int tile = tile0 + it;
+    const int tile = tile_of(it);
     if (!has_keys || tile < my0) return;
     const char* st = ring + S * KS_STAGE_BYTES;
     u32x4 qop[4];
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) qop[ds] = reinterpret_cast<const u32x4*>(st + 1024 * ds)[lane];
     const f32x4 lv = reinterpret_cast<const f32x4*>(st + 4096 + 256 * w)[g];
+    float nl[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) nl[r] = -lv[r] * LOG2E;
     f32x4 sc[4];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
@@ -820,7 +826,7 @@ __global__ __launch_bounds__(256) void key_score_kernel(KeyScoreArgs a) {
       const int key = j * BS + 16 * kt + l16;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][r], c, -lv[r] * LOG2E));
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][r], c, nl[r]));
         if (edge) {
           const int t = t0 + r;
           if (t >= a.Nq || key >= a.Nk || (a.causal && key > t + a.qoff)) p = 0.f;
