@@ -728,10 +728,11 @@ struct KeyScoreArgs {
 };
 
 constexpr int KS_STAGES = 4;
+constexpr int KS_WAVES = 4;  // key blocks (waves) sharing each staged query tile (8 measured slower)
 constexpr int KS_STAGE_BYTES = 4096 + 4 * 256;  // Q tile, then one 64-float lse copy per wave
 
-template <bool BF16>
-__global__ __launch_bounds__(256) void key_score_kernel(KeyScoreArgs a) {
+template <bool BF16, int NW>
+__global__ __launch_bounds__(64 * NW) void key_score_kernel(KeyScoreArgs a) {
   __shared__ __attribute__((aligned(16))) char ring[KS_STAGES * KS_STAGE_BYTES];
   const int logical = static_cast<int>(xcd_remap(blockIdx.x, static_cast<int64_t>(a.BH) * a.Mkg));
   const int bh = logical / a.Mkg;
@@ -740,7 +741,7 @@ __global__ __launch_bounds__(256) void key_score_kernel(KeyScoreArgs a) {
   const int hk = hh / a.group;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int lane = lane_id(), l16 = lane & 15, g = lane >> 4;
-  const int j = 4 * jg + w;  // this wave's key block (none when j >= Mk)
+  const int j = NW * jg + w;  // this wave's key block (none when j >= Mk)
   const float c = a.scale_log2;
   constexpr float LOG2E = 1.4426950408889634f;
 
@@ -764,7 +765,7 @@ __global__ __launch_bounds__(256) void key_score_kernel(KeyScoreArgs a) {
     const int t_first = a.causal ? blk * BS - a.qoff : 0;
     return t_first <= 0 ? 0 : t_first / 16;
   };
-  const int tile0 = first_tile(4 * jg);
+  const int tile0 = first_tile(NW * jg);
   const int my0 = first_tile(j);
   const int ntiles = (a.Nq + 15) / 16;
   const int nt = ntiles > tile0 ? ntiles - tile0 : 0;
@@ -772,10 +773,13 @@ __global__ __launch_bounds__(256) void key_score_kernel(KeyScoreArgs a) {
   // Tiles are walked from the last one down, so the workgroups of a head,
   // which start together, read the same tiles at about the same time (L2).
   auto tile_of = [&](int it) { return ntiles - 1 - it; };
-  // Staging of tile tile_of(it): wave w moves Q dims 32 w .. 32 w + 31 of the
-  // tile's 16 queries (lane L: query L % 16, dims 32 w + 8 (L / 16) .. + 7,
-  // landing at 16 L: the A operand of MFMA k-step w) and its own lse copy.
+  // Staging of tile tile_of(it): wave w < 4 moves Q dims 32 w .. 32 w + 31
+  // of the tile's 16 queries (lane L: query L % 16, dims 32 w + 8 (L / 16)
+  // .. + 7, landing at 16 L: the A operand of MFMA k-step w) and lse copy w;
+  // waves 4 .. 7 (NW = 8) stage nothing and read lse copy w % 4.
+  const bool stager = w < 4;
   auto issue = [&](int it) {
+    if (!stager) return;
     char* st = ring + (it % KS_STAGES) * KS_STAGE_BYTES;
     const int q = 16 * tile_of(it) + l16;
     const int qc = q < a.Nq ? q : a.Nq - 1;  // clamped, masked below
@@ -791,7 +795,7 @@ __global__ __launch_bounds__(256) void key_score_kernel(KeyScoreArgs a) {
   // compiler sees the staging of tile it + 3 cannot alias this tile's reads.
   auto step = [&](int it, auto stage_tag) {
     constexpr int S = decltype(stage_tag)::value;
-    const int ahead = nt - 1 - it;  // tiles it + 1, it + 2 may be in flight (2 loads each)
+    const int ahead = stager ? nt - 1 - it : 0;  // tiles it + 1, it + 2 may be in flight
     if (ahead >= 2)
       __builtin_amdgcn_s_waitcnt(0x0f74);  // vmcnt(4)
     else if (ahead == 1)
@@ -806,7 +810,7 @@ __global__ __launch_bounds__(256) void key_score_kernel(KeyScoreArgs a) {
     u32x4 qop[4];
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) qop[ds] = reinterpret_cast<const u32x4*>(st + 1024 * ds)[lane];
-    const f32x4 lv = reinterpret_cast<const f32x4*>(st + 4096 + 256 * w)[g];
+    const f32x4 lv = reinterpret_cast<const f32x4*>(st + 4096 + 256 * (w & 3))[g];
     float nl[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) nl[r] = -lv[r] * LOG2E;
@@ -1227,7 +1231,7 @@ extern "C" cab_status_t cab_attn_key_scores(
   a.Nq = static_cast<int32_t>(N_q);
   a.Nk = static_cast<int32_t>(N_k);
   a.Mk = static_cast<int32_t>(ceil_div(N_k, BS));
-  a.Mkg = static_cast<int32_t>(ceil_div(a.Mk, 4));
+  a.Mkg = static_cast<int32_t>(ceil_div(a.Mk, KS_WAVES));
   a.qoff = static_cast<int32_t>(N_k - N_q);
   a.causal = causal ? 1 : 0;
   a.accumulate = accumulate ? 1 : 0;
@@ -1235,8 +1239,8 @@ extern "C" cab_status_t cab_attn_key_scores(
   const dim3 grid(static_cast<unsigned>(B * H * a.Mkg));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == CAB_BF16)
-    key_score_kernel<true><<<grid, 256, 0, s>>>(a);
+    key_score_kernel<true, KS_WAVES><<<grid, 64 * KS_WAVES, 0, s>>>(a);
   else
-    key_score_kernel<false><<<grid, 256, 0, s>>>(a);
+    key_score_kernel<false, KS_WAVES><<<grid, 64 * KS_WAVES, 0, s>>>(a);
   return launch_status(fn);
 }
