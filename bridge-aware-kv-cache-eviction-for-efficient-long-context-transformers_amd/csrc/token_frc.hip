@@ -15,7 +15,8 @@
 // T_i = (sum_j relu(kn_i . kn_j) S_j) / (r_i + 1e-8). keys_prep_kernel
 // writes kn as bf16 hi/lo planes in MFMA operand order; gram_kernel<PASS>
 // computes 32x32 tiles of kn kn^T on MFMA (hi*hi + hi*lo + lo*hi, fp32
-// accumulate) and folds each tile into per-row sums of relu(g) * w_j
+// accumulate; column operands staged once per workgroup through LDS) and
+// folds each tile into per-row sums of relu(g) * w_j
 // (w = 1, then w = S); gram_finalize_kernel adds the column-split partials
 // in a fixed order. Algorithmic work: 2 N^2 D flops per Gram pass.
 #include "cab_internal.h"
@@ -272,14 +273,30 @@ struct GramArgs {
   int64_t Np, tiles, col_tiles;
 };
 
-// Wave w of workgroup (x, y) owns row tile 4x + w and walks column tiles
-// [y col_tiles, (y + 1) col_tiles): each 32x32 tile of kn kn^T is folded
-// into 16 per-lane row partials (lane l: column l % 32, rows
-// 8 (e / 4) + 4 (l / 32) + e % 4), added over the lanes at the end.
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int GRAM_STAGES = 3;
+
+// Wave w of workgroup (x, y) owns row tile 4x + w (its A operands in
+// registers) and the four waves walk the same column tiles
+// [y col_tiles, (y + 1) col_tiles). Each column tile's B operands (hi and
+// lo, 1 KB per k-step and plane) and, in pass 1, its 32 weights are staged
+// once per workgroup into a ring of three LDS stages by global_load_lds, two
+// tiles ahead (wave w moves k-steps w DK / 2 .. of plane w / 2). Each 32x32
+// tile of kn kn^T is folded into 16 per-lane row partials (lane l: column
+// l % 32, rows 8 (e / 4) + 4 (l / 32) + e % 4), added over the lanes at the
+// end.
 template <int DK, int PASS>
 __global__ __launch_bounds__(256, DK <= 8 ? 2 : 1) void gram_kernel(GramArgs a) {
+  constexpr int PLANE_BYTES = DK * 1024;           // one plane's k-steps of a column tile
+  constexpr int STAGE_BYTES = 2 * PLANE_BYTES + 1024;  // hi, lo, 4 weight copies of 256 B
+  constexpr int PER_WAVE = DK / 2;                 // 1 KB operand loads per wave and tile
+  constexpr int NDMA = PER_WAVE + (PASS == 1 ? 1 : 0);
+  static_assert(NDMA < 16, "vmcnt immediate");
+  __shared__ __attribute__((aligned(16))) char ring[GRAM_STAGES * STAGE_BYTES];
   const int lane = lane_id();
-  const int64_t rt = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int64_t rt = static_cast<int64_t>(blockIdx.x) * 4 + w;
   u32x4 ah[DK], al[DK];
 #pragma unroll
   for (int s = 0; s < DK; ++s) {
@@ -291,26 +308,54 @@ __global__ __launch_bounds__(256, DK <= 8 ? 2 : 1) void gram_kernel(GramArgs a) 
   for (int e = 0; e < 16; ++e) p[e] = 0.f;
   const int64_t c0 = static_cast<int64_t>(blockIdx.y) * a.col_tiles;
   const int64_t c1 = c0 + a.col_tiles < a.tiles ? c0 + a.col_tiles : a.tiles;
-  for (int64_t ct = c0; ct < c1; ++ct) {
-    u32x4 bh[DK], bl[DK];
+  const int nt = static_cast<int>(c1 - c0);
+
+  const int plane = (w * PER_WAVE) / DK, s0 = (w * PER_WAVE) % DK;
+  const u32x4* src_plane = plane == 0 ? a.hi : a.lo;
+  auto issue = [&](int it) {
+    const int64_t ct = c0 + it;
+    char* st = ring + (it % GRAM_STAGES) * STAGE_BYTES;
 #pragma unroll
-    for (int s = 0; s < DK; ++s) {
-      bh[s] = a.hi[(ct * DK + s) * 64 + lane];
-      bl[s] = a.lo[(ct * DK + s) * 64 + lane];
-    }
-    const float wc = PASS == 0 ? 1.f : a.w[ct * 32 + (lane & 31)];
+    for (int q = 0; q < PER_WAVE; ++q)
+      __builtin_amdgcn_global_load_lds(src_plane + (ct * DK + s0 + q) * 64 + lane,
+                                       (lds_void*)(st + plane * PLANE_BYTES + (s0 + q) * 1024), 16,
+                                       0, 0);
+    if constexpr (PASS == 1)
+      __builtin_amdgcn_global_load_lds(a.w + ct * 32 + (lane & 31),
+                                       (lds_void*)(st + 2 * PLANE_BYTES + 256 * w), 4, 0, 0);
+  };
+  for (int it = 0; it < GRAM_STAGES - 1 && it < nt; ++it) issue(it);
+  // Tile it lives in stage it % 3, a compile-time constant below, so the
+  // compiler sees the staging of tile it + 2 cannot alias this tile's reads.
+  auto step = [&](int it, auto stage_tag) {
+    constexpr int S = decltype(stage_tag)::value;
+    if (it + 1 < nt)
+      __builtin_amdgcn_s_waitcnt(0x0f70 | NDMA);  // vmcnt(NDMA): tile it + 1 may be in flight
+    else
+      __builtin_amdgcn_s_waitcnt(0x0f70);         // vmcnt(0)
+    __builtin_amdgcn_s_barrier();  // every wave's part of tile it landed; stage (S + 2) % 3 is free
+    if (it + GRAM_STAGES - 1 < nt) issue(it + GRAM_STAGES - 1);
+    const char* st = ring + S * STAGE_BYTES;
+    const float wc = PASS == 0 ? 1.f : reinterpret_cast<const float*>(st + 2 * PLANE_BYTES + 256 * w)[lane & 31];
     f32x16 acc = {};
 #pragma unroll
     for (int s = 0; s < DK; ++s) {
+      const u32x4 bh = reinterpret_cast<const u32x4*>(st + s * 1024)[lane];
+      const u32x4 bl = reinterpret_cast<const u32x4*>(st + PLANE_BYTES + s * 1024)[lane];
       acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, al[s]),
-                                                    __builtin_bit_cast(bf16x8, bh[s]), acc, 0, 0, 0);
+                                                    __builtin_bit_cast(bf16x8, bh), acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ah[s]),
-                                                    __builtin_bit_cast(bf16x8, bl[s]), acc, 0, 0, 0);
+                                                    __builtin_bit_cast(bf16x8, bl), acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ah[s]),
-                                                    __builtin_bit_cast(bf16x8, bh[s]), acc, 0, 0, 0);
+                                                    __builtin_bit_cast(bf16x8, bh), acc, 0, 0, 0);
     }
 #pragma unroll
     for (int e = 0; e < 16; ++e) p[e] = fmaf(fmaxf(acc[e], 0.f), wc, p[e]);
+  };
+  for (int it = 0; it < nt; it += GRAM_STAGES) {
+    step(it, std::integral_constant<int, 0>{});
+    if (it + 1 < nt) step(it + 1, std::integral_constant<int, 1>{});
+    if (it + 2 < nt) step(it + 2, std::integral_constant<int, 2>{});
   }
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
