@@ -173,7 +173,8 @@ __global__ __launch_bounds__(256) void symmetrize_kernel(SymArgs a) {
 // Key form
 // ---------------------------------------------------------------------------
 
-constexpr int GRAM_ROWS = 128;  // rows per workgroup (4 waves x 32)
+constexpr int GRAM_WAVES = 8;                // waves (32-row tiles) per Gram workgroup
+constexpr int GRAM_ROWS = 32 * GRAM_WAVES;   // rows per workgroup
 
 // Operand planes: for row tile t (32 rows) and k-step s (16 dims), lane
 // L = (row % 32) + 32 * h holds dims 16 s + 8 h .. + 7 as one 16-byte value
@@ -277,26 +278,27 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int GRAM_STAGES = 3;
 
-// Wave w of workgroup (x, y) owns row tile 4x + w (its A operands in
-// registers) and the four waves walk the same column tiles
+// Wave w of workgroup (x, y) owns row tile GRAM_WAVES x + w (its A operands
+// in registers) and the waves walk the same column tiles
 // [y col_tiles, (y + 1) col_tiles). Each column tile's B operands (hi and
 // lo, 1 KB per k-step and plane) and, in pass 1, its 32 weights are staged
 // once per workgroup into a ring of three LDS stages by global_load_lds, two
-// tiles ahead (wave w moves k-steps w DK / 2 .. of plane w / 2). Each 32x32
+// tiles ahead (the waves split the 2 DK 1 KB loads evenly). Each 32x32
 // tile of kn kn^T is folded into 16 per-lane row partials (lane l: column
 // l % 32, rows 8 (e / 4) + 4 (l / 32) + e % 4), added over the lanes at the
 // end.
 template <int DK, int PASS>
-__global__ __launch_bounds__(256, DK <= 8 ? 2 : 1) void gram_kernel(GramArgs a) {
+__global__ __launch_bounds__(64 * GRAM_WAVES) void gram_kernel(GramArgs a) {
   constexpr int PLANE_BYTES = DK * 1024;           // one plane's k-steps of a column tile
-  constexpr int STAGE_BYTES = 2 * PLANE_BYTES + 1024;  // hi, lo, 4 weight copies of 256 B
-  constexpr int PER_WAVE = DK / 2;                 // 1 KB operand loads per wave and tile
+  constexpr int STAGE_BYTES = 2 * PLANE_BYTES + 256 * GRAM_WAVES;  // hi, lo, weight copies
+  constexpr int PER_WAVE = 2 * DK / GRAM_WAVES;    // 1 KB operand loads per wave and tile
+  static_assert(PER_WAVE * GRAM_WAVES == 2 * DK, "operand loads split evenly over the waves");
   constexpr int NDMA = PER_WAVE + (PASS == 1 ? 1 : 0);
   static_assert(NDMA < 16, "vmcnt immediate");
   __shared__ __attribute__((aligned(16))) char ring[GRAM_STAGES * STAGE_BYTES];
   const int lane = lane_id();
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-  const int64_t rt = static_cast<int64_t>(blockIdx.x) * 4 + w;
+  const int64_t rt = static_cast<int64_t>(blockIdx.x) * GRAM_WAVES + w;
   u32x4 ah[DK], al[DK];
 #pragma unroll
   for (int s = 0; s < DK; ++s) {
@@ -430,7 +432,7 @@ cab_status_t launch_rows(const void* A, int64_t n, int64_t lda, float* s, float*
 template <int DK, int PASS>
 void launch_gram(const GramArgs& g, const KeyLayout& L, hipStream_t st) {
   gram_kernel<DK, PASS><<<dim3(static_cast<unsigned>(L.Np / GRAM_ROWS), static_cast<unsigned>(L.cs)),
-                          256, 0, st>>>(g);
+                          64 * GRAM_WAVES, 0, st>>>(g);
 }
 
 }  // namespace
