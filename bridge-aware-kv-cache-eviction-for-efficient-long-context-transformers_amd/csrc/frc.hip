@@ -164,39 +164,58 @@ __global__ __launch_bounds__(256) void affinity_kernel(AffArgs a) {
       mn = a.mm[bh * 2 + 0];
       mx = a.mm[bh * 2 + 1];
     }
-    const size_t pbase = static_cast<size_t>(bh) * a.Mp * a.Mp;
+    // The normalised 64 x 64 tile goes through LDS so that every plane is
+    // written as whole 16-byte row chunks: X rows from the tile's rows, XT
+    // rows from its columns (zero outside M: the planes are Mp x Mp).
+    __shared__ float stile[AT][AT + 1];
     float rowpart[16];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      uint32_t hi2[2], lo2[2];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int e = 4 * g + r;
-        const int64_t i = row0 + 8 * g + 4 * half + r;
-        float v = 0.f;
-        if (i < a.M && j < a.M) {
-          v = acc[e] * a.alpha;
-          if (a.normalization == CAB_NORM_MINMAX) v = normalize_minmax(v, mn, mx);
-          if (a.affinity) a.affinity[(static_cast<size_t>(bh) * a.M + i) * a.M + j] = v;
-        }
-        rowpart[e] = v;
-        const uint16_t h = f32_to_bf16(v);
-        const uint16_t l = f32_to_bf16(v - bf16_to_f32(h));
-        a.xhi[pbase + i * a.Mp + j] = h;
-        a.xlo[pbase + i * a.Mp + j] = l;
-        const uint32_t sh = (r & 1) * 16;
-        if ((r & 1) == 0) {
-          hi2[r >> 1] = h;
-          lo2[r >> 1] = l;
-        } else {
-          hi2[r >> 1] |= static_cast<uint32_t>(h) << sh;
-          lo2[r >> 1] |= static_cast<uint32_t>(l) << sh;
-        }
+    for (int e = 0; e < 16; ++e) {
+      const int il = wi * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+      const int64_t i = row0 + 8 * (e >> 2) + 4 * half + (e & 3);
+      float v = 0.f;
+      if (i < a.M && j < a.M) {
+        v = acc[e] * a.alpha;
+        if (a.normalization == CAB_NORM_MINMAX) v = normalize_minmax(v, mn, mx);
       }
-      // Transposed planes: XT[j][i .. i+3] as one 8-byte store.
-      const int64_t i0 = row0 + 8 * g + 4 * half;
-      *reinterpret_cast<u32x2*>(a.xthi + pbase + j * a.Mp + i0) = u32x2{hi2[0], hi2[1]};
-      *reinterpret_cast<u32x2*>(a.xtlo + pbase + j * a.Mp + i0) = u32x2{lo2[0], lo2[1]};
+      rowpart[e] = v;
+      stile[il][wj * 32 + (lane & 31)] = v;
+    }
+    __syncthreads();
+    const size_t pbase = static_cast<size_t>(bh) * a.Mp * a.Mp;
+    const int64_t ti0 = ti * AT, tj0 = tj * AT;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int cid = threadIdx.x + 256 * q;  // 64 rows x 8 chunks of 8 values
+      const int r = cid >> 3, c8 = (cid & 7) * 8;
+      u32x4 h4, l4, th4, tl4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x0 = stile[r][c8 + 2 * e], x1 = stile[r][c8 + 2 * e + 1];    // X row ti0 + r
+        const float y0 = stile[c8 + 2 * e][r], y1 = stile[c8 + 2 * e + 1][r];    // XT row tj0 + r
+        const uint16_t hx0 = f32_to_bf16(x0), hx1 = f32_to_bf16(x1);
+        const uint16_t hy0 = f32_to_bf16(y0), hy1 = f32_to_bf16(y1);
+        h4[e] = static_cast<uint32_t>(hx0) | (static_cast<uint32_t>(hx1) << 16);
+        l4[e] = static_cast<uint32_t>(f32_to_bf16(x0 - bf16_to_f32(hx0))) |
+                (static_cast<uint32_t>(f32_to_bf16(x1 - bf16_to_f32(hx1))) << 16);
+        th4[e] = static_cast<uint32_t>(hy0) | (static_cast<uint32_t>(hy1) << 16);
+        tl4[e] = static_cast<uint32_t>(f32_to_bf16(y0 - bf16_to_f32(hy0))) |
+                 (static_cast<uint32_t>(f32_to_bf16(y1 - bf16_to_f32(hy1))) << 16);
+      }
+      const size_t xo = pbase + static_cast<size_t>(ti0 + r) * a.Mp + tj0 + c8;
+      const size_t to = pbase + static_cast<size_t>(tj0 + r) * a.Mp + ti0 + c8;
+      *reinterpret_cast<u32x4*>(a.xhi + xo) = h4;
+      *reinterpret_cast<u32x4*>(a.xlo + xo) = l4;
+      *reinterpret_cast<u32x4*>(a.xthi + to) = th4;
+      *reinterpret_cast<u32x4*>(a.xtlo + to) = tl4;
+    }
+    if (a.affinity) {
+      // fp32 diagnostic, rows of the tile inside M (coalesced along j)
+      for (int e = threadIdx.x; e < AT * AT; e += 256) {
+        const int r = e >> 6, c = e & 63;
+        const int64_t i = ti0 + r, jj = tj0 + c;
+        if (i < a.M && jj < a.M) a.affinity[(static_cast<size_t>(bh) * a.M + i) * a.M + jj] = stile[r][c];
+      }
     }
     if (a.rspart) {
       // Row sums over the tile's 64 columns: 32 lanes per wave, 2 waves.
