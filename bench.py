@@ -417,6 +417,7 @@ def main() -> int:
     result_bridge = None
     result_fp32 = None
     result_evict = None
+    result_tfrc = None
     if not args.attn_only:
         # ---------------- config 4 in fp32 (split bf16 operands, fp32 output)
         q32, k32, v32 = (t.float() for t in (q, k, v))
