@@ -164,3 +164,64 @@ def test_caches_prune_to_the_selected_positions(cuda):
             assert torch.equal(cache.value_cache[0], cache.key_cache[0] + 0.5)
             assert len(cache.importance_tracker) in (len(pos), len(pos) - 1)
         assert cache.total_evictions > 3
+
+
+def test_cab_cache_reference_demo_replay(cuda):
+    """The reference's CABCache demo (cab_cache.py:270-327): 200 decode steps
+    over 4 layers, max_cache_size 100, sparsity 0.9, eviction interval 5,
+    random attention on layer 0. Every selection the cache makes is checked
+    bit for bit against the oracle on the same fp32 importance scores; after
+    every eviction each layer holds exactly its old rows at the kept
+    positions; the statistics follow the evictions."""
+    from cab_attention.cache import CABCache
+    cache = CABCache(max_cache_size=100, sparsity=0.9, local_ratio=0.3, bridge_ratio=0.2,
+                     importance_ratio=0.5, eviction_interval=5, device="cuda")
+    calls = []
+    policy = cache.eviction_policy
+    inner = policy.select_indices
+
+    def recording(cache_len, keep_size, importance_scores, attention_matrix=None, device="cuda"):
+        keep, diag = inner(cache_len, keep_size, importance_scores, attention_matrix, device)
+        sc = None if importance_scores is None else importance_scores.detach().float().cpu().numpy().copy()
+        calls.append((cache_len, keep_size, sc, keep.cpu().numpy()))
+        return keep, diag
+
+    policy.select_indices = recording
+    B, H, D, layers = 1, 8, 64, 4
+    g = torch.Generator().manual_seed(5)
+    ids = [[] for _ in range(layers)]  # token id of each stored row, per layer
+    evicted_tokens = 0
+    for step in range(200):
+        for layer in range(layers):
+            tok = float(step * 10 + layer)
+            kv = torch.full((B, H, 1, D), tok, device=cuda)
+            att = None
+            if layer == 0 and cache.get_seq_length(0) > 0:
+                n = cache.get_seq_length(0)
+                att = torch.rand((B, H, 1, n), generator=g).to(cuda)
+                att = att / att.sum(dim=-1, keepdim=True)
+            before = len(calls)
+            old = [list(x) for x in ids]
+            ids[layer].append(tok)
+            cache.update(kv, kv + 0.25, layer, att)
+            if len(calls) > before:  # an eviction: every layer keeps the same positions
+                cache_len, keep_size, sc, keep = calls[-1]
+                local = int(keep_size * 0.3)
+                bridge = int(keep_size * 0.2)
+                imp = keep_size - local - bridge
+                want, _, _ = O.evict_select(sc, cache_len, min(local, cache_len), imp,
+                                            min(bridge, cache_len), True, 1 if sc is not None else 3)
+                assert np.array_equal(keep, want), f"step {step} layer {layer}"
+                evicted_tokens += cache_len - keep.size
+                ids = [[row[int(k)] for k in keep] for row in (old[:layer] + [ids[layer]] + old[layer + 1:])]
+            for l2 in range(layers):
+                if l2 < len(cache.key_cache) and cache.key_cache[l2] is not None:
+                    got = cache.key_cache[l2][0, 0, :, 0].cpu().tolist()
+                    assert got == ids[l2], f"step {step} layer {l2}"
+                    assert torch.equal(cache.value_cache[l2], cache.key_cache[l2] + 0.25)
+    assert cache.total_evictions == len(calls) > 10
+    st = cache.get_stats()
+    assert st["total_evictions"] == len(calls)
+    assert st["total_tokens_evicted"] == evicted_tokens
+    assert st["total_tokens_processed"] == 200 * layers
+    assert len(cache) == cache.get_seq_length(0) <= int(100 * 1.1) + 1
