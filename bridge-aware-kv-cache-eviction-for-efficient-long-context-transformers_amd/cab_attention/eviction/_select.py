@@ -9,6 +9,7 @@ import torch
 from .. import _native as nat
 
 BRIDGE_NONE, BRIDGE_MEDIAN, BRIDGE_SCORES, BRIDGE_POSITIONAL = 0, 1, 2, 3
+MULTI_MIN = 1 << 15  # cache_len from which cab_evict_select needs its workspace
 
 
 def planned_counts(cache_len: int, local: int, imp: int, bridge: int, has_scores: bool,
@@ -52,11 +53,14 @@ def select_positions(cache_len: int, scores: torch.Tensor | None, local: int, im
     keep = torch.empty(max(cache_len, 1), dtype=torch.int64, device=dev)
     counts = torch.empty(4, dtype=torch.int32, device=dev)
     cat = torch.empty(max(cache_len, 1), dtype=torch.uint8, device=dev) if category else None
+    # Large caches run one workgroup per segment with a workspace.
+    wbytes = int(lib.cab_evict_select_workspace_bytes(cache_len)) if cache_len >= MULTI_MIN else 0
+    ws = torch.empty(wbytes, dtype=torch.uint8, device=dev) if wbytes else None
     with torch.cuda.device(dev):
         st = lib.cab_evict_select(nat.ptr(scores), 0 if scores is None else scores.numel(),
                                   nat.ptr(bridge_scores), cache_len, local, imp, bridge,
                                   int(bool(fallback)), mode, keep.data_ptr(), counts.data_ptr(),
-                                  nat.ptr(cat), nat.stream_ptr(dev))
+                                  nat.ptr(cat), nat.ptr(ws), wbytes, nat.stream_ptr(dev))
     nat.check("cab_evict_select", st)
     n_loc, n_imp, n_br = planned_counts(cache_len, local, imp, bridge, scores is not None,
                                         fallback, mode)

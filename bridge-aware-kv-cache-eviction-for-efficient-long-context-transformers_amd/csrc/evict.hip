@@ -464,6 +464,393 @@ __global__ __launch_bounds__(SEL_THREADS) void evict_select_kernel(SelArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Multi-workgroup selection (caches of MULTI_MIN positions and more). The
+// same selection as evict_select_kernel, spread over one workgroup per
+// MSEG-position segment: the kept set is a bitmap in the workspace (each
+// workgroup owns its segment's words), each radix pass adds its segment's
+// LDS histogram into a global histogram row, and every workgroup re-derives
+// the threshold from the rows of the earlier passes. Ranks in position order
+// come from per-segment counts (a prefix over the earlier segments) and,
+// inside a segment, the per-wave ballot ranks of the single-workgroup path.
+// ---------------------------------------------------------------------------
+constexpr int MSEG = 4096;           // positions per workgroup (4 waves x 1024)
+constexpr int MTHREADS = 256;
+constexpr int MULTI_MIN = 1 << 15;   // cache_len from which the multi-workgroup path runs
+constexpr int MHIST_ROWS = 9;        // importance 0..2, median 3..5, bridges 6..8
+
+struct MArgs {
+  const float* scores;
+  const float* bridge;
+  int64_t* keep;
+  int32_t* counts;
+  uint8_t* category;
+  uint32_t* bits;    // ceil(n / 32) words
+  uint32_t* hist;    // [MHIST_ROWS][SEL_BINS]
+  int32_t* segcnt;   // [G]
+  int32_t* state;    // [0]: NaN scores among the median's candidates
+  int32_t n, n_scores, G;
+  int32_t local, n_imp, n_br, imp_fallback_lo;  // imp_fallback_lo: first fallback position, or n
+};
+
+struct MStep {
+  KeySrc src;
+  int32_t hbase, pass, need;
+  int32_t med_hbase, med_need;  // KEY_DIST: the median's rows and rank
+  int32_t first, count;         // positional ranks
+  uint8_t cat;
+};
+
+struct Resolved {
+  uint32_t prefix;
+  int need;  // how many keys equal to prefix complete the selection (after 3 passes)
+  int eq;    // keys equal to prefix (after 3 passes)
+};
+
+// The threshold after npass recorded passes of the radix select for rank
+// need (histogram rows h0 ..); every thread of the workgroup gets it.
+__device__ Resolved resolve(const uint32_t* hist, int h0, int npass, int need, int* sm) {
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    uint32_t prefix = 0u;
+    int rem = need, eq = 0;
+    for (int p = 0; p < npass; ++p) {
+      const int shift = p == 0 ? 21 : p == 1 ? 10 : 0;
+      const int nb = p == 2 ? 1024 : 2048;
+      const uint32_t* h = hist + static_cast<int64_t>(h0 + p) * SEL_BINS;
+      const int per = nb / 64;
+      int sum = 0;
+      for (int b = 0; b < per; ++b) sum += static_cast<int>(h[lane * per + b]);
+      const int incl = wave_incl_scan(sum);
+      const uint64_t hit = __ballot(incl >= rem);
+      const int owner = hit ? __builtin_ctzll(hit) : 63;
+      const int run0 = __builtin_amdgcn_readlane(incl - sum, owner);
+      const int hv = lane < per ? static_cast<int>(h[owner * per + lane]) : 0;
+      const int incl2 = run0 + wave_incl_scan(hv);
+      const uint64_t hit2 = __ballot(lane < per && incl2 >= rem);
+      const int j = hit2 ? __builtin_ctzll(hit2) : per - 1;
+      const int below = __builtin_amdgcn_readlane(incl2 - hv, j);
+      eq = __builtin_amdgcn_readlane(hv, j);
+      prefix |= static_cast<uint32_t>(owner * per + j) << shift;
+      rem -= below;
+    }
+    if (lane == 0) {
+      sm[0] = static_cast<int>(prefix);
+      sm[1] = rem;
+      sm[2] = eq;
+    }
+  }
+  __syncthreads();
+  Resolved r{static_cast<uint32_t>(sm[0]), sm[1], sm[2]};
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ uint32_t prefix_mask(int npass) {
+  return npass == 0 ? 0u : npass == 1 ? 0xffe00000u : npass == 2 ? 0xfffffc00u : 0xffffffffu;
+}
+
+// This wave's positions of the workgroup's segment: [beg, end).
+__device__ __forceinline__ void mseg_wave(int n, int* beg, int* end) {
+  const int s0 = blockIdx.x * MSEG + (threadIdx.x >> 6) * (MSEG / 4);
+  *beg = s0 < n ? s0 : n;
+  *end = s0 + MSEG / 4 < n ? s0 + MSEG / 4 : n;
+}
+
+// Walks this wave's quarter of the segment in position order (256 positions
+// per step, lane l on 4l .. 4l + 3): f(p, cand, key), called by every lane.
+// sbits: the segment's bitmap words in LDS.
+template <int KIND, class F>
+__device__ __forceinline__ void mwalk(int n, const uint32_t* sbits, const KeySrc s, F f) {
+  int beg, end;
+  mseg_wave(n, &beg, &end);
+  const int lane4 = 4 * lane_id();
+  const int s0 = blockIdx.x * MSEG;
+#pragma unroll 1
+  for (int base = beg; base < end; base += 256) {
+    const int p = base + lane4;
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (KIND != KEY_NONE && p < end) x = load4(s, p, end);
+    uint32_t cand = 0u;
+    if (p < end) {
+      cand = ~(sbits[(p - s0) >> 5] >> (p & 31)) & 0xfu;
+      if (end - p < 4) cand &= (1u << (end - p)) - 1u;
+    }
+    u32x4 k = {0u, 0u, 0u, 0u};
+    if (KIND != KEY_NONE) {
+      k[0] = key_of<KIND>(x.x, s.med);
+      k[1] = key_of<KIND>(x.y, s.med);
+      k[2] = key_of<KIND>(x.z, s.med);
+      k[3] = key_of<KIND>(x.w, s.med);
+    }
+    f(p, cand, k);
+  }
+}
+
+__device__ __forceinline__ void mload_bits(const MArgs& a, uint32_t* sbits) {
+  const int w0 = blockIdx.x * (MSEG / 32), words = (a.n + 31) >> 5;
+  for (int t = threadIdx.x; t < MSEG / 32; t += MTHREADS) sbits[t] = w0 + t < words ? a.bits[w0 + t] : 0u;
+  __syncthreads();
+}
+
+__device__ __forceinline__ void mstore_bits(const MArgs& a, const uint32_t* sbits) {
+  __syncthreads();
+  const int w0 = blockIdx.x * (MSEG / 32), words = (a.n + 31) >> 5;
+  for (int t = threadIdx.x; t < MSEG / 32; t += MTHREADS)
+    if (w0 + t < words) a.bits[w0 + t] = sbits[t];
+}
+
+__device__ __forceinline__ void mmark(uint32_t* sbits, int p, uint32_t m, uint8_t* category, uint8_t cat) {
+  if (!m) return;
+  atomicOr(&sbits[(p - static_cast<int>(blockIdx.x) * MSEG) >> 5], m << (p & 31));
+  if (category)
+    for (int e = 0; e < 4; ++e)
+      if ((m >> e) & 1u) category[p + e] = cat;
+}
+
+// Sum of segcnt over the segments before this one.
+__device__ __forceinline__ int mseg_start(const MArgs& a, int* sm) {
+  int v = 0;
+  for (int g = threadIdx.x; g < static_cast<int>(blockIdx.x); g += MTHREADS) v += a.segcnt[g];
+  v = wave_sum(v);
+  if (lane_id() == 0) sm[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const int r = sm[0] + sm[1] + sm[2] + sm[3];
+  __syncthreads();
+  return r;
+}
+
+// Exclusive prefix of the four waves' totals, plus the workgroup's start.
+__device__ __forceinline__ int mwave_start(int mine, int* sm) {
+  if (lane_id() == 0) sm[threadIdx.x >> 6] = mine;
+  __syncthreads();
+  int s = 0;
+  for (int w = 0; w < static_cast<int>(threadIdx.x >> 6); ++w) s += sm[w];
+  __syncthreads();
+  return s;
+}
+
+// Bitmap words of the local window and (no scores) of the fallback range;
+// clears the histograms and counters.
+__global__ __launch_bounds__(MTHREADS) void msel_init_kernel(MArgs a) {
+  const int words = (a.n + 31) >> 5;
+  const int l0 = a.n - a.local, f0 = a.imp_fallback_lo;
+  for (int t = threadIdx.x; t < MSEG / 32; t += MTHREADS) {
+    const int w = blockIdx.x * (MSEG / 32) + t;
+    if (w >= words) continue;
+    uint32_t m = 0u;
+    for (int j = 0; j < 32; ++j) {
+      const int p = 32 * w + j;
+      if (p < a.n && (p >= l0 || (p >= f0 && p < l0))) m |= 1u << j;
+    }
+    a.bits[w] = m;
+  }
+  if (a.category) {
+    const int s0 = blockIdx.x * MSEG, s1 = s0 + MSEG < a.n ? s0 + MSEG : a.n;
+    for (int p = s0 + threadIdx.x; p < s1; p += MTHREADS) {
+      if (p >= l0) a.category[p] = 1;
+      else if (p >= f0) a.category[p] = 2;
+    }
+  }
+  for (int i = blockIdx.x * MTHREADS + threadIdx.x; i < MHIST_ROWS * SEL_BINS; i += a.G * MTHREADS)
+    a.hist[i] = 0u;
+  if (blockIdx.x == 0 && threadIdx.x == 0) a.state[0] = 0;
+}
+
+template <int KIND>
+__device__ __forceinline__ KeySrc msrc_resolved(const MArgs& a, const MStep& st, int* sm) {
+  KeySrc s = st.src;
+  if (KIND == KEY_DIST) {
+    const Resolved m = resolve(a.hist, st.med_hbase, 3, st.med_need, sm);
+    s.med = a.state[0] ? __uint_as_float(0x7fc00000u) : key_float(m.prefix);
+  }
+  return s;
+}
+
+// Radix pass st.pass of a selection: the segment's histogram of the
+// candidates matching the prefix of the earlier passes, added into row
+// hbase + pass.
+template <int KIND>
+__global__ __launch_bounds__(MTHREADS) void msel_hist_kernel(MArgs a, MStep st) {
+  __shared__ uint32_t sbits[MSEG / 32];
+  __shared__ uint32_t hist[SEL_BINS];
+  __shared__ int sm[4];
+  const KeySrc s = msrc_resolved<KIND>(a, st, sm);
+  const uint32_t prefix = st.pass ? resolve(a.hist, st.hbase, st.pass, st.need, sm).prefix : 0u;
+  const uint32_t mask = prefix_mask(st.pass);
+  const int shift = st.pass == 0 ? 21 : st.pass == 1 ? 10 : 0;
+  const uint32_t nbm = st.pass == 2 ? 1023u : 2047u;
+  for (int b = threadIdx.x; b < SEL_BINS; b += MTHREADS) hist[b] = 0u;
+  mload_bits(a, sbits);  // (its barrier also orders the clearing)
+  int nan = 0;
+  mwalk<KIND>(a.n, sbits, s, [&](int, uint32_t cand, u32x4 k) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool act = ((cand >> e) & 1u) && (k[e] & mask) == prefix;
+      hist_add(hist, act, (k[e] >> shift) & nbm);
+      if (KIND == KEY_ASC) nan += (act && k[e] == NAN_KEY) ? 1 : 0;
+    }
+  });
+  __syncthreads();
+  uint32_t* row = a.hist + static_cast<int64_t>(st.hbase + st.pass) * SEL_BINS;
+  for (int b = threadIdx.x; b < SEL_BINS; b += MTHREADS)
+    if (hist[b]) atomicAdd(&row[b], hist[b]);
+  if (KIND == KEY_ASC && st.pass == 0) {
+    nan = wave_sum(nan);
+    if (lane_id() == 0 && nan) atomicAdd(&a.state[0], nan);
+  }
+}
+
+// Keys below the threshold are kept; keys equal to it too when all of them
+// complete the selection, else their count per segment goes to segcnt.
+template <int KIND>
+__global__ __launch_bounds__(MTHREADS) void msel_mark_kernel(MArgs a, MStep st) {
+  __shared__ uint32_t sbits[MSEG / 32];
+  __shared__ int sm[4];
+  const KeySrc s = msrc_resolved<KIND>(a, st, sm);
+  const Resolved th = resolve(a.hist, st.hbase, 3, st.need, sm);
+  const bool all_eq = th.need == th.eq;
+  mload_bits(a, sbits);
+  int eq = 0;
+  mwalk<KIND>(a.n, sbits, s, [&](int p, uint32_t cand, u32x4 k) {
+    uint32_t m = 0u, q = 0u;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (!((cand >> e) & 1u)) continue;
+      if (k[e] < th.prefix) m |= 1u << e;
+      if (k[e] == th.prefix) q |= 1u << e;
+    }
+    if (all_eq)
+      m |= q;
+    else
+      eq += __popc(q);
+    mmark(sbits, p, m, a.category, st.cat);
+  });
+  mstore_bits(a, sbits);
+  eq = wave_sum(eq);
+  if (lane_id() == 0) sm[threadIdx.x >> 6] = eq;
+  __syncthreads();
+  if (threadIdx.x == 0) a.segcnt[blockIdx.x] = sm[0] + sm[1] + sm[2] + sm[3];
+}
+
+// Position-ordered marking of the candidates with q set whose global rank
+// lies in [first, first + count); wave_tot: the waves' counts of such
+// candidates, start: those of the earlier segments.
+template <int KIND, class Q>
+__device__ __forceinline__ void mmark_ranked(const MArgs& a, const KeySrc s, uint32_t* sbits, int start,
+                                             int first, int count, Q q_of, uint8_t cat, int* sm) {
+  int mine = 0;
+  mwalk<KIND>(a.n, sbits, s, [&](int, uint32_t cand, u32x4 k) { mine += __popc(q_of(cand, k)); });
+  int carry = start + mwave_start(wave_sum(mine), sm);
+  mwalk<KIND>(a.n, sbits, s, [&](int p, uint32_t cand, u32x4 k) {
+    const uint32_t q = q_of(cand, k);
+    int below, tot;
+    lane_offsets<3>(__popc(q), &below, &tot);
+    if (carry < first + count && carry + tot > first) {
+      uint32_t m = 0u;
+      int r = carry + below;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (!((q >> e) & 1u)) continue;
+        if (r >= first && r < first + count) m |= 1u << e;
+        ++r;
+      }
+      mmark(sbits, p, m, a.category, cat);
+    }
+    carry += tot;
+  });
+}
+
+// Ties: the first need keys equal to the threshold, in position order.
+template <int KIND>
+__global__ __launch_bounds__(MTHREADS) void msel_tie_kernel(MArgs a, MStep st) {
+  __shared__ uint32_t sbits[MSEG / 32];
+  __shared__ int sm[4];
+  const KeySrc s = msrc_resolved<KIND>(a, st, sm);
+  const Resolved th = resolve(a.hist, st.hbase, 3, st.need, sm);
+  if (th.need == th.eq) return;  // the mark pass kept them all (uniform)
+  const int start = mseg_start(a, sm);
+  if (start >= th.need) return;
+  mload_bits(a, sbits);
+  const uint32_t key = th.prefix;
+  mmark_ranked<KIND>(a, s, sbits, start, 0, th.need, [key](uint32_t cand, u32x4 k) {
+    uint32_t q = 0u;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (((cand >> e) & 1u) && k[e] == key) q |= 1u << e;
+    return q;
+  }, st.cat, sm);
+  mstore_bits(a, sbits);
+}
+
+// Positional bridges: candidates per segment, then ranks [first, first + count).
+__global__ __launch_bounds__(MTHREADS) void msel_rank_count_kernel(MArgs a) {
+  __shared__ uint32_t sbits[MSEG / 32];
+  __shared__ int sm[4];
+  mload_bits(a, sbits);
+  const KeySrc none = {nullptr, 0, 0.f};
+  int mine = 0;
+  mwalk<KEY_NONE>(a.n, sbits, none, [&](int, uint32_t cand, u32x4) { mine += __popc(cand); });
+  mine = wave_sum(mine);
+  if (lane_id() == 0) sm[threadIdx.x >> 6] = mine;
+  __syncthreads();
+  if (threadIdx.x == 0) a.segcnt[blockIdx.x] = sm[0] + sm[1] + sm[2] + sm[3];
+}
+
+__global__ __launch_bounds__(MTHREADS) void msel_rank_mark_kernel(MArgs a, MStep st) {
+  __shared__ uint32_t sbits[MSEG / 32];
+  __shared__ int sm[4];
+  const int start = mseg_start(a, sm);
+  if (start >= st.first + st.count) return;
+  mload_bits(a, sbits);
+  const KeySrc none = {nullptr, 0, 0.f};
+  mmark_ranked<KEY_NONE>(a, none, sbits, start, st.first, st.count,
+                         [](uint32_t cand, u32x4) { return cand; }, st.cat, sm);
+  mstore_bits(a, sbits);
+}
+
+// Kept positions per segment, then the ascending list, the evicted
+// categories and the counts.
+__global__ __launch_bounds__(MTHREADS) void msel_compact_count_kernel(MArgs a) {
+  __shared__ int sm[4];
+  const int w0 = blockIdx.x * (MSEG / 32), words = (a.n + 31) >> 5;
+  int c = 0;
+  for (int t = threadIdx.x; t < MSEG / 32; t += MTHREADS)
+    if (w0 + t < words) c += __popc(a.bits[w0 + t]);
+  c = wave_sum(c);
+  if (lane_id() == 0) sm[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) a.segcnt[blockIdx.x] = sm[0] + sm[1] + sm[2] + sm[3];
+}
+
+__global__ __launch_bounds__(MTHREADS) void msel_compact_write_kernel(MArgs a) {
+  __shared__ int sm[4];
+  const int start = mseg_start(a, sm);
+  const int words = (a.n + 31) >> 5;
+  // wave v: words 32 v .. 32 v + 31 of the segment, lane l < 32 one word
+  const int lane = lane_id();
+  const int w = blockIdx.x * (MSEG / 32) + (threadIdx.x >> 6) * 32 + lane;
+  const uint32_t bits = lane < 32 && w < words ? a.bits[w] : 0u;
+  int below, tot;
+  lane_offsets<6>(__popc(bits), &below, &tot);
+  const int pos = start + mwave_start(tot, sm) + below;
+  int64_t* out = a.keep + pos;
+  for (uint32_t m = bits; m; m &= m - 1) *out++ = 32 * w + __builtin_ctz(m);
+  if (a.category && lane < 32 && w < words) {
+    const int hi = 32 * w + 32 < a.n ? 32 * w + 32 : a.n;
+    for (int i = 32 * w; i < hi; ++i)
+      if (!((bits >> (i & 31)) & 1u)) a.category[i] = 0;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    int total = 0;
+    for (int g = 0; g < a.G; ++g) total += a.segcnt[g];
+    a.counts[0] = a.local;
+    a.counts[1] = a.n_imp;
+    a.counts[2] = a.n_br;
+    a.counts[3] = total;
+  }
+}
+
 // Bridge scores from an attention matrix A [n, n] (row stride `ld`) and the
 // importance positions (category == 2): from[j] = sum_{i imp} A[i, j],
 // to[j] = sum_{i imp} A[j, i], score[j] = from[j] to[j]. Fixed summation order.
@@ -514,12 +901,61 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(GatherArgs a) {
 
 using namespace cab;
 
+namespace {
+
+struct MLayout {
+  int64_t G;
+  size_t off_bits, off_hist, off_seg, off_state, total;
+};
+
+MLayout mlayout(int64_t n) {
+  MLayout L;
+  L.G = ceil_div(n > 0 ? n : 1, MSEG);
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += static_cast<size_t>(round_up(static_cast<int64_t>(bytes), 256));
+    return at;
+  };
+  L.off_bits = take(static_cast<size_t>(L.G) * (MSEG / 32) * 4);
+  L.off_hist = take(static_cast<size_t>(MHIST_ROWS) * SEL_BINS * 4);
+  L.off_seg = take(static_cast<size_t>(L.G) * 4);
+  L.off_state = take(64 * 4);
+  L.total = o;
+  return L;
+}
+
+// One radix selection (three histogram passes, the mark pass, the tie pass).
+template <int KIND>
+cab_status_t msel_select(const MArgs& a, MStep st, hipStream_t s, const char* fn) {
+  const dim3 grid(static_cast<unsigned>(a.G));
+  for (int pass = 0; pass < 3; ++pass) {
+    st.pass = pass;
+    msel_hist_kernel<KIND><<<grid, MTHREADS, 0, s>>>(a, st);
+    cab_status_t r = launch_status(fn);
+    if (r != CAB_OK) return r;
+  }
+  msel_mark_kernel<KIND><<<grid, MTHREADS, 0, s>>>(a, st);
+  cab_status_t r = launch_status(fn);
+  if (r != CAB_OK) return r;
+  msel_tie_kernel<KIND><<<grid, MTHREADS, 0, s>>>(a, st);
+  return launch_status(fn);
+}
+
+}  // namespace
+
+extern "C" size_t cab_evict_select_workspace_bytes(int64_t cache_len) {
+  if (cache_len < 0 || cache_len > SEL_MAX_LEN) return 0;
+  return mlayout(cache_len).total;
+}
+
 extern "C" cab_status_t cab_evict_select(const float* importance_scores, int64_t n_scores,
                                          const float* bridge_scores, int64_t cache_len,
                                          int32_t local_budget, int32_t importance_budget,
                                          int32_t bridge_budget, int importance_fallback,
                                          int bridge_mode, int64_t* keep_indices, int32_t* counts,
-                                         uint8_t* category, void* stream) {
+                                         uint8_t* category, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
   const char* fn = "cab_evict_select";
   clear_error();
   CAB_REQUIRE(cache_len >= 0 && cache_len <= SEL_MAX_LEN, CAB_ESHAPE,
@@ -535,20 +971,123 @@ extern "C" cab_status_t cab_evict_select(const float* importance_scores, int64_t
   CAB_REQUIRE(bridge_mode != 2 || bridge_scores != nullptr, CAB_EINVAL,
               "%s: bridge_mode 2 needs bridge scores", fn);
   CAB_REQUIRE(keep_indices != nullptr && counts != nullptr, CAB_EINVAL, "%s: null output", fn);
-  SelArgs a;
+  const bool multi = cache_len >= MULTI_MIN;
+  const MLayout L = mlayout(cache_len);
+  if (multi) {
+    CAB_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, CAB_EWORKSPACE,
+                "%s: workspace of %zu bytes given, %zu needed", fn, workspace_bytes, L.total);
+    CAB_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, CAB_EWORKSPACE,
+                "%s: workspace not 256-byte aligned", fn);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int32_t n = static_cast<int32_t>(cache_len);
+  const int32_t n_sc = static_cast<int32_t>(n_scores < cache_len ? n_scores : cache_len);
+  if (!multi) {
+    SelArgs a;
+    a.scores = importance_scores;
+    a.bridge = bridge_scores;
+    a.keep = keep_indices;
+    a.counts = counts;
+    a.category = category;
+    a.n = n;
+    a.n_scores = n_sc;
+    a.local = local_budget;
+    a.imp = importance_budget;
+    a.bridge_budget = bridge_budget;
+    a.imp_fallback = importance_fallback ? 1 : 0;
+    a.bridge_mode = bridge_mode;
+    evict_select_kernel<<<1, SEL_THREADS, 0, s>>>(a);
+    return launch_status(fn);
+  }
+
+  // The plan evict_select_kernel follows, known from the budgets alone.
+  const bool has_scores = importance_scores != nullptr;
+  const int32_t free0 = n - local_budget;
+  int32_t n_imp = 0, f0 = n;
+  if (has_scores) {
+    n_imp = importance_budget < free0 ? importance_budget : free0;
+  } else if (importance_fallback && importance_budget > 0) {
+    f0 = n - local_budget - importance_budget > 0 ? n - local_budget - importance_budget : 0;
+    n_imp = free0 - f0;
+  }
+  const int32_t free1 = free0 - n_imp;
+  int mode = bridge_mode;
+  if (mode == 2 && n_imp == 0) mode = has_scores ? 1 : 3;
+  if (mode == 1 && !has_scores) mode = 3;
+  int32_t n_br = 0;
+  if (bridge_budget > 0 && free1 > 0 && mode != 0) {
+    n_br = bridge_budget < free1 ? bridge_budget : free1;
+    if (mode == 3 && n_br > free1 - free1 / 3) n_br = free1 - free1 / 3;
+  }
+
+  char* ws = static_cast<char*>(workspace);
+  MArgs a;
   a.scores = importance_scores;
   a.bridge = bridge_scores;
   a.keep = keep_indices;
   a.counts = counts;
   a.category = category;
-  a.n = static_cast<int32_t>(cache_len);
-  a.n_scores = static_cast<int32_t>(n_scores < cache_len ? n_scores : cache_len);
+  a.bits = reinterpret_cast<uint32_t*>(ws + L.off_bits);
+  a.hist = reinterpret_cast<uint32_t*>(ws + L.off_hist);
+  a.segcnt = reinterpret_cast<int32_t*>(ws + L.off_seg);
+  a.state = reinterpret_cast<int32_t*>(ws + L.off_state);
+  a.n = n;
+  a.n_scores = n_sc;
+  a.G = static_cast<int32_t>(L.G);
   a.local = local_budget;
-  a.imp = importance_budget;
-  a.bridge_budget = bridge_budget;
-  a.imp_fallback = importance_fallback ? 1 : 0;
-  a.bridge_mode = bridge_mode;
-  evict_select_kernel<<<1, SEL_THREADS, 0, static_cast<hipStream_t>(stream)>>>(a);
+  a.n_imp = n_imp;
+  a.n_br = n_br;
+  a.imp_fallback_lo = has_scores ? n : f0;
+  const dim3 grid(static_cast<unsigned>(L.G));
+  msel_init_kernel<<<grid, MTHREADS, 0, s>>>(a);
+  cab_status_t r = launch_status(fn);
+  if (r != CAB_OK) return r;
+  MStep st{};
+  st.src = KeySrc{importance_scores, n_sc, 0.f};
+  if (has_scores && n_imp > 0) {
+    st.hbase = 0;
+    st.need = n_imp;
+    st.cat = 2;
+    if ((r = msel_select<KEY_DESC>(a, st, s, fn)) != CAB_OK) return r;
+  }
+  if (n_br > 0) {
+    if (mode == 1) {
+      MStep md = st;  // the lower median: the ((free1 - 1) / 2 + 1)-th smallest score
+      md.hbase = 3;
+      md.need = (free1 - 1) / 2 + 1;
+      for (int pass = 0; pass < 3; ++pass) {
+        md.pass = pass;
+        msel_hist_kernel<KEY_ASC><<<grid, MTHREADS, 0, s>>>(a, md);
+        if ((r = launch_status(fn)) != CAB_OK) return r;
+      }
+      MStep bs = st;
+      bs.hbase = 6;
+      bs.need = n_br;
+      bs.med_hbase = 3;
+      bs.med_need = md.need;
+      bs.cat = 3;
+      if ((r = msel_select<KEY_DIST>(a, bs, s, fn)) != CAB_OK) return r;
+    } else if (mode == 2) {
+      MStep bs = st;
+      bs.src = KeySrc{bridge_scores, n, 0.f};
+      bs.hbase = 6;
+      bs.need = n_br;
+      bs.cat = 3;
+      if ((r = msel_select<KEY_DESC>(a, bs, s, fn)) != CAB_OK) return r;
+    } else {
+      msel_rank_count_kernel<<<grid, MTHREADS, 0, s>>>(a);
+      if ((r = launch_status(fn)) != CAB_OK) return r;
+      MStep rk = st;
+      rk.first = free1 / 3;
+      rk.count = n_br;
+      rk.cat = 3;
+      msel_rank_mark_kernel<<<grid, MTHREADS, 0, s>>>(a, rk);
+      if ((r = launch_status(fn)) != CAB_OK) return r;
+    }
+  }
+  msel_compact_count_kernel<<<grid, MTHREADS, 0, s>>>(a);
+  if ((r = launch_status(fn)) != CAB_OK) return r;
+  msel_compact_write_kernel<<<grid, MTHREADS, 0, s>>>(a);
   return launch_status(fn);
 }
 

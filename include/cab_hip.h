@@ -49,7 +49,7 @@ enum { CAB_NORM_NONE = 0, CAB_NORM_MINMAX = 1 };
 /* FRC combination (experiments/longbench_qa/config.py:465; test.ipynb:111-145). */
 enum { CAB_FRC_ADDITIVE = 0, CAB_FRC_MULTIPLICATIVE = 1, CAB_FRC_AUGMENTED = 2 };
 
-#define CAB_ABI_VERSION 5
+#define CAB_ABI_VERSION 6
 
 int cab_abi_version(void);
 const char* cab_last_error(void);
@@ -285,15 +285,20 @@ cab_status_t cab_attn_key_scores(const void* q, const void* k, const float* lse,
  * A kept position is never selected again. Outputs: keep_indices (int64,
  * ascending, up to cache_len entries), counts = {local, importance, bridge,
  * total} (int32) and, if not NULL, category[i] = 0 evicted, 1 local,
- * 2 importance, 3 bridge (uint8, cache_len entries). One workgroup; all
- * device buffers.
+ * 2 importance, 3 bridge (uint8, cache_len entries). All device buffers.
+ * Below 32768 positions one workgroup does the whole selection and the
+ * workspace may be NULL; from 32768 on, one workgroup per 4096-position
+ * segment, with the kept-set bitmap, histograms and segment counts in the
+ * workspace of cab_evict_select_workspace_bytes(cache_len) bytes (256-byte
+ * aligned). Both give the same positions.
  */
+size_t cab_evict_select_workspace_bytes(int64_t cache_len);
 cab_status_t cab_evict_select(const float* importance_scores, int64_t n_scores,
                               const float* bridge_scores, int64_t cache_len,
                               int32_t local_budget, int32_t importance_budget,
                               int32_t bridge_budget, int importance_fallback, int bridge_mode,
                               int64_t* keep_indices, int32_t* counts, uint8_t* category,
-                              void* stream);
+                              void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Bridge scores of the policy's attention-matrix mode (policy.py:122-131):

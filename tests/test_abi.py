@@ -38,6 +38,7 @@ def test_header_declares_the_hot_path():
                  "cab_block_topk_hybrid", "cab_flash_attn_workspace_bytes",
                  "cab_flash_attn_fwd", "cab_attn_key_scores", "cab_evict_select",
                  "cab_evict_connectivity", "cab_kv_gather", "cab_token_frc",
+                 "cab_evict_select_workspace_bytes",
                  "cab_attention_symmetrize", "cab_token_frc_keys_workspace_bytes",
                  "cab_token_frc_from_keys"):
         assert name in syms
@@ -230,7 +231,13 @@ def test_eviction_validation(lib):
     sel = lambda **kw: lib.cab_evict_select(
         kw.get("scores", FAKE), kw.get("ns", 10), None, kw.get("n", 10), kw.get("local", 2),
         kw.get("imp", 3), kw.get("br", 2), 1, kw.get("mode", 1), kw.get("keep", FAKE), FAKE, None,
-        None)
+        kw.get("ws", None), kw.get("wsb", 0), None)
+    big = 1 << 15  # from here on a workspace is required
+    wsb = lib.cab_evict_select_workspace_bytes(big)
+    assert wsb > 0 and lib.cab_evict_select_workspace_bytes((1 << 20) + 1) == 0
+    assert sel(n=big, ns=big) == nat.CAB_EWORKSPACE
+    assert sel(n=big, ns=big, ws=FAKE, wsb=wsb - 1) == nat.CAB_EWORKSPACE
+    assert sel(n=big, ns=big, ws=FAKE + 16, wsb=wsb) == nat.CAB_EWORKSPACE
     assert sel(n=(1 << 20) + 1) == nat.CAB_ESHAPE
     assert sel(local=11) == nat.CAB_EINVAL
     assert sel(imp=-1) == nat.CAB_EINVAL

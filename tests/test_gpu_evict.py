@@ -225,3 +225,33 @@ def test_cab_cache_reference_demo_replay(cuda):
     assert st["total_tokens_evicted"] == evicted_tokens
     assert st["total_tokens_processed"] == 200 * layers
     assert len(cache) == cache.get_seq_length(0) <= int(100 * 1.1) + 1
+
+
+@pytest.mark.parametrize("n", [32768, 40001, 65536 + 123])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+def test_evict_select_multi_workgroup_path(cuda, n, mode):
+    """Caches of 32768 positions and more run one workgroup per 4096-position
+    segment (workspace bitmap and histograms); positions, counts and
+    categories stay bit-exact against the oracle: normal, tie-heavy and
+    NaN/inf/-0 scores, missing and short score vectors, with and without the
+    fallback, and given bridge scores with ties across segments."""
+    rng = np.random.default_rng(n + mode)
+    budgets = [(n // 10, n // 4, n // 5), (5, n // 3, n), (0, 7, 3)]
+    for name, s in score_cases(rng, n):
+        for local, imp, br in budgets:
+            bs = rng.integers(0, 5, n).astype(np.float32) if mode == 2 else None
+            for fb in (True, False):
+                keep, cnt, cat, dev = run_select(cuda, s, n, local, imp, br, fb, mode, bridge_scores=bs)
+                wk, wc, wcat = O.evict_select(s, n, local, imp, br, fb, mode, bridge_scores=bs)
+                msg = f"{name} n={n} budgets={(local, imp, br)} fb={fb}"
+                assert tuple(cnt) == tuple(wc), msg
+                assert np.array_equal(keep, wk), msg
+                assert np.array_equal(cat, wcat), msg
+                assert list(dev) == [wc[0], wc[1], wc[2], wk.size], msg
+    for scores in (None, rng.standard_normal(n // 3).astype(np.float32)):
+        for fb in (True, False):
+            bs = rng.random(n).astype(np.float32)
+            keep, cnt, cat, _ = run_select(cuda, scores, n, 100, n // 4, n // 6, fb, mode,
+                                           bridge_scores=bs)
+            wk, wc, wcat = O.evict_select(scores, n, 100, n // 4, n // 6, fb, mode, bridge_scores=bs)
+            assert tuple(cnt) == tuple(wc) and np.array_equal(keep, wk) and np.array_equal(cat, wcat)
