@@ -2,9 +2,12 @@
 // matrix bridge scores (cab_evict_connectivity) and the multi-layer K/V
 // gather that prunes a cache to the kept positions (cab_kv_gather).
 //
-// evict_select_kernel: one workgroup of 1024 threads (16 waves) per call. The
-// kept set lives in an LDS bitmap (one bit per cache position, up to 2^20
-// positions). Each component is a k-smallest selection over the positions
+// evict_select_kernel (caches below MULTI_MIN positions): one workgroup of
+// 1024 threads (16 waves) per call. The kept set lives in an LDS bitmap (one
+// bit per cache position). Larger caches (up to 2^20 positions) run the
+// msel_* kernels further down: the same selection, one workgroup per
+// 4096-position segment, with the bitmap and the radix histograms in a
+// workspace. Each component is a k-smallest selection over the positions
 // not yet kept:
 //   local window:  the last `local` positions;
 //   importance:    the highest scores (position > score: the lower position
