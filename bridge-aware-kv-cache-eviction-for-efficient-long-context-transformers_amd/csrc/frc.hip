@@ -5,13 +5,20 @@
 //     workgroup, one 32x32 tile per wave), per-tile min/max partials.
 //  2. minmax_finalize_kernel: per-(b,h) min/max from the partials.
 //  3. affinity_kernel<EMIT>: recomputes the A tile, normalises it, and writes
-//     Ahat as a bf16 hi/lo pair (hi = bf16(Ahat), lo = bf16(Ahat - hi)) in
-//     row-major X and transposed XT planes (zero outside M), the fp32 Ahat
-//     diagnostic and, for the augmented formula, row-sum partials.
+//     Ahat in row-major X and transposed XT planes (zero outside M), the fp32
+//     Ahat diagnostic and, for the augmented formula, row-sum partials. The
+//     planes hold either
+//       - fp16 (minmax normalisation, additive or multiplicative formula):
+//         Ahat lies in [0, 1], X = f16(Ahat), XT likewise, plus the low part
+//         f16(Ahat - X) of X for the epilogue; or
+//       - a bf16 hi/lo pair (hi = bf16(Ahat), lo = bf16(Ahat - hi)) of X and
+//         of XT, for unnormalised values of any range and for the augmented
+//         formula, whose S_i + S_j cancels against 3 T.
 //  4. rowsum_finalize_kernel (augmented only).
-//  5. triangle_kernel: T = Ahat Ahat = X XT^T on MFMA as
-//     hi*hi + hi*lo + lo*hi (fp32 accumulate; the dropped lo*lo term is below
-//     2^-16 relative), 128x128 tile per workgroup, LDS double-buffered, with
+//  5. triangle_kernel: T = Ahat Ahat = X XT^T on MFMA with fp32 accumulate,
+//     one fp16 product per site (relative error <= 2^-10 + 2^-22 per product
+//     for Ahat in fp16's normal range) or hi*hi + hi*lo + lo*hi in bf16 (the
+//     dropped lo*lo term is below 2^-16 relative); LDS double-buffered, with
 //     the FRC combination fused into the epilogue.
 // Algorithmic work: 2 M^2 D flops (affinity) + 2 M^3 flops (triangles).
 #include "cab_internal.h"
@@ -22,7 +29,7 @@ namespace {
 constexpr int AT = 64;    // affinity tile
 constexpr int TT = 128;   // triangle tile
 constexpr int TT_WIDE = 256;  // wide triangle tile (large M)
-constexpr int TK = 32;    // triangle k-step
+constexpr int TK = 32;    // triangle k-slice depth
 
 struct FrcLayout {
   int64_t Mp, nta;  // padded M, affinity tiles per dim
@@ -68,6 +75,7 @@ struct AffArgs {
   uint16_t* xtlo;
   float* affinity;     // [BH][M][M] or null
   float* rspart;       // [BH][nta][Mp] or null
+  int f16_planes;      // X = f16, xlo = f16 low part of X, XT = f16 (xtlo unused)
 };
 
 // One wave computes a 32x32 tile of qc kc^T (fp32 accumulate). Lane l owns
@@ -188,7 +196,25 @@ __global__ __launch_bounds__(256) void affinity_kernel(AffArgs a) {
     for (int q = 0; q < 2; ++q) {
       const int cid = threadIdx.x + 256 * q;  // 64 rows x 8 chunks of 8 values
       const int r = cid >> 3, c8 = (cid & 7) * 8;
+      const size_t xo = pbase + static_cast<size_t>(ti0 + r) * a.Mp + tj0 + c8;
+      const size_t to = pbase + static_cast<size_t>(tj0 + r) * a.Mp + ti0 + c8;
       u32x4 h4, l4, th4, tl4;
+      if (a.f16_planes) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x0 = stile[r][c8 + 2 * e], x1 = stile[r][c8 + 2 * e + 1];
+          const float y0 = stile[c8 + 2 * e][r], y1 = stile[c8 + 2 * e + 1][r];
+          const uint16_t hx0 = f32_to_f16(x0), hx1 = f32_to_f16(x1);
+          h4[e] = static_cast<uint32_t>(hx0) | (static_cast<uint32_t>(hx1) << 16);
+          l4[e] = static_cast<uint32_t>(f32_to_f16(x0 - f16_to_f32(hx0))) |
+                  (static_cast<uint32_t>(f32_to_f16(x1 - f16_to_f32(hx1))) << 16);
+          th4[e] = static_cast<uint32_t>(f32_to_f16(y0)) | (static_cast<uint32_t>(f32_to_f16(y1)) << 16);
+        }
+        *reinterpret_cast<u32x4*>(a.xhi + xo) = h4;
+        *reinterpret_cast<u32x4*>(a.xlo + xo) = l4;
+        *reinterpret_cast<u32x4*>(a.xthi + to) = th4;
+        continue;
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float x0 = stile[r][c8 + 2 * e], x1 = stile[r][c8 + 2 * e + 1];    // X row ti0 + r
@@ -202,8 +228,6 @@ __global__ __launch_bounds__(256) void affinity_kernel(AffArgs a) {
         tl4[e] = static_cast<uint32_t>(f32_to_bf16(y0 - bf16_to_f32(hy0))) |
                  (static_cast<uint32_t>(f32_to_bf16(y1 - bf16_to_f32(hy1))) << 16);
       }
-      const size_t xo = pbase + static_cast<size_t>(ti0 + r) * a.Mp + tj0 + c8;
-      const size_t to = pbase + static_cast<size_t>(tj0 + r) * a.Mp + ti0 + c8;
       *reinterpret_cast<u32x4*>(a.xhi + xo) = h4;
       *reinterpret_cast<u32x4*>(a.xlo + xo) = l4;
       *reinterpret_cast<u32x4*>(a.xthi + to) = th4;
@@ -286,6 +310,7 @@ struct TriArgs {
   const uint16_t* xthi;
   const uint16_t* xtlo;
   const float* rowsum;  // [BH][Mp] (augmented only)
+  const float* mm;      // [BH][2] minmax of A (fp16 planes only)
   float* frc;           // [BH][M][M]
   float* tri;           // [BH][M][M] or null
   int64_t M, Mp, nt, BH;
@@ -296,31 +321,36 @@ struct TriArgs {
 // LDS operand tile in MFMA order: slot (kk, sub, lane) of 16 bytes holds the
 // 8 consecutive k values lane needs for a 32x32x16 MFMA, so every operand
 // read is one 1 KB wave access. Inside each 64-slot group the slot of lane L
-// is stored at position L ^ (4 (2 kk + L / 32)): the four threads that load
-// one row's 64 bytes then write four different LDS bank groups.
-template <int TILE>
-constexpr int tri_slots() { return (TK / 16) * (TILE / 32) * 64; }
+// is stored at position L ^ (4 (2 kk + L / 32)): the threads that load one
+// row's bytes then write different LDS bank groups.
+template <int TILE, int KD>
+constexpr int tri_slots() { return (KD / 16) * (TILE / 32) * 64; }
 
-// Thread t moves chunks t and t + THREADS of a plane's TILE x TK slice
-// (TILE rows of 4 x 16 bytes): 2 chunks per thread when THREADS = 2 TILE.
-template <int TILE, int THREADS>
+// A plane's TILE x KD slice is TILE rows of KD / 8 chunks of 16 bytes; KD / 8
+// consecutive threads read one row (KD = 64: a whole 128-byte cache line).
+// Thread t moves chunks t, t + THREADS, ...
+template <int TILE, int THREADS, int KD>
+constexpr int tri_chunks() { return TILE * (KD / 8) / THREADS; }
+
+template <int TILE, int THREADS, int KD>
 __device__ __forceinline__ void tri_load(const uint16_t* plane, int64_t row0, int64_t k0, int64_t Mp,
-                                         u32x4 (&reg)[2]) {
-  static_assert(THREADS * 2 == TILE * 4, "two 16-byte chunks per thread and plane");
+                                         u32x4 (&reg)[tri_chunks<TILE, THREADS, KD>()]) {
+  constexpr int CPR = KD / 8;  // chunks per row
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
+  for (int q = 0; q < tri_chunks<TILE, THREADS, KD>(); ++q) {
     const int cid = threadIdx.x + THREADS * q;
-    const int row = cid >> 2, kc = cid & 3;
+    const int row = cid / CPR, kc = cid % CPR;
     reg[q] = *reinterpret_cast<const u32x4*>(plane + (row0 + row) * Mp + k0 + 8 * kc);
   }
 }
 
-template <int TILE, int THREADS>
-__device__ __forceinline__ void tri_store(u32x4* lds, const u32x4 (&reg)[2]) {
+template <int TILE, int THREADS, int KD>
+__device__ __forceinline__ void tri_store(u32x4* lds, const u32x4 (&reg)[tri_chunks<TILE, THREADS, KD>()]) {
+  constexpr int CPR = KD / 8;
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
+  for (int q = 0; q < tri_chunks<TILE, THREADS, KD>(); ++q) {
     const int cid = threadIdx.x + THREADS * q;
-    const int row = cid >> 2, kc = cid & 3;
+    const int row = cid / CPR, kc = cid % CPR;
     const int kk = kc >> 1, hf = kc & 1, sub = row >> 5;
     lds[(kk * (TILE / 32) + sub) * 64 + (((row & 31) + 32 * hf) ^ (4 * (2 * kk + hf)))] = reg[q];
   }
@@ -345,22 +375,48 @@ __device__ __forceinline__ float frc_combine(int formula, float ahat, float t, f
 // rows wi TILE / WI .. and columns wj TILE / WJ .. as XS x YS MFMA tiles.
 // NBUF register buffers carry operand slices global -> registers -> LDS
 // (two LDS stages): with NBUF = 2 a slice's loads have two slices of MFMA
-// work to land, with NBUF = 1 one slice (for the wide tile, whose
-// accumulators leave room for one buffer only).
-template <int TILE, int WI, int WJ, int NBUF>
+// work to land, with NBUF = 1 one slice (for the wide bf16 tile, whose
+// accumulators leave room for one buffer of four planes only). F16 selects
+// the fp16 planes (A = X, B = XT, one product per site); otherwise the four
+// bf16 planes (A hi, A lo, B hi, B lo; three products).
+template <int TILE, int WI, int WJ, int NBUF, bool F16, int KD>
 __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
   constexpr int THREADS = WI * WJ * 64;
   constexpr int XS = TILE / WI / 32, YS = TILE / WJ / 32;
-  constexpr int SLOTS = tri_slots<TILE>();
-  __shared__ u32x4 lds[2][4][SLOTS];  // [stage][Ahi, Alo, Bhi, Blo][slot]
+  constexpr int SLOTS = tri_slots<TILE, KD>();
+  constexpr int CH = tri_chunks<TILE, THREADS, KD>();
+  static_assert(CH * THREADS == TILE * (KD / 8), "whole chunks per thread");
+  constexpr int NP = F16 ? 2 : 4;  // planes staged per slice
+  __shared__ u32x4 lds[2][NP][SLOTS];  // [stage][plane][slot]
   const int64_t total = a.BH * a.nt * a.nt;
   const int64_t logical = xcd_remap(blockIdx.x, total);
   const int64_t bh = logical / (a.nt * a.nt);
   const int64_t rem = logical - bh * a.nt * a.nt;
   const int64_t ti = rem / a.nt, tj = rem - (rem / a.nt) * a.nt;
   const size_t pbase = static_cast<size_t>(bh) * a.Mp * a.Mp;
-  const uint16_t* planes[4] = {a.xhi + pbase, a.xlo + pbase, a.xthi + pbase, a.xtlo + pbase};
-  const int64_t rows[4] = {ti * TILE, ti * TILE, tj * TILE, tj * TILE};
+  const uint16_t* planes[NP];
+  int64_t rows[NP];
+  if constexpr (F16) {
+    planes[0] = a.xhi + pbase;
+    planes[1] = a.xthi + pbase;
+    rows[0] = ti * TILE;
+    rows[1] = tj * TILE;
+  } else {
+    planes[0] = a.xhi + pbase;
+    planes[1] = a.xlo + pbase;
+    planes[2] = a.xthi + pbase;
+    planes[3] = a.xtlo + pbase;
+    rows[0] = rows[1] = ti * TILE;
+    rows[2] = rows[3] = tj * TILE;
+  }
+  // fp16 planes: a constant A (min == max) is left unnormalised and may lie
+  // outside fp16's range; its T = M c^2 is formed directly in the epilogue.
+  bool constant = false;
+  float cval = 0.f;
+  if constexpr (F16) {
+    cval = a.mm[bh * 2 + 0];
+    constant = !(a.mm[bh * 2 + 1] > cval);
+  }
 
   const int w = threadIdx.x >> 6, lane = lane_id();
   const int wi = w / WJ, wj = w - (w / WJ) * WJ;
@@ -370,95 +426,116 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
 #pragma unroll
     for (int y = 0; y < YS; ++y) acc[x][y] = f32x16{};
 
-  const int nk = static_cast<int>(a.Mp / TK);
+  const int nk = static_cast<int>(a.Mp / KD);
   auto compute = [&](auto st_tag) {
     constexpr int st = decltype(st_tag)::value;
 #pragma unroll
-    for (int kk = 0; kk < TK / 16; ++kk) {
-      bf16x8 bh8[YS], bl[YS];
+    for (int kk = 0; kk < KD / 16; ++kk) {
       const int lsw = lane ^ (4 * (2 * kk + (lane >> 5)));
+      if constexpr (F16) {
+        f16x8 b8[YS];
 #pragma unroll
-      for (int y = 0; y < YS; ++y) {
-        const int sb = (kk * (TILE / 32) + YS * wj + y) * 64 + lsw;
-        bh8[y] = __builtin_bit_cast(bf16x8, lds[st][2][sb]);
-        bl[y] = __builtin_bit_cast(bf16x8, lds[st][3][sb]);
-      }
-      // A operands one 32-row strip at a time (fewer live registers).
+        for (int y = 0; y < YS; ++y)
+          b8[y] = __builtin_bit_cast(f16x8, lds[st][1][(kk * (TILE / 32) + YS * wj + y) * 64 + lsw]);
 #pragma unroll
-      for (int x = 0; x < XS; ++x) {
-        const int sa = (kk * (TILE / 32) + XS * wi + x) * 64 + lsw;
-        const bf16x8 ah = __builtin_bit_cast(bf16x8, lds[st][0][sa]);
-        const bf16x8 al = __builtin_bit_cast(bf16x8, lds[st][1][sa]);
+        for (int x = 0; x < XS; ++x) {
+          const f16x8 a8 =
+              __builtin_bit_cast(f16x8, lds[st][0][(kk * (TILE / 32) + XS * wi + x) * 64 + lsw]);
+#pragma unroll
+          for (int y = 0; y < YS; ++y)
+            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a8, b8[y], acc[x][y], 0, 0, 0);
+        }
+      } else {
+        bf16x8 bh8[YS], bl[YS];
 #pragma unroll
         for (int y = 0; y < YS; ++y) {
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh8[y], acc[x][y], 0, 0, 0);
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl[y], acc[x][y], 0, 0, 0);
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh8[y], acc[x][y], 0, 0, 0);
+          const int sb = (kk * (TILE / 32) + YS * wj + y) * 64 + lsw;
+          bh8[y] = __builtin_bit_cast(bf16x8, lds[st][2][sb]);
+          bl[y] = __builtin_bit_cast(bf16x8, lds[st][3][sb]);
+        }
+        // A operands one 32-row strip at a time (fewer live registers).
+#pragma unroll
+        for (int x = 0; x < XS; ++x) {
+          const int sa = (kk * (TILE / 32) + XS * wi + x) * 64 + lsw;
+          const bf16x8 ah = __builtin_bit_cast(bf16x8, lds[st][0][sa]);
+          const bf16x8 al = __builtin_bit_cast(bf16x8, lds[st][1][sa]);
+#pragma unroll
+          for (int y = 0; y < YS; ++y) {
+            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh8[y], acc[x][y], 0, 0, 0);
+            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl[y], acc[x][y], 0, 0, 0);
+            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh8[y], acc[x][y], 0, 0, 0);
+          }
         }
       }
     }
   };
 
-  if constexpr (NBUF == 2) {
-    // The registers of slice kt + 2 are loaded while slice kt is multiplied.
-    u32x4 reg[2][4][2];
+  // The loop's barriers are uniform: `constant` depends on bh alone.
+  if (!constant) {
+    if constexpr (NBUF == 2) {
+      // The registers of slice kt + 2 are loaded while slice kt is multiplied.
+      u32x4 reg[2][NP][CH];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) tri_load<TILE, THREADS>(planes[p], rows[p], 0, a.Mp, reg[0][p]);
-    if (nk > 1) {
+      for (int p = 0; p < NP; ++p) tri_load<TILE, THREADS, KD>(planes[p], rows[p], 0, a.Mp, reg[0][p]);
+      if (nk > 1) {
 #pragma unroll
-      for (int p = 0; p < 4; ++p) tri_load<TILE, THREADS>(planes[p], rows[p], TK, a.Mp, reg[1][p]);
-    }
-    auto slice = [&](int kt, auto buf_tag) {
-      constexpr int st = decltype(buf_tag)::value;  // register buffer and LDS stage kt % 2
-#pragma unroll
-      for (int p = 0; p < 4; ++p) tri_store<TILE, THREADS>(lds[st][p], reg[st][p]);
-      __syncthreads();
-      if (kt + 2 < nk) {
-#pragma unroll
-        for (int p = 0; p < 4; ++p)
-          tri_load<TILE, THREADS>(planes[p], rows[p], static_cast<int64_t>(kt + 2) * TK, a.Mp,
-                                  reg[st][p]);
+        for (int p = 0; p < NP; ++p) tri_load<TILE, THREADS, KD>(planes[p], rows[p], KD, a.Mp, reg[1][p]);
       }
-      compute(buf_tag);
-    };
-    for (int kt = 0; kt < nk; kt += 2) {
-      slice(kt, std::integral_constant<int, 0>{});
-      if (kt + 1 < nk) slice(kt + 1, std::integral_constant<int, 1>{});
-    }
-  } else {
-    // One register buffer: slice kt + 1 is stored to the other LDS stage
-    // after slice kt is multiplied, then slice kt + 2 is loaded.
-    u32x4 reg[4][2];
+      auto slice = [&](int kt, auto buf_tag) {
+        constexpr int st = decltype(buf_tag)::value;  // register buffer and LDS stage kt % 2
 #pragma unroll
-    for (int p = 0; p < 4; ++p) tri_load<TILE, THREADS>(planes[p], rows[p], 0, a.Mp, reg[p]);
+        for (int p = 0; p < NP; ++p) tri_store<TILE, THREADS, KD>(lds[st][p], reg[st][p]);
+        lds_barrier();
+        if (kt + 2 < nk) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) tri_store<TILE, THREADS>(lds[0][p], reg[p]);
-    if (nk > 1) {
-#pragma unroll
-      for (int p = 0; p < 4; ++p) tri_load<TILE, THREADS>(planes[p], rows[p], TK, a.Mp, reg[p]);
-    }
-    __syncthreads();
-    auto slice = [&](int kt, auto st_tag) {
-      constexpr int st = decltype(st_tag)::value;  // LDS stage of slice kt
-      compute(st_tag);
-      if (kt + 1 < nk) {
-#pragma unroll
-        for (int p = 0; p < 4; ++p) tri_store<TILE, THREADS>(lds[st ^ 1][p], reg[p]);
+          for (int p = 0; p < NP; ++p)
+            tri_load<TILE, THREADS, KD>(planes[p], rows[p], static_cast<int64_t>(kt + 2) * KD, a.Mp,
+                                    reg[st][p]);
+        }
+        compute(buf_tag);
+      };
+      for (int kt = 0; kt < nk; kt += 2) {
+        slice(kt, std::integral_constant<int, 0>{});
+        if (kt + 1 < nk) slice(kt + 1, std::integral_constant<int, 1>{});
       }
-      if (kt + 2 < nk) {
+    } else {
+      // One register buffer: slice kt + 1 is stored to the other LDS stage
+      // after slice kt is multiplied, then slice kt + 2 is loaded.
+      u32x4 reg[NP][CH];
 #pragma unroll
-        for (int p = 0; p < 4; ++p)
-          tri_load<TILE, THREADS>(planes[p], rows[p], static_cast<int64_t>(kt + 2) * TK, a.Mp, reg[p]);
+      for (int p = 0; p < NP; ++p) tri_load<TILE, THREADS, KD>(planes[p], rows[p], 0, a.Mp, reg[p]);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) tri_store<TILE, THREADS, KD>(lds[0][p], reg[p]);
+      if (nk > 1) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) tri_load<TILE, THREADS, KD>(planes[p], rows[p], KD, a.Mp, reg[p]);
       }
-      __syncthreads();
-    };
-    for (int kt = 0; kt < nk; kt += 2) {
-      slice(kt, std::integral_constant<int, 0>{});
-      if (kt + 1 < nk) slice(kt + 1, std::integral_constant<int, 1>{});
+      lds_barrier();
+      auto slice = [&](int kt, auto st_tag) {
+        constexpr int st = decltype(st_tag)::value;  // LDS stage of slice kt
+        compute(st_tag);
+        if (kt + 1 < nk) {
+#pragma unroll
+          for (int p = 0; p < NP; ++p) tri_store<TILE, THREADS, KD>(lds[st ^ 1][p], reg[p]);
+        }
+        if (kt + 2 < nk) {
+#pragma unroll
+          for (int p = 0; p < NP; ++p)
+            tri_load<TILE, THREADS, KD>(planes[p], rows[p], static_cast<int64_t>(kt + 2) * KD, a.Mp, reg[p]);
+        }
+        lds_barrier();
+      };
+      for (int kt = 0; kt < nk; kt += 2) {
+        slice(kt, std::integral_constant<int, 0>{});
+        if (kt + 1 < nk) slice(kt + 1, std::integral_constant<int, 1>{});
+      }
     }
   }
 
-  // Epilogue: F = combine(Ahat, T) for the wave's block.
+  // Epilogue: F = combine(Ahat, T) for the wave's block. The 16 Ahat values
+  // of each 32 x 32 accumulator are loaded together before its stores, so
+  // their latencies overlap (the stores could alias the planes for all the
+  // compiler knows, which would otherwise serialise load, store, load, ...).
   const int half = lane >> 5;
   const size_t obase = static_cast<size_t>(bh) * a.M * a.M;
 #pragma unroll
@@ -468,12 +545,29 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
     const float sj = a.formula == CAB_FRC_AUGMENTED ? a.rowsum[bh * a.Mp + j] : 0.f;
 #pragma unroll
     for (int x = 0; x < XS; ++x) {
+      const int64_t i0 = ti * TILE + wi * (TILE / WI) + x * 32 + 4 * half;
+      // Rows past M (< Mp) lie inside the zero-padded planes.
+      uint16_t hi[16], lo[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int64_t i = ti * TILE + wi * (TILE / WI) + x * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+        const int64_t i = i0 + 8 * (e >> 2) + (e & 3);
+        hi[e] = a.xhi[pbase + i * a.Mp + j];
+        lo[e] = a.xlo[pbase + i * a.Mp + j];
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t i = i0 + 8 * (e >> 2) + (e & 3);
         if (i >= a.M) continue;
-        const float t = acc[x][y][e];
-        const float ahat = bf16_to_f32(a.xhi[pbase + i * a.Mp + j]) + bf16_to_f32(a.xlo[pbase + i * a.Mp + j]);
+        float t = acc[x][y][e], ahat;
+        if constexpr (F16) {
+          ahat = f16_to_f32(hi[e]) + f16_to_f32(lo[e]);
+          if (constant) {
+            ahat = cval;
+            t = static_cast<float>(a.M) * cval * cval;
+          }
+        } else {
+          ahat = bf16_to_f32(hi[e]) + bf16_to_f32(lo[e]);
+        }
         const float si = a.formula == CAB_FRC_AUGMENTED ? a.rowsum[bh * a.Mp + i] : 0.f;
         a.frc[obase + i * a.M + j] = frc_combine(a.formula, ahat, t, a.lambda, si, sj);
         if (a.tri) a.tri[obase + i * a.M + j] = t;
@@ -556,6 +650,10 @@ extern "C" cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_
   a.xtlo = reinterpret_cast<uint16_t*>(ws + L.off_xtlo);
   a.affinity = affinity;
   a.rspart = formula == CAB_FRC_AUGMENTED ? reinterpret_cast<float*>(ws + L.off_rspart) : nullptr;
+  // fp16 planes where Ahat is known to lie in [0, 1] and the formula does not
+  // cancel T against row sums.
+  const bool f16 = normalization == CAB_NORM_MINMAX && formula != CAB_FRC_AUGMENTED;
+  a.f16_planes = f16 ? 1 : 0;
 
   if (normalization == CAB_NORM_MINMAX) {
     switch (dtype) {
@@ -590,6 +688,7 @@ extern "C" cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_
   t.xthi = a.xthi;
   t.xtlo = a.xtlo;
   t.rowsum = reinterpret_cast<const float*>(ws + L.off_rs);
+  t.mm = reinterpret_cast<const float*>(ws + L.off_mm);
   t.frc = frc;
   t.tri = triangles;
   t.M = M;
@@ -603,9 +702,14 @@ extern "C" cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_
   t.nt = L.Mp / (wide ? TT_WIDE : TT);
   const int64_t blocks = BH * t.nt * t.nt;
   CAB_REQUIRE(blocks <= INT32_MAX, CAB_ESHAPE, "cab_block_frc: problem too large");
-  if (wide)
-    triangle_kernel<TT_WIDE, 2, 4, 1><<<static_cast<unsigned>(blocks), 512, 0, s>>>(t);
+  const unsigned nb = static_cast<unsigned>(blocks);
+  if (wide && f16)
+    triangle_kernel<TT_WIDE, 2, 4, 2, true, TK><<<nb, 512, 0, s>>>(t);
+  else if (wide)
+    triangle_kernel<TT_WIDE, 2, 4, 1, false, TK><<<nb, 512, 0, s>>>(t);
+  else if (f16)
+    triangle_kernel<TT, 2, 2, 2, true, TK><<<nb, 256, 0, s>>>(t);
   else
-    triangle_kernel<TT, 2, 2, 2><<<static_cast<unsigned>(blocks), 256, 0, s>>>(t);
+    triangle_kernel<TT, 2, 2, 2, false, TK><<<nb, 256, 0, s>>>(t);
   return launch_status("cab_block_frc/triangles");
 }

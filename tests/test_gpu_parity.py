@@ -108,6 +108,21 @@ def assert_frc_close(got, want_f, ahat, tri, lam, rtol=1e-3):
     assert worst <= 1.0, f"FRC error {worst:.3g} x bound"
 
 
+def assert_tri_close(got, want_t, ahat, normalization, rtol=1e-3):
+    """T with minmax normalisation comes from one fp16 product per site
+    (Ahat in [0, 1]): |dT| <= (2^-10 + 2^-22 + fp32 accumulation) |Ahat| @ |Ahat|,
+    checked at the 1e-3 the FRC scores are held to, and on average at 1e-4.
+    Unnormalised T uses the bf16 hi/lo products (about 2^-16 relative)."""
+    t = np32(got)
+    if normalization != "minmax":
+        np.testing.assert_allclose(t, want_t, rtol=1e-4, atol=1e-4 * np.abs(want_t).max())
+        return
+    absprod = np.matmul(np.abs(ahat), np.abs(ahat))
+    rel = np.abs(t - want_t) / (absprod + 1e-6)
+    assert rel.max() <= rtol, f"T error {rel.max():.3g} of |Ahat| @ |Ahat|"
+    assert rel.mean() <= 1e-4, f"mean T error {rel.mean():.3g} of |Ahat| @ |Ahat|"
+
+
 @pytest.mark.parametrize("dt", ["bf16", "fp16", "fp32"])
 @pytest.mark.parametrize("M", [100, 257, 512])
 @pytest.mark.parametrize("formula,normalization", [("additive", "minmax"),
@@ -123,7 +138,7 @@ def test_frc_parity(cuda, dt, M, formula, normalization):
     of, oa, ot = O.compute_block_frc(np32(qc), np32(kc), lambda_redundancy=lam, formula=formula,
                                      normalization=normalization)
     np.testing.assert_allclose(np32(a), oa, rtol=1e-5, atol=1e-5 * max(1.0, np.abs(oa).max()))
-    np.testing.assert_allclose(np32(t), ot, rtol=1e-4, atol=1e-4 * np.abs(ot).max())
+    assert_tri_close(t, ot, oa, normalization)
     if formula == "multiplicative":
         np.testing.assert_allclose(np32(f), of, rtol=1e-3, atol=1e-5)
     else:
@@ -141,11 +156,31 @@ def test_frc_parity_wide_tile(cuda, H, M, formula):
     kc = seeded((B, H, M, D), 16, torch.bfloat16, scale=3.0)
     f, a, t = compute_block_frc(qc.to(cuda), kc.to(cuda), lambda_redundancy=lam, formula=formula)
     of, oa, ot = O.compute_block_frc(np32(qc), np32(kc), lambda_redundancy=lam, formula=formula)
-    np.testing.assert_allclose(np32(t), ot, rtol=1e-4, atol=1e-4 * np.abs(ot).max())
+    assert_tri_close(t, ot, oa, "minmax")
     if formula == "multiplicative":
         np.testing.assert_allclose(np32(f), of, rtol=1e-3, atol=1e-5)
     else:
         assert_frc_close(f, of, oa, ot, lam)
+
+
+@pytest.mark.parametrize("formula", ["additive", "multiplicative"])
+def test_frc_constant_affinity(cuda, formula):
+    """min == max: minmax normalisation leaves A unnormalised
+    (CAB_Attention_Colab.ipynb:249). Here A = (2^20 + 3) / sqrt(128) everywhere,
+    beyond fp16's range, so T = M c^2 must not pass through the fp16 planes."""
+    from cab_attention.kernels import compute_block_frc
+    B, H, M, D = 1, 2, 300, 128
+    qc = torch.zeros(B, H, M, D)
+    kc = torch.zeros(B, H, M, D)
+    qc[..., 0] = float(2 ** 20 + 3)
+    kc[..., 0] = 1.0
+    qc[0, 1] = 0.0  # second head: A = 0
+    f, a, t = compute_block_frc(qc.to(cuda), kc.to(cuda), formula=formula)
+    of, oa, ot = O.compute_block_frc(qc.numpy(), kc.numpy(), formula=formula)
+    assert oa[0, 0].min() == oa[0, 0].max() > 65504.0  # unnormalised, outside fp16
+    np.testing.assert_allclose(np32(a), oa, rtol=1e-6)
+    np.testing.assert_allclose(np32(t), ot, rtol=1e-5)
+    np.testing.assert_allclose(np32(f), of, rtol=1e-5, atol=1e-6)
 
 
 def test_frc_no_diagnostics_matches(cuda):
