@@ -76,6 +76,8 @@ struct AffArgs {
   float* affinity;     // [BH][M][M] or null
   float* rspart;       // [BH][nta][Mp] or null
   int f16_planes;      // X = f16, xlo = f16 low part of X, XT = f16 (xtlo unused)
+  int fused;           // with f16_planes: XT = f16(I - lambda Ahat^T), xlo unused
+  float lambda;
 };
 
 // One wave computes a 32x32 tile of qc kc^T (fp32 accumulate). Lane l owns
@@ -199,6 +201,25 @@ __global__ __launch_bounds__(256) void affinity_kernel(AffArgs a) {
       const size_t xo = pbase + static_cast<size_t>(ti0 + r) * a.Mp + tj0 + c8;
       const size_t to = pbase + static_cast<size_t>(tj0 + r) * a.Mp + ti0 + c8;
       u32x4 h4, l4, th4, tl4;
+      if (a.fused) {
+        // XT row tj0 + r, column ti0 + c: delta - lambda Ahat[ti0 + c][tj0 + r]
+        // (the delta only inside M; the planes are zero beyond it).
+        const int64_t jrow = tj0 + r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x0 = stile[r][c8 + 2 * e], x1 = stile[r][c8 + 2 * e + 1];
+          const int64_t k0 = ti0 + c8 + 2 * e;
+          const float d0 = (k0 == jrow && k0 < a.M) ? 1.f : 0.f;
+          const float d1 = (k0 + 1 == jrow && k0 + 1 < a.M) ? 1.f : 0.f;
+          const float y0 = d0 - a.lambda * stile[c8 + 2 * e][r];
+          const float y1 = d1 - a.lambda * stile[c8 + 2 * e + 1][r];
+          h4[e] = static_cast<uint32_t>(f32_to_f16(x0)) | (static_cast<uint32_t>(f32_to_f16(x1)) << 16);
+          th4[e] = static_cast<uint32_t>(f32_to_f16(y0)) | (static_cast<uint32_t>(f32_to_f16(y1)) << 16);
+        }
+        *reinterpret_cast<u32x4*>(a.xhi + xo) = h4;
+        *reinterpret_cast<u32x4*>(a.xthi + to) = th4;
+        continue;
+      }
       if (a.f16_planes) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -316,6 +337,7 @@ struct TriArgs {
   int64_t M, Mp, nt, BH;
   float lambda;
   int formula;
+  int fused;            // fp16 planes with XT = I - lambda Ahat^T: the accumulator is F
 };
 
 // LDS operand tile in MFMA order: slot (kk, sub, lane) of 16 bytes holds the
@@ -532,48 +554,78 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
     }
   }
 
-  // Epilogue: F = combine(Ahat, T) for the wave's block. The 16 Ahat values
-  // of each 32 x 32 accumulator are loaded together before its stores, so
-  // their latencies overlap (the stores could alias the planes for all the
-  // compiler knows, which would otherwise serialise load, store, load, ...).
+  // Epilogue: F = combine(Ahat, T) for the wave's block, one code path per
+  // formula (the switch is uniform). The Ahat values of each 32 x 32
+  // accumulator are loaded together before its stores, so their latencies
+  // overlap (the stores could alias the planes for all the compiler knows).
+  // With fp16 planes the additive formula reads X alone: F = Ahat - lambda T
+  // then errs by at most 2^-12 |Ahat|, far inside the bound on F.
   const int half = lane >> 5;
+  const int64_t ib = ti * TILE + wi * (TILE / WI) + 4 * half;
+  const int64_t jb = tj * TILE + wj * (TILE / WJ) + (lane & 31);
   const size_t obase = static_cast<size_t>(bh) * a.M * a.M;
+  auto epilogue = [&](auto form_tag) {
+    constexpr int FORM = decltype(form_tag)::value;
+    constexpr bool FUSED = FORM < 0;  // F = X (I - lambda X) accumulated directly
+    constexpr bool LO = !(F16 && (FORM == CAB_FRC_ADDITIVE || FUSED));
 #pragma unroll
-  for (int y = 0; y < YS; ++y) {
-    const int64_t j = tj * TILE + wj * (TILE / WJ) + y * 32 + (lane & 31);
-    if (j >= a.M) continue;
-    const float sj = a.formula == CAB_FRC_AUGMENTED ? a.rowsum[bh * a.Mp + j] : 0.f;
+    for (int y = 0; y < YS; ++y) {
+      const int64_t j = jb + y * 32;
+      if (j >= a.M) continue;
+      const float sj = FORM == CAB_FRC_AUGMENTED ? a.rowsum[bh * a.Mp + j] : 0.f;
 #pragma unroll
-    for (int x = 0; x < XS; ++x) {
-      const int64_t i0 = ti * TILE + wi * (TILE / WI) + x * 32 + 4 * half;
-      // Rows past M (< Mp) lie inside the zero-padded planes.
-      uint16_t hi[16], lo[16];
+      for (int x = 0; x < XS; ++x) {
+        const int64_t i0 = ib + x * 32;
+        // Rows past M (< Mp) lie inside the zero-padded planes.
+        const uint16_t* xh = a.xhi + pbase + i0 * a.Mp + j;
+        const uint16_t* xl = a.xlo + pbase + i0 * a.Mp + j;
+        const int mp = static_cast<int>(a.Mp);
+        uint16_t hi[16], lo[16];
+        if constexpr (!FUSED) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int64_t i = i0 + 8 * (e >> 2) + (e & 3);
-        hi[e] = a.xhi[pbase + i * a.Mp + j];
-        lo[e] = a.xlo[pbase + i * a.Mp + j];
-      }
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int64_t i = i0 + 8 * (e >> 2) + (e & 3);
-        if (i >= a.M) continue;
-        float t = acc[x][y][e], ahat;
-        if constexpr (F16) {
-          ahat = f16_to_f32(hi[e]) + f16_to_f32(lo[e]);
-          if (constant) {
-            ahat = cval;
-            t = static_cast<float>(a.M) * cval * cval;
+          for (int e = 0; e < 16; ++e) {
+            const int r = 8 * (e >> 2) + (e & 3);
+            hi[e] = xh[r * mp];
+            if constexpr (LO) lo[e] = xl[r * mp];
           }
-        } else {
-          ahat = bf16_to_f32(hi[e]) + bf16_to_f32(lo[e]);
         }
-        const float si = a.formula == CAB_FRC_AUGMENTED ? a.rowsum[bh * a.Mp + i] : 0.f;
-        a.frc[obase + i * a.M + j] = frc_combine(a.formula, ahat, t, a.lambda, si, sj);
-        if (a.tri) a.tri[obase + i * a.M + j] = t;
+        float* fo = a.frc + obase + i0 * a.M + j;
+        float* to = a.tri ? a.tri + obase + i0 * a.M + j : nullptr;
+        const int m = static_cast<int>(a.M);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = 8 * (e >> 2) + (e & 3);
+          if (i0 + r >= a.M) continue;
+          float t = acc[x][y][e], ahat;
+          if constexpr (FUSED) {
+            float f = constant ? cval - a.lambda * (static_cast<float>(a.M) * cval * cval) : t;
+            fo[r * m] = isfinite(f) ? f : 0.f;
+            continue;
+          } else if constexpr (F16) {
+            ahat = f16_to_f32(hi[e]);
+            if constexpr (LO) ahat += f16_to_f32(lo[e]);
+            if (constant) {
+              ahat = cval;
+              t = static_cast<float>(a.M) * cval * cval;
+            }
+          } else {
+            ahat = bf16_to_f32(hi[e]) + bf16_to_f32(lo[e]);
+          }
+          const float si = FORM == CAB_FRC_AUGMENTED ? a.rowsum[bh * a.Mp + i0 + r] : 0.f;
+          fo[r * m] = frc_combine(FORM, ahat, t, a.lambda, si, sj);
+          if (to) to[r * m] = t;
+        }
       }
     }
-  }
+  };
+  if (a.fused)
+    epilogue(std::integral_constant<int, -1>{});
+  else if (a.formula == CAB_FRC_ADDITIVE)
+    epilogue(std::integral_constant<int, CAB_FRC_ADDITIVE>{});
+  else if (a.formula == CAB_FRC_MULTIPLICATIVE)
+    epilogue(std::integral_constant<int, CAB_FRC_MULTIPLICATIVE>{});
+  else
+    epilogue(std::integral_constant<int, CAB_FRC_AUGMENTED>{});
 }
 
 template <typename T>
@@ -654,6 +706,12 @@ extern "C" cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_
   // cancel T against row sums.
   const bool f16 = normalization == CAB_NORM_MINMAX && formula != CAB_FRC_AUGMENTED;
   a.f16_planes = f16 ? 1 : 0;
+  // Additive formula without the T diagnostic: F = Ahat (I - lambda Ahat) in
+  // one GEMM (|lambda| bounded so that I - lambda Ahat fits fp16).
+  const bool fused = f16 && formula == CAB_FRC_ADDITIVE && triangles == nullptr &&
+                     std::fabs(lambda_redundancy) <= 1024.f;
+  a.fused = fused ? 1 : 0;
+  a.lambda = lambda_redundancy;
 
   if (normalization == CAB_NORM_MINMAX) {
     switch (dtype) {
@@ -696,6 +754,7 @@ extern "C" cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_
   t.BH = BH;
   t.lambda = lambda_redundancy;
   t.formula = formula;
+  t.fused = fused ? 1 : 0;
   // The 256-wide tile stages half the bytes per flop; it is used when Mp
   // allows it and its tiles still give every CU work.
   const bool wide = L.Mp % TT_WIDE == 0 && BH * (L.Mp / TT_WIDE) * (L.Mp / TT_WIDE) >= 256;

@@ -184,13 +184,61 @@ def test_frc_constant_affinity(cuda, formula):
 
 
 def test_frc_no_diagnostics_matches(cuda):
+    """Without diagnostics the additive formula is one GEMM, F = Ahat (I - lambda Ahat);
+    the multiplicative one keeps the T path. Both stay within the FRC bound
+    and agree with the diagnostics call to within it."""
     from cab_attention.kernels import compute_block_frc
     qc = seeded((2, 2, 300, 128), 13, torch.bfloat16).to(cuda)
     kc = seeded((2, 2, 300, 128), 14, torch.bfloat16).to(cuda)
-    f1, a1, t1 = compute_block_frc(qc, kc)
-    f2, a2, t2 = compute_block_frc(qc, kc, diagnostics=False)
-    assert a2 is None and t2 is None
-    assert torch.equal(f1, f2)
+    for formula in ("additive", "multiplicative"):
+        f1, a1, t1 = compute_block_frc(qc, kc, formula=formula)
+        f2, a2, t2 = compute_block_frc(qc, kc, formula=formula, diagnostics=False)
+        assert a2 is None and t2 is None
+        of, oa, ot = O.compute_block_frc(np32(qc), np32(kc), formula=formula)
+        if formula == "multiplicative":
+            assert torch.equal(f1, f2)
+        else:
+            assert_frc_close(f2, of, oa, ot, 0.5)
+            assert_frc_close(f1, of, oa, ot, 0.5)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp16", "fp32"])
+@pytest.mark.parametrize("M", [1, 100, 257, 512])
+@pytest.mark.parametrize("lam", [0.5, 0.0, -2.0, 3.0])
+def test_frc_fused_additive(cuda, dt, M, lam):
+    """The additive formula without the T diagnostic: the triangle GEMM takes
+    B = I - lambda Ahat (fp16), so its accumulator is F itself."""
+    from cab_attention.kernels import compute_block_frc
+    B, H, D = 1, 2, 128
+    qc = seeded((B, H, M, D), 21, DTYPES[dt], scale=3.0)
+    kc = seeded((B, H, M, D), 22, DTYPES[dt], scale=3.0)
+    f, a, t = compute_block_frc(qc.to(cuda), kc.to(cuda), lambda_redundancy=lam, diagnostics=False)
+    of, oa, ot = O.compute_block_frc(np32(qc), np32(kc), lambda_redundancy=lam)
+    assert a is None and t is None
+    assert_frc_close(f, of, oa, ot, lam)
+
+
+def test_frc_fused_additive_wide_tile(cuda):
+    """Config-3 geometry per head (M = 2000, 256-wide tiles) on the fused path."""
+    from cab_attention.kernels import compute_block_frc
+    qc = seeded((1, 4, 2000, 128), 23, torch.bfloat16)
+    kc = seeded((1, 4, 2000, 128), 24, torch.bfloat16)
+    f, _, _ = compute_block_frc(qc.to(cuda), kc.to(cuda), diagnostics=False)
+    of, oa, ot = O.compute_block_frc(np32(qc), np32(kc))
+    assert_frc_close(f, of, oa, ot, 0.5)
+
+
+def test_frc_fused_constant_affinity(cuda):
+    """min == max on the fused path: F = c - lambda M c^2 without the planes."""
+    from cab_attention.kernels import compute_block_frc
+    qc = torch.zeros(1, 2, 300, 128)
+    kc = torch.zeros(1, 2, 300, 128)
+    qc[..., 0] = float(2 ** 20 + 3)
+    kc[..., 0] = 1.0
+    qc[0, 1] = 0.0
+    f, _, _ = compute_block_frc(qc.to(cuda), kc.to(cuda), diagnostics=False)
+    of, _, _ = O.compute_block_frc(qc.numpy(), kc.numpy())
+    np.testing.assert_allclose(np32(f), of, rtol=1e-5, atol=1e-6)
 
 
 def test_bridge_known_answer_on_gpu(cuda):
