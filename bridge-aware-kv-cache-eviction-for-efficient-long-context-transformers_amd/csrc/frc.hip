@@ -1,8 +1,9 @@
 // Coarse Forman-Ricci curvature (cab_block_frc).
 //
 // Pipeline per (b, h), Mp = M rounded up to 128:
-//  1. affinity_kernel<STATS>: A = qc kc^T * alpha on MFMA (64x64 tile per
-//     workgroup, one 32x32 tile per wave), per-tile min/max partials.
+//  1. affinity_kernel<STATS>: A = qc kc^T * alpha on MFMA (128x128 tile per
+//     workgroup, a 64x64 quadrant of four 32x32 tiles per wave), per-tile
+//     min/max partials.
 //  2. minmax_finalize_kernel: per-(b,h) min/max from the partials.
 //  3. affinity_kernel<EMIT>: recomputes the A tile, normalises it, and writes
 //     Ahat in row-major X and transposed XT planes (zero outside M), the fp32
@@ -10,7 +11,9 @@
 //     planes hold either
 //       - fp16 (minmax normalisation, additive or multiplicative formula):
 //         Ahat lies in [0, 1], X = f16(Ahat), XT likewise, plus the low part
-//         f16(Ahat - X) of X for the epilogue; or
+//         f16(Ahat - X) of X for the epilogue; for the additive formula
+//         without the T diagnostic, XT = f16(I - lambda Ahat)^T instead, so
+//         that the GEMM accumulates F = Ahat (I - lambda Ahat) itself; or
 //       - a bf16 hi/lo pair (hi = bf16(Ahat), lo = bf16(Ahat - hi)) of X and
 //         of XT, for unnormalised values of any range and for the augmented
 //         formula, whose S_i + S_j cancels against 3 T.
@@ -26,13 +29,14 @@
 namespace cab {
 namespace {
 
-constexpr int AT = 64;    // affinity tile
+constexpr int AT = 64;    // affinity quadrant (one wave; row-sum partials per AT columns)
+constexpr int AW = 128;   // affinity tile per workgroup (2 x 2 quadrants)
 constexpr int TT = 128;   // triangle tile
 constexpr int TT_WIDE = 256;  // wide triangle tile (large M)
 constexpr int TK = 32;    // triangle k-slice depth
 
 struct FrcLayout {
-  int64_t Mp, nta;  // padded M, affinity tiles per dim
+  int64_t Mp, nta, ntw;  // padded M, AT column blocks and AW workgroup tiles per dim
   size_t plane;     // bytes of one [BH][Mp][Mp] bf16 plane
   size_t off_xhi, off_xlo, off_xthi, off_xtlo, off_mmpart, off_mm, off_rspart, off_rs, total;
 };
@@ -41,6 +45,7 @@ FrcLayout frc_layout(int64_t BH, int64_t M) {
   FrcLayout L;
   L.Mp = round_up(M, TT);
   L.nta = L.Mp / AT;
+  L.ntw = L.Mp / AW;
   L.plane = static_cast<size_t>(BH) * L.Mp * L.Mp * 2;
   size_t o = 0;
   auto take = [&](size_t bytes) {
@@ -52,7 +57,7 @@ FrcLayout frc_layout(int64_t BH, int64_t M) {
   L.off_xlo = take(L.plane);
   L.off_xthi = take(L.plane);
   L.off_xtlo = take(L.plane);
-  L.off_mmpart = take(static_cast<size_t>(BH) * L.nta * L.nta * 2 * sizeof(float));
+  L.off_mmpart = take(static_cast<size_t>(BH) * L.ntw * L.ntw * 2 * sizeof(float));
   L.off_mm = take(static_cast<size_t>(BH) * 2 * sizeof(float));
   L.off_rspart = take(static_cast<size_t>(BH) * L.nta * L.Mp * sizeof(float));
   L.off_rs = take(static_cast<size_t>(BH) * L.Mp * sizeof(float));
@@ -63,11 +68,11 @@ FrcLayout frc_layout(int64_t BH, int64_t M) {
 struct AffArgs {
   const void* qc;
   const void* kc;
-  int64_t M, Mp, nta;
+  int64_t M, Mp, nta, ntw;
   int32_t D;
   float alpha;
   int normalization;
-  float* mmpart;       // [BH][nta*nta][2]
+  float* mmpart;       // [BH][ntw*ntw][2]
   const float* mm;     // [BH][2]
   uint16_t* xhi;       // [BH][Mp][Mp]
   uint16_t* xlo;
@@ -80,76 +85,110 @@ struct AffArgs {
   float lambda;
 };
 
-// One wave computes a 32x32 tile of qc kc^T (fp32 accumulate). Lane l owns
-// column l % 32 and rows 8 * (e / 4) + 4 * (l / 32) + e % 4 of acc[e].
+// One wave computes a 64x64 quadrant of qc kc^T (fp32 accumulate) as 2 x 2
+// MFMA tiles: acc[x][y] covers rows row0 + 32 x .., columns col0 + 32 y ..;
+// lane l owns column l % 32 and rows 8 * (e / 4) + 4 * (l / 32) + e % 4 of
+// each tile's element e.
 template <typename T>
-__device__ __forceinline__ f32x16 aff_tile(const void* qcv, const void* kcv, int64_t row0,
-                                           int64_t col0, int64_t M, int D, int lane) {
-  f32x16 acc = {};
-  const int64_t r = row0 + (lane & 31), c = col0 + (lane & 31);
+__device__ __forceinline__ void aff_quad(const void* qcv, const void* kcv, int64_t row0,
+                                         int64_t col0, int64_t M, int D, int lane,
+                                         f32x16 (&acc)[2][2]) {
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) acc[x][y] = f32x16{};
   const int half = lane >> 5;
+  int64_t r[2], c[2];
+  bool ra[2], cb[2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    r[x] = row0 + 32 * x + (lane & 31);
+    c[x] = col0 + 32 * x + (lane & 31);
+    ra[x] = r[x] < M;
+    cb[x] = c[x] < M;
+  }
   if constexpr (sizeof(T) == 4) {
     // fp32: 32x32x2 MFMA; lane half h holds k = 8q + 4h + s in step s.
-    const float* qa = static_cast<const float*>(qcv) + r * D;
-    const float* kb = static_cast<const float*>(kcv) + c * D;
-    const bool ra = r < M, cb = c < M;
+    const float* q = static_cast<const float*>(qcv);
+    const float* k = static_cast<const float*>(kcv);
     for (int k0 = 0; k0 < D; k0 += 8) {
-      f32x4 av = {0.f, 0.f, 0.f, 0.f}, bv = {0.f, 0.f, 0.f, 0.f};
-      if (ra) av = *reinterpret_cast<const f32x4*>(qa + k0 + 4 * half);
-      if (cb) bv = *reinterpret_cast<const f32x4*>(kb + k0 + 4 * half);
+      f32x4 av[2], bv[2];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[s], bv[s], acc, 0, 0, 0);
+      for (int x = 0; x < 2; ++x) {
+        av[x] = ra[x] ? *reinterpret_cast<const f32x4*>(q + r[x] * D + k0 + 4 * half) : f32x4{};
+        bv[x] = cb[x] ? *reinterpret_cast<const f32x4*>(k + c[x] * D + k0 + 4 * half) : f32x4{};
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int y = 0; y < 2; ++y)
+            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[x][s], bv[y][s], acc[x][y], 0, 0, 0);
     }
   } else {
-    const uint16_t* qa = static_cast<const uint16_t*>(qcv) + r * D;
-    const uint16_t* kb = static_cast<const uint16_t*>(kcv) + c * D;
-    const bool ra = r < M, cb = c < M;
+    const uint16_t* q = static_cast<const uint16_t*>(qcv);
+    const uint16_t* k = static_cast<const uint16_t*>(kcv);
     for (int k0 = 0; k0 < D; k0 += 16) {
-      u32x4 av = {0u, 0u, 0u, 0u}, bv = {0u, 0u, 0u, 0u};
       const bool kin = k0 + 8 * half < D;  // D % 16 == 8: the upper half is past the row
-      if (ra && kin) av = *reinterpret_cast<const u32x4*>(qa + k0 + 8 * half);
-      if (cb && kin) bv = *reinterpret_cast<const u32x4*>(kb + k0 + 8 * half);
-      if constexpr (std::is_same<T, bf16_t>::value)
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av),
-                                                      __builtin_bit_cast(bf16x8, bv), acc, 0, 0, 0);
-      else
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, av),
-                                                     __builtin_bit_cast(f16x8, bv), acc, 0, 0, 0);
+      u32x4 av[2], bv[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        av[x] = ra[x] && kin ? *reinterpret_cast<const u32x4*>(q + r[x] * D + k0 + 8 * half) : u32x4{};
+        bv[x] = cb[x] && kin ? *reinterpret_cast<const u32x4*>(k + c[x] * D + k0 + 8 * half) : u32x4{};
+      }
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) {
+          if constexpr (std::is_same<T, bf16_t>::value)
+            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8, av[x]), __builtin_bit_cast(bf16x8, bv[y]), acc[x][y], 0, 0, 0);
+          else
+            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                __builtin_bit_cast(f16x8, av[x]), __builtin_bit_cast(f16x8, bv[y]), acc[x][y], 0, 0, 0);
+        }
     }
   }
-  return acc;
 }
 
 __device__ __forceinline__ float normalize_minmax(float a, float mn, float mx) {
   return mx > mn ? (a - mn) / (mx - mn + 1e-8f) : a;
 }
 
+// A 128 x 128 tile per workgroup; wave w computes quadrant (w / 2, w % 2).
 template <typename T, bool EMIT>
 __global__ __launch_bounds__(256) void affinity_kernel(AffArgs a) {
   const int64_t bh = blockIdx.y;
   const int64_t tile = blockIdx.x;
-  const int64_t ti = tile / a.nta, tj = tile - (tile / a.nta) * a.nta;
+  const int64_t ti = tile / a.ntw, tj = tile - (tile / a.ntw) * a.ntw;
   const int w = threadIdx.x >> 6, lane = lane_id();
   const int wi = w >> 1, wj = w & 1;
-  const int64_t row0 = ti * AT + wi * 32, col0 = tj * AT + wj * 32;
+  const int64_t row0 = ti * AW + wi * AT, col0 = tj * AW + wj * AT;
   const size_t esz = sizeof(T) == 4 ? 4 : 2;
   const char* qcb = static_cast<const char*>(a.qc) + static_cast<size_t>(bh) * a.M * a.D * esz;
   const char* kcb = static_cast<const char*>(a.kc) + static_cast<size_t>(bh) * a.M * a.D * esz;
-  f32x16 acc = aff_tile<T>(qcb, kcb, row0, col0, a.M, a.D, lane);
+  f32x16 acc[2][2];
+  aff_quad<T>(qcb, kcb, row0, col0, a.M, a.D, lane, acc);
 
-  const int64_t j = col0 + (lane & 31);
   const int half = lane >> 5;
+  // Row and column of element e of MFMA tile (x, y), relative to the quadrant.
+  auto qrow = [&](int x, int e) { return 32 * x + 8 * (e >> 2) + 4 * half + (e & 3); };
+  auto qcol = [&](int y) { return 32 * y + (lane & 31); };
   if constexpr (!EMIT) {
     float mn = INFINITY, mx = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int64_t i = row0 + 8 * (e >> 2) + 4 * half + (e & 3);
-      if (i < a.M && j < a.M) {
-        const float v = acc[e] * a.alpha;
-        mn = fminf(mn, v);
-        mx = fmaxf(mx, v);
-      }
-    }
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int y = 0; y < 2; ++y)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          if (row0 + qrow(x, e) < a.M && col0 + qcol(y) < a.M) {
+            const float v = acc[x][y][e] * a.alpha;
+            mn = fminf(mn, v);
+            mx = fmaxf(mx, v);
+          }
+        }
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       mn = fminf(mn, shfl_xor_f32(mn, off));
@@ -164,7 +203,7 @@ __global__ __launch_bounds__(256) void affinity_kernel(AffArgs a) {
     if (threadIdx.x == 0) {
       float m0 = fminf(fminf(red[0][0], red[1][0]), fminf(red[2][0], red[3][0]));
       float m1 = fmaxf(fmaxf(red[0][1], red[1][1]), fmaxf(red[2][1], red[3][1]));
-      float* p = a.mmpart + (bh * a.nta * a.nta + tile) * 2;
+      float* p = a.mmpart + (bh * a.ntw * a.ntw + tile) * 2;
       p[0] = m0;
       p[1] = m1;
     }
@@ -174,115 +213,116 @@ __global__ __launch_bounds__(256) void affinity_kernel(AffArgs a) {
       mn = a.mm[bh * 2 + 0];
       mx = a.mm[bh * 2 + 1];
     }
-    // The normalised 64 x 64 tile goes through LDS so that every plane is
-    // written as whole 16-byte row chunks: X rows from the tile's rows, XT
-    // rows from its columns (zero outside M: the planes are Mp x Mp).
-    __shared__ float stile[AT][AT + 1];
-    float rowpart[16];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int il = wi * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
-      const int64_t i = row0 + 8 * (e >> 2) + 4 * half + (e & 3);
-      float v = 0.f;
-      if (i < a.M && j < a.M) {
-        v = acc[e] * a.alpha;
-        if (a.normalization == CAB_NORM_MINMAX) v = normalize_minmax(v, mn, mx);
-      }
-      rowpart[e] = v;
-      stile[il][wj * 32 + (lane & 31)] = v;
-    }
-    __syncthreads();
-    const size_t pbase = static_cast<size_t>(bh) * a.Mp * a.Mp;
-    const int64_t ti0 = ti * AT, tj0 = tj * AT;
+    for (int x = 0; x < 2; ++x)
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int cid = threadIdx.x + 256 * q;  // 64 rows x 8 chunks of 8 values
-      const int r = cid >> 3, c8 = (cid & 7) * 8;
-      const size_t xo = pbase + static_cast<size_t>(ti0 + r) * a.Mp + tj0 + c8;
-      const size_t to = pbase + static_cast<size_t>(tj0 + r) * a.Mp + ti0 + c8;
-      u32x4 h4, l4, th4, tl4;
-      if (a.fused) {
-        // XT row tj0 + r, column ti0 + c: delta - lambda Ahat[ti0 + c][tj0 + r]
-        // (the delta only inside M; the planes are zero beyond it).
-        const int64_t jrow = tj0 + r;
+      for (int y = 0; y < 2; ++y)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float x0 = stile[r][c8 + 2 * e], x1 = stile[r][c8 + 2 * e + 1];
-          const int64_t k0 = ti0 + c8 + 2 * e;
-          const float d0 = (k0 == jrow && k0 < a.M) ? 1.f : 0.f;
-          const float d1 = (k0 + 1 == jrow && k0 + 1 < a.M) ? 1.f : 0.f;
-          const float y0 = d0 - a.lambda * stile[c8 + 2 * e][r];
-          const float y1 = d1 - a.lambda * stile[c8 + 2 * e + 1][r];
-          h4[e] = static_cast<uint32_t>(f32_to_f16(x0)) | (static_cast<uint32_t>(f32_to_f16(x1)) << 16);
-          th4[e] = static_cast<uint32_t>(f32_to_f16(y0)) | (static_cast<uint32_t>(f32_to_f16(y1)) << 16);
+        for (int e = 0; e < 16; ++e) {
+          float v = 0.f;
+          if (row0 + qrow(x, e) < a.M && col0 + qcol(y) < a.M) {
+            v = acc[x][y][e] * a.alpha;
+            if (a.normalization == CAB_NORM_MINMAX) v = normalize_minmax(v, mn, mx);
+          }
+          acc[x][y][e] = v;
         }
-        *reinterpret_cast<u32x4*>(a.xhi + xo) = h4;
-        *reinterpret_cast<u32x4*>(a.xthi + to) = th4;
-        continue;
+    if (a.rspart) {
+      // Row sums over the quadrant's 64 columns (one AT column block).
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float sum = acc[x][0][e] + acc[x][1][e];
+#pragma unroll
+          for (int off = 1; off < 32; off <<= 1) sum += shfl_xor_f32(sum, off);
+          if ((lane & 31) == 0)
+            a.rspart[(static_cast<size_t>(bh) * a.nta + col0 / AT) * a.Mp + row0 + qrow(x, e)] = sum;
+        }
+    }
+    // Each normalised 64 x 64 quadrant goes through LDS in turn, so that every
+    // plane is written as whole 16-byte row chunks: X rows from the
+    // quadrant's rows, XT rows from its columns (zero outside M: the planes
+    // are Mp x Mp).
+    __shared__ float stile[AT][AT + 1];
+    const size_t pbase = static_cast<size_t>(bh) * a.Mp * a.Mp;
+    for (int qd = 0; qd < 4; ++qd) {
+      if (qd > 0) __syncthreads();  // the previous quadrant's reads are done
+      if (w == qd) {
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int y = 0; y < 2; ++y)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) stile[qrow(x, e)][qcol(y)] = acc[x][y][e];
       }
-      if (a.f16_planes) {
+      __syncthreads();
+      const int64_t ti0 = ti * AW + AT * (qd >> 1), tj0 = tj * AW + AT * (qd & 1);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int cid = threadIdx.x + 256 * q;  // 64 rows x 8 chunks of 8 values
+        const int r = cid >> 3, c8 = (cid & 7) * 8;
+        const size_t xo = pbase + static_cast<size_t>(ti0 + r) * a.Mp + tj0 + c8;
+        const size_t to = pbase + static_cast<size_t>(tj0 + r) * a.Mp + ti0 + c8;
+        u32x4 h4, l4, th4, tl4;
+        if (a.fused) {
+          // XT row tj0 + r, column ti0 + c: delta - lambda Ahat[ti0 + c][tj0 + r]
+          // (the delta only inside M; the planes are zero beyond it).
+          const int64_t jrow = tj0 + r;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float x0 = stile[r][c8 + 2 * e], x1 = stile[r][c8 + 2 * e + 1];
+            const int64_t k0 = ti0 + c8 + 2 * e;
+            const float d0 = (k0 == jrow && k0 < a.M) ? 1.f : 0.f;
+            const float d1 = (k0 + 1 == jrow && k0 + 1 < a.M) ? 1.f : 0.f;
+            const float y0 = d0 - a.lambda * stile[c8 + 2 * e][r];
+            const float y1 = d1 - a.lambda * stile[c8 + 2 * e + 1][r];
+            h4[e] = static_cast<uint32_t>(f32_to_f16(x0)) | (static_cast<uint32_t>(f32_to_f16(x1)) << 16);
+            th4[e] = static_cast<uint32_t>(f32_to_f16(y0)) | (static_cast<uint32_t>(f32_to_f16(y1)) << 16);
+          }
+          *reinterpret_cast<u32x4*>(a.xhi + xo) = h4;
+          *reinterpret_cast<u32x4*>(a.xthi + to) = th4;
+          continue;
+        }
+        if (a.f16_planes) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float x0 = stile[r][c8 + 2 * e], x1 = stile[r][c8 + 2 * e + 1];
+            const float y0 = stile[c8 + 2 * e][r], y1 = stile[c8 + 2 * e + 1][r];
+            const uint16_t hx0 = f32_to_f16(x0), hx1 = f32_to_f16(x1);
+            h4[e] = static_cast<uint32_t>(hx0) | (static_cast<uint32_t>(hx1) << 16);
+            l4[e] = static_cast<uint32_t>(f32_to_f16(x0 - f16_to_f32(hx0))) |
+                    (static_cast<uint32_t>(f32_to_f16(x1 - f16_to_f32(hx1))) << 16);
+            th4[e] = static_cast<uint32_t>(f32_to_f16(y0)) | (static_cast<uint32_t>(f32_to_f16(y1)) << 16);
+          }
+          *reinterpret_cast<u32x4*>(a.xhi + xo) = h4;
+          *reinterpret_cast<u32x4*>(a.xlo + xo) = l4;
+          *reinterpret_cast<u32x4*>(a.xthi + to) = th4;
+          continue;
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float x0 = stile[r][c8 + 2 * e], x1 = stile[r][c8 + 2 * e + 1];
-          const float y0 = stile[c8 + 2 * e][r], y1 = stile[c8 + 2 * e + 1][r];
-          const uint16_t hx0 = f32_to_f16(x0), hx1 = f32_to_f16(x1);
+          const float x0 = stile[r][c8 + 2 * e], x1 = stile[r][c8 + 2 * e + 1];    // X row ti0 + r
+          const float y0 = stile[c8 + 2 * e][r], y1 = stile[c8 + 2 * e + 1][r];    // XT row tj0 + r
+          const uint16_t hx0 = f32_to_bf16(x0), hx1 = f32_to_bf16(x1);
+          const uint16_t hy0 = f32_to_bf16(y0), hy1 = f32_to_bf16(y1);
           h4[e] = static_cast<uint32_t>(hx0) | (static_cast<uint32_t>(hx1) << 16);
-          l4[e] = static_cast<uint32_t>(f32_to_f16(x0 - f16_to_f32(hx0))) |
-                  (static_cast<uint32_t>(f32_to_f16(x1 - f16_to_f32(hx1))) << 16);
-          th4[e] = static_cast<uint32_t>(f32_to_f16(y0)) | (static_cast<uint32_t>(f32_to_f16(y1)) << 16);
+          l4[e] = static_cast<uint32_t>(f32_to_bf16(x0 - bf16_to_f32(hx0))) |
+                  (static_cast<uint32_t>(f32_to_bf16(x1 - bf16_to_f32(hx1))) << 16);
+          th4[e] = static_cast<uint32_t>(hy0) | (static_cast<uint32_t>(hy1) << 16);
+          tl4[e] = static_cast<uint32_t>(f32_to_bf16(y0 - bf16_to_f32(hy0))) |
+                   (static_cast<uint32_t>(f32_to_bf16(y1 - bf16_to_f32(hy1))) << 16);
         }
         *reinterpret_cast<u32x4*>(a.xhi + xo) = h4;
         *reinterpret_cast<u32x4*>(a.xlo + xo) = l4;
         *reinterpret_cast<u32x4*>(a.xthi + to) = th4;
-        continue;
+        *reinterpret_cast<u32x4*>(a.xtlo + to) = tl4;
       }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float x0 = stile[r][c8 + 2 * e], x1 = stile[r][c8 + 2 * e + 1];    // X row ti0 + r
-        const float y0 = stile[c8 + 2 * e][r], y1 = stile[c8 + 2 * e + 1][r];    // XT row tj0 + r
-        const uint16_t hx0 = f32_to_bf16(x0), hx1 = f32_to_bf16(x1);
-        const uint16_t hy0 = f32_to_bf16(y0), hy1 = f32_to_bf16(y1);
-        h4[e] = static_cast<uint32_t>(hx0) | (static_cast<uint32_t>(hx1) << 16);
-        l4[e] = static_cast<uint32_t>(f32_to_bf16(x0 - bf16_to_f32(hx0))) |
-                (static_cast<uint32_t>(f32_to_bf16(x1 - bf16_to_f32(hx1))) << 16);
-        th4[e] = static_cast<uint32_t>(hy0) | (static_cast<uint32_t>(hy1) << 16);
-        tl4[e] = static_cast<uint32_t>(f32_to_bf16(y0 - bf16_to_f32(hy0))) |
-                 (static_cast<uint32_t>(f32_to_bf16(y1 - bf16_to_f32(hy1))) << 16);
-      }
-      *reinterpret_cast<u32x4*>(a.xhi + xo) = h4;
-      *reinterpret_cast<u32x4*>(a.xlo + xo) = l4;
-      *reinterpret_cast<u32x4*>(a.xthi + to) = th4;
-      *reinterpret_cast<u32x4*>(a.xtlo + to) = tl4;
-    }
-    if (a.affinity) {
-      // fp32 diagnostic, rows of the tile inside M (coalesced along j)
-      for (int e = threadIdx.x; e < AT * AT; e += 256) {
-        const int r = e >> 6, c = e & 63;
-        const int64_t i = ti0 + r, jj = tj0 + c;
-        if (i < a.M && jj < a.M) a.affinity[(static_cast<size_t>(bh) * a.M + i) * a.M + jj] = stile[r][c];
-      }
-    }
-    if (a.rspart) {
-      // Row sums over the tile's 64 columns: 32 lanes per wave, 2 waves.
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        float s = rowpart[e];
-#pragma unroll
-        for (int off = 1; off < 32; off <<= 1) s += shfl_xor_f32(s, off);
-        rowpart[e] = s;
-      }
-      __shared__ float rs[2][32];
-      if ((lane & 31) == 0 && wj == 1) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) rs[wi][8 * (e >> 2) + 4 * half + (e & 3)] = rowpart[e];
-      }
-      __syncthreads();
-      if ((lane & 31) == 0 && wj == 0) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int il = 8 * (e >> 2) + 4 * half + (e & 3);
-          const int64_t i = row0 + il;
-          a.rspart[(static_cast<size_t>(bh) * a.nta + tj) * a.Mp + i] = rowpart[e] + rs[wi][il];
+      if (a.affinity) {
+        // fp32 diagnostic, rows of the quadrant inside M (coalesced along j)
+        for (int e = threadIdx.x; e < AT * AT; e += 256) {
+          const int r = e >> 6, c = e & 63;
+          const int64_t i = ti0 + r, jj = tj0 + c;
+          if (i < a.M && jj < a.M) a.affinity[(static_cast<size_t>(bh) * a.M + i) * a.M + jj] = stile[r][c];
         }
       }
     }
@@ -630,7 +670,7 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
 
 template <typename T>
 void launch_affinity(const AffArgs& a, int64_t BH, bool emit, hipStream_t s) {
-  dim3 grid(static_cast<unsigned>(a.nta * a.nta), static_cast<unsigned>(BH));
+  dim3 grid(static_cast<unsigned>(a.ntw * a.ntw), static_cast<unsigned>(BH));
   if (emit)
     affinity_kernel<T, true><<<grid, 256, 0, s>>>(a);
   else
@@ -691,6 +731,7 @@ extern "C" cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_
   a.M = M;
   a.Mp = L.Mp;
   a.nta = L.nta;
+  a.ntw = L.ntw;
   a.D = static_cast<int32_t>(D);
   a.alpha = static_cast<float>(static_cast<double>(scale) / static_cast<double>(temperature));
   a.normalization = normalization;
@@ -722,7 +763,7 @@ extern "C" cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_
     cab_status_t st = launch_status("cab_block_frc/affinity_stats");
     if (st != CAB_OK) return st;
     minmax_finalize_kernel<<<static_cast<unsigned>(BH), 256, 0, s>>>(
-        a.mmpart, L.nta * L.nta, reinterpret_cast<float*>(ws + L.off_mm));
+        a.mmpart, L.ntw * L.ntw, reinterpret_cast<float*>(ws + L.off_mm));
     st = launch_status("cab_block_frc/minmax_finalize");
     if (st != CAB_OK) return st;
   }
