@@ -374,7 +374,7 @@ struct TriArgs {
   const float* mm;      // [BH][2] minmax of A (fp16 planes only)
   float* frc;           // [BH][M][M]
   float* tri;           // [BH][M][M] or null
-  int64_t M, Mp, nt, BH;
+  int64_t M, Mp, nti, ntj, BH;  // nti x ntj tiles per (b, h)
   float lambda;
   int formula;
   int fused;            // fp16 planes with XT = I - lambda Ahat^T: the accumulator is F
@@ -433,44 +433,41 @@ __device__ __forceinline__ float frc_combine(int formula, float ahat, float t, f
   return f;
 }
 
-// T tile of TILE x TILE per workgroup of WI x WJ waves; wave (wi, wj) owns
-// rows wi TILE / WI .. and columns wj TILE / WJ .. as XS x YS MFMA tiles.
-// NBUF register buffers carry operand slices global -> registers -> LDS
-// (two LDS stages): with NBUF = 2 a slice's loads have two slices of MFMA
-// work to land, with NBUF = 1 one slice (for the wide bf16 tile, whose
-// accumulators leave room for one buffer of four planes only). F16 selects
-// the fp16 planes (A = X, B = XT, one product per site); otherwise the four
-// bf16 planes (A hi, A lo, B hi, B lo; three products).
-template <int TILE, int WI, int WJ, int NBUF, bool F16, int KD>
+// T tile of TI x TJ per workgroup of WI x WJ waves; wave (wi, wj) owns rows
+// wi TI / WI .. and columns wj TJ / WJ .. as XS x YS MFMA tiles. NBUF
+// register buffers carry operand slices global -> registers -> LDS (two LDS
+// stages): with NBUF = 2 a slice's loads have two slices of MFMA work to
+// land, with NBUF = 1 one slice (for the wide bf16 tile, whose accumulators
+// leave room for one buffer of four planes only). F16 selects the fp16 planes
+// (A = X, B = XT, one product per site); otherwise the bf16 hi / lo planes of
+// both operands (three products).
+template <int TI, int TJ, int WI, int WJ, int NBUF, bool F16, int KD>
 __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
   constexpr int THREADS = WI * WJ * 64;
-  constexpr int XS = TILE / WI / 32, YS = TILE / WJ / 32;
-  constexpr int SLOTS = tri_slots<TILE, KD>();
-  constexpr int CH = tri_chunks<TILE, THREADS, KD>();
-  static_assert(CH * THREADS == TILE * (KD / 8), "whole chunks per thread");
-  constexpr int NP = F16 ? 2 : 4;  // planes staged per slice
-  __shared__ u32x4 lds[2][NP][SLOTS];  // [stage][plane][slot]
-  const int64_t total = a.BH * a.nt * a.nt;
+  constexpr int XS = TI / WI / 32, YS = TJ / WJ / 32;
+  constexpr int SA = tri_slots<TI, KD>(), SB = tri_slots<TJ, KD>();
+  constexpr int CA = tri_chunks<TI, THREADS, KD>(), CB = tri_chunks<TJ, THREADS, KD>();
+  static_assert(CA * THREADS == TI * (KD / 8) && CB * THREADS == TJ * (KD / 8),
+                "whole chunks per thread");
+  constexpr int NH = F16 ? 1 : 2;           // planes per operand: hi (and lo)
+  constexpr int STAGE = NH * (SA + SB);     // slots per LDS stage: A planes, then B planes
+  __shared__ u32x4 lds[2 * STAGE];
+  const int64_t per = a.nti * a.ntj;
+  const int64_t total = a.BH * per;
   const int64_t logical = xcd_remap(blockIdx.x, total);
-  const int64_t bh = logical / (a.nt * a.nt);
-  const int64_t rem = logical - bh * a.nt * a.nt;
-  const int64_t ti = rem / a.nt, tj = rem - (rem / a.nt) * a.nt;
+  const int64_t bh = logical / per;
+  const int64_t rem = logical - bh * per;
+  const int64_t ti = rem / a.ntj, tj = rem - (rem / a.ntj) * a.ntj;
   const size_t pbase = static_cast<size_t>(bh) * a.Mp * a.Mp;
-  const uint16_t* planes[NP];
-  int64_t rows[NP];
-  if constexpr (F16) {
-    planes[0] = a.xhi + pbase;
-    planes[1] = a.xthi + pbase;
-    rows[0] = ti * TILE;
-    rows[1] = tj * TILE;
-  } else {
-    planes[0] = a.xhi + pbase;
-    planes[1] = a.xlo + pbase;
-    planes[2] = a.xthi + pbase;
-    planes[3] = a.xtlo + pbase;
-    rows[0] = rows[1] = ti * TILE;
-    rows[2] = rows[3] = tj * TILE;
+  const uint16_t* pa[NH];
+  const uint16_t* pb[NH];
+  pa[0] = a.xhi + pbase;
+  pb[0] = a.xthi + pbase;
+  if constexpr (!F16) {
+    pa[NH - 1] = a.xlo + pbase;
+    pb[NH - 1] = a.xtlo + pbase;
   }
+  const int64_t ra = ti * TI, rb = tj * TJ;
   // fp16 planes: a constant A (min == max) is left unnormalised and may lie
   // outside fp16's range; its T = M c^2 is formed directly in the epilogue.
   bool constant = false;
@@ -491,6 +488,8 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
   const int nk = static_cast<int>(a.Mp / KD);
   auto compute = [&](auto st_tag) {
     constexpr int st = decltype(st_tag)::value;
+    const u32x4* la = lds + st * STAGE;
+    const u32x4* lb = la + NH * SA;
 #pragma unroll
     for (int kk = 0; kk < KD / 16; ++kk) {
       const int lsw = lane ^ (4 * (2 * kk + (lane >> 5)));
@@ -498,11 +497,10 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
         f16x8 b8[YS];
 #pragma unroll
         for (int y = 0; y < YS; ++y)
-          b8[y] = __builtin_bit_cast(f16x8, lds[st][1][(kk * (TILE / 32) + YS * wj + y) * 64 + lsw]);
+          b8[y] = __builtin_bit_cast(f16x8, lb[(kk * (TJ / 32) + YS * wj + y) * 64 + lsw]);
 #pragma unroll
         for (int x = 0; x < XS; ++x) {
-          const f16x8 a8 =
-              __builtin_bit_cast(f16x8, lds[st][0][(kk * (TILE / 32) + XS * wi + x) * 64 + lsw]);
+          const f16x8 a8 = __builtin_bit_cast(f16x8, la[(kk * (TI / 32) + XS * wi + x) * 64 + lsw]);
 #pragma unroll
           for (int y = 0; y < YS; ++y)
             acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a8, b8[y], acc[x][y], 0, 0, 0);
@@ -511,16 +509,16 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
         bf16x8 bh8[YS], bl[YS];
 #pragma unroll
         for (int y = 0; y < YS; ++y) {
-          const int sb = (kk * (TILE / 32) + YS * wj + y) * 64 + lsw;
-          bh8[y] = __builtin_bit_cast(bf16x8, lds[st][2][sb]);
-          bl[y] = __builtin_bit_cast(bf16x8, lds[st][3][sb]);
+          const int sb = (kk * (TJ / 32) + YS * wj + y) * 64 + lsw;
+          bh8[y] = __builtin_bit_cast(bf16x8, lb[sb]);
+          bl[y] = __builtin_bit_cast(bf16x8, lb[SB + sb]);
         }
         // A operands one 32-row strip at a time (fewer live registers).
 #pragma unroll
         for (int x = 0; x < XS; ++x) {
-          const int sa = (kk * (TILE / 32) + XS * wi + x) * 64 + lsw;
-          const bf16x8 ah = __builtin_bit_cast(bf16x8, lds[st][0][sa]);
-          const bf16x8 al = __builtin_bit_cast(bf16x8, lds[st][1][sa]);
+          const int sa = (kk * (TI / 32) + XS * wi + x) * 64 + lsw;
+          const bf16x8 ah = __builtin_bit_cast(bf16x8, la[sa]);
+          const bf16x8 al = __builtin_bit_cast(bf16x8, la[SA + sa]);
 #pragma unroll
           for (int y = 0; y < YS; ++y) {
             acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh8[y], acc[x][y], 0, 0, 0);
@@ -531,29 +529,33 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
       }
     }
   };
+  u32x4 rga[NBUF][NH][CA], rgb[NBUF][NH][CB];
+  auto load = [&](int buf, int kt) {
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      tri_load<TI, THREADS, KD>(pa[h], ra, static_cast<int64_t>(kt) * KD, a.Mp, rga[buf][h]);
+      tri_load<TJ, THREADS, KD>(pb[h], rb, static_cast<int64_t>(kt) * KD, a.Mp, rgb[buf][h]);
+    }
+  };
+  auto store = [&](int buf, int st) {
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      tri_store<TI, THREADS, KD>(lds + st * STAGE + h * SA, rga[buf][h]);
+      tri_store<TJ, THREADS, KD>(lds + st * STAGE + NH * SA + h * SB, rgb[buf][h]);
+    }
+  };
 
   // The loop's barriers are uniform: `constant` depends on bh alone.
   if (!constant) {
     if constexpr (NBUF == 2) {
       // The registers of slice kt + 2 are loaded while slice kt is multiplied.
-      u32x4 reg[2][NP][CH];
-#pragma unroll
-      for (int p = 0; p < NP; ++p) tri_load<TILE, THREADS, KD>(planes[p], rows[p], 0, a.Mp, reg[0][p]);
-      if (nk > 1) {
-#pragma unroll
-        for (int p = 0; p < NP; ++p) tri_load<TILE, THREADS, KD>(planes[p], rows[p], KD, a.Mp, reg[1][p]);
-      }
+      load(0, 0);
+      if (nk > 1) load(1, 1);
       auto slice = [&](int kt, auto buf_tag) {
         constexpr int st = decltype(buf_tag)::value;  // register buffer and LDS stage kt % 2
-#pragma unroll
-        for (int p = 0; p < NP; ++p) tri_store<TILE, THREADS, KD>(lds[st][p], reg[st][p]);
+        store(st, st);
         lds_barrier();
-        if (kt + 2 < nk) {
-#pragma unroll
-          for (int p = 0; p < NP; ++p)
-            tri_load<TILE, THREADS, KD>(planes[p], rows[p], static_cast<int64_t>(kt + 2) * KD, a.Mp,
-                                    reg[st][p]);
-        }
+        if (kt + 2 < nk) load(st, kt + 2);
         compute(buf_tag);
       };
       for (int kt = 0; kt < nk; kt += 2) {
@@ -563,28 +565,15 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
     } else {
       // One register buffer: slice kt + 1 is stored to the other LDS stage
       // after slice kt is multiplied, then slice kt + 2 is loaded.
-      u32x4 reg[NP][CH];
-#pragma unroll
-      for (int p = 0; p < NP; ++p) tri_load<TILE, THREADS, KD>(planes[p], rows[p], 0, a.Mp, reg[p]);
-#pragma unroll
-      for (int p = 0; p < NP; ++p) tri_store<TILE, THREADS, KD>(lds[0][p], reg[p]);
-      if (nk > 1) {
-#pragma unroll
-        for (int p = 0; p < NP; ++p) tri_load<TILE, THREADS, KD>(planes[p], rows[p], KD, a.Mp, reg[p]);
-      }
+      load(0, 0);
+      store(0, 0);
+      if (nk > 1) load(0, 1);
       lds_barrier();
       auto slice = [&](int kt, auto st_tag) {
         constexpr int st = decltype(st_tag)::value;  // LDS stage of slice kt
         compute(st_tag);
-        if (kt + 1 < nk) {
-#pragma unroll
-          for (int p = 0; p < NP; ++p) tri_store<TILE, THREADS, KD>(lds[st ^ 1][p], reg[p]);
-        }
-        if (kt + 2 < nk) {
-#pragma unroll
-          for (int p = 0; p < NP; ++p)
-            tri_load<TILE, THREADS, KD>(planes[p], rows[p], static_cast<int64_t>(kt + 2) * KD, a.Mp, reg[p]);
-        }
+        if (kt + 1 < nk) store(0, st ^ 1);
+        if (kt + 2 < nk) load(0, kt + 2);
         lds_barrier();
       };
       for (int kt = 0; kt < nk; kt += 2) {
@@ -601,8 +590,8 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
   // With fp16 planes the additive formula reads X alone: F = Ahat - lambda T
   // then errs by at most 2^-12 |Ahat|, far inside the bound on F.
   const int half = lane >> 5;
-  const int64_t ib = ti * TILE + wi * (TILE / WI) + 4 * half;
-  const int64_t jb = tj * TILE + wj * (TILE / WJ) + (lane & 31);
+  const int64_t ib = ti * TI + wi * (TI / WI) + 4 * half;
+  const int64_t jb = tj * TJ + wj * (TJ / WJ) + (lane & 31);
   const size_t obase = static_cast<size_t>(bh) * a.M * a.M;
   auto epilogue = [&](auto form_tag) {
     constexpr int FORM = decltype(form_tag)::value;
@@ -796,20 +785,21 @@ extern "C" cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_
   t.lambda = lambda_redundancy;
   t.formula = formula;
   t.fused = fused ? 1 : 0;
-  // The 256-wide tile stages half the bytes per flop; it is used when Mp
-  // allows it and its tiles still give every CU work.
+  // The 256-wide tile (8 waves) stages half the bytes per flop of the
+  // 128-wide one (4 waves); it is used when Mp allows it and its tiles still
+  // give every CU work.
   const bool wide = L.Mp % TT_WIDE == 0 && BH * (L.Mp / TT_WIDE) * (L.Mp / TT_WIDE) >= 256;
-  t.nt = L.Mp / (wide ? TT_WIDE : TT);
-  const int64_t blocks = BH * t.nt * t.nt;
+  t.nti = t.ntj = L.Mp / (wide ? TT_WIDE : TT);
+  const int64_t blocks = BH * t.nti * t.ntj;
   CAB_REQUIRE(blocks <= INT32_MAX, CAB_ESHAPE, "cab_block_frc: problem too large");
   const unsigned nb = static_cast<unsigned>(blocks);
   if (wide && f16)
-    triangle_kernel<TT_WIDE, 2, 4, 2, true, TK><<<nb, 512, 0, s>>>(t);
+    triangle_kernel<TT_WIDE, TT_WIDE, 2, 4, 2, true, TK><<<nb, 512, 0, s>>>(t);
   else if (wide)
-    triangle_kernel<TT_WIDE, 2, 4, 1, false, TK><<<nb, 512, 0, s>>>(t);
+    triangle_kernel<TT_WIDE, TT_WIDE, 2, 4, 1, false, TK><<<nb, 512, 0, s>>>(t);
   else if (f16)
-    triangle_kernel<TT, 2, 2, 2, true, TK><<<nb, 256, 0, s>>>(t);
+    triangle_kernel<TT, TT, 2, 2, 2, true, TK><<<nb, 256, 0, s>>>(t);
   else
-    triangle_kernel<TT, 2, 2, 2, false, TK><<<nb, 256, 0, s>>>(t);
+    triangle_kernel<TT, TT, 2, 2, 2, false, TK><<<nb, 256, 0, s>>>(t);
   return launch_status("cab_block_frc/triangles");
 }
