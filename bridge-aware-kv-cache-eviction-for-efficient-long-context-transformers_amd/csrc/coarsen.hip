@@ -112,7 +112,7 @@ template <typename T, int L>
 __global__ __launch_bounds__(256) void coarsen_kernel(CoarsenArgs a) {
   using elem = typename Chunk<T>::elem;
   constexpr int R = 64 / L;  // rows per step
-  constexpr int U = 8;       // steps loaded before reduction
+  constexpr int U = 4;       // steps loaded before reduction (more waves beat deeper batches)
   const int lane = lane_id();
   const int64_t units = a.B * a.H * a.M;
   const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
