@@ -2,8 +2,9 @@
 //
 // One wave64 per FRC row. The row's M scores are read once (coalesced, lane l
 // holds columns j = 64 c + l) and mapped to order-preserving uint32 keys in
-// registers. The k-th smallest key is found by a 4-pass radix select (8 bits
-// per pass, a 256-bin LDS histogram per wave, a wave-wide prefix scan).
+// registers. The k-th smallest key is found by a radix select (one pass per
+// key byte that the candidates do not all share, a 256-bin LDS histogram per
+// wave, a wave-wide prefix scan, ending early at a bin of one key).
 // A last pass in ascending j keeps every key below the threshold and the
 // first (in j) keys equal to it, assigns output slots with a prefix
 // popcount, and writes the compact ascending index list and, optionally, the
@@ -43,14 +44,15 @@ __device__ __forceinline__ uint32_t order_key(float f, bool high) {
 }
 
 // theta = the need-th smallest key among the candidates (the largest theta
-// with count(key < theta) < need), by a radix select over the key's four
-// bytes, most significant first: each pass histograms the next byte of the
-// candidates that still match the chosen prefix in the wave's LDS histogram,
-// and a wave-wide scan picks the bin where the running count reaches need.
-// The histogram keeps HSUB interleaved copies of every bin (lane % HSUB
-// picks one), so that the many keys of a row that share a byte do not all
-// update one LDS word. Returns in need_eq how many keys equal to theta (the
-// first ones in j order) complete the selection.
+// with count(key < theta) < need), by a radix select over the key bits, most
+// significant byte first. A byte every candidate shares (a wave-wide AND /
+// OR) needs no pass; otherwise a pass histograms that byte of the candidates
+// that match the prefix chosen so far in the wave's LDS histogram, and a
+// wave-wide scan picks the bin where the running count reaches need. A bin
+// holding a single key ends the search: that key is theta. The histogram keeps HSUB interleaved copies of every bin
+// (lane % HSUB picks one), so that keys of a row that share the digit do not
+// all update one LDS word. Returns in need_eq how many keys equal to theta
+// (the first ones in j order) complete the selection.
 constexpr int HSUB = 8;
 // Orders one wave's LDS accesses across its lanes (the histogram is shared
 // by the lanes of a wave; other waves of the workgroup may have exited).
@@ -63,13 +65,37 @@ template <int NCH, typename Cand>
 __device__ __forceinline__ uint32_t kth_key(const uint32_t (&key)[NCH], Cand is_cand, int64_t need,
                                             int64_t& need_eq, uint32_t* hist) {
   const int lane = lane_id();
-  uint32_t prefix = 0u, pmask = 0u;
-  int64_t rem = need;  // rank still to find among the keys matching the prefix
   need_eq = 0;
   if (need <= 0) return 0u;
+  uint32_t kand = 0xffffffffu, kor = 0u;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+    if (is_cand(c)) {
+      kand &= key[c];
+      kor |= key[c];
+    }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    kand &= static_cast<uint32_t>(__shfl_xor(static_cast<int>(kand), off, 64));
+    kor |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(kor), off, 64));
+  }
+  const uint32_t diff = kand ^ kor;
+  if (diff == 0u) {  // every candidate holds the same key
+    need_eq = need;
+    return kand;
+  }
+  uint32_t prefix = 0u, pmask = 0u;
+  int64_t rem = need;  // rank still to find among the keys matching the prefix
+  bool done = false;
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
+    if (done) break;
+    if (((diff >> shift) & 255u) == 0u) {  // every candidate shares this byte
+      prefix |= kand & (255u << shift);
+      pmask |= 255u << shift;
+      continue;
+    }
     wave_sync();  // the previous pass's reads are done
     // Layout: 16-byte slot (q, l) at index 64 q + l holds copies 4 (q % 2) .. +3
     // of bin 4 l + q / 2, so lane l clears and sums its own four bins with
@@ -105,22 +131,36 @@ __device__ __forceinline__ uint32_t kth_key(const uint32_t (&key)[NCH], Cand is_
     // First lane whose bins reach rank rem; inside it, the first such bin.
     const uint64_t reach = ballot64(static_cast<int64_t>(incl) >= rem);
     const int src = __builtin_ctzll(reach);
-    uint32_t run = excl, bin = 0u;
+    uint32_t run = excl, bin = 0u, bcnt = 0u;
     bool found = false;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       if (!found && static_cast<int64_t>(run + hv[q]) >= rem) {
         found = true;
         bin = 4u * lane + q;
+        bcnt = hv[q];
       } else if (!found) {
         run += hv[q];
       }
     }
     const uint32_t sel_bin = __shfl(bin, src, 64);
     const uint32_t below = __shfl(run, src, 64);
+    const uint32_t sel_cnt = __shfl(bcnt, src, 64);
     rem -= below;
     prefix |= sel_bin << shift;
     pmask |= 255u << shift;
+    if (sel_cnt == 1u && shift > 0) {
+      // One candidate left (rem == 1): theta is its key.
+      uint32_t kv = 0u;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+        if (is_cand(c) && (key[c] & pmask) == prefix) kv = key[c];
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1)
+        kv |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(kv), off, 64));
+      prefix = kv;
+      done = true;
+    }
   }
   need_eq = rem;  // keys below theta: need - rem; the rest are ties at theta
   return prefix;

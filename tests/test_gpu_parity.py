@@ -287,6 +287,30 @@ def test_topk_bit_exact(cuda, M, flags):
         np.testing.assert_array_equal(mask.cpu().numpy(), omask)
 
 
+@pytest.mark.parametrize("M", [5, 100, 2000])
+@pytest.mark.parametrize("flags", [(False, True, False), (True, False, True)])
+def test_topk_shared_key_bytes(cuda, M, flags):
+    """Rows whose candidate keys share leading bytes (the search skips those
+    bytes), share every byte (all ties), differ in the last byte only, or
+    leave a single key in a bin early (the search stops there)."""
+    from cab_attention.kernels import generate_block_index
+    select_high, keep_diag, causal = flags
+    g = torch.Generator().manual_seed(100 + M)
+    f = torch.empty(1, 5, M, M)
+    f[0, 0] = 3.5                                                       # one key everywhere
+    f[0, 1] = 1.0 + torch.randint(0, 200, (M, M), generator=g).float() * 2.0 ** -23  # last bits only
+    f[0, 2] = -250.0 + 3.0 * torch.randn(M, M, generator=g)             # one or two binades
+    f[0, 3] = torch.randn(M, M, generator=g) * 1e-30                    # tiny, both signs
+    f[0, 4] = torch.randint(0, 3, (M, M), generator=g).float() * 2.0 ** 20 + 7.0
+    for sp in (0.95, 0.5):
+        idx, cnt, mask = generate_block_index(f.to(cuda), sp, select_high=select_high,
+                                              keep_diagonal=keep_diag, causal=causal, dense=True)
+        omask, oidx, ocnt = O.generate_block_mask(f.numpy(), sp, select_high, keep_diag, causal)
+        np.testing.assert_array_equal(cnt.cpu().numpy(), ocnt)
+        np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
+        np.testing.assert_array_equal(mask.cpu().numpy(), omask)
+
+
 @pytest.mark.parametrize("M", [7, 100, 513, 2000])
 @pytest.mark.parametrize("ratio", [0.0, 0.3, 0.5, 1.0])
 @pytest.mark.parametrize("flags", [(True, True, False), (False, True, True), (True, False, True)])
