@@ -287,8 +287,9 @@ def token_frc_section(args, dev):
     """Token-level FRC: compute_frc on a [16384, 16384] fp32 attention graph
     (two HBM passes, priced as 2 * 4 N^2 bytes) and
     FRCTracker.compute_from_keys on keys [1, 8, 16384, 128] bf16 (two MFMA
-    Gram passes, priced as 2 * 2 N^2 D useful flops; the hi/lo split's
-    extra products are not counted)."""
+    Gram passes over the symmetric kn kn^T, priced as 2 * N^2 D useful flops,
+    its upper triangle; the hi/lo split's extra products and the diagonal
+    blocks' lower halves are not counted)."""
     import torch
     from cab_attention.kernels import frc_from_keys, token_frc
     iters = max(3, args.steps // 2)
@@ -303,7 +304,7 @@ def token_frc_section(args, dev):
     keys = seeded_gpu((1, 8, n, 128), 32, torch.bfloat16, dev)
     frc_from_keys(keys)
     k_ms = time_events(lambda: frc_from_keys(keys), iters)
-    k_flops = 2 * 2 * n * n * 128
+    k_flops = 2 * n * n * 128
     del keys
     torch.cuda.empty_cache()
     log(f"token FRC: matrix {m_ms:.3f} ms ({m_bytes / (m_ms * 1e-3) / 1e9:.0f} GB/s), "

@@ -16,9 +16,14 @@
 // writes kn as bf16 hi/lo planes in MFMA operand order; gram_kernel<PASS>
 // computes 32x32 tiles of kn kn^T on MFMA (hi*hi + hi*lo + lo*hi, fp32
 // accumulate; column operands staged once per workgroup through LDS) and
-// folds each tile into per-row sums of relu(g) * w_j
-// (w = 1, then w = S); gram_finalize_kernel adds the column-split partials
-// in a fixed order. Algorithmic work: 2 N^2 D flops per Gram pass.
+// folds each tile into per-row sums of relu(g) * w_j (w = 1, then w = S).
+// The Gram matrix is symmetric, so only the tiles at or right of each
+// 256-row block's diagonal block are formed: those right of it also fold
+// their columns, relu(g) * w_i summed over the block's rows, into the sums of
+// the rows j they stand for. gram_finalize_kernel adds the row partials of
+// the column splits and the column partials of the earlier row blocks, in a
+// fixed order. Algorithmic work: N^2 D flops per Gram pass (the upper
+// triangle), plus the 256 x 256 diagonal blocks in full.
 #include "cab_internal.h"
 
 namespace cab {
@@ -181,19 +186,37 @@ constexpr int GRAM_ROWS = 32 * GRAM_WAVES;   // rows per workgroup
 // at index (t * dk + s) * 64 + L. This is the operand order of
 // mfma_f32_32x32x16_bf16 for A (rows) and B (columns) alike.
 struct KeyLayout {
-  int64_t Np, dk, cs, col_tiles;  // padded rows, k-steps, column splits, col tiles per split
-  size_t off_hi, off_lo, off_r, off_s, off_part, total;
+  int64_t Np, dk, rb, tiles;  // padded rows, k-steps, 256-row blocks, 32-column tiles
+  int64_t col_tiles, cs, wgs;  // tiles per workgroup, most splits of a row block, workgroups
+  size_t off_hi, off_lo, off_r, off_s, off_part, off_cpart, total;
 };
+
+// Column splits of row block x: its tiles run from 8 x (the diagonal block)
+// to the last one.
+__host__ __device__ __forceinline__ int64_t gram_splits(int64_t x, int64_t tiles, int64_t col_tiles) {
+  return (tiles - 8 * x + col_tiles - 1) / col_tiles;
+}
 
 KeyLayout key_layout(int64_t N, int64_t D) {
   KeyLayout L;
   L.Np = round_up(N > 0 ? N : 1, GRAM_ROWS);
   L.dk = D <= 64 ? 4 : D <= 128 ? 8 : 16;
-  const int64_t row_blocks = L.Np / GRAM_ROWS, tiles = L.Np / 32;
-  L.cs = ceil_div(512, row_blocks);
-  if (L.cs > tiles) L.cs = tiles;
-  L.col_tiles = ceil_div(tiles, L.cs);
-  L.cs = ceil_div(tiles, L.col_tiles);
+  L.rb = L.Np / GRAM_ROWS;
+  L.tiles = L.Np / 32;
+  // About 512 workgroups (two rounds over the CUs) over the upper-triangle
+  // tiles, at least 8 tiles each; splits up to 10 % longer are taken when
+  // they keep the count at 512 (each row block's last split is shorter).
+  const int64_t work = L.rb * L.tiles - 4 * L.rb * (L.rb - 1);
+  L.col_tiles = ceil_div(work, 512);
+  if (L.col_tiles < 8) L.col_tiles = 8;
+  const int64_t longest = L.col_tiles + L.col_tiles / 10;
+  for (;;) {
+    L.wgs = 0;
+    for (int64_t x = 0; x < L.rb; ++x) L.wgs += gram_splits(x, L.tiles, L.col_tiles);
+    if (L.wgs <= 512 || L.col_tiles >= longest || L.col_tiles >= L.tiles) break;
+    ++L.col_tiles;
+  }
+  L.cs = gram_splits(0, L.tiles, L.col_tiles);
   const size_t plane = static_cast<size_t>(L.Np) * L.dk * 16 * 2;
   size_t o = 0;
   auto take = [&](size_t bytes) {
@@ -206,6 +229,7 @@ KeyLayout key_layout(int64_t N, int64_t D) {
   L.off_r = take(static_cast<size_t>(L.Np) * 4);
   L.off_s = take(static_cast<size_t>(L.Np) * 4);
   L.off_part = take(static_cast<size_t>(L.cs) * L.Np * 4);
+  L.off_cpart = take(static_cast<size_t>(L.rb) * L.Np * 4);
   L.total = o;
   return L;
 }
@@ -270,23 +294,27 @@ struct GramArgs {
   const u32x4* hi;
   const u32x4* lo;
   const float* w;  // pass 1: S (zero past N)
-  float* part;     // [cs][Np]
-  int64_t Np, tiles, col_tiles;
+  float* part;     // [cs][Np] row partials per column split
+  float* cpart;    // [Np][rb] column partials per row block (columns right of its diagonal block)
+  int64_t Np, tiles, col_tiles, rb;
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int GRAM_STAGES = 3;
 
-// Wave w of workgroup (x, y) owns row tile GRAM_WAVES x + w (its A operands
-// in registers) and the waves walk the same column tiles
-// [y col_tiles, (y + 1) col_tiles). Each column tile's B operands (hi and
-// lo, 1 KB per k-step and plane) and, in pass 1, its 32 weights are staged
-// once per workgroup into a ring of three LDS stages by global_load_lds, two
-// tiles ahead (the waves split the 2 DK 1 KB loads evenly). Each 32x32
-// tile of kn kn^T is folded into 16 per-lane row partials (lane l: column
-// l % 32, rows 8 (e / 4) + 4 (l / 32) + e % 4), added over the lanes at the
-// end.
+// Workgroup b stands for split y of row block x (the splits of the blocks in
+// order). Wave w owns row tile GRAM_WAVES x + w (its A operands in
+// registers) and the waves walk the same column tiles 8 x + [y col_tiles,
+// (y + 1) col_tiles). Each column tile's B operands (hi and lo, 1 KB per
+// k-step and plane) and, in pass 1, its 32 weights are staged once per
+// workgroup into a ring of three LDS stages by global_load_lds, two tiles
+// ahead (the waves split the 2 DK 1 KB loads evenly). Each 32x32 tile of
+// kn kn^T is folded into 16 per-lane row partials (lane l: column l % 32, rows
+// 8 (e / 4) + 4 (l / 32) + e % 4), added over the lanes at the end. A tile
+// right of the diagonal block also yields its 32 column sums over the wave's
+// rows; the waves' sums meet in LDS and wave 0 adds them in order after the
+// next barrier.
 template <int DK, int PASS>
 __global__ __launch_bounds__(64 * GRAM_WAVES) void gram_kernel(GramArgs a) {
   constexpr int PLANE_BYTES = DK * 1024;           // one plane's k-steps of a column tile
@@ -296,19 +324,34 @@ __global__ __launch_bounds__(64 * GRAM_WAVES) void gram_kernel(GramArgs a) {
   constexpr int NDMA = PER_WAVE + (PASS == 1 ? 1 : 0);
   static_assert(NDMA < 16, "vmcnt immediate");
   __shared__ __attribute__((aligned(16))) char ring[GRAM_STAGES * STAGE_BYTES];
+  __shared__ float cbuf[GRAM_STAGES][GRAM_WAVES][32];
   const int lane = lane_id();
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-  const int64_t rt = static_cast<int64_t>(blockIdx.x) * GRAM_WAVES + w;
+  int64_t x = 0, y = blockIdx.x;
+  for (;;) {
+    const int64_t n = gram_splits(x, a.tiles, a.col_tiles);
+    if (y < n) break;
+    y -= n;
+    ++x;
+  }
+  const int64_t rt = x * GRAM_WAVES + w;
+  const int64_t diag_end = (x + 1) * GRAM_WAVES;  // first column tile right of the diagonal block
   u32x4 ah[DK], al[DK];
 #pragma unroll
   for (int s = 0; s < DK; ++s) {
     ah[s] = a.hi[(rt * DK + s) * 64 + lane];
     al[s] = a.lo[(rt * DK + s) * 64 + lane];
   }
+  const int half = lane >> 5;
+  // Row weights of this lane's 16 rows (for the column sums).
+  float wr[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e)
+    wr[e] = PASS == 0 ? 1.f : a.w[rt * 32 + 8 * (e >> 2) + 4 * half + (e & 3)];
   float p[16];
 #pragma unroll
   for (int e = 0; e < 16; ++e) p[e] = 0.f;
-  const int64_t c0 = static_cast<int64_t>(blockIdx.y) * a.col_tiles;
+  const int64_t c0 = x * GRAM_WAVES + y * a.col_tiles;
   const int64_t c1 = c0 + a.col_tiles < a.tiles ? c0 + a.col_tiles : a.tiles;
   const int nt = static_cast<int>(c1 - c0);
 
@@ -326,17 +369,30 @@ __global__ __launch_bounds__(64 * GRAM_WAVES) void gram_kernel(GramArgs a) {
       __builtin_amdgcn_global_load_lds(a.w + ct * 32 + (lane & 31),
                                        (lds_void*)(st + 2 * PLANE_BYTES + 256 * w), 4, 0, 0);
   };
+  // Wave 0 adds the waves' column sums of tile it (staged in cbuf[S]).
+  auto flush_cols = [&](int it, int S) {
+    const int64_t ct = c0 + it;
+    if (w == 0 && ct >= diag_end && lane < 32) {
+      float v = 0.f;
+#pragma unroll
+      for (int q = 0; q < GRAM_WAVES; ++q) v += cbuf[S][q][lane];
+      a.cpart[(ct * 32 + lane) * a.rb + x] = v;
+    }
+  };
   for (int it = 0; it < GRAM_STAGES - 1 && it < nt; ++it) issue(it);
   // Tile it lives in stage it % 3, a compile-time constant below, so the
   // compiler sees the staging of tile it + 2 cannot alias this tile's reads.
   auto step = [&](int it, auto stage_tag) {
     constexpr int S = decltype(stage_tag)::value;
+    // vmcnt(NDMA) (tile it + 1 may be in flight) or vmcnt(0), and lgkmcnt(0):
+    // the column sums this wave wrote to cbuf are in LDS before the barrier.
     if (it + 1 < nt)
-      __builtin_amdgcn_s_waitcnt(0x0f70 | NDMA);  // vmcnt(NDMA): tile it + 1 may be in flight
+      __builtin_amdgcn_s_waitcnt(0x0070 | NDMA);
     else
-      __builtin_amdgcn_s_waitcnt(0x0f70);         // vmcnt(0)
+      __builtin_amdgcn_s_waitcnt(0x0070);
     __builtin_amdgcn_s_barrier();  // every wave's part of tile it landed; stage (S + 2) % 3 is free
     if (it + GRAM_STAGES - 1 < nt) issue(it + GRAM_STAGES - 1);
+    if (it > 0) flush_cols(it - 1, (S + GRAM_STAGES - 1) % GRAM_STAGES);
     const char* st = ring + S * STAGE_BYTES;
     const float wc = PASS == 0 ? 1.f : reinterpret_cast<const float*>(st + 2 * PLANE_BYTES + 256 * w)[lane & 31];
     f32x16 acc = {};
@@ -353,28 +409,37 @@ __global__ __launch_bounds__(64 * GRAM_WAVES) void gram_kernel(GramArgs a) {
     }
 #pragma unroll
     for (int e = 0; e < 16; ++e) p[e] = fmaf(fmaxf(acc[e], 0.f), wc, p[e]);
+    if (c0 + it >= diag_end) {
+      float cs = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) cs = fmaf(fmaxf(acc[e], 0.f), wr[e], cs);
+      cs += shfl_xor_f32(cs, 32);
+      if (lane < 32) cbuf[S][w][lane] = cs;
+    }
   };
   for (int it = 0; it < nt; it += GRAM_STAGES) {
     step(it, std::integral_constant<int, 0>{});
     if (it + 1 < nt) step(it + 1, std::integral_constant<int, 1>{});
     if (it + 2 < nt) step(it + 2, std::integral_constant<int, 2>{});
   }
+  __syncthreads();
+  flush_cols(nt - 1, (nt - 1) % GRAM_STAGES);
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
 #pragma unroll
     for (int off = 1; off < 32; off <<= 1) p[e] += shfl_xor_f32(p[e], off);
   }
   if ((lane & 31) == 0) {
-    const int half = lane >> 5;
-    float* out = a.part + static_cast<int64_t>(blockIdx.y) * a.Np + rt * 32;
+    float* out = a.part + y * a.Np + rt * 32;
 #pragma unroll
     for (int e = 0; e < 16; ++e) out[8 * (e >> 2) + 4 * half + (e & 3)] = p[e];
   }
 }
 
 struct FinArgs {
-  const float* part;  // [cs][Np]
-  int64_t cs, Np, N;
+  const float* part;   // [cs][Np] row partials per column split
+  const float* cpart;  // [Np][rb] column partials per row block
+  int64_t tiles, col_tiles, rb, Np, N;
   float* r;           // workspace row sums
   float* s;           // workspace strengths (zero past N)
   float* out_s;       // optional outputs
@@ -387,8 +452,14 @@ template <int PASS>
 __global__ __launch_bounds__(256) void gram_finalize_kernel(FinArgs a) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= a.Np) return;
+  // Row i of block xi: its splits' row partials, then the column partials
+  // of the blocks above it, in order.
+  const int64_t xi = i / GRAM_ROWS;
+  const int64_t ns = gram_splits(xi, a.tiles, a.col_tiles);
   float sum = 0.f;
-  for (int64_t c = 0; c < a.cs; ++c) sum += a.part[c * a.Np + i];
+  for (int64_t c = 0; c < ns; ++c) sum += a.part[c * a.Np + i];
+  const float* cp = a.cpart + i * a.rb;
+  for (int64_t xb = 0; xb < xi; ++xb) sum += cp[xb];
   if constexpr (PASS == 0) {
     const float s = i < a.N ? sum / (sum + 1e-8f) : 0.f;
     a.r[i] = sum;
@@ -431,8 +502,7 @@ cab_status_t launch_rows(const void* A, int64_t n, int64_t lda, float* s, float*
 
 template <int DK, int PASS>
 void launch_gram(const GramArgs& g, const KeyLayout& L, hipStream_t st) {
-  gram_kernel<DK, PASS><<<dim3(static_cast<unsigned>(L.Np / GRAM_ROWS), static_cast<unsigned>(L.cs)),
-                          64 * GRAM_WAVES, 0, st>>>(g);
+  gram_kernel<DK, PASS><<<static_cast<unsigned>(L.wgs), 64 * GRAM_WAVES, 0, st>>>(g);
 }
 
 }  // namespace
@@ -513,14 +583,14 @@ extern "C" cab_status_t cab_token_frc_from_keys(const void* keys, cab_dtype_t dt
               workspace_bytes, L.total);
   CAB_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, CAB_EWORKSPACE,
               "%s: workspace not 256-byte aligned", fn);
-  CAB_REQUIRE(L.Np / 4 <= INT32_MAX && L.Np / GRAM_ROWS <= INT32_MAX, CAB_ESHAPE, "%s: N too large",
-              fn);
+  CAB_REQUIRE(L.Np / 4 <= INT32_MAX && L.wgs <= INT32_MAX, CAB_ESHAPE, "%s: N too large", fn);
   char* ws = static_cast<char*>(workspace);
   u32x4* hi = reinterpret_cast<u32x4*>(ws + L.off_hi);
   u32x4* lo = reinterpret_cast<u32x4*>(ws + L.off_lo);
   float* r = reinterpret_cast<float*>(ws + L.off_r);
   float* s = reinterpret_cast<float*>(ws + L.off_s);
   float* part = reinterpret_cast<float*>(ws + L.off_part);
+  float* cpart = reinterpret_cast<float*>(ws + L.off_cpart);
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   PrepArgs pa{keys, H, B * H, N, D, L.Np, L.dk, {strides[0], strides[1], strides[2], strides[3]},
@@ -534,8 +604,8 @@ extern "C" cab_status_t cab_token_frc_from_keys(const void* keys, cab_dtype_t dt
   cab_status_t rc = launch_status(fn);
   if (rc != CAB_OK) return rc;
 
-  GramArgs g{hi, lo, s, part, L.Np, L.Np / 32, L.col_tiles};
-  FinArgs f{part, L.cs, L.Np, N, r, s, strengths, triangles, row_sums, frc};
+  GramArgs g{hi, lo, s, part, cpart, L.Np, L.tiles, L.col_tiles, L.rb};
+  FinArgs f{part, cpart, L.tiles, L.col_tiles, L.rb, L.Np, N, r, s, strengths, triangles, row_sums, frc};
   const unsigned fgrid = static_cast<unsigned>(ceil_div(L.Np, 256));
   for (int pass = 0; pass < 2; ++pass) {
     if (L.dk == 4) {
