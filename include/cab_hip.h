@@ -92,7 +92,11 @@ size_t cab_block_frc_workspace_bytes(int64_t B, int64_t H, int64_t M, int64_t D,
  *
  * A = qc kc^T * scale / temperature (fp32 accumulate on MFMA);
  * Ahat = minmax(A) per (b,h) ((A-min)/(max-min+1e-8), A unchanged if max==min)
- * or A; T = Ahat @ Ahat (MFMA, bf16 hi/lo split, fp32 accumulate);
+ * or A; T = Ahat @ Ahat on MFMA with fp32 accumulate: under minmax with the
+ * additive or multiplicative formula, one fp16 product per site (Ahat in
+ * [0, 1]; |dT| <= 1e-3 (|Ahat| @ |Ahat|)), otherwise bf16 hi/lo operands
+ * (three products, about 2^-16 relative). Additive without `triangles`: F is
+ * accumulated directly as Ahat (I - lambda Ahat) (|lambda| <= 1024).
  * additive: F = Ahat - lambda T; multiplicative: F = Ahat / (1 + lambda T /
  * (Ahat + 1e-8)); non-finite F -> 0; augmented: 4 Ahat - S_i - S_j + 3 T on
  * entries with Ahat > 0 and 1000 elsewhere (S = row sums of Ahat).
