@@ -329,6 +329,7 @@ __global__ __launch_bounds__(64 * GRAM_WAVES) void gram_kernel(GramArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   int64_t x = 0, y = blockIdx.x;
   for (;;) {
+    if (x >= a.rb) return;  // past the last split (uniform per workgroup)
     const int64_t n = gram_splits(x, a.tiles, a.col_tiles);
     if (y < n) break;
     y -= n;
