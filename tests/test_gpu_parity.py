@@ -400,6 +400,37 @@ def test_predictor_end_to_end(cuda, cfg):
     assert_masks_agree(mask, diag["frc_scores"], of, omask, O.keep_count(M, 0.95), True, causal)
 
 
+@pytest.mark.parametrize("cfg", [
+    (1, 8, 4096, 128, "fp32", False),
+    (1, 4, 8192, 128, "bf16", True),
+    (2, 2, 6000, 128, "fp16", False),
+])
+def test_predictor_without_diagnostics(cuda, cfg):
+    """The call CABAttention and the benchmark make (no diagnostics), where the
+    additive FRC is accumulated as Ahat (I - lambda Ahat) in one GEMM: its mask
+    is the top-k of those scores, the scores are within the FRC bound, and the
+    mask agrees with the oracle's away from the row thresholds."""
+    from cab_attention import CoarseCurvaturePredictor
+    from cab_attention.kernels import coarsen_qk_max_l2, compute_block_frc, generate_block_mask
+    B, H, N, D, dt, causal = cfg
+    q = seeded((B, H, N, D), 1, DTYPES[dt]).to(cuda)
+    k = seeded((B, H, N, D), 2, DTYPES[dt]).to(cuda)
+    pred = CoarseCurvaturePredictor(block_size=64, sparsity=0.95, lambda_redundancy=0.5,
+                                    causal=causal)
+    mask = pred(q, k)
+    qc, kc = coarsen_qk_max_l2(q, k, 64)[:2]
+    f, a, t = compute_block_frc(qc, kc, lambda_redundancy=0.5, diagnostics=False)
+    assert a is None and t is None
+    assert torch.equal(mask, generate_block_mask(f, 0.95, causal=causal))
+    oqc, _ = O.coarsen_max_l2(np32(q.cpu()), 64)
+    okc, _ = O.coarsen_max_l2(np32(k.cpu()), 64)
+    of, oa, ot = O.compute_block_frc(oqc, okc, lambda_redundancy=0.5)
+    omask, _, _ = O.generate_block_mask(of, 0.95, causal=causal)
+    M = (N + 63) // 64
+    assert_frc_close(f, of, oa, ot, 0.5)
+    assert_masks_agree(mask, f, of, omask, O.keep_count(M, 0.95), True, causal)
+
+
 # ---------------------------------------------------------------------------
 # Block-sparse attention
 # ---------------------------------------------------------------------------
