@@ -1,11 +1,11 @@
 // Coarse Forman-Ricci curvature (cab_block_frc).
 //
 // Pipeline per (b, h), Mp = M rounded up to 128:
-//  1. affinity_kernel<STATS>: A = qc kc^T * alpha on MFMA (128x128 tile per
-//     workgroup, a 64x64 quadrant of four 32x32 tiles per wave), per-tile
-//     min/max partials.
+//  1. affinity_stats_kernel: A = qc kc^T * alpha on MFMA (256x256 tile per
+//     workgroup, 64x128 of eight 32x32 tiles per wave), per-tile min/max
+//     partials.
 //  2. minmax_finalize_kernel: per-(b,h) min/max from the partials.
-//  3. affinity_kernel<EMIT>: recomputes the A tile, normalises it, and writes
+//  3. affinity_kernel (EMIT): recomputes the A tile, normalises it, and writes
 //     Ahat in row-major X and transposed XT planes (zero outside M), the fp32
 //     Ahat diagnostic and, for the augmented formula, row-sum partials. The
 //     planes hold either
@@ -72,7 +72,7 @@ struct AffArgs {
   int32_t D;
   float alpha;
   int normalization;
-  float* mmpart;       // [BH][ntw*ntw][2]
+  float* mmpart;       // [BH][ns*ns][2], ns = ceil(Mp / 256) STATS tiles per dim
   const float* mm;     // [BH][2]
   uint16_t* xhi;       // [BH][Mp][Mp]
   uint16_t* xlo;
@@ -85,45 +85,49 @@ struct AffArgs {
   float lambda;
 };
 
-// One wave computes a 64x64 quadrant of qc kc^T (fp32 accumulate) as 2 x 2
-// MFMA tiles: acc[x][y] covers rows row0 + 32 x .., columns col0 + 32 y ..;
-// lane l owns column l % 32 and rows 8 * (e / 4) + 4 * (l / 32) + e % 4 of
-// each tile's element e.
-template <typename T>
-__device__ __forceinline__ void aff_quad(const void* qcv, const void* kcv, int64_t row0,
-                                         int64_t col0, int64_t M, int D, int lane,
-                                         f32x16 (&acc)[2][2]) {
+// One wave computes a 64 x 32 YT block of qc kc^T (fp32 accumulate) as
+// 2 x YT MFMA tiles: acc[x][y] covers rows row0 + 32 x .., columns
+// col0 + 32 y ..; lane l owns column l % 32 and rows 8 * (e / 4) +
+// 4 * (l / 32) + e % 4 of each tile's element e.
+template <typename T, int YT>
+__device__ __forceinline__ void aff_block(const void* qcv, const void* kcv, int64_t row0,
+                                          int64_t col0, int64_t M, int D, int lane,
+                                          f32x16 (&acc)[2][YT]) {
 #pragma unroll
   for (int x = 0; x < 2; ++x)
 #pragma unroll
-    for (int y = 0; y < 2; ++y) acc[x][y] = f32x16{};
+    for (int y = 0; y < YT; ++y) acc[x][y] = f32x16{};
   const int half = lane >> 5;
-  int64_t r[2], c[2];
-  bool ra[2], cb[2];
+  int64_t r[2], c[YT];
+  bool ra[2], cb[YT];
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
     r[x] = row0 + 32 * x + (lane & 31);
-    c[x] = col0 + 32 * x + (lane & 31);
     ra[x] = r[x] < M;
-    cb[x] = c[x] < M;
+  }
+#pragma unroll
+  for (int y = 0; y < YT; ++y) {
+    c[y] = col0 + 32 * y + (lane & 31);
+    cb[y] = c[y] < M;
   }
   if constexpr (sizeof(T) == 4) {
     // fp32: 32x32x2 MFMA; lane half h holds k = 8q + 4h + s in step s.
     const float* q = static_cast<const float*>(qcv);
     const float* k = static_cast<const float*>(kcv);
     for (int k0 = 0; k0 < D; k0 += 8) {
-      f32x4 av[2], bv[2];
+      f32x4 av[2], bv[YT];
 #pragma unroll
-      for (int x = 0; x < 2; ++x) {
+      for (int x = 0; x < 2; ++x)
         av[x] = ra[x] ? *reinterpret_cast<const f32x4*>(q + r[x] * D + k0 + 4 * half) : f32x4{};
-        bv[x] = cb[x] ? *reinterpret_cast<const f32x4*>(k + c[x] * D + k0 + 4 * half) : f32x4{};
-      }
+#pragma unroll
+      for (int y = 0; y < YT; ++y)
+        bv[y] = cb[y] ? *reinterpret_cast<const f32x4*>(k + c[y] * D + k0 + 4 * half) : f32x4{};
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int x = 0; x < 2; ++x)
 #pragma unroll
-          for (int y = 0; y < 2; ++y)
+          for (int y = 0; y < YT; ++y)
             acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[x][s], bv[y][s], acc[x][y], 0, 0, 0);
     }
   } else {
@@ -131,16 +135,17 @@ __device__ __forceinline__ void aff_quad(const void* qcv, const void* kcv, int64
     const uint16_t* k = static_cast<const uint16_t*>(kcv);
     for (int k0 = 0; k0 < D; k0 += 16) {
       const bool kin = k0 + 8 * half < D;  // D % 16 == 8: the upper half is past the row
-      u32x4 av[2], bv[2];
+      u32x4 av[2], bv[YT];
 #pragma unroll
-      for (int x = 0; x < 2; ++x) {
+      for (int x = 0; x < 2; ++x)
         av[x] = ra[x] && kin ? *reinterpret_cast<const u32x4*>(q + r[x] * D + k0 + 8 * half) : u32x4{};
-        bv[x] = cb[x] && kin ? *reinterpret_cast<const u32x4*>(k + c[x] * D + k0 + 8 * half) : u32x4{};
-      }
+#pragma unroll
+      for (int y = 0; y < YT; ++y)
+        bv[y] = cb[y] && kin ? *reinterpret_cast<const u32x4*>(k + c[y] * D + k0 + 8 * half) : u32x4{};
 #pragma unroll
       for (int x = 0; x < 2; ++x)
 #pragma unroll
-        for (int y = 0; y < 2; ++y) {
+        for (int y = 0; y < YT; ++y) {
           if constexpr (std::is_same<T, bf16_t>::value)
             acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                 __builtin_bit_cast(bf16x8, av[x]), __builtin_bit_cast(bf16x8, bv[y]), acc[x][y], 0, 0, 0);
@@ -156,8 +161,67 @@ __device__ __forceinline__ float normalize_minmax(float a, float mn, float mx) {
   return mx > mn ? (a - mn) / (mx - mn + 1e-8f) : a;
 }
 
-// A 128 x 128 tile per workgroup; wave w computes quadrant (w / 2, w % 2).
-template <typename T, bool EMIT>
+// STATS pass: per-tile min / max of A. A 256 x 256 tile per workgroup of 8
+// waves; wave w computes rows 64 (w / 2) .., columns 128 (w % 2) .. as 2 x 4
+// MFMA tiles (eight accumulators share each operand load).
+constexpr int AS = 256;  // STATS tile per workgroup
+
+template <typename T>
+__global__ __launch_bounds__(512) void affinity_stats_kernel(AffArgs a) {
+  const int64_t bh = blockIdx.y;
+  const int64_t tile = blockIdx.x;
+  const int64_t ns = (a.Mp + AS - 1) / AS;
+  const int64_t ti = tile / ns, tj = tile - (tile / ns) * ns;
+  const int w = threadIdx.x >> 6, lane = lane_id();
+  const int64_t row0 = ti * AS + (w >> 1) * 64, col0 = tj * AS + (w & 1) * 128;
+  const size_t esz = sizeof(T) == 4 ? 4 : 2;
+  const char* qcb = static_cast<const char*>(a.qc) + static_cast<size_t>(bh) * a.M * a.D * esz;
+  const char* kcb = static_cast<const char*>(a.kc) + static_cast<size_t>(bh) * a.M * a.D * esz;
+  f32x16 acc[2][4];
+  aff_block<T, 4>(qcb, kcb, row0, col0, a.M, a.D, lane, acc);
+  const int half = lane >> 5;
+  float mn = INFINITY, mx = -INFINITY;
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 4; ++y)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t i = row0 + 32 * x + 8 * (e >> 2) + 4 * half + (e & 3);
+        const int64_t j = col0 + 32 * y + (lane & 31);
+        if (i < a.M && j < a.M) {
+          const float v = acc[x][y][e] * a.alpha;
+          mn = fminf(mn, v);
+          mx = fmaxf(mx, v);
+        }
+      }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    mn = fminf(mn, shfl_xor_f32(mn, off));
+    mx = fmaxf(mx, shfl_xor_f32(mx, off));
+  }
+  __shared__ float red[8][2];
+  if (lane == 0) {
+    red[w][0] = mn;
+    red[w][1] = mx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float m0 = red[0][0], m1 = red[0][1];
+#pragma unroll
+    for (int q = 1; q < 8; ++q) {
+      m0 = fminf(m0, red[q][0]);
+      m1 = fmaxf(m1, red[q][1]);
+    }
+    float* p = a.mmpart + (bh * ns * ns + tile) * 2;
+    p[0] = m0;
+    p[1] = m1;
+  }
+}
+
+// EMIT pass: a 128 x 128 tile per workgroup; wave w computes quadrant
+// (w / 2, w % 2), normalises it and writes the planes.
+template <typename T>
 __global__ __launch_bounds__(256) void affinity_kernel(AffArgs a) {
   const int64_t bh = blockIdx.y;
   const int64_t tile = blockIdx.x;
@@ -169,161 +233,127 @@ __global__ __launch_bounds__(256) void affinity_kernel(AffArgs a) {
   const char* qcb = static_cast<const char*>(a.qc) + static_cast<size_t>(bh) * a.M * a.D * esz;
   const char* kcb = static_cast<const char*>(a.kc) + static_cast<size_t>(bh) * a.M * a.D * esz;
   f32x16 acc[2][2];
-  aff_quad<T>(qcb, kcb, row0, col0, a.M, a.D, lane, acc);
+  aff_block<T, 2>(qcb, kcb, row0, col0, a.M, a.D, lane, acc);
 
   const int half = lane >> 5;
   // Row and column of element e of MFMA tile (x, y), relative to the quadrant.
   auto qrow = [&](int x, int e) { return 32 * x + 8 * (e >> 2) + 4 * half + (e & 3); };
   auto qcol = [&](int y) { return 32 * y + (lane & 31); };
-  if constexpr (!EMIT) {
-    float mn = INFINITY, mx = -INFINITY;
+  float mn = 0.f, mx = 0.f;
+  if (a.normalization == CAB_NORM_MINMAX) {
+    mn = a.mm[bh * 2 + 0];
+    mx = a.mm[bh * 2 + 1];
+  }
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float v = 0.f;
+        if (row0 + qrow(x, e) < a.M && col0 + qcol(y) < a.M) {
+          v = acc[x][y][e] * a.alpha;
+          if (a.normalization == CAB_NORM_MINMAX) v = normalize_minmax(v, mn, mx);
+        }
+        acc[x][y][e] = v;
+      }
+  if (a.rspart) {
+    // Row sums over the quadrant's 64 columns (one AT column block).
 #pragma unroll
     for (int x = 0; x < 2; ++x)
 #pragma unroll
-      for (int y = 0; y < 2; ++y)
+      for (int e = 0; e < 16; ++e) {
+        float sum = acc[x][0][e] + acc[x][1][e];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          if (row0 + qrow(x, e) < a.M && col0 + qcol(y) < a.M) {
-            const float v = acc[x][y][e] * a.alpha;
-            mn = fminf(mn, v);
-            mx = fmaxf(mx, v);
-          }
-        }
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      mn = fminf(mn, shfl_xor_f32(mn, off));
-      mx = fmaxf(mx, shfl_xor_f32(mx, off));
-    }
-    __shared__ float red[4][2];
-    if (lane == 0) {
-      red[w][0] = mn;
-      red[w][1] = mx;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float m0 = fminf(fminf(red[0][0], red[1][0]), fminf(red[2][0], red[3][0]));
-      float m1 = fmaxf(fmaxf(red[0][1], red[1][1]), fmaxf(red[2][1], red[3][1]));
-      float* p = a.mmpart + (bh * a.ntw * a.ntw + tile) * 2;
-      p[0] = m0;
-      p[1] = m1;
-    }
-  } else {
-    float mn = 0.f, mx = 0.f;
-    if (a.normalization == CAB_NORM_MINMAX) {
-      mn = a.mm[bh * 2 + 0];
-      mx = a.mm[bh * 2 + 1];
-    }
-#pragma unroll
-    for (int x = 0; x < 2; ++x)
-#pragma unroll
-      for (int y = 0; y < 2; ++y)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          float v = 0.f;
-          if (row0 + qrow(x, e) < a.M && col0 + qcol(y) < a.M) {
-            v = acc[x][y][e] * a.alpha;
-            if (a.normalization == CAB_NORM_MINMAX) v = normalize_minmax(v, mn, mx);
-          }
-          acc[x][y][e] = v;
-        }
-    if (a.rspart) {
-      // Row sums over the quadrant's 64 columns (one AT column block).
+        for (int off = 1; off < 32; off <<= 1) sum += shfl_xor_f32(sum, off);
+        if ((lane & 31) == 0)
+          a.rspart[(static_cast<size_t>(bh) * a.nta + col0 / AT) * a.Mp + row0 + qrow(x, e)] = sum;
+      }
+  }
+  // Each normalised 64 x 64 quadrant goes through LDS in turn, so that every
+  // plane is written as whole 16-byte row chunks: X rows from the
+  // quadrant's rows, XT rows from its columns (zero outside M: the planes
+  // are Mp x Mp).
+  __shared__ float stile[AT][AT + 1];
+  const size_t pbase = static_cast<size_t>(bh) * a.Mp * a.Mp;
+  for (int qd = 0; qd < 4; ++qd) {
+    if (qd > 0) __syncthreads();  // the previous quadrant's reads are done
+    if (w == qd) {
 #pragma unroll
       for (int x = 0; x < 2; ++x)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          float sum = acc[x][0][e] + acc[x][1][e];
+        for (int y = 0; y < 2; ++y)
 #pragma unroll
-          for (int off = 1; off < 32; off <<= 1) sum += shfl_xor_f32(sum, off);
-          if ((lane & 31) == 0)
-            a.rspart[(static_cast<size_t>(bh) * a.nta + col0 / AT) * a.Mp + row0 + qrow(x, e)] = sum;
-        }
+          for (int e = 0; e < 16; ++e) stile[qrow(x, e)][qcol(y)] = acc[x][y][e];
     }
-    // Each normalised 64 x 64 quadrant goes through LDS in turn, so that every
-    // plane is written as whole 16-byte row chunks: X rows from the
-    // quadrant's rows, XT rows from its columns (zero outside M: the planes
-    // are Mp x Mp).
-    __shared__ float stile[AT][AT + 1];
-    const size_t pbase = static_cast<size_t>(bh) * a.Mp * a.Mp;
-    for (int qd = 0; qd < 4; ++qd) {
-      if (qd > 0) __syncthreads();  // the previous quadrant's reads are done
-      if (w == qd) {
+    __syncthreads();
+    const int64_t ti0 = ti * AW + AT * (qd >> 1), tj0 = tj * AW + AT * (qd & 1);
 #pragma unroll
-        for (int x = 0; x < 2; ++x)
-#pragma unroll
-          for (int y = 0; y < 2; ++y)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) stile[qrow(x, e)][qcol(y)] = acc[x][y][e];
-      }
-      __syncthreads();
-      const int64_t ti0 = ti * AW + AT * (qd >> 1), tj0 = tj * AW + AT * (qd & 1);
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int cid = threadIdx.x + 256 * q;  // 64 rows x 8 chunks of 8 values
-        const int r = cid >> 3, c8 = (cid & 7) * 8;
-        const size_t xo = pbase + static_cast<size_t>(ti0 + r) * a.Mp + tj0 + c8;
-        const size_t to = pbase + static_cast<size_t>(tj0 + r) * a.Mp + ti0 + c8;
-        u32x4 h4, l4, th4, tl4;
-        if (a.fused) {
-          // XT row tj0 + r, column ti0 + c: delta - lambda Ahat[ti0 + c][tj0 + r]
-          // (the delta only inside M; the planes are zero beyond it).
-          const int64_t jrow = tj0 + r;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float x0 = stile[r][c8 + 2 * e], x1 = stile[r][c8 + 2 * e + 1];
-            const int64_t k0 = ti0 + c8 + 2 * e;
-            const float d0 = (k0 == jrow && k0 < a.M) ? 1.f : 0.f;
-            const float d1 = (k0 + 1 == jrow && k0 + 1 < a.M) ? 1.f : 0.f;
-            const float y0 = d0 - a.lambda * stile[c8 + 2 * e][r];
-            const float y1 = d1 - a.lambda * stile[c8 + 2 * e + 1][r];
-            h4[e] = static_cast<uint32_t>(f32_to_f16(x0)) | (static_cast<uint32_t>(f32_to_f16(x1)) << 16);
-            th4[e] = static_cast<uint32_t>(f32_to_f16(y0)) | (static_cast<uint32_t>(f32_to_f16(y1)) << 16);
-          }
-          *reinterpret_cast<u32x4*>(a.xhi + xo) = h4;
-          *reinterpret_cast<u32x4*>(a.xthi + to) = th4;
-          continue;
-        }
-        if (a.f16_planes) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float x0 = stile[r][c8 + 2 * e], x1 = stile[r][c8 + 2 * e + 1];
-            const float y0 = stile[c8 + 2 * e][r], y1 = stile[c8 + 2 * e + 1][r];
-            const uint16_t hx0 = f32_to_f16(x0), hx1 = f32_to_f16(x1);
-            h4[e] = static_cast<uint32_t>(hx0) | (static_cast<uint32_t>(hx1) << 16);
-            l4[e] = static_cast<uint32_t>(f32_to_f16(x0 - f16_to_f32(hx0))) |
-                    (static_cast<uint32_t>(f32_to_f16(x1 - f16_to_f32(hx1))) << 16);
-            th4[e] = static_cast<uint32_t>(f32_to_f16(y0)) | (static_cast<uint32_t>(f32_to_f16(y1)) << 16);
-          }
-          *reinterpret_cast<u32x4*>(a.xhi + xo) = h4;
-          *reinterpret_cast<u32x4*>(a.xlo + xo) = l4;
-          *reinterpret_cast<u32x4*>(a.xthi + to) = th4;
-          continue;
-        }
+    for (int q = 0; q < 2; ++q) {
+      const int cid = threadIdx.x + 256 * q;  // 64 rows x 8 chunks of 8 values
+      const int r = cid >> 3, c8 = (cid & 7) * 8;
+      const size_t xo = pbase + static_cast<size_t>(ti0 + r) * a.Mp + tj0 + c8;
+      const size_t to = pbase + static_cast<size_t>(tj0 + r) * a.Mp + ti0 + c8;
+      u32x4 h4, l4, th4, tl4;
+      if (a.fused) {
+        // XT row tj0 + r, column ti0 + c: delta - lambda Ahat[ti0 + c][tj0 + r]
+        // (the delta only inside M; the planes are zero beyond it).
+        const int64_t jrow = tj0 + r;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float x0 = stile[r][c8 + 2 * e], x1 = stile[r][c8 + 2 * e + 1];    // X row ti0 + r
-          const float y0 = stile[c8 + 2 * e][r], y1 = stile[c8 + 2 * e + 1][r];    // XT row tj0 + r
-          const uint16_t hx0 = f32_to_bf16(x0), hx1 = f32_to_bf16(x1);
-          const uint16_t hy0 = f32_to_bf16(y0), hy1 = f32_to_bf16(y1);
+          const float x0 = stile[r][c8 + 2 * e], x1 = stile[r][c8 + 2 * e + 1];
+          const int64_t k0 = ti0 + c8 + 2 * e;
+          const float d0 = (k0 == jrow && k0 < a.M) ? 1.f : 0.f;
+          const float d1 = (k0 + 1 == jrow && k0 + 1 < a.M) ? 1.f : 0.f;
+          const float y0 = d0 - a.lambda * stile[c8 + 2 * e][r];
+          const float y1 = d1 - a.lambda * stile[c8 + 2 * e + 1][r];
+          h4[e] = static_cast<uint32_t>(f32_to_f16(x0)) | (static_cast<uint32_t>(f32_to_f16(x1)) << 16);
+          th4[e] = static_cast<uint32_t>(f32_to_f16(y0)) | (static_cast<uint32_t>(f32_to_f16(y1)) << 16);
+        }
+        *reinterpret_cast<u32x4*>(a.xhi + xo) = h4;
+        *reinterpret_cast<u32x4*>(a.xthi + to) = th4;
+        continue;
+      }
+      if (a.f16_planes) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x0 = stile[r][c8 + 2 * e], x1 = stile[r][c8 + 2 * e + 1];
+          const float y0 = stile[c8 + 2 * e][r], y1 = stile[c8 + 2 * e + 1][r];
+          const uint16_t hx0 = f32_to_f16(x0), hx1 = f32_to_f16(x1);
           h4[e] = static_cast<uint32_t>(hx0) | (static_cast<uint32_t>(hx1) << 16);
-          l4[e] = static_cast<uint32_t>(f32_to_bf16(x0 - bf16_to_f32(hx0))) |
-                  (static_cast<uint32_t>(f32_to_bf16(x1 - bf16_to_f32(hx1))) << 16);
-          th4[e] = static_cast<uint32_t>(hy0) | (static_cast<uint32_t>(hy1) << 16);
-          tl4[e] = static_cast<uint32_t>(f32_to_bf16(y0 - bf16_to_f32(hy0))) |
-                   (static_cast<uint32_t>(f32_to_bf16(y1 - bf16_to_f32(hy1))) << 16);
+          l4[e] = static_cast<uint32_t>(f32_to_f16(x0 - f16_to_f32(hx0))) |
+                  (static_cast<uint32_t>(f32_to_f16(x1 - f16_to_f32(hx1))) << 16);
+          th4[e] = static_cast<uint32_t>(f32_to_f16(y0)) | (static_cast<uint32_t>(f32_to_f16(y1)) << 16);
         }
         *reinterpret_cast<u32x4*>(a.xhi + xo) = h4;
         *reinterpret_cast<u32x4*>(a.xlo + xo) = l4;
         *reinterpret_cast<u32x4*>(a.xthi + to) = th4;
-        *reinterpret_cast<u32x4*>(a.xtlo + to) = tl4;
+        continue;
       }
-      if (a.affinity) {
-        // fp32 diagnostic, rows of the quadrant inside M (coalesced along j)
-        for (int e = threadIdx.x; e < AT * AT; e += 256) {
-          const int r = e >> 6, c = e & 63;
-          const int64_t i = ti0 + r, jj = tj0 + c;
-          if (i < a.M && jj < a.M) a.affinity[(static_cast<size_t>(bh) * a.M + i) * a.M + jj] = stile[r][c];
-        }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x0 = stile[r][c8 + 2 * e], x1 = stile[r][c8 + 2 * e + 1];    // X row ti0 + r
+        const float y0 = stile[c8 + 2 * e][r], y1 = stile[c8 + 2 * e + 1][r];    // XT row tj0 + r
+        const uint16_t hx0 = f32_to_bf16(x0), hx1 = f32_to_bf16(x1);
+        const uint16_t hy0 = f32_to_bf16(y0), hy1 = f32_to_bf16(y1);
+        h4[e] = static_cast<uint32_t>(hx0) | (static_cast<uint32_t>(hx1) << 16);
+        l4[e] = static_cast<uint32_t>(f32_to_bf16(x0 - bf16_to_f32(hx0))) |
+                (static_cast<uint32_t>(f32_to_bf16(x1 - bf16_to_f32(hx1))) << 16);
+        th4[e] = static_cast<uint32_t>(hy0) | (static_cast<uint32_t>(hy1) << 16);
+        tl4[e] = static_cast<uint32_t>(f32_to_bf16(y0 - bf16_to_f32(hy0))) |
+                 (static_cast<uint32_t>(f32_to_bf16(y1 - bf16_to_f32(hy1))) << 16);
+      }
+      *reinterpret_cast<u32x4*>(a.xhi + xo) = h4;
+      *reinterpret_cast<u32x4*>(a.xlo + xo) = l4;
+      *reinterpret_cast<u32x4*>(a.xthi + to) = th4;
+      *reinterpret_cast<u32x4*>(a.xtlo + to) = tl4;
+    }
+    if (a.affinity) {
+      // fp32 diagnostic, rows of the quadrant inside M (coalesced along j)
+      for (int e = threadIdx.x; e < AT * AT; e += 256) {
+        const int r = e >> 6, c = e & 63;
+        const int64_t i = ti0 + r, jj = tj0 + c;
+        if (i < a.M && jj < a.M) a.affinity[(static_cast<size_t>(bh) * a.M + i) * a.M + jj] = stile[r][c];
       }
     }
   }
@@ -659,11 +689,14 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
 
 template <typename T>
 void launch_affinity(const AffArgs& a, int64_t BH, bool emit, hipStream_t s) {
-  dim3 grid(static_cast<unsigned>(a.ntw * a.ntw), static_cast<unsigned>(BH));
-  if (emit)
-    affinity_kernel<T, true><<<grid, 256, 0, s>>>(a);
-  else
-    affinity_kernel<T, false><<<grid, 256, 0, s>>>(a);
+  if (emit) {
+    affinity_kernel<T><<<dim3(static_cast<unsigned>(a.ntw * a.ntw), static_cast<unsigned>(BH)), 256, 0,
+                         s>>>(a);
+  } else {
+    const int64_t ns = ceil_div(a.Mp, AS);
+    affinity_stats_kernel<T><<<dim3(static_cast<unsigned>(ns * ns), static_cast<unsigned>(BH)), 512, 0,
+                               s>>>(a);
+  }
 }
 
 }  // namespace
@@ -752,7 +785,7 @@ extern "C" cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_
     cab_status_t st = launch_status("cab_block_frc/affinity_stats");
     if (st != CAB_OK) return st;
     minmax_finalize_kernel<<<static_cast<unsigned>(BH), 256, 0, s>>>(
-        a.mmpart, L.ntw * L.ntw, reinterpret_cast<float*>(ws + L.off_mm));
+        a.mmpart, ceil_div(L.Mp, AS) * ceil_div(L.Mp, AS), reinterpret_cast<float*>(ws + L.off_mm));
     st = launch_status("cab_block_frc/minmax_finalize");
     if (st != CAB_OK) return st;
   }
