@@ -468,7 +468,8 @@ __device__ __forceinline__ float frc_combine(int formula, float ahat, float t, f
 // register buffers carry operand slices global -> registers -> LDS (two LDS
 // stages): with NBUF = 2 a slice's loads have two slices of MFMA work to
 // land, with NBUF = 1 one slice (for the wide bf16 tile, whose accumulators
-// leave room for one buffer of four planes only). F16 selects the fp16 planes
+// leave room for one buffer of four planes only); NBUF = 0 is the ping-pong
+// schedule of two wave groups (fp16 256 x 256 tile). F16 selects the fp16 planes
 // (A = X, B = XT, one product per site); otherwise the bf16 hi / lo planes of
 // both operands (three products).
 template <int TI, int TJ, int WI, int WJ, int NBUF, bool F16, int KD>
@@ -559,7 +560,8 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
       }
     }
   };
-  u32x4 rga[NBUF][NH][CA], rgb[NBUF][NH][CB];
+  constexpr int NB = NBUF > 0 ? NBUF : 1;  // register buffers (ping-pong: its own, below)
+  u32x4 rga[NB][NH][CA], rgb[NB][NH][CB];
   auto load = [&](int buf, int kt) {
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
@@ -577,7 +579,83 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
 
   // The loop's barriers are uniform: `constant` depends on bh alone.
   if (!constant) {
-    if constexpr (NBUF == 2) {
+    if constexpr (NBUF == 0) {
+      // Ping-pong: wave group gp = wi (waves 4 gp .. 4 gp + 3, one per SIMD)
+      // stages its own 128 A rows and half of the B rows of each slice. In
+      // each slice, group 0 multiplies while group 1 stores slice kt + 1 and
+      // loads slice kt + 2, then the roles swap, so every SIMD has one wave on
+      // the MFMAs and one on memory. Slice kt + 1 is complete in LDS after
+      // the slice's second barrier, and its stage was last read (slice kt - 1)
+      // before the first.
+      static_assert(WI == 2 && THREADS == 512 && F16, "ping-pong: two groups of four waves");
+      constexpr int CPR = KD / 8;                        // 16-byte chunks per row
+      constexpr int HA = TI / 2, HB = TJ / 2;            // rows per group and operand
+      constexpr int CAH = HA * CPR / 256, CBH = HB * CPR / 256;
+      static_assert(CAH * 256 == HA * CPR && CBH * 256 == HB * CPR, "whole chunks per thread");
+      const int gp = wi, tg = threadIdx.x & 255;
+      u32x4 pra[CAH], prb[CBH];
+      auto pload = [&](int kt) {
+        const int64_t k0 = static_cast<int64_t>(kt) * KD;
+#pragma unroll
+        for (int q = 0; q < CAH; ++q) {
+          const int cid = tg + 256 * q, row = gp * HA + cid / CPR, kc = cid % CPR;
+          pra[q] = *reinterpret_cast<const u32x4*>(pa[0] + (ra + row) * a.Mp + k0 + 8 * kc);
+        }
+#pragma unroll
+        for (int q = 0; q < CBH; ++q) {
+          const int cid = tg + 256 * q, row = gp * HB + cid / CPR, kc = cid % CPR;
+          prb[q] = *reinterpret_cast<const u32x4*>(pb[0] + (rb + row) * a.Mp + k0 + 8 * kc);
+        }
+      };
+      auto pstore = [&](int st) {
+        u32x4* la = lds + st * STAGE;
+        u32x4* lb = la + SA;
+#pragma unroll
+        for (int q = 0; q < CAH; ++q) {
+          const int cid = tg + 256 * q, row = gp * HA + cid / CPR, kc = cid % CPR;
+          const int kk = kc >> 1, hf = kc & 1, sub = row >> 5;
+          la[(kk * (TI / 32) + sub) * 64 + (((row & 31) + 32 * hf) ^ (4 * (2 * kk + hf)))] = pra[q];
+        }
+#pragma unroll
+        for (int q = 0; q < CBH; ++q) {
+          const int cid = tg + 256 * q, row = gp * HB + cid / CPR, kc = cid % CPR;
+          const int kk = kc >> 1, hf = kc & 1, sub = row >> 5;
+          lb[(kk * (TJ / 32) + sub) * 64 + (((row & 31) + 32 * hf) ^ (4 * (2 * kk + hf)))] = prb[q];
+        }
+      };
+      pload(0);
+      pstore(0);
+      if (nk > 1) pload(1);
+      lds_barrier();
+      auto slice = [&](int kt, auto st_tag) {
+        constexpr int st = decltype(st_tag)::value;  // LDS stage of slice kt
+        auto mem = [&]() {
+          if (kt + 1 < nk) pstore(st ^ 1);
+          if (kt + 2 < nk) pload(kt + 2);
+        };
+        // The multiplying group runs at raised wave priority.
+        if (gp == 0) {
+          __builtin_amdgcn_s_setprio(1);
+          compute(st_tag);
+          __builtin_amdgcn_s_setprio(0);
+        } else {
+          mem();
+        }
+        lds_barrier();
+        if (gp == 0) {
+          mem();
+        } else {
+          __builtin_amdgcn_s_setprio(1);
+          compute(st_tag);
+          __builtin_amdgcn_s_setprio(0);
+        }
+        lds_barrier();
+      };
+      for (int kt = 0; kt < nk; kt += 2) {
+        slice(kt, std::integral_constant<int, 0>{});
+        if (kt + 1 < nk) slice(kt + 1, std::integral_constant<int, 1>{});
+      }
+    } else if constexpr (NBUF == 2) {
       // The registers of slice kt + 2 are loaded while slice kt is multiplied.
       load(0, 0);
       if (nk > 1) load(1, 1);
@@ -827,7 +905,7 @@ extern "C" cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_
   CAB_REQUIRE(blocks <= INT32_MAX, CAB_ESHAPE, "cab_block_frc: problem too large");
   const unsigned nb = static_cast<unsigned>(blocks);
   if (wide && f16)
-    triangle_kernel<TT_WIDE, TT_WIDE, 2, 4, 2, true, TK><<<nb, 512, 0, s>>>(t);
+    triangle_kernel<TT_WIDE, TT_WIDE, 2, 4, 0, true, 2 * TK><<<nb, 512, 0, s>>>(t);
   else if (wide)
     triangle_kernel<TT_WIDE, TT_WIDE, 2, 4, 1, false, TK><<<nb, 512, 0, s>>>(t);
   else if (f16)
