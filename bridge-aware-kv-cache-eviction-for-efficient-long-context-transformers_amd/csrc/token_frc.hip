@@ -243,8 +243,10 @@ struct PrepArgs {
 };
 
 // One wave per position: lane l (l < 32) owns dims 8 (l % 32) .. + 7, and
-// the two lane halves sum the even and odd (b, h) slices.
-template <typename T>
+// the two lane halves sum the even and odd (b, h) slices. VEC: unit dim
+// stride and 16-byte aligned rows, so a lane's dims are one or two 16-byte
+// loads per slice.
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void keys_prep_kernel(PrepArgs a) {
   const int64_t n = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (n >= a.Np) return;
@@ -255,10 +257,24 @@ __global__ __launch_bounds__(256) void keys_prep_kernel(PrepArgs a) {
     for (int64_t bh = par; bh < a.bh; bh += 2) {
       const int64_t b = bh / a.H, h = bh - (bh / a.H) * a.H;
       const T* p = base + b * a.st[0] + h * a.st[1] + n * a.st[2];
+      if constexpr (VEC) {
+        if (8 * g < a.D) {  // D % 8 == 0 on this path
+          float v[8];
+          if constexpr (sizeof(T) == 4) {
+            ld_vec<T>(p + 8 * g, v);
+            ld_vec<T>(p + 8 * g + 4, v + 4);
+          } else {
+            ld_vec<T>(p + 8 * g, v);
+          }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int64_t d = 8 * g + e;
-        if (d < a.D) x[e] += ld_elem<T>(p + d * a.st[3]);
+          for (int e = 0; e < 8; ++e) x[e] += v[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int64_t d = 8 * g + e;
+          if (d < a.D) x[e] += ld_elem<T>(p + d * a.st[3]);
+        }
       }
     }
   }
@@ -597,10 +613,25 @@ extern "C" cab_status_t cab_token_frc_from_keys(const void* keys, cab_dtype_t dt
   PrepArgs pa{keys, H, B * H, N, D, L.Np, L.dk, {strides[0], strides[1], strides[2], strides[3]},
               hi, lo};
   const unsigned pgrid = static_cast<unsigned>(L.Np / 4);
+  // 16-byte loads when each position's D values are contiguous and every
+  // row start (all b, h, n strides) keeps 16-byte alignment.
+  const int64_t esz = dtype == CAB_F32 ? 4 : 2;
+  const bool vec = strides[3] == 1 && D % 8 == 0 && reinterpret_cast<uintptr_t>(keys) % 16 == 0 &&
+                   (strides[0] * esz) % 16 == 0 && (strides[1] * esz) % 16 == 0 &&
+                   (strides[2] * esz) % 16 == 0;
   switch (dtype) {
-    case CAB_F32: keys_prep_kernel<float><<<pgrid, 256, 0, st>>>(pa); break;
-    case CAB_BF16: keys_prep_kernel<bf16_t><<<pgrid, 256, 0, st>>>(pa); break;
-    default: keys_prep_kernel<f16_t><<<pgrid, 256, 0, st>>>(pa); break;
+    case CAB_F32:
+      vec ? keys_prep_kernel<float, true><<<pgrid, 256, 0, st>>>(pa)
+          : keys_prep_kernel<float, false><<<pgrid, 256, 0, st>>>(pa);
+      break;
+    case CAB_BF16:
+      vec ? keys_prep_kernel<bf16_t, true><<<pgrid, 256, 0, st>>>(pa)
+          : keys_prep_kernel<bf16_t, false><<<pgrid, 256, 0, st>>>(pa);
+      break;
+    default:
+      vec ? keys_prep_kernel<f16_t, true><<<pgrid, 256, 0, st>>>(pa)
+          : keys_prep_kernel<f16_t, false><<<pgrid, 256, 0, st>>>(pa);
+      break;
   }
   cab_status_t rc = launch_status(fn);
   if (rc != CAB_OK) return rc;
