@@ -14,8 +14,15 @@
 // the row's magnitude keys for its magnitude quota, marks those blocks taken,
 // and then searches the FRC keys of the remaining candidates.
 //
+// Rows longer than 8192 (up to the 32768 the FRC stage accepts) go to
+// topk_stream_kernel: the same search and tie rules with the row read again
+// from memory on every pass instead of held in registers. Its hybrid form
+// marks the magnitude picks by their threshold and the position of the last
+// kept tie.
+//
 // HBM traffic per row: 4 M bytes read (8 M hybrid); 4 k + 4 (+ M for the
-// dense mask) bytes written. Bound by HBM bandwidth.
+// dense mask) bytes written. Bound by HBM bandwidth. The streaming kernel
+// reads the row once per pass (up to 6 passes, mostly from L2 and MALL).
 #include "cab_internal.h"
 
 namespace cab {
@@ -61,19 +68,34 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_wave_barrier();
 }
 
-template <int NCH, typename Cand>
-__device__ __forceinline__ uint32_t kth_key(const uint32_t (&key)[NCH], Cand is_cand, int64_t need,
+// Runs f(c) for the row's chunks c (lane l holds column 64 c + l): NCH
+// chunks unrolled (keys in registers), or nch chunks in a loop when NCH == 0.
+template <int NCH, typename F>
+__device__ __forceinline__ void for_chunks(int nch, F f) {
+  if constexpr (NCH > 0) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) f(c);
+  } else {
+#pragma unroll 4
+    for (int c = 0; c < nch; ++c) f(c);
+  }
+}
+
+// key(c) is this lane's key in chunk c: a register, or (NCH == 0) a load.
+template <int NCH, typename Key, typename Cand>
+__device__ __forceinline__ uint32_t kth_key(Key key, Cand is_cand, int nch, int64_t need,
                                             int64_t& need_eq, uint32_t* hist) {
   const int lane = lane_id();
   need_eq = 0;
   if (need <= 0) return 0u;
   uint32_t kand = 0xffffffffu, kor = 0u;
-#pragma unroll
-  for (int c = 0; c < NCH; ++c)
+  for_chunks<NCH>(nch, [&](int c) {
     if (is_cand(c)) {
-      kand &= key[c];
-      kor |= key[c];
+      const uint32_t kc = key(c);
+      kand &= kc;
+      kor |= kc;
     }
+  });
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
     kand &= static_cast<uint32_t>(__shfl_xor(static_cast<int>(kand), off, 64));
@@ -105,13 +127,15 @@ __device__ __forceinline__ uint32_t kth_key(const uint32_t (&key)[NCH], Cand is_
     for (int q = 0; q < HSUB; ++q) slots[64 * q + lane] = u32x4{0u, 0u, 0u, 0u};
     wave_sync();
     const uint32_t sub = static_cast<uint32_t>(lane % HSUB);
-#pragma unroll
-    for (int c = 0; c < NCH; ++c)
-      if (is_cand(c) && (key[c] & pmask) == prefix) {
-        const uint32_t bn = (key[c] >> shift) & 255u;
+    for_chunks<NCH>(nch, [&](int c) {
+      if (!is_cand(c)) return;
+      const uint32_t kc = key(c);
+      if ((kc & pmask) == prefix) {
+        const uint32_t bn = (kc >> shift) & 255u;
         const uint32_t q = 2u * (bn & 3u) + (sub >> 2);
         atomicAdd(&hist[4u * (64u * q + (bn >> 2)) + (sub & 3u)], 1u);
       }
+    });
     wave_sync();
     // Bins 4 lane .. 4 lane + 3: inclusive prefix counts across the wave.
     uint32_t hv[4] = {0u, 0u, 0u, 0u};
@@ -152,9 +176,11 @@ __device__ __forceinline__ uint32_t kth_key(const uint32_t (&key)[NCH], Cand is_
     if (sel_cnt == 1u && shift > 0) {
       // One candidate left (rem == 1): theta is its key.
       uint32_t kv = 0u;
-#pragma unroll
-      for (int c = 0; c < NCH; ++c)
-        if (is_cand(c) && (key[c] & pmask) == prefix) kv = key[c];
+      for_chunks<NCH>(nch, [&](int c) {
+        if (!is_cand(c)) return;
+        const uint32_t kc = key(c);
+        if ((kc & pmask) == prefix) kv = kc;
+      });
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1)
         kv |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(kv), off, 64));
@@ -227,7 +253,8 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
       for (int c = 0; c < NCH; ++c) mkey[c] = 64 * c + lane < Mi ? order_key(v[c], true) : 0xffffffffu;
     }
     int64_t meq = 0;
-    const uint32_t mtheta = kth_key(mkey, is_cand, need_m, meq, hist);
+    const uint32_t mtheta =
+        kth_key<NCH>([&](int c) { return mkey[c]; }, is_cand, NCH, need_m, meq, hist);
     int64_t eq_seen = 0;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
@@ -245,7 +272,8 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   // FRC order for the rest of the row.
   const int64_t need_f = need - need_m;
   int64_t need_eq = 0;
-  const uint32_t theta = kth_key(key, is_cand_f, need_f, need_eq, hist);
+  const uint32_t theta =
+      kth_key<NCH>([&](int c) { return key[c]; }, is_cand_f, NCH, need_f, need_eq, hist);
 
   int64_t pos = 0, eq_seen = 0;
   int32_t* out = a.kv_idx + row * a.k;
@@ -268,6 +296,95 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   if (lane == 0) a.kv_cnt[row] = static_cast<int32_t>(pos);
 }
 
+// One wave per row for M > 8192: every pass reads the row's keys again
+// (lane l, columns 64 c + l, coalesced). Same selection and tie rules as
+// topk_kernel; in the hybrid form a candidate is taken by magnitude when its
+// key is below the magnitude threshold, or equal to it and no later in j
+// than the last tie the quota keeps.
+template <bool HYB>
+__global__ __launch_bounds__(256) void topk_stream_kernel(TopkArgs a) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;  // uniform per wave
+  const int lane = lane_id();
+  const int64_t i = row % a.M;
+  const int64_t ncand = a.causal ? i + 1 : a.M;
+  const int64_t krow = min(static_cast<int64_t>(a.k), ncand);
+  const bool kd = a.keep_diagonal != 0;
+  const int64_t need = kd ? krow - 1 : krow;
+  const float* f = a.frc + row * a.M;
+  const float* mg = HYB ? a.mag + row * a.M : nullptr;
+  const bool high = a.select_high != 0;
+  const uint64_t lt_mask = lanemask_lt();
+  __shared__ uint32_t hist_all[4][256 * HSUB];
+  uint32_t* hist = hist_all[threadIdx.x >> 6];
+  const int Mi = static_cast<int>(a.M), nch = (Mi + 63) / 64;
+  const int ncand_i = static_cast<int>(ncand), i_i = static_cast<int>(i);
+  auto is_cand = [&](int c) {
+    const int j = 64 * c + lane;
+    return j < ncand_i && !(kd && j == i_i);
+  };
+  auto fkey = [&](int c) {
+    const int j = 64 * c + lane;
+    return j < Mi ? order_key(f[j], high) : 0xffffffffu;
+  };
+  auto mkey = [&](int c) {
+    const int j = 64 * c + lane;
+    return j < Mi ? order_key(mg[j], true) : 0xffffffffu;
+  };
+
+  int64_t need_m = 0;
+  uint32_t mtheta = 0u;
+  int jm_last = -1;  // the last tie at mtheta (in j) the quota keeps
+  if constexpr (HYB) {
+    need_m = min(static_cast<int64_t>(a.kmag), need);
+    int64_t meq = 0;
+    mtheta = kth_key<0>(mkey, is_cand, nch, need_m, meq, hist);
+    if (need_m > 0 && meq > 0) {
+      int64_t seen = 0;
+      for (int c = 0; c < nch && jm_last < 0; ++c) {  // uniform: ballots only
+        const bool eq = is_cand(c) && mkey(c) == mtheta;
+        const uint64_t eqb = ballot64(eq);
+        const int64_t r = meq - 1 - seen;  // its rank among this chunk's ties
+        if (r < __popcll(eqb)) {
+          const uint64_t hit = ballot64(eq && __popcll(eqb & lt_mask) == r);
+          jm_last = 64 * c + __builtin_ctzll(hit);
+        }
+        seen += __popcll(eqb);
+      }
+    }
+  }
+  auto taken = [&](int c) {
+    if (!HYB || need_m <= 0 || !is_cand(c)) return false;
+    const uint32_t mk = mkey(c);
+    return mk < mtheta || (mk == mtheta && 64 * c + lane <= jm_last);
+  };
+  auto is_cand_f = [&](int c) { return is_cand(c) && !taken(c); };
+
+  const int64_t need_f = need - need_m;
+  int64_t need_eq = 0;
+  const uint32_t theta = kth_key<0>(fkey, is_cand_f, nch, need_f, need_eq, hist);
+
+  int64_t pos = 0, eq_seen = 0;
+  int32_t* out = a.kv_idx + row * a.k;
+  for (int c = 0; c < nch; ++c) {
+    const int j = 64 * c + lane;
+    const bool tk = taken(c);
+    const bool cand = need_f > 0 && is_cand(c) && !tk;
+    const uint32_t kc = cand ? fkey(c) : 0xffffffffu;
+    const bool eq = cand && kc == theta;
+    const uint64_t eqb = ballot64(eq);
+    const int64_t eq_rank = eq_seen + __popcll(eqb & lt_mask);
+    const bool sel = (cand && kc < theta) || (eq && eq_rank < need_eq) || tk || (kd && j == i_i);
+    const uint64_t selb = ballot64(sel);
+    if (sel) out[pos + __popcll(selb & lt_mask)] = j;
+    if (a.dense && j < Mi) a.dense[row * a.M + j] = sel ? 1 : 0;
+    pos += __popcll(selb);
+    eq_seen += __popcll(eqb);
+  }
+  for (int64_t p = pos + lane; p < a.k; p += 64) out[p] = -1;
+  if (lane == 0) a.kv_cnt[row] = static_cast<int32_t>(pos);
+}
+
 template <bool HYB>
 void launch_topk(const TopkArgs& a, dim3 grid, hipStream_t s) {
   const int64_t nch = ceil_div(a.M, 64);
@@ -278,7 +395,8 @@ void launch_topk(const TopkArgs& a, dim3 grid, hipStream_t s) {
   else if (nch <= 16) topk_kernel<16, HYB><<<grid, 256, 0, s>>>(a);
   else if (nch <= 32) topk_kernel<32, HYB><<<grid, 256, 0, s>>>(a);
   else if (nch <= 64) topk_kernel<64, HYB><<<grid, 256, 0, s>>>(a);
-  else topk_kernel<128, HYB><<<grid, 256, 0, s>>>(a);
+  else if (nch <= 128) topk_kernel<128, HYB><<<grid, 256, 0, s>>>(a);
+  else topk_stream_kernel<HYB><<<grid, 256, 0, s>>>(a);
 }
 
 cab_status_t topk_common(const char* fn, const float* frc, const float* mag, int64_t B, int64_t H,
@@ -287,7 +405,7 @@ cab_status_t topk_common(const char* fn, const float* frc, const float* mag, int
                          void* stream, bool hybrid) {
   clear_error();
   CAB_REQUIRE(B >= 0 && H >= 0 && M >= 0, CAB_ESHAPE, "%s: negative size", fn);
-  CAB_REQUIRE(M <= 8192, CAB_ESHAPE, "%s: M=%lld exceeds 8192", fn, (long long)M);
+  CAB_REQUIRE(M <= 32768, CAB_ESHAPE, "%s: M=%lld exceeds 32768", fn, (long long)M);
   CAB_REQUIRE(k >= 1, CAB_EINVAL, "%s: k=%d must be >= 1", fn, (int)k);
   CAB_REQUIRE(M == 0 || k <= M, CAB_EINVAL, "%s: k=%d exceeds M=%lld", fn, (int)k, (long long)M);
   CAB_REQUIRE(!hybrid || (kmag >= 0 && kmag <= k), CAB_EINVAL,

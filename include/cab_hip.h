@@ -124,7 +124,8 @@ cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_t dtype,
  * counts toward k).
  * frc: contiguous fp32 [B,H,M,M]. kv_idx: int32 [B,H,M,k], ascending, tail
  * filled with -1. kv_cnt: int32 [B,H,M]. dense_mask: uint8 0/1 [B,H,M,M] or NULL.
- * M <= 8192.
+ * M <= 32768 (rows longer than 8192 take a slower kernel that re-reads the
+ * row from memory on each search pass).
  */
 cab_status_t cab_block_topk(const float* frc, int64_t B, int64_t H, int64_t M, int32_t k,
                             int select_high, int keep_diagonal, int causal,

@@ -102,7 +102,7 @@ def test_topk_validation(lib):
                                            FAKE, FAKE, None, None)
     assert call(k=0) == nat.CAB_EINVAL
     assert call(k=65) == nat.CAB_EINVAL
-    assert call(M=9000, k=3) == nat.CAB_ESHAPE
+    assert call(M=32769, k=3) == nat.CAB_ESHAPE
     assert call(M=0) == nat.CAB_OK
     hyb = lambda **kw: lib.cab_block_topk_hybrid(FAKE, kw.get("mag", FAKE), 1, 1, 64, 3,
                                                  kw.get("kmag", 1), 1, 1, 0, FAKE, FAKE, None, None)

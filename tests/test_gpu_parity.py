@@ -337,6 +337,34 @@ def test_topk_hybrid_bit_exact(cuda, M, ratio, flags):
     assert torch.equal(m2.cpu(), torch.from_numpy(omask))
 
 
+@pytest.mark.parametrize("flags", [(False, True, False), (True, False, True)])
+def test_topk_long_rows(cuda, flags):
+    """M > 8192 takes the streaming kernel (the row re-read on every pass):
+    ties, an all-ties head, and the hybrid quota, bit-exact."""
+    from cab_attention.kernels import generate_block_index
+    select_high, keep_diag, causal = flags
+    M = 8200
+    g = torch.Generator().manual_seed(8200)
+    f = torch.randint(-20, 20, (1, 2, M, M), generator=g).float()
+    f[0, 1] = 3.5
+    mag = torch.randint(0, 10, (1, 2, M, M), generator=g).float()
+    omask, oidx, ocnt = O.generate_block_mask(f.numpy(), 0.95, select_high, keep_diag, causal)
+    idx, cnt, mask = generate_block_index(f.to(cuda), 0.95, select_high=select_high,
+                                          keep_diagonal=keep_diag, causal=causal, dense=True)
+    np.testing.assert_array_equal(cnt.cpu().numpy(), ocnt)
+    np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
+    np.testing.assert_array_equal(mask.cpu().numpy(), omask)
+    del omask, mask
+    omask, oidx, ocnt = O.generate_block_mask(f.numpy(), 0.95, select_high, keep_diag, causal,
+                                              magnitude_scores=mag.numpy(), magnitude_ratio=0.5)
+    idx, cnt, mask = generate_block_index(f.to(cuda), 0.95, select_high=select_high,
+                                          keep_diagonal=keep_diag, causal=causal, dense=True,
+                                          magnitude_scores=mag.to(cuda), magnitude_ratio=0.5)
+    np.testing.assert_array_equal(cnt.cpu().numpy(), ocnt)
+    np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
+    np.testing.assert_array_equal(mask.cpu().numpy(), omask)
+
+
 def test_topk_nan_inf(cuda):
     from cab_attention.kernels import generate_block_index
     f = torch.tensor([[[[0.0, float("nan"), -float("inf"), float("inf"), -0.0, 1.0]] * 6]])
