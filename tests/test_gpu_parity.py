@@ -228,6 +228,23 @@ def test_frc_fused_additive_wide_tile(cuda):
     assert_frc_close(f, of, oa, ot, 0.5)
 
 
+def test_frc_and_selection_beyond_8192(cuda):
+    """M = 8200 (above the register top-k): the fused FRC scores within the
+    term-magnitude bound, then the streaming selection on those scores
+    bit-exact against the oracle's selection of the same scores."""
+    from cab_attention.kernels import compute_block_frc, generate_block_index
+    qc = seeded((1, 1, 8200, 128), 31, torch.bfloat16)
+    kc = seeded((1, 1, 8200, 128), 32, torch.bfloat16)
+    f, _, _ = compute_block_frc(qc.to(cuda), kc.to(cuda), diagnostics=False)
+    of, oa, ot = O.compute_block_frc(np32(qc), np32(kc))
+    assert_frc_close(f, of, oa, ot, 0.5)
+    del of, oa, ot
+    idx, cnt, _ = generate_block_index(f, 0.95, keep_diagonal=True, causal=True)
+    _, oidx, ocnt = O.generate_block_mask(np32(f), 0.95, False, True, True)
+    np.testing.assert_array_equal(cnt.cpu().numpy(), ocnt)
+    np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
+
+
 def test_frc_fused_constant_affinity(cuda):
     """min == max on the fused path: F = c - lambda M c^2 without the planes."""
     from cab_attention.kernels import compute_block_frc
