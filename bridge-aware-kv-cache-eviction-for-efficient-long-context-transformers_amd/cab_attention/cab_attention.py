@@ -14,16 +14,18 @@ import torch
 from torch import nn
 
 from .coarse_predictor import CoarseCurvaturePredictor
-from .kernels.sparse_attention import block_sparse_attention
+from .kernels.sparse_attention import (SUPPORTED_BLOCK_SIZES, SUPPORTED_HEAD_DIMS,
+                                       block_sparse_attention)
 
 
 class CABAttention(nn.Module):
     """Curvature-aware block-sparse multi-head self-attention.
 
     Args:
-        dim: model width; ``dim % num_heads == 0``.
+        dim: model width; ``dim % num_heads == 0`` and ``dim / num_heads``
+            (the head dim) 64 or 128.
         num_heads: attention heads.
-        block_size: tokens per block (predictor and executor).
+        block_size: tokens per block (predictor and executor); 64.
         sparsity: fraction of key blocks pruned per query block.
         lambda_redundancy: FRC redundancy weight.
         causal: token-causal attention (the predictor keeps only j <= i).
@@ -37,6 +39,13 @@ class CABAttention(nn.Module):
         super().__init__()
         if dim % num_heads:
             raise ValueError(f"dim={dim} is not divisible by num_heads={num_heads}")
+        if dim // num_heads not in SUPPORTED_HEAD_DIMS:
+            raise ValueError(f"head_dim = dim / num_heads = {dim // num_heads} is not supported by "
+                             f"the block-sparse executor (head_dim in {SUPPORTED_HEAD_DIMS})")
+        if int(block_size) not in SUPPORTED_BLOCK_SIZES:
+            raise ValueError(f"block_size={block_size} is not supported by the block-sparse "
+                             f"executor (block_size in {SUPPORTED_BLOCK_SIZES}); "
+                             "CoarseCurvaturePredictor alone accepts any block size")
         self.dim = dim
         self.num_heads = num_heads
         self.head_dim = dim // num_heads

@@ -1,6 +1,7 @@
-"""One-launch pruning of every layer's K and V to the kept positions
-(``cab_kv_gather``), replacing the reference caches' per-layer
-``cache[:, :, keep_indices, :]`` (cab_cache.py:207-210, h2o_cache.py:146-149)."""
+"""Row gathers over cache tensors through ``cab_kv_gather``: every layer's K
+and V pruned to the kept positions in one launch per 32 tensors, in place of
+the per-layer ``cache[:, :, keep_indices, :]`` of the reference caches
+(cab_cache.py:207-210, h2o_cache.py:146-149)."""
 
 from __future__ import annotations
 
@@ -11,11 +12,56 @@ import torch
 
 from .. import _native as nat
 
+MAX_TENSORS_PER_LAUNCH = 32
+
+
+def _rows_aligned(t: torch.Tensor) -> bool:
+    es = t.element_size()
+    return (t.stride(3) == 1 and t.data_ptr() % 16 == 0 and (t.shape[3] * es) % 16 == 0
+            and all((s * es) % 16 == 0 for s in t.stride()[:3]))
+
+
+def gather_into(srcs: Sequence[torch.Tensor], dsts: Sequence[torch.Tensor],
+                keep_indices: torch.Tensor, n_src: int) -> None:
+    """``dst[:, :, t, :] = src[:, :, keep[t], :]`` for pairs of ``[B, H, *, D]``
+    views that share B, H, D, dtype and one stride set per side (rows 16-byte
+    aligned). ``keep`` is int64 on the tensors' device; positions outside
+    ``[0, n_src)`` give zero rows."""
+    srcs, dsts = list(srcs), list(dsts)
+    if not srcs:
+        return
+    ref = srcs[0]
+    B, H, _, D = ref.shape
+    n_keep = keep_indices.numel()
+    if n_keep == 0 or B == 0 or H == 0:
+        return
+    es = ref.element_size()
+    sstr, dstr = ref.stride(), dsts[0].stride()
+    for s, d in zip(srcs, dsts):
+        if (s.stride() != sstr or d.stride() != dstr or s.dtype != ref.dtype
+                or d.dtype != ref.dtype or s.shape[:2] != ref.shape[:2] or s.shape[3] != D
+                or d.shape[3] != D or d.shape[2] < n_keep
+                or not _rows_aligned(s) or not _rows_aligned(d)):
+            raise ValueError("gather_into: tensors must share shape, dtype, strides and 16-byte rows")
+    dev = ref.device
+    ss = (ctypes.c_int64 * 4)(sstr[0] * es, sstr[1] * es, sstr[2] * es, 0)
+    ds = (ctypes.c_int64 * 4)(dstr[0] * es, dstr[1] * es, dstr[2] * es, 0)
+    lib = nat.load()
+    with torch.cuda.device(dev):
+        for at in range(0, len(srcs), MAX_TENSORS_PER_LAUNCH):
+            part_s = srcs[at:at + MAX_TENSORS_PER_LAUNCH]
+            part_d = dsts[at:at + MAX_TENSORS_PER_LAUNCH]
+            src_arr = (ctypes.c_void_p * len(part_s))(*[s.data_ptr() for s in part_s])
+            dst_arr = (ctypes.c_void_p * len(part_d))(*[d.data_ptr() for d in part_d])
+            st = lib.cab_kv_gather(src_arr, dst_arr, len(part_s), B, H, n_src, D * es, ss, ds,
+                                   keep_indices.data_ptr(), n_keep, nat.stream_ptr(dev))
+            nat.check("cab_kv_gather", st)
+
 
 def gather_positions(tensors: Sequence[torch.Tensor], keep_indices: torch.Tensor) -> List[torch.Tensor]:
     """``[t[:, :, keep_indices, :] for t in tensors]`` for ``[B, H, N, D]``
-    tensors of one shape and dtype, written by one kernel per 32 tensors.
-    Positions outside [0, N) give zero rows."""
+    tensors of one shape and dtype, into new contiguous tensors. Positions
+    outside ``[0, N)`` give zero rows."""
     tensors = list(tensors)
     if not tensors:
         return []
@@ -27,45 +73,26 @@ def gather_positions(tensors: Sequence[torch.Tensor], keep_indices: torch.Tensor
             raise ValueError("all cache tensors must share one shape and dtype")
     dev = nat.require_device(*tensors, keep_indices)
     B, H, N, D = ref.shape
+    if (D * ref.element_size()) % 16 != 0:
+        raise ValueError("cab_kv_gather moves whole 16-byte row chunks: D * element size "
+                         f"must be a multiple of 16 (got {D} x {ref.element_size()})")
     idx = keep_indices.detach().reshape(-1).to(torch.int64).contiguous()
-    n_keep = idx.numel()
-    row_bytes = D * ref.element_size()
-    srcs = []
-    for t in tensors:
-        ok = (t.stride(3) == 1 and t.data_ptr() % 16 == 0 and row_bytes % 16 == 0
-              and all((s * t.element_size()) % 16 == 0 for s in t.stride()[:3]))
-        srcs.append(t if ok else t.contiguous())
-    outs = [torch.empty((B, H, n_keep, D), dtype=ref.dtype, device=dev) for _ in tensors]
-    if n_keep == 0 or B == 0 or H == 0:
-        return outs
-    es = ref.element_size()
-    sstr = srcs[0].stride()
-    if any(s.stride() != sstr for s in srcs):
+    srcs = [t if _rows_aligned(t) else t.contiguous() for t in tensors]
+    if any(s.stride() != srcs[0].stride() for s in srcs):
         srcs = [s.contiguous() for s in srcs]
-        sstr = srcs[0].stride()
-    src_arr = (ctypes.c_void_p * len(srcs))(*[s.data_ptr() for s in srcs])
-    dst_arr = (ctypes.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
-    ss = (ctypes.c_int64 * 4)(sstr[0] * es, sstr[1] * es, sstr[2] * es, 0)
-    ds_ = outs[0].stride()
-    ds = (ctypes.c_int64 * 4)(ds_[0] * es, ds_[1] * es, ds_[2] * es, 0)
-    lib = nat.load()
-    with torch.cuda.device(dev):
-        st = lib.cab_kv_gather(src_arr, dst_arr, len(srcs), B, H, N, row_bytes, ss, ds,
-                               idx.data_ptr(), n_keep, nat.stream_ptr(dev))
-    nat.check("cab_kv_gather", st)
+    outs = [torch.empty((B, H, idx.numel(), D), dtype=ref.dtype, device=dev) for _ in tensors]
+    gather_into(srcs, outs, idx, N)
     return outs
 
 
 def prune_layers(key_cache: list, value_cache: list, keep_indices: torch.Tensor):
-    """Prunes the non-None layers of both lists in place (new tensors)."""
-    layers = [i for i, k in enumerate(key_cache) if k is not None]
-    if not layers:
-        return
+    """Replaces the non-None entries of both per-layer lists by their rows at
+    ``keep_indices`` (new tensors; layers of one shape share launches)."""
     groups = {}
-    for i in layers:
-        k, v = key_cache[i], value_cache[i]
-        groups.setdefault((tuple(k.shape), k.dtype), []).append(i)
-    for (_, _), ids in groups.items():
+    for i, k in enumerate(key_cache):
+        if k is not None:
+            groups.setdefault((tuple(k.shape), k.dtype), []).append(i)
+    for ids in groups.values():
         outs = gather_positions([key_cache[i] for i in ids] + [value_cache[i] for i in ids],
                                 keep_indices)
         for n, i in enumerate(ids):

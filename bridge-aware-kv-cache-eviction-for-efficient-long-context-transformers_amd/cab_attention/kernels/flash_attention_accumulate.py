@@ -40,7 +40,7 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: fl
     """Dense attention ``softmax(q k^T * scale) v`` (``cab_flash_attn_fwd``).
 
     q: ``[B, H, N_q, D]``; k, v: ``[B, H_kv, N_k, D]`` with ``H % H_kv == 0``
-    (query head h reads K / V head ``h // (H // H_kv)``); D = 128; bf16, fp16
+    (query head h reads K / V head ``h // (H // H_kv)``); D = 64 or 128; bf16, fp16
     or fp32. ``causal`` lets query t see keys ``s <= t + N_k - N_q``. Returns
     the output ``[B, H, N_q, D]`` and, with ``return_lse``, the fp32
     natural-log log-sum-exp ``[B, H, N_q]``.
@@ -128,7 +128,7 @@ def flash_attention_with_cumulative_scores(
 
     Args:
         q: ``[B, H, N_q, D]``; k, v: ``[B, H_kv, N_k, D]`` (``H_kv`` divides
-            ``H``). bf16 or fp16, D = 128.
+            ``H``). bf16 or fp16, D = 64 or 128.
         cumulative_scores: optional fp32 ``[B, H, N_old]`` running totals. They
             are added to (not reset); when ``N_old < N_k`` they are first
             extended with zeros for the new key positions, as in the

@@ -15,6 +15,11 @@ import torch
 
 from .. import _native as nat
 
+# What the executor kernel is built for; anything else is rejected by the
+# C ABI (CAB_ESHAPE) rather than computed approximately.
+SUPPORTED_HEAD_DIMS = (64, 128)
+SUPPORTED_BLOCK_SIZES = (64,)
+
 
 def _check_lists(kv_idx, kv_cnt, B, H, M):
     if kv_idx.dim() != 4 or tuple(kv_idx.shape[:3]) != (B, H, M):
@@ -43,7 +48,7 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     """``out[t] = softmax_s(q_t . k_s * scale) v_s`` over the key blocks
     ``kv_idx[b, h, i, :kv_cnt[b, h, i]]`` of the query block i holding t.
 
-    q, k, v: ``[B, H, N, D]`` bf16, fp16 or fp32 (D = 128, block_size = 64;
+    q, k, v: ``[B, H, N, D]`` bf16, fp16 or fp32 (D = 64 or 128, block_size = 64;
     fp32 runs on split bf16 hi + lo operands, three MFMA products each); causal
     drops keys s > t; a query with no key gets 0; ``scale`` (> 0) defaults to
     ``1/sqrt(D)``. Index entries outside ``[0, M)`` are skipped. ``out`` may be

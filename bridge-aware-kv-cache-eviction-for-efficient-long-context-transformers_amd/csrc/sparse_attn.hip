@@ -1,5 +1,7 @@
-// Block-sparse attention forward (cab_block_sparse_attn_fwd), D = 128,
-// block_size = 64.
+// Block-sparse attention forward (cab_block_sparse_attn_fwd), head dim
+// D = 64 or 128 (a template parameter of every kernel below), block_size = 64.
+// The comments give the D = 128 sizes; D = 64 halves every per-block byte
+// count, the k-steps of S^T and the O^T tiles.
 //
 // Two kernels:
 //  1. pack_vt_kernel: V [B, H, N, D] -> V^T tiles in MFMA operand order
@@ -48,17 +50,35 @@ namespace cab {
 namespace {
 
 constexpr int BS = 64;                       // tokens per block
-constexpr int HD = 128;                      // head dim
-constexpr int TILE_SLOTS = 1024;             // 16-byte slots per packed V^T tile
-constexpr size_t TILE_BYTES = TILE_SLOTS * 16;
 constexpr float RESCALE_LOG2 = 8.0f;         // lazy rescale threshold (2^8)
 constexpr int LIST_MAX = 2048;               // kv lists up to this length are staged in LDS
-// fp32 block image: [K hi rows][K lo rows][V^T hi tile][V^T lo tile], 16 KB each.
-constexpr size_t SPLIT_BLOCK_BYTES = 4 * TILE_BYTES;
 
-// Bytes of packed data per (b, h, key block) for an input dtype.
-constexpr size_t block_bytes(cab_dtype_t dt) {
-  return dt == CAB_F32 ? SPLIT_BLOCK_BYTES : TILE_BYTES;
+// Sizes that follow from the head dim HD (64 or 128).
+template <int HD>
+struct Dims {
+  static_assert(HD == 64 || HD == 128, "head dim 64 or 128");
+  static constexpr int CPR = HD / 8;                // 16-byte chunks per 16-bit K row
+  static constexpr int ROW_BYTES = 2 * HD;          // one 16-bit K row
+  static constexpr int NDS = HD / 32;               // 32-deep k-steps of S^T = K Q^T
+  static constexpr int NDT = HD / 16;               // 16-row tiles of O^T
+  static constexpr int TILE_SLOTS = BS * HD / 8;    // 16-byte slots of a K block or V^T tile
+  static constexpr int TILE_BYTES = TILE_SLOTS * 16;
+  static constexpr int NI = TILE_BYTES / 4096;      // 1 KB staging loads per wave and tile
+  static constexpr int ROWS_PER_LOAD = 1024 / ROW_BYTES;  // K rows one 1 KB load covers
+  // Merge buffer of one query half: O^T partials, running maxima, row sums.
+  static constexpr int XCHG_FLOATS = NDT * 2 * 4 * 64 + 2 * 2 * 64;
+  // Chunk c of K row R sits at chunk position c ^ kswz(R): the 16 rows one
+  // operand read touches then fall into 16 distinct 16-byte bank groups
+  // (a 128-byte row pairs rows R, R + 1 in one 256-byte bank cycle).
+  __host__ __device__ static constexpr int kswz(int R) {
+    return HD == 128 ? (R & 15) : ((R >> 1) & 7);
+  }
+};
+
+// Bytes of packed data per (b, h, key block) for an input dtype: the V^T tile,
+// or for fp32 the block image [K hi rows][K lo rows][V^T hi][V^T lo].
+constexpr size_t block_bytes(cab_dtype_t dt, int hd) {
+  return static_cast<size_t>(dt == CAB_F32 ? 4 : 1) * BS * hd * 2;
 }
 
 struct AttnArgs {
@@ -124,12 +144,15 @@ __device__ __forceinline__ void split8(const f32x4& x0, const f32x4& x1, u32x4& 
   lo = u32x4{a[1], b[1], e[1], f[1]};
 }
 
-typedef uint16_t VRows[HD + 8];  // one block of V rows in LDS, padded
+// One block of V rows in LDS, padded.
+template <int HD>
+using VRows = uint16_t[HD + 8];
 
 // V^T tile slot (dt, s, L) (index (2 dt + s) * 64 + L) holds, for d = 16 dt + L % 16
 // and g = L / 16, the 8 values V[32 s + 4 g + r][d] (r = 0..3) followed by
 // V[32 s + 16 + 4 g + r][d] (r = 0..3).
-__device__ __forceinline__ u32x4 vt_slot(const VRows* vs, int slot) {
+template <int HD>
+__device__ __forceinline__ u32x4 vt_slot(const VRows<HD>* vs, int slot) {
   const int row = slot >> 6, L = slot & 63;
   const int dt = row >> 1, s = row & 1, g = L >> 4;
   const int d = 16 * dt + (L & 15);
@@ -145,30 +168,33 @@ __device__ __forceinline__ u32x4 vt_slot(const VRows* vs, int slot) {
   return x;
 }
 
-__device__ __forceinline__ void vrows_put(VRows* vs, int key, int c, const u32x4& x) {
+template <int HD>
+__device__ __forceinline__ void vrows_put(VRows<HD>* vs, int key, int c, const u32x4& x) {
   *reinterpret_cast<u32x2*>(&vs[key][8 * c]) = u32x2{x[0], x[1]};
   *reinterpret_cast<u32x2*>(&vs[key][8 * c + 4]) = u32x2{x[2], x[3]};
 }
 
+template <int HD>
 __global__ __launch_bounds__(256) void pack_vt_kernel(PackArgs a) {
-  __shared__ VRows vs[BS];
+  using G = Dims<HD>;
+  __shared__ VRows<HD> vs[BS];
   const int64_t bh = blockIdx.y, j = blockIdx.x;
   const int64_t b = bh / a.H, h = bh - (bh / a.H) * a.H;
   const uint16_t* vb = a.v + b * a.vs[0] + h * a.vs[1];
   const int tid = threadIdx.x;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int cid = tid + 256 * r;  // 1024 chunks of 8 values
-    const int key = cid >> 4, c = cid & 15;
+  for (int r = 0; r < G::TILE_SLOTS / 256; ++r) {
+    const int cid = tid + 256 * r;  // TILE_SLOTS chunks of 8 values
+    const int key = cid / G::CPR, c = cid % G::CPR;
     const int64_t t = j * BS + key;
     const u32x4 x = t < a.N ? *reinterpret_cast<const u32x4*>(vb + t * a.vs[2] + 8 * c)
                             : u32x4{0u, 0u, 0u, 0u};
-    vrows_put(vs, key, c, x);
+    vrows_put<HD>(vs, key, c, x);
   }
   __syncthreads();
-  u32x4* out = reinterpret_cast<u32x4*>(a.vt) + (bh * a.M + j) * TILE_SLOTS;
+  u32x4* out = reinterpret_cast<u32x4*>(a.vt) + (bh * a.M + j) * G::TILE_SLOTS;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) out[tid + 256 * r] = vt_slot(vs, tid + 256 * r);
+  for (int r = 0; r < G::TILE_SLOTS / 256; ++r) out[tid + 256 * r] = vt_slot<HD>(vs, tid + 256 * r);
 }
 
 struct SplitPackArgs {
@@ -179,12 +205,16 @@ struct SplitPackArgs {
   int64_t H, N, M;
 };
 
-// fp32 K and V of key block j -> its 64 KB block image (zero past N):
-//   K hi / K lo: 64 rows x 256 bytes, the 16-byte chunks of row R stored at
-//     position c ^ (R % 16) (the LDS layout the K operand reads expect);
+// fp32 K and V of key block j -> its block image (64 KB at D = 128; zero
+// past N):
+//   K hi / K lo: 64 rows x 2 D bytes, the 16-byte chunks of row R stored at
+//     position c ^ kswz(R) (the LDS layout the K operand reads expect);
 //   V^T hi / V^T lo: pack_vt_kernel's tile layout.
+template <int HD>
 __global__ __launch_bounds__(256) void pack_split_kernel(SplitPackArgs a) {
-  __shared__ VRows vh[BS], vl[BS];
+  using G = Dims<HD>;
+  constexpr int TILE_SLOTS = G::TILE_SLOTS;
+  __shared__ VRows<HD> vh[BS], vl[BS];
   const int64_t bh = blockIdx.y, j = blockIdx.x;
   const int64_t b = bh / a.H, h = bh - (bh / a.H) * a.H;
   const float* kb = a.k + b * a.ks[0] + h * a.ks[1];
@@ -193,9 +223,9 @@ __global__ __launch_bounds__(256) void pack_split_kernel(SplitPackArgs a) {
   u32x4* out = reinterpret_cast<u32x4*>(a.img) + (bh * a.M + j) * (4 * TILE_SLOTS);
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int cid = tid + 256 * r;  // 1024 chunks of 8 values
-    const int key = cid >> 4, c = cid & 15;
+  for (int r = 0; r < TILE_SLOTS / 256; ++r) {
+    const int cid = tid + 256 * r;  // TILE_SLOTS chunks of 8 values
+    const int key = cid / G::CPR, c = cid % G::CPR;
     const int64_t t = j * BS + key;
     const bool in = t < a.N;
     const float* kp = kb + t * a.ks[2] + 8 * c;
@@ -206,19 +236,19 @@ __global__ __launch_bounds__(256) void pack_split_kernel(SplitPackArgs a) {
     const f32x4 v1 = in ? *reinterpret_cast<const f32x4*>(vp + 4) : zero;
     u32x4 hi, lo;
     split8(k0, k1, hi, lo);
-    const int pos = 16 * key + (c ^ (key & 15));
+    const int pos = G::CPR * key + (c ^ G::kswz(key));
     out[pos] = hi;
     out[TILE_SLOTS + pos] = lo;
     split8(v0, v1, hi, lo);
-    vrows_put(vh, key, c, hi);
-    vrows_put(vl, key, c, lo);
+    vrows_put<HD>(vh, key, c, hi);
+    vrows_put<HD>(vl, key, c, lo);
   }
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
+  for (int r = 0; r < TILE_SLOTS / 256; ++r) {
     const int slot = tid + 256 * r;
-    out[2 * TILE_SLOTS + slot] = vt_slot(vh, slot);
-    out[3 * TILE_SLOTS + slot] = vt_slot(vl, slot);
+    out[2 * TILE_SLOTS + slot] = vt_slot<HD>(vh, slot);
+    out[3 * TILE_SLOTS + slot] = vt_slot<HD>(vl, slot);
   }
 }
 
@@ -269,48 +299,54 @@ constexpr float M_EMPTY = -1.0e30f;
 
 // Online-softmax state of one wave: 32 queries (two tiles of 16, query on
 // the lane axis) against one key half of every kept block.
+template <int HD>
 struct WaveAcc {
-  u32x4 qreg[2][4];  // Q^T B operand: qreg[qt][ds] = Q[q0 + 16 qt + l % 16][32 ds + 8 g .. +8]
-  u32x4 qlo[2][4];   // fp32 inputs: the lo halves of qreg (unused otherwise)
-  f32x4 oacc[8][2];  // O^T[16 dt + 4 g + r][q0 + 16 qt + l % 16]
-  f32x4 lacc[2];     // row sums (all four r equal)
-  float m_run[2];    // running maximum of the raw scores
-  float nmc[2];      // -m_run * c
+  static constexpr int NDS = Dims<HD>::NDS, NDT = Dims<HD>::NDT;
+  u32x4 qreg[2][NDS];  // Q^T B operand: qreg[qt][ds] = Q[q0 + 16 qt + l % 16][32 ds + 8 g .. +8]
+  u32x4 qlo[2][NDS];   // fp32 inputs: the lo halves of qreg (unused otherwise)
+  f32x4 oacc[NDT][2];  // O^T[16 dt + 4 g + r][q0 + 16 qt + l % 16]
+  f32x4 lacc[2];       // row sums (all four r equal)
+  float m_run[2];      // running maximum of the raw scores
+  float nmc[2];        // -m_run * c
 };
 
 // A wave's place in its group of four: key half kh, query half qh.
+template <int HD>
 struct WaveGeo {
   int kh, qh, lane, g, l16;
-  uint32_t kread[4];  // K operand byte offsets inside a K stage
+  uint32_t kread[Dims<HD>::NDS];  // K operand byte offsets inside a K stage
 };
 
-__device__ __forceinline__ WaveGeo wave_geo(int w4) {
-  WaveGeo ge;
+template <int HD>
+__device__ __forceinline__ WaveGeo<HD> wave_geo(int w4) {
+  using G = Dims<HD>;
+  WaveGeo<HD> ge;
   ge.kh = w4 & 1;
   ge.qh = (w4 >> 1) & 1;
   ge.lane = lane_id();
   ge.g = ge.lane >> 4;
   ge.l16 = ge.lane & 15;
   // K operand (key 32 kh + 16 tt + l % 16, dims 32 ds + 8 g .. +8) inside a
-  // stage: row R = 32 kh + 16 tt + l % 16 (R % 16 = l % 16), chunk 4 ds + g,
-  // stored XOR-swizzled at chunk position (4 ds + g) ^ (R % 16).
+  // stage: row R = 32 kh + 16 tt + l % 16, chunk 4 ds + g, stored
+  // XOR-swizzled at chunk position (4 ds + g) ^ kswz(R); kswz(R) depends on
+  // l % 16 only, so tt adds a fixed 16 rows (the caller's offset).
 #pragma unroll
-  for (int ds = 0; ds < 4; ++ds)
-    ge.kread[ds] = 256 * (32 * ge.kh + ge.l16) + 16 * ((4 * ds + ge.g) ^ ge.l16);
+  for (int ds = 0; ds < G::NDS; ++ds)
+    ge.kread[ds] = G::ROW_BYTES * (32 * ge.kh + ge.l16) + 16 * ((4 * ds + ge.g) ^ G::kswz(ge.l16));
   return ge;
 }
 
 // Loads the wave's 32 queries (from token q0; rows at or past N are zero;
 // fp32 queries split into qreg / qlo) and clears the accumulators.
-template <cab_dtype_t DT>
-__device__ __forceinline__ void acc_init(WaveAcc& s, const WaveGeo& ge, const void* qv,
+template <cab_dtype_t DT, int HD>
+__device__ __forceinline__ void acc_init(WaveAcc<HD>& s, const WaveGeo<HD>& ge, const void* qv,
                                          int64_t qs2, int q0, int N, float c) {
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     const int qtok = q0 + 16 * qt + ge.l16;
     const bool in = q0 >= 0 && qtok < N;
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds) {
+    for (int ds = 0; ds < Dims<HD>::NDS; ++ds) {
       if constexpr (DT == CAB_F32) {
         const float* qp = static_cast<const float*>(qv) + qtok * qs2 + 32 * ds + 8 * ge.g;
         const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -324,7 +360,7 @@ __device__ __forceinline__ void acc_init(WaveAcc& s, const WaveGeo& ge, const vo
     }
     s.lacc[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) s.oacc[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < Dims<HD>::NDT; ++dt) s.oacc[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
     s.m_run[qt] = M_EMPTY;
     s.nmc[qt] = -M_EMPTY * c;
   }
@@ -332,13 +368,15 @@ __device__ __forceinline__ void acc_init(WaveAcc& s, const WaveGeo& ge, const vo
 
 // Marks the queries as loaded: later waits in the block loop then never
 // have to cover the Q loads.
-template <cab_dtype_t DT>
-__device__ __forceinline__ void acc_q_ready(WaveAcc& s) {
-  asm volatile("" ::"v"(s.qreg[0][0]), "v"(s.qreg[0][1]), "v"(s.qreg[0][2]), "v"(s.qreg[0][3]),
-               "v"(s.qreg[1][0]), "v"(s.qreg[1][1]), "v"(s.qreg[1][2]), "v"(s.qreg[1][3]));
-  if constexpr (DT == CAB_F32)
-    asm volatile("" ::"v"(s.qlo[0][0]), "v"(s.qlo[0][1]), "v"(s.qlo[0][2]), "v"(s.qlo[0][3]),
-                 "v"(s.qlo[1][0]), "v"(s.qlo[1][1]), "v"(s.qlo[1][2]), "v"(s.qlo[1][3]));
+template <cab_dtype_t DT, int HD>
+__device__ __forceinline__ void acc_q_ready(WaveAcc<HD>& s) {
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int ds = 0; ds < Dims<HD>::NDS; ++ds) {
+      asm volatile("" ::"v"(s.qreg[qt][ds]));
+      if constexpr (DT == CAB_F32) asm volatile("" ::"v"(s.qlo[qt][ds]));
+    }
 }
 
 // Whether key block j needs per-key masks for query block i: an invalid
@@ -354,28 +392,32 @@ __device__ __forceinline__ bool block_needs_mask(int j, int i, bool valid, int N
 // fp32 (split operands, the lo halves 16 KB past the hi ones in LDS):
 // 48 + 48 + 4 MFMA. Keys at or past Nk and (causal) keys after t + qoff for
 // query t are dropped.
-template <cab_dtype_t DT>
-__device__ __forceinline__ void acc_block(WaveAcc& s, const WaveGeo& ge, const char* ks,
+template <cab_dtype_t DT, int HD>
+__device__ __forceinline__ void acc_block(WaveAcc<HD>& s, const WaveGeo<HD>& ge, const char* ks,
                                           const u32x4* vts, int j, int i, bool valid, int Nk,
                                           bool causal, int qoff, float c) {
+  using G = Dims<HD>;
+  constexpr int NDS = G::NDS, NDT = G::NDT;
+  constexpr int TT_BYTES = 16 * G::ROW_BYTES;  // 16 K rows
   constexpr bool BF16 = DT != CAB_F16;
   constexpr bool SPLIT = DT == CAB_F32;
   const uint32_t one2 = BF16 ? 0x3f803f80u : 0x3c003c00u;
   const u32x4 ones = {one2, one2, one2, one2};
-  u32x4 kop[4][2], vop[8];
-  u32x4 klo[4][2], vlo[8];  // SPLIT only
+  u32x4 kop[NDS][2], vop[NDT];
+  u32x4 klo[NDS][2], vlo[NDT];  // SPLIT only
 #pragma unroll
-  for (int ds = 0; ds < 4; ++ds)
+  for (int ds = 0; ds < NDS; ++ds)
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      kop[ds][tt] = *reinterpret_cast<const u32x4*>(ks + ge.kread[ds] + 4096 * tt);
+      kop[ds][tt] = *reinterpret_cast<const u32x4*>(ks + ge.kread[ds] + TT_BYTES * tt);
       if constexpr (SPLIT)
-        klo[ds][tt] = *reinterpret_cast<const u32x4*>(ks + TILE_BYTES + ge.kread[ds] + 4096 * tt);
+        klo[ds][tt] =
+            *reinterpret_cast<const u32x4*>(ks + G::TILE_BYTES + ge.kread[ds] + TT_BYTES * tt);
     }
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) {
+  for (int dt = 0; dt < NDT; ++dt) {
     vop[dt] = vts[(dt * 2 + ge.kh) * 64 + ge.lane];
-    if constexpr (SPLIT) vlo[dt] = vts[TILE_SLOTS + (dt * 2 + ge.kh) * 64 + ge.lane];
+    if constexpr (SPLIT) vlo[dt] = vts[G::TILE_SLOTS + (dt * 2 + ge.kh) * 64 + ge.lane];
   }
 
   // sc[tt][qt][r] = score(key 32 kh + 16 tt + 4 g + r, query 32 qh + 16 qt + l % 16)
@@ -385,7 +427,7 @@ __device__ __forceinline__ void acc_block(WaveAcc& s, const WaveGeo& ge, const c
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) sc[tt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int ds = 0; ds < 4; ++ds)
+  for (int ds = 0; ds < NDS; ++ds)
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -431,7 +473,7 @@ __device__ __forceinline__ void acc_block(WaveAcc& s, const WaveGeo& ge, const c
       const float alpha = __builtin_amdgcn_exp2f((s.m_run[qt] - m_new) * c);
       s.lacc[qt] *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) s.oacc[dt][qt] *= alpha;
+      for (int dt = 0; dt < NDT; ++dt) s.oacc[dt][qt] *= alpha;
       s.m_run[qt] = m_new;
       s.nmc[qt] = -m_new * c;
     }
@@ -457,7 +499,7 @@ __device__ __forceinline__ void acc_block(WaveAcc& s, const WaveGeo& ge, const c
     }
   }
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
+  for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
       if constexpr (SPLIT) {
@@ -475,29 +517,30 @@ __device__ __forceinline__ void acc_block(WaveAcc& s, const WaveGeo& ge, const c
 
 // Merge of the two key halves of a query half through LDS: the kh = 1 wave
 // exports (acc_export), and after a workgroup barrier the kh = 0 wave
-// combines and writes out, lse (acc_store).
-constexpr int XCHG_FLOATS = 8 * 2 * 4 * 64 + 2 * 2 * 64;  // per query half
-
-__device__ __forceinline__ void acc_export(const WaveAcc& s, const WaveGeo& ge, float* xo) {
-  float* xm = xo + 8 * 2 * 4 * 64;
+// combines and writes out, lse (acc_store). Dims<HD>::XCHG_FLOATS per query half.
+template <int HD>
+__device__ __forceinline__ void acc_export(const WaveAcc<HD>& s, const WaveGeo<HD>& ge, float* xo) {
+  constexpr int NDT = Dims<HD>::NDT;
+  float* xm = xo + NDT * 2 * 4 * 64;
   float* xl = xm + 2 * 64;
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     xm[qt * 64 + ge.lane] = s.m_run[qt];
     xl[qt * 64 + ge.lane] = s.lacc[qt][0];
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) xo[((dt * 2 + qt) * 4 + r) * 64 + ge.lane] = s.oacc[dt][qt][r];
   }
 }
 
-template <cab_dtype_t DT>
-__device__ __forceinline__ void acc_store(const WaveAcc& s, const WaveGeo& ge, const float* xo,
-                                          void* obase, int64_t os2, float* lse_row, int q0,
-                                          int N, float c) {
+template <cab_dtype_t DT, int HD>
+__device__ __forceinline__ void acc_store(const WaveAcc<HD>& s, const WaveGeo<HD>& ge,
+                                          const float* xo, void* obase, int64_t os2,
+                                          float* lse_row, int q0, int N, float c) {
   constexpr bool BF16 = DT != CAB_F16;
-  const float* xm = xo + 8 * 2 * 4 * 64;
+  constexpr int NDT = Dims<HD>::NDT;
+  const float* xm = xo + NDT * 2 * 4 * 64;
   const float* xl = xm + 2 * 64;
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
@@ -510,7 +553,7 @@ __device__ __forceinline__ void acc_store(const WaveAcc& s, const WaveGeo& ge, c
     const int qtok = q0 + 16 * qt + ge.l16;
     if (qtok < N) {
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
+      for (int dt = 0; dt < NDT; ++dt) {
         float o[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -530,22 +573,27 @@ __device__ __forceinline__ void acc_store(const WaveAcc& s, const WaveGeo& ge, c
   }
 }
 
-// K staging offsets. K lands row-major, 64 rows x 256 bytes, the 16-byte
-// chunks of row R XOR-swizzled (chunk c at position c ^ (R % 16)) so that the
-// operand reads are bank-conflict free; one instruction fetches four whole
-// rows (full 128-byte lines): lane L takes row 4 x + L / 16 (x = the
-// instruction's 4-row group), stored chunk L % 16.
-__device__ __forceinline__ uint32_t k_lane_off(int group4, int lane, int64_t krow_bytes) {
-  const int row = 4 * group4 + (lane >> 4);
-  return static_cast<uint32_t>(row * krow_bytes + 16 * ((lane & 15) ^ (row & 15)));
+// K staging offsets. K lands row-major, 64 rows x 2 D bytes, the 16-byte
+// chunks of row R XOR-swizzled (chunk c at position c ^ kswz(R)) so that the
+// operand reads are bank-conflict free; one instruction fetches 1 KB of
+// whole rows (4 rows at D = 128, 8 at D = 64; full 128-byte lines): lane L
+// takes row RPL x + L / CPR (x = the instruction's row group), chunk
+// position L % CPR, i.e. source chunk (L % CPR) ^ kswz(row).
+template <int HD>
+__device__ __forceinline__ uint32_t k_lane_off(int group, int lane, int64_t krow_bytes) {
+  using G = Dims<HD>;
+  const int row = G::ROWS_PER_LOAD * group + lane / G::CPR;
+  return static_cast<uint32_t>(row * krow_bytes + 16 * ((lane % G::CPR) ^ G::kswz(row)));
 }
 
-__device__ __forceinline__ const char* k_lane_ptr_clamped(const char* kbytes, int j, int group4,
+template <int HD>
+__device__ __forceinline__ const char* k_lane_ptr_clamped(const char* kbytes, int j, int group,
                                                           int lane, int N, int64_t krow_bytes) {
-  const int rr = 4 * group4 + (lane >> 4);
+  using G = Dims<HD>;
+  const int rr = G::ROWS_PER_LOAD * group + lane / G::CPR;
   const int row = j * BS + rr;
   const int64_t rb = (row < N ? row : N - 1) * krow_bytes;
-  return kbytes + rb + 16 * ((lane & 15) ^ (rr & 15));
+  return kbytes + rb + 16 * ((lane % G::CPR) ^ G::kswz(rr));
 }
 
 // ---------------------------------------------------------------------------
@@ -558,11 +606,15 @@ __device__ __forceinline__ const char* k_lane_ptr_clamped(const char* kbytes, in
 // up to the causal limit, in order).
 constexpr int LIST_LDS = 0, LIST_GLOBAL = 1, LIST_DENSE = 2;
 
-template <cab_dtype_t DT, int LIST>
+template <cab_dtype_t DT, int LIST, int HD>
 __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(AttnArgs a) {
+  using G = Dims<HD>;
   constexpr bool SPLIT = DT == CAB_F32;
+  constexpr int TILE_SLOTS = G::TILE_SLOTS;
+  constexpr int TILE_BYTES = G::TILE_BYTES;
+  constexpr int NI = G::NI;
   constexpr int STAGE_SLOTS = (SPLIT ? 4 : 2) * TILE_SLOTS;
-  constexpr int64_t BLOCK_BYTES = static_cast<int64_t>(block_bytes(DT));
+  constexpr int64_t BLOCK_BYTES = static_cast<int64_t>(block_bytes(DT, HD));
   // One LDS object: [stage 0][stage 1][list], a stage being [K][V^T] or
   // [K hi][K lo][V^T hi][V^T lo]; the merge at the end reuses the stages.
   __shared__ u32x4 smem[2 * STAGE_SLOTS + LIST_MAX / 4];
@@ -578,7 +630,7 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
   const int hk = hh / a.group;                        // K / V head
   const int64_t bhk = static_cast<int64_t>(b) * (a.H / a.group) + hk;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-  const WaveGeo ge = wave_geo(w);
+  const WaveGeo<HD> ge = wave_geo<HD>(w);
   const float c = a.scale_log2;
 
   const void* qb = SPLIT ? static_cast<const void*>(static_cast<const float*>(a.q) + b * a.qs[0] +
@@ -613,21 +665,22 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
       return p;
   };
 
-  // Staging of key block j by the 4 waves: wave w fetches K rows 16 w .. +15
-  // (4 instructions) and V^T slot rows 4 w .. 4 w + 3 (1 KB each). fp32: the
-  // block image is a copy of the stage; wave w copies its 16 KB quarter w.
+  // Staging of key block j by the 4 waves: wave w fetches its NI KB of K
+  // rows (rows 16 w .. +15 at D = 128) and of the V^T tile, one 1 KB load
+  // each. fp32: the block image is a copy of the stage; wave w copies its
+  // quarter w (one tile's bytes).
   const int64_t krow_bytes = a.ks[2] * 2;
   const int64_t kblk_bytes = BS * krow_bytes;
-  uint32_t koff[4];
+  uint32_t koff[NI];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) koff[r] = k_lane_off(4 * w + r, ge.lane, krow_bytes);
-  const int voff = w * 4096 + 16 * ge.lane;
+  for (int r = 0; r < NI; ++r) koff[r] = k_lane_off<HD>(NI * w + r, ge.lane, krow_bytes);
+  const int voff = w * NI * 1024 + 16 * ge.lane;
   auto stage = [&](int j, u32x4* kst, u32x4* vst) {
     if constexpr (SPLIT) {
       const char* gp = vtbytes + j * BLOCK_BYTES + w * TILE_BYTES + 16 * ge.lane;
       char* lp = reinterpret_cast<char*>(kst) + w * TILE_BYTES;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
+      for (int r = 0; r < TILE_BYTES / 4096; ++r) {
         dma16<0>(gp + 4096 * r, lp + 4096 * r);
         dma16<1024>(gp + 4096 * r, lp + 4096 * r);
         dma16<2048>(gp + 4096 * r, lp + 4096 * r);
@@ -635,35 +688,35 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
       }
       return;
     }
-    char* kl = reinterpret_cast<char*>(kst) + w * 4096;
+    char* kl = reinterpret_cast<char*>(kst) + w * NI * 1024;
     if ((j + 1) * BS <= Nk) {
       const char* kbj = kbytes + j * kblk_bytes;
-      dma16<0>(kbj + koff[0], kl);
-      dma16<0>(kbj + koff[1], kl + 1024);
-      dma16<0>(kbj + koff[2], kl + 2048);
-      dma16<0>(kbj + koff[3], kl + 3072);
+#pragma unroll
+      for (int r = 0; r < NI; ++r) dma16<0>(kbj + koff[r], kl + 1024 * r);
     } else {
-      dma16<0>(k_lane_ptr_clamped(kbytes, j, 4 * w + 0, ge.lane, Nk, krow_bytes), kl);
-      dma16<0>(k_lane_ptr_clamped(kbytes, j, 4 * w + 1, ge.lane, Nk, krow_bytes), kl + 1024);
-      dma16<0>(k_lane_ptr_clamped(kbytes, j, 4 * w + 2, ge.lane, Nk, krow_bytes), kl + 2048);
-      dma16<0>(k_lane_ptr_clamped(kbytes, j, 4 * w + 3, ge.lane, Nk, krow_bytes), kl + 3072);
+#pragma unroll
+      for (int r = 0; r < NI; ++r)
+        dma16<0>(k_lane_ptr_clamped<HD>(kbytes, j, NI * w + r, ge.lane, Nk, krow_bytes),
+                 kl + 1024 * r);
     }
     const char* vp = vtbytes + static_cast<int64_t>(j) * TILE_BYTES + voff;
-    char* vl = reinterpret_cast<char*>(vst) + w * 4096;
+    char* vl = reinterpret_cast<char*>(vst) + w * NI * 1024;
     dma16<0>(vp, vl);
     dma16<1024>(vp, vl);
-    dma16<2048>(vp, vl);
-    dma16<3072>(vp, vl);
+    if constexpr (NI == 4) {
+      dma16<2048>(vp, vl);
+      dma16<3072>(vp, vl);
+    }
   };
 
-  WaveAcc st;
-  acc_init<DT>(st, ge, qb, a.qs[2], i * BS + 32 * ge.qh, N, c);
+  WaveAcc<HD> st;
+  acc_init<DT, HD>(st, ge, qb, a.qs[2], i * BS + 32 * ge.qh, N, c);
 
   if (cnt > 0) {
     int jraw = entry(0);
     auto block_of = [&](int j) { return (j >= 0 && j < Mk) ? j : 0; };
     stage(block_of(jraw), stage_k(0), stage_v(0));
-    acc_q_ready<DT>(st);
+    acc_q_ready<DT, HD>(st);
 
     // Block p lives in LDS stage PAR = p % 2 (compile time, so the compiler
     // sees the staging of block p + 1 into the other stage cannot alias).
@@ -678,8 +731,8 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
         jnext = entry(p + 1);
         stage(block_of(jnext), stage_k(PAR ^ 1), stage_v(PAR ^ 1));
       }
-      acc_block<DT>(st, ge, reinterpret_cast<const char*>(stage_k(PAR)), stage_v(PAR), j, i,
-                    valid, Nk, a.causal, a.qoff, c);
+      acc_block<DT, HD>(st, ge, reinterpret_cast<const char*>(stage_k(PAR)), stage_v(PAR), j,
+                        i, valid, Nk, a.causal, a.qoff, c);
       jraw = jnext;
     };
     for (int p = 0; p < cnt; p += 2) {
@@ -689,13 +742,14 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
   }
 
   __syncthreads();
-  float* xo = reinterpret_cast<float*>(smem) + ge.qh * XCHG_FLOATS;
-  if (ge.kh == 1) acc_export(st, ge, xo);
+  static_assert(2 * G::XCHG_FLOATS * 4 <= 2 * STAGE_SLOTS * 16, "merge buffer fits the stages");
+  float* xo = reinterpret_cast<float*>(smem) + ge.qh * G::XCHG_FLOATS;
+  if (ge.kh == 1) acc_export<HD>(st, ge, xo);
   __syncthreads();
   void* ob = SPLIT ? static_cast<void*>(static_cast<float*>(a.o) + b * a.os[0] + hh * a.os[1])
                    : static_cast<void*>(static_cast<uint16_t*>(a.o) + b * a.os[0] + hh * a.os[1]);
   if (ge.kh == 0)
-    acc_store<DT>(st, ge, xo, ob, a.os[2],
+    acc_store<DT, HD>(st, ge, xo, ob, a.os[2],
                     a.lse ? a.lse + static_cast<int64_t>(bh) * N : nullptr, i * BS + 32 * ge.qh,
                     N, c);
 }
@@ -729,10 +783,16 @@ struct KeyScoreArgs {
 
 constexpr int KS_STAGES = 4;
 constexpr int KS_WAVES = 4;  // key blocks (waves) sharing each staged query tile (8 measured slower)
-constexpr int KS_STAGE_BYTES = 4096 + 4 * 256;  // Q tile, then one 64-float lse copy per wave
 
-template <bool BF16, int NW>
+// One ring stage: the Q tile (16 queries x D, 32 D bytes), then one 64-float
+// lse copy per wave.
+template <int HD>
+constexpr int ks_stage_bytes() { return 32 * HD + 4 * 256; }
+
+template <bool BF16, int NW, int HD>
 __global__ __launch_bounds__(64 * NW) void key_score_kernel(KeyScoreArgs a) {
+  constexpr int NDS = Dims<HD>::NDS;
+  constexpr int KS_STAGE_BYTES = ks_stage_bytes<HD>();
   __shared__ __attribute__((aligned(16))) char ring[KS_STAGES * KS_STAGE_BYTES];
   const int logical = static_cast<int>(xcd_remap(blockIdx.x, static_cast<int64_t>(a.BH) * a.Mkg));
   const int bh = logical / a.Mkg;
@@ -750,12 +810,12 @@ __global__ __launch_bounds__(64 * NW) void key_score_kernel(KeyScoreArgs a) {
   const float* lb = a.lse + static_cast<int64_t>(bh) * a.Nq;
 
   // K^T operand: kop[kt][ds] = K[16 kt + l16][32 ds + 8 g .. +8] (zero past Nk).
-  u32x4 kop[4][4];
+  u32x4 kop[4][NDS];
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt) {
     const int key = j * BS + 16 * kt + l16;
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds)
+    for (int ds = 0; ds < NDS; ++ds)
       kop[kt][ds] = key < a.Nk ? *reinterpret_cast<const u32x4*>(kb + key * a.ks[2] + 32 * ds + 8 * g)
                                : u32x4{0u, 0u, 0u, 0u};
   }
@@ -773,19 +833,22 @@ __global__ __launch_bounds__(64 * NW) void key_score_kernel(KeyScoreArgs a) {
   // Tiles are walked from the last one down, so the workgroups of a head,
   // which start together, read the same tiles at about the same time (L2).
   auto tile_of = [&](int it) { return ntiles - 1 - it; };
-  // Staging of tile tile_of(it): wave w < 4 moves Q dims 32 w .. 32 w + 31
+  // Staging of tile tile_of(it): wave w < NDS moves Q dims 32 w .. 32 w + 31
   // of the tile's 16 queries (lane L: query L % 16, dims 32 w + 8 (L / 16)
-  // .. + 7, landing at 16 L: the A operand of MFMA k-step w) and lse copy w;
-  // waves 4 .. 7 (NW = 8) stage nothing and read lse copy w % 4.
+  // .. + 7, landing at 16 L: the A operand of MFMA k-step w); waves w < 4
+  // move lse copy w (one load per tile for waves NDS .. 3); waves 4 .. 7
+  // (NW = 8) stage nothing and read lse copy w % 4.
   const bool stager = w < 4;
+  const bool qstager = w < NDS;
   auto issue = [&](int it) {
     if (!stager) return;
     char* st = ring + (it % KS_STAGES) * KS_STAGE_BYTES;
     const int q = 16 * tile_of(it) + l16;
     const int qc = q < a.Nq ? q : a.Nq - 1;  // clamped, masked below
-    __builtin_amdgcn_global_load_lds(qb + qc * a.qs[2] + 32 * w + 8 * g,
-                                     (lds_void*)(st + 1024 * w), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(lb + qc, (lds_void*)(st + 4096 + 256 * w), 4, 0, 0);
+    if (qstager)
+      __builtin_amdgcn_global_load_lds(qb + qc * a.qs[2] + 32 * w + 8 * g,
+                                       (lds_void*)(st + 1024 * w), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(lb + qc, (lds_void*)(st + 32 * HD + 256 * w), 4, 0, 0);
   };
 
   float colsum[4] = {0.f, 0.f, 0.f, 0.f};
@@ -796,21 +859,29 @@ __global__ __launch_bounds__(64 * NW) void key_score_kernel(KeyScoreArgs a) {
   auto step = [&](int it, auto stage_tag) {
     constexpr int S = decltype(stage_tag)::value;
     const int ahead = stager ? nt - 1 - it : 0;  // tiles it + 1, it + 2 may be in flight
-    if (ahead >= 2)
-      __builtin_amdgcn_s_waitcnt(0x0f74);  // vmcnt(4)
-    else if (ahead == 1)
-      __builtin_amdgcn_s_waitcnt(0x0f72);  // vmcnt(2)
-    else
+    // A Q stager has two loads per tile in flight, an lse-only stager one.
+    if (ahead >= 2) {
+      if (qstager)
+        __builtin_amdgcn_s_waitcnt(0x0f74);  // vmcnt(4)
+      else
+        __builtin_amdgcn_s_waitcnt(0x0f72);  // vmcnt(2)
+    } else if (ahead == 1) {
+      if (qstager)
+        __builtin_amdgcn_s_waitcnt(0x0f72);  // vmcnt(2)
+      else
+        __builtin_amdgcn_s_waitcnt(0x0f71);  // vmcnt(1)
+    } else {
       __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    }
     __builtin_amdgcn_s_barrier();  // every wave's part of tile it landed; stage (S + 3) % 4 is free
     if (it + KS_STAGES - 1 < nt) issue(it + KS_STAGES - 1);
     const int tile = tile_of(it);
     if (!has_keys || tile < my0) return;
     const char* st = ring + S * KS_STAGE_BYTES;
-    u32x4 qop[4];
+    u32x4 qop[NDS];
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds) qop[ds] = reinterpret_cast<const u32x4*>(st + 1024 * ds)[lane];
-    const f32x4 lv = reinterpret_cast<const f32x4*>(st + 4096 + 256 * (w & 3))[g];
+    for (int ds = 0; ds < NDS; ++ds) qop[ds] = reinterpret_cast<const u32x4*>(st + 1024 * ds)[lane];
+    const f32x4 lv = reinterpret_cast<const f32x4*>(st + 32 * HD + 256 * (w & 3))[g];
     float nl[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) nl[r] = -lv[r] * LOG2E;
@@ -819,7 +890,7 @@ __global__ __launch_bounds__(64 * NW) void key_score_kernel(KeyScoreArgs a) {
     for (int kt = 0; kt < 4; ++kt) {
       sc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ds = 0; ds < 4; ++ds) sc[kt] = mfma16<BF16>(qop[ds], kop[kt][ds], sc[kt]);
+      for (int ds = 0; ds < NDS; ++ds) sc[kt] = mfma16<BF16>(qop[ds], kop[kt][ds], sc[kt]);
     }
     // sc[kt][r]: query 16 tile + 4 g + r, key j BS + 16 kt + l16.
     const int t0 = 16 * tile + 4 * g;
@@ -881,7 +952,8 @@ cab_status_t check_common(const char* fn, cab_dtype_t dtype, int64_t B, int64_t 
                 "%s: dtype %d unsupported (bf16 or fp16; fp32 runs through "
                 "cab_block_sparse_attn_fwd)", fn, (int)dtype);
   CAB_REQUIRE(B >= 0 && H >= 0 && N >= 0, CAB_ESHAPE, "%s: negative size", fn);
-  CAB_REQUIRE(D == HD, CAB_ESHAPE, "%s: head dim %lld unsupported (128)", fn, (long long)D);
+  CAB_REQUIRE(D == 64 || D == 128, CAB_ESHAPE, "%s: head dim %lld unsupported (64 or 128)", fn,
+              (long long)D);
   CAB_REQUIRE(block_size == BS, CAB_ESHAPE, "%s: block_size %d unsupported (64)", fn,
               (int)block_size);
   const int64_t M = ceil_div(N, BS);
@@ -905,8 +977,8 @@ cab_status_t check_tensor(const char* fn, const char* name, const void* ptr,
 }
 
 cab_status_t check_packed(const char* fn, const void* vt, size_t bytes, int64_t B, int64_t H,
-                          int64_t M, cab_dtype_t dtype) {
-  const size_t need = static_cast<size_t>(B * H * M) * block_bytes(dtype);
+                          int64_t M, cab_dtype_t dtype, int64_t D) {
+  const size_t need = static_cast<size_t>(B * H * M) * block_bytes(dtype, static_cast<int>(D));
   CAB_REQUIRE(vt != nullptr && bytes >= need, CAB_EWORKSPACE,
               "%s: workspace of %zu bytes given, %zu needed", fn, bytes, need);
   CAB_REQUIRE(reinterpret_cast<uintptr_t>(vt) % 16 == 0, CAB_EWORKSPACE,
@@ -932,7 +1004,7 @@ cab_status_t check_attn(const char* fn, const void* q, const void* k, const int6
 }
 
 cab_status_t launch_pack(const char* fn, const void* v, const int64_t* v_strides, int64_t B,
-                         int64_t H, int64_t N, void* vt, hipStream_t s) {
+                         int64_t H, int64_t N, int64_t D, void* vt, hipStream_t s) {
   PackArgs p;
   p.v = static_cast<const uint16_t*>(v);
   p.vt = static_cast<uint16_t*>(vt);
@@ -940,13 +1012,17 @@ cab_status_t launch_pack(const char* fn, const void* v, const int64_t* v_strides
   p.H = H;
   p.N = N;
   p.M = ceil_div(N, BS);
-  pack_vt_kernel<<<dim3(static_cast<unsigned>(p.M), static_cast<unsigned>(B * H)), 256, 0, s>>>(p);
+  const dim3 grid(static_cast<unsigned>(p.M), static_cast<unsigned>(B * H));
+  if (D == 64)
+    pack_vt_kernel<64><<<grid, 256, 0, s>>>(p);
+  else
+    pack_vt_kernel<128><<<grid, 256, 0, s>>>(p);
   return launch_status(fn);
 }
 
 cab_status_t launch_pack_split(const char* fn, const void* k, const int64_t* k_strides,
                                const void* v, const int64_t* v_strides, int64_t B, int64_t H,
-                               int64_t N, void* img, hipStream_t s) {
+                               int64_t N, int64_t D, void* img, hipStream_t s) {
   SplitPackArgs p;
   p.k = static_cast<const float*>(k);
   p.v = static_cast<const float*>(v);
@@ -958,25 +1034,28 @@ cab_status_t launch_pack_split(const char* fn, const void* k, const int64_t* k_s
   p.H = H;
   p.N = N;
   p.M = ceil_div(N, BS);
-  pack_split_kernel<<<dim3(static_cast<unsigned>(p.M), static_cast<unsigned>(B * H)), 256, 0, s>>>(
-      p);
+  const dim3 grid(static_cast<unsigned>(p.M), static_cast<unsigned>(B * H));
+  if (D == 64)
+    pack_split_kernel<64><<<grid, 256, 0, s>>>(p);
+  else
+    pack_split_kernel<128><<<grid, 256, 0, s>>>(p);
   return launch_status(fn);
 }
 
-template <cab_dtype_t DT>
+template <cab_dtype_t DT, int HD>
 void launch_attn_kernel(int list, dim3 grid, hipStream_t s, const AttnArgs& a) {
   if (list == LIST_LDS)
-    attn_fwd_kernel<DT, LIST_LDS><<<grid, 256, 0, s>>>(a);
+    attn_fwd_kernel<DT, LIST_LDS, HD><<<grid, 256, 0, s>>>(a);
   else if (list == LIST_GLOBAL)
-    attn_fwd_kernel<DT, LIST_GLOBAL><<<grid, 256, 0, s>>>(a);
+    attn_fwd_kernel<DT, LIST_GLOBAL, HD><<<grid, 256, 0, s>>>(a);
   else
-    attn_fwd_kernel<DT, LIST_DENSE><<<grid, 256, 0, s>>>(a);
+    attn_fwd_kernel<DT, LIST_DENSE, HD><<<grid, 256, 0, s>>>(a);
 }
 
 // Problem geometry of one executor call: query heads H over Hkv K / V heads,
-// Nq query and Nk key tokens, the causal offset and the list mode.
+// Nq query and Nk key tokens, head dim D, the causal offset and the list mode.
 struct AttnGeom {
-  int64_t B, H, Hkv, Nq, Nk;
+  int64_t B, H, Hkv, Nq, Nk, D;
   int64_t qoff;
   int list;
 };
@@ -1012,18 +1091,27 @@ cab_status_t launch_attn(const char* fn, const void* q, const void* k, const voi
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   a.causal = causal ? 1 : 0;
   const dim3 grid(static_cast<unsigned>(g.B * g.H * M));
-  if (dtype == CAB_BF16)
-    launch_attn_kernel<CAB_BF16>(g.list, grid, s, a);
-  else if (dtype == CAB_F16)
-    launch_attn_kernel<CAB_F16>(g.list, grid, s, a);
-  else
-    launch_attn_kernel<CAB_F32>(g.list, grid, s, a);
+  if (g.D == 64) {
+    if (dtype == CAB_BF16)
+      launch_attn_kernel<CAB_BF16, 64>(g.list, grid, s, a);
+    else if (dtype == CAB_F16)
+      launch_attn_kernel<CAB_F16, 64>(g.list, grid, s, a);
+    else
+      launch_attn_kernel<CAB_F32, 64>(g.list, grid, s, a);
+  } else {
+    if (dtype == CAB_BF16)
+      launch_attn_kernel<CAB_BF16, 128>(g.list, grid, s, a);
+    else if (dtype == CAB_F16)
+      launch_attn_kernel<CAB_F16, 128>(g.list, grid, s, a);
+    else
+      launch_attn_kernel<CAB_F32, 128>(g.list, grid, s, a);
+  }
   return launch_status(fn);
 }
 
 // The sparse entry points: one K / V head per query head, Nq = Nk = N.
-AttnGeom sparse_geom(int64_t B, int64_t H, int64_t N, int32_t kmax) {
-  return AttnGeom{B, H, H, N, N, 0, kmax <= LIST_MAX ? LIST_LDS : LIST_GLOBAL};
+AttnGeom sparse_geom(int64_t B, int64_t H, int64_t N, int64_t D, int32_t kmax) {
+  return AttnGeom{B, H, H, N, N, D, 0, kmax <= LIST_MAX ? LIST_LDS : LIST_GLOBAL};
 }
 
 }  // namespace
@@ -1031,8 +1119,8 @@ AttnGeom sparse_geom(int64_t B, int64_t H, int64_t N, int32_t kmax) {
 extern "C" size_t cab_block_sparse_attn_workspace_bytes(cab_dtype_t dtype, int64_t B, int64_t H,
                                                         int64_t N, int64_t D, int32_t block_size) {
   if (dtype != CAB_BF16 && dtype != CAB_F16 && dtype != CAB_F32) return 0;
-  if (B <= 0 || H <= 0 || N <= 0 || D != HD || block_size != BS) return 0;
-  return static_cast<size_t>(B * H * ceil_div(N, BS)) * block_bytes(dtype);
+  if (B <= 0 || H <= 0 || N <= 0 || (D != 64 && D != 128) || block_size != BS) return 0;
+  return static_cast<size_t>(B * H * ceil_div(N, BS)) * block_bytes(dtype, static_cast<int>(D));
 }
 
 extern "C" cab_status_t cab_block_sparse_attn_pack_v(const void* v, cab_dtype_t dtype, int64_t B,
@@ -1047,8 +1135,8 @@ extern "C" cab_status_t cab_block_sparse_attn_pack_v(const void* v, cab_dtype_t 
   const int64_t M = ceil_div(N, BS);
   if (B == 0 || H == 0 || M == 0) return CAB_OK;
   if ((st = check_tensor(fn, "v", v, v_strides, 2)) != CAB_OK) return st;
-  if ((st = check_packed(fn, workspace, workspace_bytes, B, H, M, dtype)) != CAB_OK) return st;
-  return launch_pack(fn, v, v_strides, B, H, N, workspace, static_cast<hipStream_t>(stream));
+  if ((st = check_packed(fn, workspace, workspace_bytes, B, H, M, dtype, D)) != CAB_OK) return st;
+  return launch_pack(fn, v, v_strides, B, H, N, D, workspace, static_cast<hipStream_t>(stream));
 }
 
 extern "C" cab_status_t cab_block_sparse_attn_fwd_packed(
@@ -1066,8 +1154,8 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd_packed(
   if ((st = check_attn(fn, q, k, q_strides, k_strides, o_strides, out, kv_idx, kv_cnt, kmax,
                        scale, 2)) != CAB_OK)
     return st;
-  if ((st = check_packed(fn, vt, vt_bytes, B, H, M, dtype)) != CAB_OK) return st;
-  return launch_attn(fn, q, k, vt, dtype, sparse_geom(B, H, N, kmax), q_strides, k_strides,
+  if ((st = check_packed(fn, vt, vt_bytes, B, H, M, dtype, D)) != CAB_OK) return st;
+  return launch_attn(fn, q, k, vt, dtype, sparse_geom(B, H, N, D, kmax), q_strides, k_strides,
                      o_strides, kv_idx, kv_cnt, kmax, scale, causal, out, lse,
                      static_cast<hipStream_t>(stream));
 }
@@ -1094,15 +1182,15 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
                        scale, esize)) != CAB_OK)
     return st;
   if ((st = check_tensor(fn, "v", v, v_strides, esize)) != CAB_OK) return st;
-  if ((st = check_packed(fn, workspace, workspace_bytes, B, H, M, dtype)) != CAB_OK) return st;
+  if ((st = check_packed(fn, workspace, workspace_bytes, B, H, M, dtype, D)) != CAB_OK) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == CAB_F32)
     st = launch_pack_split("cab_block_sparse_attn_fwd/pack_split", k, k_strides, v, v_strides, B,
-                           H, N, workspace, s);
+                           H, N, D, workspace, s);
   else
-    st = launch_pack("cab_block_sparse_attn_fwd/pack_v", v, v_strides, B, H, N, workspace, s);
+    st = launch_pack("cab_block_sparse_attn_fwd/pack_v", v, v_strides, B, H, N, D, workspace, s);
   if (st != CAB_OK) return st;
-  return launch_attn(fn, q, k, workspace, dtype, sparse_geom(B, H, N, kmax), q_strides, k_strides,
+  return launch_attn(fn, q, k, workspace, dtype, sparse_geom(B, H, N, D, kmax), q_strides, k_strides,
                      o_strides, kv_idx, kv_cnt, kmax, scale, causal, out, lse, s);
 }
 
@@ -1113,7 +1201,7 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
 namespace {
 
 // Shape checks of the dense entry points: H query heads over H_kv K / V
-// heads (H % H_kv == 0), N_q queries, N_k keys, D = 128.
+// heads (H % H_kv == 0), N_q queries, N_k keys, D = 64 or 128.
 cab_status_t check_dense(const char* fn, cab_dtype_t dtype, bool allow_f32, int64_t B, int64_t H,
                          int64_t H_kv, int64_t N_q, int64_t N_k, int64_t D) {
   if (allow_f32)
@@ -1124,7 +1212,8 @@ cab_status_t check_dense(const char* fn, cab_dtype_t dtype, bool allow_f32, int6
                 "%s: dtype %d unsupported (bf16 or fp16)", fn, (int)dtype);
   CAB_REQUIRE(B >= 0 && H >= 0 && H_kv >= 0 && N_q >= 0 && N_k >= 0, CAB_ESHAPE,
               "%s: negative size", fn);
-  CAB_REQUIRE(D == HD, CAB_ESHAPE, "%s: head dim %lld unsupported (128)", fn, (long long)D);
+  CAB_REQUIRE(D == 64 || D == 128, CAB_ESHAPE, "%s: head dim %lld unsupported (64 or 128)", fn,
+              (long long)D);
   CAB_REQUIRE(H_kv > 0 ? H % H_kv == 0 : H == 0, CAB_ESHAPE,
               "%s: %lld query heads are not a multiple of %lld K/V heads", fn, (long long)H,
               (long long)H_kv);
@@ -1139,8 +1228,8 @@ cab_status_t check_dense(const char* fn, cab_dtype_t dtype, bool allow_f32, int6
 extern "C" size_t cab_flash_attn_workspace_bytes(cab_dtype_t dtype, int64_t B, int64_t H_kv,
                                                  int64_t N_k, int64_t D) {
   if (dtype != CAB_BF16 && dtype != CAB_F16 && dtype != CAB_F32) return 0;
-  if (B <= 0 || H_kv <= 0 || N_k <= 0 || D != HD) return 0;
-  return static_cast<size_t>(B * H_kv * ceil_div(N_k, BS)) * block_bytes(dtype);
+  if (B <= 0 || H_kv <= 0 || N_k <= 0 || (D != 64 && D != 128)) return 0;
+  return static_cast<size_t>(B * H_kv * ceil_div(N_k, BS)) * block_bytes(dtype, static_cast<int>(D));
 }
 
 extern "C" cab_status_t cab_flash_attn_fwd(
@@ -1167,7 +1256,7 @@ extern "C" cab_status_t cab_flash_attn_fwd(
   if (N_k == 0 || H_kv == 0) {
     // No keys: every row attends to nothing (output 0, lse -inf); K, V and
     // the workspace are not read (q stands in for their addresses).
-    const AttnGeom g{B, H, H_kv > 0 ? H_kv : H, N_q, 0, -N_q, LIST_DENSE};
+    const AttnGeom g{B, H, H_kv > 0 ? H_kv : H, N_q, 0, D, -N_q, LIST_DENSE};
     return launch_attn(fn, q, q, q, dtype, g, q_strides, q_strides, o_strides, nullptr, nullptr,
                        1, scale, causal, out, lse, s);
   }
@@ -1176,18 +1265,18 @@ extern "C" cab_status_t cab_flash_attn_fwd(
   CAB_REQUIRE(k_strides[2] <= (int64_t{1} << 24), CAB_ESHAPE,
               "%s: k token stride %lld too large (<= 2^24 elements)", fn, (long long)k_strides[2]);
   const int64_t Mk = ceil_div(N_k, BS);
-  const size_t need = static_cast<size_t>(B * H_kv * Mk) * block_bytes(dtype);
+  const size_t need = static_cast<size_t>(B * H_kv * Mk) * block_bytes(dtype, static_cast<int>(D));
   CAB_REQUIRE(workspace != nullptr && workspace_bytes >= need, CAB_EWORKSPACE,
               "%s: workspace of %zu bytes given, %zu needed", fn, workspace_bytes, need);
   CAB_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, CAB_EWORKSPACE,
               "%s: workspace not 16-byte aligned", fn);
   if (dtype == CAB_F32)
     st = launch_pack_split("cab_flash_attn_fwd/pack_split", k, k_strides, v, v_strides, B, H_kv,
-                           N_k, workspace, s);
+                           N_k, D, workspace, s);
   else
-    st = launch_pack("cab_flash_attn_fwd/pack_v", v, v_strides, B, H_kv, N_k, workspace, s);
+    st = launch_pack("cab_flash_attn_fwd/pack_v", v, v_strides, B, H_kv, N_k, D, workspace, s);
   if (st != CAB_OK) return st;
-  const AttnGeom g{B, H, H_kv, N_q, N_k, N_k - N_q, LIST_DENSE};
+  const AttnGeom g{B, H, H_kv, N_q, N_k, D, N_k - N_q, LIST_DENSE};
   return launch_attn(fn, q, k, workspace, dtype, g, q_strides, k_strides, o_strides, nullptr,
                      nullptr, 1, scale, causal, out, lse, s);
 }
@@ -1238,9 +1327,16 @@ extern "C" cab_status_t cab_attn_key_scores(
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   const dim3 grid(static_cast<unsigned>(B * H * a.Mkg));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == CAB_BF16)
-    key_score_kernel<true, KS_WAVES><<<grid, 64 * KS_WAVES, 0, s>>>(a);
-  else
-    key_score_kernel<false, KS_WAVES><<<grid, 64 * KS_WAVES, 0, s>>>(a);
+  if (D == 64) {
+    if (dtype == CAB_BF16)
+      key_score_kernel<true, KS_WAVES, 64><<<grid, 64 * KS_WAVES, 0, s>>>(a);
+    else
+      key_score_kernel<false, KS_WAVES, 64><<<grid, 64 * KS_WAVES, 0, s>>>(a);
+  } else {
+    if (dtype == CAB_BF16)
+      key_score_kernel<true, KS_WAVES, 128><<<grid, 64 * KS_WAVES, 0, s>>>(a);
+    else
+      key_score_kernel<false, KS_WAVES, 128><<<grid, 64 * KS_WAVES, 0, s>>>(a);
+  }
   return launch_status(fn);
 }

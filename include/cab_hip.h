@@ -49,7 +49,7 @@ enum { CAB_NORM_NONE = 0, CAB_NORM_MINMAX = 1 };
 /* FRC combination (experiments/longbench_qa/config.py:465; test.ipynb:111-145). */
 enum { CAB_FRC_ADDITIVE = 0, CAB_FRC_MULTIPLICATIVE = 1, CAB_FRC_AUGMENTED = 2 };
 
-#define CAB_ABI_VERSION 6
+#define CAB_ABI_VERSION 7
 
 int cab_abi_version(void);
 const char* cab_last_error(void);
@@ -174,7 +174,7 @@ size_t cab_block_sparse_attn_workspace_bytes(cab_dtype_t dtype, int64_t B, int64
  * products per product, fp32 output; relative error near 2^-16 per product).
  * q, k, v: [B,H,N,D] (strides), out: [B,H,N,D] (strides), dtype bf16, fp16
  * or fp32.
- * block_size == 64, D == 128, scale > 0. kv_idx: contiguous int32
+ * block_size == 64, D == 64 or 128, scale > 0. kv_idx: contiguous int32
  * [B,H,M,kmax], kv_cnt: contiguous int32 [B,H,M]. lse: fp32 [B,H,N]
  * natural-log log-sum-exp of the scaled scores (-inf for a query with no
  * key), or NULL. workspace: cab_block_sparse_attn_workspace_bytes(dtype, ...)
@@ -197,8 +197,8 @@ cab_status_t cab_block_sparse_attn_fwd(const void* q, const void* k, const void*
  * unchanged) or time the attention kernel alone. No counterpart in the
  * reference: its executor has no V preparation step.
  *
- * cab_block_sparse_attn_pack_v: writes V's packed V^T tiles (16 KB per
- * (b, h, key block), zero past N) into `workspace`
+ * cab_block_sparse_attn_pack_v: writes V's packed V^T tiles (64 * D * 2 bytes
+ * per (b, h, key block), zero past N) into `workspace`
  * (cab_block_sparse_attn_workspace_bytes() bytes, 16-byte aligned).
  * bf16 / fp16 only (CAB_EDTYPE for fp32, whose packed form also holds K).
  */
@@ -234,7 +234,7 @@ cab_status_t cab_block_sparse_attn_fwd_packed(const void* q, const void* k, cons
  * scores (-inf for a query that sees no key), or lse = NULL. H query heads
  * share H_kv K / V heads (query head h reads K / V head h / (H / H_kv)).
  * q, out: [B,H,N_q,D]; k, v: [B,H_kv,N_k,D] (strides); lse: contiguous fp32
- * [B,H,N_q]. D == 128; bf16, fp16 or fp32 (fp32: split bf16 MFMA as in
+ * [B,H,N_q]. D == 64 or 128; bf16, fp16 or fp32 (fp32: split bf16 MFMA as in
  * cab_block_sparse_attn_fwd). workspace: cab_flash_attn_workspace_bytes()
  * bytes, 16-byte aligned, overwritten.
  *

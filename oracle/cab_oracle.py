@@ -84,11 +84,18 @@ __all__ = [
     "dense_masked_attention",
     "global_topk_mask",
     "estimate_flops",
+    "frc_tolerance",
+    "mask_far_differences",
     "NORM_CHUNK",
+    "FRC_RTOL",
 ]
 
 # Elements summed sequentially per partial before the pairwise tree.
 NORM_CHUNK = 8
+
+# Relative FRC tolerance of the north star (fp32 accumulation), applied to
+# the magnitude of F's two terms because F = Ahat - lambda T cancels.
+FRC_RTOL = 1e-3
 
 
 def num_blocks(n: int, block_size: int) -> int:
@@ -309,6 +316,64 @@ def generate_block_mask(frc, sparsity: float, select_high: bool = False,
     return mask, kv_idx, kv_cnt
 
 
+def frc_tolerance(ahat, lambda_redundancy: float, t_abs=None) -> np.ndarray:
+    """Per-entry FRC tolerance ``FRC_RTOL * (|Ahat| + |lambda| (|Ahat| @ |Ahat|))``.
+
+    ``t_abs`` may pass ``|Ahat| @ |Ahat|`` when it is known (under minmax
+    normalisation Ahat >= 0, so it is the oracle's own T).
+    """
+    a = np.abs(np.asarray(ahat, dtype=np.float64))
+    if t_abs is None:
+        t_abs = np.matmul(a, a)
+    return FRC_RTOL * (a + abs(float(lambda_redundancy)) * np.asarray(t_abs, dtype=np.float64))
+
+
+def mask_far_differences(gpu_mask, frc, tol, k: int, keep_diagonal: bool = True,
+                         causal: bool = False, select_high: bool = False):
+    """Compares a device mask with the oracle's selection on the oracle's
+    scores ``frc`` and tolerances ``tol`` (``frc_tolerance``).
+
+    A differing entry (i, j) is a near-tie when its score lies within
+    ``tol[i, j] + tol[i, t]`` of the row's threshold score, t being the
+    oracle's threshold entry (the last one kept): two scores each within
+    their tolerance of the oracle's can only swap order inside that band.
+    Returns ``(agreement, far)``: the fraction of identical entries and the
+    number of differing entries that are not near-ties (0 for a pass).
+    """
+    f = np.asarray(frc, dtype=np.float64)
+    gm = np.asarray(gpu_mask, dtype=bool)
+    b, h, m, _ = f.shape
+    want = np.zeros_like(gm)
+    far = 0
+    for bb in range(b):
+        for hh in range(h):
+            for i in range(m):
+                ncand = i + 1 if causal else m
+                cand = np.arange(ncand)
+                others = cand[cand != i] if keep_diagonal else cand
+                need = min(k, ncand) - (1 if keep_diagonal else 0)
+                keys = order_keys(f[bb, hh, i, others], select_high)
+                order = others[np.argsort(keys, kind="stable")]
+                kept = order[:need]
+                row = np.zeros(m, dtype=bool)
+                row[kept] = True
+                if keep_diagonal:
+                    row[i] = True
+                want[bb, hh, i] = row
+                diff = np.flatnonzero(row != gm[bb, hh, i])
+                if diff.size == 0:
+                    continue
+                if need <= 0:
+                    far += diff.size
+                    continue
+                t = kept[-1]
+                theta = f[bb, hh, i, t]
+                for j in diff:
+                    if abs(f[bb, hh, i, j] - theta) > tol[bb, hh, i, j] + tol[bb, hh, i, t]:
+                        far += 1
+    return float((want == gm).mean()), far
+
+
 def expand_block_mask(block_mask: np.ndarray, block_size: int, seq_len: int) -> np.ndarray:
     """Token-level mask from a block mask (methods.py:103-119)."""
     t = np.repeat(np.repeat(block_mask, block_size, axis=-2), block_size, axis=-1)
@@ -334,7 +399,8 @@ def global_topk_mask(scores: np.ndarray, sparsity: float, largest: bool) -> np.n
 # ---------------------------------------------------------------------------
 
 def sparse_attention(q, k, v, kv_idx, kv_cnt, block_size: int, scale=None,
-                     causal: bool = False, heads=None, query_blocks=None) -> np.ndarray:
+                     causal: bool = False, heads=None, query_blocks=None,
+                     compute_dtype=np.float64) -> np.ndarray:
     """Softmax attention over the kept key blocks of each query block.
 
     ``O_t = sum_s softmax_s(q_t . k_s * scale) v_s`` over the tokens s of
@@ -344,10 +410,13 @@ def sparse_attention(q, k, v, kv_idx, kv_cnt, block_size: int, scale=None,
     methods.py:103-119). ``scale`` defaults to 1/sqrt(D). float64 output
     ``[B,H,N,D]``; ``heads`` restricts the work to a list of (b, h) pairs and
     ``query_blocks`` to a list of block rows (other outputs stay 0).
+    ``compute_dtype=np.float32`` runs the same steps in float32 (the
+    reference's torch path upcasts bf16 inputs to fp32): the CPU baseline's
+    timing mode, not a checker.
     """
-    q = np.asarray(q, dtype=np.float64)
-    k = np.asarray(k, dtype=np.float64)
-    v = np.asarray(v, dtype=np.float64)
+    q = np.asarray(q, dtype=compute_dtype)
+    k = np.asarray(k, dtype=compute_dtype)
+    v = np.asarray(v, dtype=compute_dtype)
     b, h, n, d = q.shape
     if scale is None:
         scale = 1.0 / math.sqrt(d)
@@ -364,12 +433,12 @@ def sparse_attention(q, k, v, kv_idx, kv_cnt, block_size: int, scale=None,
             blocks = kv_idx[bb, hh, i, :cnt]
             toks = np.concatenate([np.arange(j * block_size, min((j + 1) * block_size, n))
                                    for j in blocks])
-            s = (q[bb, hh, t0:t1] @ k[bb, hh, toks].T) * scale
+            s = (q[bb, hh, t0:t1] @ k[bb, hh, toks].T) * q.dtype.type(scale)
             if causal:
                 s = np.where(toks[None, :] > np.arange(t0, t1)[:, None], -np.inf, s)
             mx = s.max(axis=-1, keepdims=True)
             valid = np.isfinite(mx)
-            e = np.exp(np.where(valid, s - np.where(valid, mx, 0.0), -np.inf))
+            e = np.exp(np.where(valid, s - np.where(valid, mx, 0), -np.inf))
             den = e.sum(axis=-1, keepdims=True)
             p = np.divide(e, den, out=np.zeros_like(e), where=den > 0)
             out[bb, hh, t0:t1] = p @ v[bb, hh, toks]

@@ -116,7 +116,9 @@ def test_attention_validation(lib):
     assert ws(nat.CAB_BF16, 1, 8, 65, 128, 64) == 8 * 2 * 16384
     assert ws(nat.CAB_F16, 1, 8, 65, 128, 64) == 8 * 2 * 16384
     assert ws(nat.CAB_F32, 1, 8, 65, 128, 64) == 8 * 2 * 65536  # split K and V^T images
-    assert ws(nat.CAB_BF16, 1, 8, 64, 64, 64) == 0
+    assert ws(nat.CAB_BF16, 1, 8, 64, 64, 64) == 8 * 8192   # head dim 64: 8 KB tiles
+    assert ws(nat.CAB_F32, 1, 8, 64, 64, 64) == 8 * 32768
+    assert ws(nat.CAB_BF16, 1, 8, 64, 96, 64) == 0
     assert ws(7, 1, 8, 64, 128, 64) == 0
     st = _s4(8 * 64 * 128, 64 * 128, 128, 1)
     call = lambda **kw: lib.cab_block_sparse_attn_fwd(
@@ -139,7 +141,7 @@ def test_attention_validation(lib):
     pack = lambda **kw: lib.cab_block_sparse_attn_pack_v(
         kw.get("v", FAKE), nat.CAB_BF16, 1, 8, 64, kw.get("D", 128), st, 64, FAKE,
         kw.get("wsb", 1 << 30), None)
-    assert pack(D=64) == nat.CAB_ESHAPE
+    assert pack(D=96) == nat.CAB_ESHAPE
     assert pack(v=None) == nat.CAB_EINVAL
     assert pack(wsb=100) == nat.CAB_EWORKSPACE
     assert lib.cab_block_sparse_attn_pack_v(FAKE, nat.CAB_F32, 1, 8, 64, 128, st, 64, FAKE,
@@ -194,6 +196,13 @@ def test_module_contract_on_host():
     assert a.predictor.sparsity == 0.95
     with pytest.raises(ValueError):
         CABAttention(dim=500, num_heads=8)
+    # the executor runs head dims 64 and 128 and block size 64 only: rejected
+    # at construction, not in forward
+    CABAttention(dim=1024, num_heads=8)
+    with pytest.raises(ValueError, match="head_dim"):
+        CABAttention(dim=768, num_heads=8)
+    with pytest.raises(ValueError, match="block_size"):
+        CABAttention(dim=512, num_heads=8, block_size=128)
     with pytest.raises(ValueError):
         CoarseCurvaturePredictor(sparsity=1.5)
 
@@ -204,14 +213,15 @@ def test_dense_attention_validation(lib):
     ws = lib.cab_flash_attn_workspace_bytes
     assert ws(nat.CAB_BF16, 1, 2, 65, 128) == 2 * 2 * 16384
     assert ws(nat.CAB_F32, 1, 2, 65, 128) == 2 * 2 * 65536
-    assert ws(nat.CAB_BF16, 1, 2, 65, 64) == 0
+    assert ws(nat.CAB_BF16, 1, 2, 65, 64) == 2 * 2 * 8192
+    assert ws(nat.CAB_BF16, 1, 2, 65, 80) == 0
     st = _s4(8 * 64 * 128, 64 * 128, 128, 1)
     fwd = lambda **kw: lib.cab_flash_attn_fwd(
         FAKE, FAKE, FAKE, kw.get("dt", nat.CAB_BF16), 1, kw.get("H", 8), kw.get("Hkv", 2), 64, 64,
         kw.get("D", 128), st, st, st, kw.get("os", st), kw.get("scale", 0.088), 1, FAKE, None,
         kw.get("ws", FAKE), kw.get("wsb", 1 << 30), None)
     assert fwd(dt=9) == nat.CAB_EDTYPE
-    assert fwd(D=64) == nat.CAB_ESHAPE
+    assert fwd(D=80) == nat.CAB_ESHAPE
     assert fwd(H=8, Hkv=3) == nat.CAB_ESHAPE
     assert fwd(scale=0.0) == nat.CAB_EINVAL
     assert fwd(os=_s4(1, 1, 1, 3)) == nat.CAB_ESHAPE

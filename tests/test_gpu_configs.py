@@ -1,0 +1,130 @@
+"""BASELINE.json configs 2, 3 and 5 at their stated sizes, through the C ABI,
+against the float64 oracle on the same seeded inputs:
+
+- config 2 (B=1 H=32 N=32768 bf16): coarsening bit-exact on every head, FRC
+  within the term-magnitude bound on every head, predictor masks (fused
+  scores and diagnostics path) equal to the oracle's except at near-ties;
+- config 3 (B=2 H=8 N=128000 bf16): CoarseCurvaturePredictor.forward end to
+  end, compared with the oracle on two (b, h) units;
+- config 5 (B=1 H=8 N=131072 bf16, sparsity 0.99, k=20, planted bridges):
+  mask agreement and bridge flags equal to the oracle's on all eight heads,
+  keeping the lowest and the highest scores.
+
+Masks may differ only where an oracle score lies within the stated FRC
+tolerance 1e-3 (|Ahat| + |lambda| |Ahat| @ |Ahat|) of the row threshold.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cab_oracle as O
+from test_gpu_parity import assert_frc_close, bits, np32, seeded
+
+pytestmark = pytest.mark.gpu
+
+LAM = 0.5
+
+
+def masks_agree(gpu_mask, of, oa, ot, k, causal=False, select_high=False, max_frac=0.01):
+    tol = O.frc_tolerance(oa, LAM, t_abs=ot)
+    agree, far = O.mask_far_differences(gpu_mask.cpu().numpy(), of, tol, k, True, causal,
+                                        select_high)
+    assert far == 0, f"{far} mask entries differ away from the row threshold"
+    assert 1.0 - agree <= max_frac, agree
+    return agree
+
+
+def test_config2_full_size(cuda):
+    from cab_attention import CoarseCurvaturePredictor
+    from cab_attention.kernels import coarsen_qk_max_l2, compute_block_frc
+    B, H, N, D, bs, sp = 1, 32, 32768, 128, 64, 0.95
+    print(f"config2 B={B} H={H} N={N}", flush=True)
+    q = seeded((B, H, N, D), 1, torch.bfloat16)
+    k = seeded((B, H, N, D), 2, torch.bfloat16)
+    qd, kd = q.to(cuda), k.to(cuda)
+    qc, kc, qi, ki = coarsen_qk_max_l2(qd, kd, bs, return_indices=True)
+    oq, oqi = O.coarsen_max_l2(np32(q), bs)
+    ok, oki = O.coarsen_max_l2(np32(k), bs)
+    np.testing.assert_array_equal(qi.cpu().numpy(), oqi)
+    np.testing.assert_array_equal(ki.cpu().numpy(), oki)
+    np.testing.assert_array_equal(bits(qc), bits(torch.from_numpy(oq).to(torch.bfloat16)))
+    np.testing.assert_array_equal(bits(kc), bits(torch.from_numpy(ok).to(torch.bfloat16)))
+    of, oa, ot = O.compute_block_frc(oq, ok, lambda_redundancy=LAM)
+    f, a, t = compute_block_frc(qc, kc, lambda_redundancy=LAM)
+    assert_frc_close(f, of, oa, ot, LAM)
+    fused, _, _ = compute_block_frc(qc, kc, lambda_redundancy=LAM, diagnostics=False)
+    assert_frc_close(fused, of, oa, ot, LAM)
+    M = N // bs
+    kk = O.keep_count(M, sp)
+    assert kk == 25
+    pred = CoarseCurvaturePredictor(block_size=bs, sparsity=sp, lambda_redundancy=LAM)
+    mask = pred(qd, kd)
+    assert mask.shape == (B, H, M, M) and int(mask.sum()) == B * H * M * kk
+    masks_agree(mask, of, oa, ot, kk)
+    mask_d, diag = pred(qd, kd, return_diagnostics=True)
+    masks_agree(mask_d, of, oa, ot, kk)
+    assert diag["num_blocks"] == M
+
+
+def test_config3_predictor_end_to_end(cuda):
+    from cab_attention import CoarseCurvaturePredictor
+    from cab_attention.kernels import coarsen_qk_max_l2, compute_block_frc
+    B, H, N, D, bs, sp = 2, 8, 128000, 128, 64, 0.95
+    print(f"config3 B={B} H={H} N={N}", flush=True)
+    q = seeded((B, H, N, D), 1, torch.bfloat16)
+    k = seeded((B, H, N, D), 2, torch.bfloat16)
+    qd, kd = q.to(cuda), k.to(cuda)
+    pred = CoarseCurvaturePredictor(block_size=bs, sparsity=sp, lambda_redundancy=LAM)
+    mask = pred(qd, kd)
+    M = N // bs
+    kk = O.keep_count(M, sp)
+    assert kk == 100 and mask.shape == (B, H, M, M)
+    assert torch.all(mask.sum(-1) == kk)
+    assert torch.all(mask.diagonal(dim1=-2, dim2=-1))
+    qc, kc = coarsen_qk_max_l2(qd, kd, bs)
+    fused, _, _ = compute_block_frc(qc, kc, lambda_redundancy=LAM, diagnostics=False)
+    for b, h in ((0, 0), (1, 7)):
+        print(f"config3 oracle unit b={b} h={h}", flush=True)
+        oq, _ = O.coarsen_max_l2(np32(q[b:b + 1, h:h + 1]), bs)
+        ok, _ = O.coarsen_max_l2(np32(k[b:b + 1, h:h + 1]), bs)
+        np.testing.assert_array_equal(bits(qc[b:b + 1, h:h + 1]),
+                                      bits(torch.from_numpy(oq).to(torch.bfloat16)))
+        np.testing.assert_array_equal(bits(kc[b:b + 1, h:h + 1]),
+                                      bits(torch.from_numpy(ok).to(torch.bfloat16)))
+        of, oa, ot = O.compute_block_frc(oq, ok, lambda_redundancy=LAM)
+        assert_frc_close(fused[b:b + 1, h:h + 1], of, oa, ot, LAM)
+        masks_agree(mask[b:b + 1, h:h + 1], of, oa, ot, kk)
+
+
+@pytest.mark.parametrize("select_high", [False, True])
+def test_config5_bridges_as_stated(cuda, select_high):
+    import bench
+    from cab_attention import CoarseCurvaturePredictor
+    B, H, N, D, bs, sp = 1, 8, 131072, 128, 64, 0.99
+    print(f"config5 B={B} H={H} N={N} select_high={select_high}", flush=True)
+    q, k, pairs = bench.bridge_inputs(B, H, N, D, 5, cuda, torch.bfloat16)
+    assert len(pairs) == 4
+    M = N // bs
+    kk = O.keep_count(M, sp)
+    assert kk == 20
+    pred = CoarseCurvaturePredictor(block_size=bs, sparsity=sp, lambda_redundancy=LAM,
+                                    select_high=select_high)
+    mask = pred(q, k)
+    assert torch.all(mask.sum(-1) == kk)
+    oq, _ = O.coarsen_max_l2(np32(q), bs)
+    ok, _ = O.coarsen_max_l2(np32(k), bs)
+    of, oa, ot = O.compute_block_frc(oq, ok, lambda_redundancy=LAM)
+    masks_agree(mask, of, oa, ot, kk, select_high=select_high)
+    om = O.generate_block_mask(of, sp, select_high=select_high)[0]
+    gm = mask.cpu().numpy()
+    tol = O.frc_tolerance(oa, LAM, t_abs=ot)
+    for h in range(H):
+        for i, j in pairs:
+            if gm[0, h, i, j] != om[0, h, i, j]:
+                # only a near-tie at the row threshold may flip a bridge
+                row = of[0, h, i]
+                others = np.array([x for x in range(M) if x != i])
+                keys = O.order_keys(row[others], select_high)
+                t = others[np.argsort(keys, kind="stable")][kk - 2]
+                assert abs(row[j] - row[t]) <= tol[0, h, i, j] + tol[0, h, i, t], (h, i, j)

@@ -14,6 +14,10 @@ DTYPES = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}
 # Output: bf16 / fp16 rounding of the inputs' products and of P; fp32: the
 # north-star tolerance (split bf16 operands). lse: fp32 softmax statistics.
 ATOL = {"bf16": 2e-2, "fp16": 5e-3, "fp32": 1e-3}
+# lse = m + log(sum P) over the same rounded P the output uses: a bf16 P
+# entry carries a relative rounding of up to 2^-9, fp16 2^-11, which a row
+# with few keys passes into its lse almost unaveraged.
+LSE_ATOL = {"bf16": 2e-3, "fp16": 1e-3, "fp32": 1e-3}
 
 
 def seeded(shape, seed, dtype, scale=1.0):
@@ -41,12 +45,13 @@ SHAPES = [  # (H, H_kv, N_q, N_k)
 ]
 
 
+@pytest.mark.parametrize("D", [128, 64])
 @pytest.mark.parametrize("dt", ["bf16", "fp16", "fp32"])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("H,Hkv,Nq,Nk", SHAPES)
-def test_flash_attention_and_key_scores(cuda, dt, causal, H, Hkv, Nq, Nk):
+def test_flash_attention_and_key_scores(cuda, dt, causal, H, Hkv, Nq, Nk, D):
     from cab_attention.kernels import flash_attention, key_scores
-    B, D = 1, 128
+    B = 1
     q = seeded((B, H, Nq, D), 1, DTYPES[dt])
     k = seeded((B, Hkv, Nk, D), 2, DTYPES[dt])
     v = seeded((B, Hkv, Nk, D), 3, DTYPES[dt])
@@ -57,7 +62,7 @@ def test_flash_attention_and_key_scores(cuda, dt, causal, H, Hkv, Nq, Nk):
     got_lse = np64(lse)
     fin = np.isfinite(w_lse)
     assert np.array_equal(np.isfinite(got_lse), fin)
-    np.testing.assert_allclose(got_lse[fin], w_lse[fin], atol=1e-3, rtol=1e-4)
+    np.testing.assert_allclose(got_lse[fin], w_lse[fin], atol=LSE_ATOL[dt], rtol=1e-4)
     if dt != "fp32":
         sc = key_scores(q.to(cuda), k.to(cuda), lse, causal=causal)
         assert_scores_close(sc, w_sc, Nq)
@@ -121,11 +126,12 @@ def test_accumulation_module_and_strided_views(cuda):
     assert mod.get_cumulative_scores() is None
 
 
-def test_flash_attention_longer_sequence(cuda):
+@pytest.mark.parametrize("D", [128, 64])
+def test_flash_attention_longer_sequence(cuda, D):
     """N = 4096 causal with grouped heads: outputs on sampled rows and every
     key total against the oracle."""
     from cab_attention.kernels import flash_attention_with_cumulative_scores
-    B, H, Hkv, N, D = 1, 2, 1, 4096, 128
+    B, H, Hkv, N = 1, 2, 1, 4096
     q = seeded((B, H, N, D), 41, torch.bfloat16)
     k = seeded((B, Hkv, N, D), 42, torch.bfloat16)
     v = seeded((B, Hkv, N, D), 43, torch.bfloat16)

@@ -368,6 +368,63 @@ def test_sparse_attention_constant_scores_and_empty_rows():
     assert np.all(got[0, 0, 16:24] == 0)
 
 
+def test_sparse_attention_float32_mode_tracks_float64():
+    """The CPU baseline's float32 mode runs the same steps as the float64
+    checker: outputs agree to float32 rounding, empty rows stay 0."""
+    rng = np.random.default_rng(3)
+    q, k, v = (rng.standard_normal((1, 2, 300, 64)).astype(np.float32) for _ in range(3))
+    f = rng.standard_normal((1, 2, 5, 5)).astype(np.float32)
+    _, idx, cnt = O.generate_block_mask(f, 0.5, causal=True)
+    cnt[0, 1, 2] = 0
+    a = O.sparse_attention(q, k, v, idx, cnt, 64, causal=True)
+    b = O.sparse_attention(q, k, v, idx, cnt, 64, causal=True, compute_dtype=np.float32)
+    assert b.dtype == np.float32
+    np.testing.assert_allclose(b, a, atol=1e-5)
+    assert np.all(b[0, 1, 128:192] == 0)
+
+
+def test_frc_tolerance_closed_form():
+    """1e-3 (|Ahat| + |lambda| |Ahat| @ |Ahat|): the |.| is taken before the
+    product (a signed Ahat would cancel inside Ahat @ Ahat), and a given
+    t_abs is used as is."""
+    a = np.array([[[[1.0, -2.0], [3.0, -4.0]]]])
+    absa = np.abs(a[0, 0])
+    want = 1e-3 * (absa + 0.5 * (absa @ absa))
+    np.testing.assert_allclose(O.frc_tolerance(a, -0.5)[0, 0], want)
+    np.testing.assert_allclose(O.frc_tolerance(a, 0.5, t_abs=np.zeros_like(a)), 1e-3 * np.abs(a))
+
+
+def test_mask_far_differences_bands():
+    """Identical masks: agreement 1, nothing far. A swap across the row
+    threshold between two scores closer than their tolerances is a near-tie;
+    the same swap with a wider gap is two far entries; the selection it
+    compares against is generate_block_mask's."""
+    rng = np.random.default_rng(8)
+    f = rng.standard_normal((1, 2, 12, 12))
+    k = 4
+    mask = O.generate_block_mask(f, 0.625)[0]
+    assert O.keep_count(12, 0.625) == k
+    tol = np.full_like(f, 1e-6)
+    assert O.mask_far_differences(mask, f, tol, k) == (1.0, 0)
+    i = 5
+    others = np.array([j for j in range(12) if j != i])
+    order = others[np.argsort(f[0, 0, i, others], kind="stable")]
+    t, u = order[k - 2], order[k - 1]  # the threshold entry and the first one left out
+    f[0, 0, i, u] = f[0, 0, i, t] + 1e-7
+    mask = O.generate_block_mask(f, 0.625)[0]
+    assert O.keep_count(12, 0.625) == k
+    swapped = mask.copy()
+    swapped[0, 0, i, t], swapped[0, 0, i, u] = False, True
+    agree, far = O.mask_far_differences(swapped, f, tol, k)
+    assert far == 0 and agree == 1 - 2 / f.size
+    f[0, 0, i, u] = f[0, 0, i, t] + 1e-3
+    agree, far = O.mask_far_differences(swapped, f, tol, k)
+    assert far == 1  # u sits 1e-3 above the threshold; t is the threshold itself
+    wide = swapped.copy()
+    wide[0, 1, 0, :] = ~wide[0, 1, 0, :]
+    assert O.mask_far_differences(wide, f, tol, k)[1] >= 1 + 8
+
+
 def test_estimate_flops_closed_form():
     e = O.estimate_flops(131072, 128)
     assert e["M"] == 2048
