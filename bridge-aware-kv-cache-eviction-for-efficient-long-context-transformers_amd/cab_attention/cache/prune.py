@@ -12,9 +12,6 @@ import torch
 
 from .. import _native as nat
 
-MAX_TENSORS_PER_LAUNCH = 32
-
-
 def _rows_aligned(t: torch.Tensor) -> bool:
     es = t.element_size()
     return (t.stride(3) == 1 and t.data_ptr() % 16 == 0 and (t.shape[3] * es) % 16 == 0
@@ -22,11 +19,12 @@ def _rows_aligned(t: torch.Tensor) -> bool:
 
 
 def gather_into(srcs: Sequence[torch.Tensor], dsts: Sequence[torch.Tensor],
-                keep_indices: torch.Tensor, n_src: int) -> None:
+                keep_indices: torch.Tensor, n_src: int, validate: bool = True) -> None:
     """``dst[:, :, t, :] = src[:, :, keep[t], :]`` for pairs of ``[B, H, *, D]``
     views that share B, H, D, dtype and one stride set per side (rows 16-byte
     aligned). ``keep`` is int64 on the tensors' device; positions outside
-    ``[0, n_src)`` give zero rows."""
+    ``[0, n_src)`` give zero rows. ``validate=False`` skips the per-tensor
+    checks for callers whose buffers hold these properties by construction."""
     srcs, dsts = list(srcs), list(dsts)
     if not srcs:
         return
@@ -37,25 +35,24 @@ def gather_into(srcs: Sequence[torch.Tensor], dsts: Sequence[torch.Tensor],
         return
     es = ref.element_size()
     sstr, dstr = ref.stride(), dsts[0].stride()
-    for s, d in zip(srcs, dsts):
-        if (s.stride() != sstr or d.stride() != dstr or s.dtype != ref.dtype
-                or d.dtype != ref.dtype or s.shape[:2] != ref.shape[:2] or s.shape[3] != D
-                or d.shape[3] != D or d.shape[2] < n_keep
-                or not _rows_aligned(s) or not _rows_aligned(d)):
-            raise ValueError("gather_into: tensors must share shape, dtype, strides and 16-byte rows")
+    if validate:
+        for s, d in zip(srcs, dsts):
+            if (s.stride() != sstr or d.stride() != dstr or s.dtype != ref.dtype
+                    or d.dtype != ref.dtype or s.shape[:2] != ref.shape[:2] or s.shape[3] != D
+                    or d.shape[3] != D or d.shape[2] < n_keep
+                    or not _rows_aligned(s) or not _rows_aligned(d)):
+                raise ValueError("gather_into: tensors must share shape, dtype, strides and "
+                                 "16-byte rows")
     dev = ref.device
     ss = (ctypes.c_int64 * 4)(sstr[0] * es, sstr[1] * es, sstr[2] * es, 0)
     ds = (ctypes.c_int64 * 4)(dstr[0] * es, dstr[1] * es, dstr[2] * es, 0)
     lib = nat.load()
-    with torch.cuda.device(dev):
-        for at in range(0, len(srcs), MAX_TENSORS_PER_LAUNCH):
-            part_s = srcs[at:at + MAX_TENSORS_PER_LAUNCH]
-            part_d = dsts[at:at + MAX_TENSORS_PER_LAUNCH]
-            src_arr = (ctypes.c_void_p * len(part_s))(*[s.data_ptr() for s in part_s])
-            dst_arr = (ctypes.c_void_p * len(part_d))(*[d.data_ptr() for d in part_d])
-            st = lib.cab_kv_gather(src_arr, dst_arr, len(part_s), B, H, n_src, D * es, ss, ds,
-                                   keep_indices.data_ptr(), n_keep, nat.stream_ptr(dev))
-            nat.check("cab_kv_gather", st)
+    src_arr = (ctypes.c_void_p * len(srcs))(*[s.data_ptr() for s in srcs])
+    dst_arr = (ctypes.c_void_p * len(dsts))(*[d.data_ptr() for d in dsts])
+    with torch.cuda.device(dev):  # the library launches one kernel per 32 tensors
+        st = lib.cab_kv_gather(src_arr, dst_arr, len(srcs), B, H, n_src, D * es, ss, ds,
+                               keep_indices.data_ptr(), n_keep, nat.stream_ptr(dev))
+    nat.check("cab_kv_gather", st)
 
 
 def gather_positions(tensors: Sequence[torch.Tensor], keep_indices: torch.Tensor) -> List[torch.Tensor]:
@@ -81,7 +78,7 @@ def gather_positions(tensors: Sequence[torch.Tensor], keep_indices: torch.Tensor
     if any(s.stride() != srcs[0].stride() for s in srcs):
         srcs = [s.contiguous() for s in srcs]
     outs = [torch.empty((B, H, idx.numel(), D), dtype=ref.dtype, device=dev) for _ in tensors]
-    gather_into(srcs, outs, idx, N)
+    gather_into(srcs, outs, idx, N, validate=False)  # normalised above; outputs are fresh
     return outs
 
 

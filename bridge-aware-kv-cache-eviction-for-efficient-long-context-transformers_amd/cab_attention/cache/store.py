@@ -114,7 +114,7 @@ class LayeredKV:
                 idx = keep.detach().reshape(-1).to(device=dev, dtype=torch.int64).contiguous()
             srcs = [L.k for L in members] + [L.v for L in members]
             dsts = [L.k_spare for L in members] + [L.v_spare for L in members]
-            gather_into(srcs, dsts, idx, length)
+            gather_into(srcs, dsts, idx, length, validate=False)  # own buffers: aligned
         for L in self.layers:
             if L is None:
                 continue

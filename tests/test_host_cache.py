@@ -14,7 +14,7 @@ from cab_attention.cache.cab_cache import CABCache
 from cab_attention.cache.h2o_cache import H2OCache
 
 
-def torch_gather_into(srcs, dsts, keep, n_src):
+def torch_gather_into(srcs, dsts, keep, n_src, validate=True):
     for s, d in zip(srcs, dsts):
         rows = torch.zeros((s.shape[0], s.shape[1], keep.numel(), s.shape[3]), dtype=s.dtype)
         ok = (keep >= 0) & (keep < n_src)
