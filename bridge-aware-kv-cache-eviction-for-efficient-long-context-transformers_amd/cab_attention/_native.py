@@ -14,7 +14,7 @@ import threading
 import torch
 
 LIB_PATH = pathlib.Path(__file__).resolve().with_name("libcab_hip.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 CAB_OK, CAB_EINVAL, CAB_EDTYPE, CAB_ESHAPE, CAB_EWORKSPACE, CAB_EHIP = range(6)
 CAB_F32, CAB_F16, CAB_BF16 = 0, 1, 2
@@ -64,6 +64,9 @@ SIGNATURES = {
     "cab_evict_select": (ctypes.c_int, [_ptr, _i64, _ptr, _i64, _i32, _i32, _i32, ctypes.c_int,
                                         ctypes.c_int, _ptr, _ptr, _ptr, _ptr, ctypes.c_size_t,
                                         _ptr]),
+    "cab_evict_select_noalloc": (ctypes.c_int, [_ptr, _i64, _ptr, _i64, _i32, _i32, _i32,
+                                                ctypes.c_int, ctypes.c_int, _ptr, _ptr, _ptr,
+                                                _ptr]),
     "cab_evict_connectivity": (ctypes.c_int, [_ptr, _i64, _i64, _ptr, _ptr, _ptr]),
     "cab_kv_gather": (ctypes.c_int, [ctypes.POINTER(_ptr), ctypes.POINTER(_ptr), _i32, _i64, _i64,
                                      _i64, _i64, _i64x4, _i64x4, _ptr, _i64, _ptr]),

@@ -32,6 +32,8 @@
 //
 // kv_gather_kernel: out[t] = in[keep[t]] for the rows of up to 32 tensors
 // per launch (every layer's K and V), 16 bytes per thread; HBM-bound.
+#include <mutex>
+
 #include "cab_internal.h"
 
 namespace cab {
@@ -911,6 +913,22 @@ struct MLayout {
   size_t off_bits, off_hist, off_seg, off_state, total;
 };
 
+// Bytes of the multi-workgroup workspace for n positions (mlayout's total).
+constexpr size_t mworkspace_bytes(int64_t n) {
+  const int64_t G = ((n > 0 ? n : 1) + MSEG - 1) / MSEG;
+  auto r256 = [](int64_t b) { return static_cast<size_t>((b + 255) / 256 * 256); };
+  return r256(G * (MSEG / 32) * 4) + r256(int64_t{MHIST_ROWS} * SEL_BINS * 4) + r256(G * 4) +
+         r256(64 * 4);
+}
+
+// Scratch of cab_evict_select_noalloc: the workspace of the largest cache
+// (SEL_MAX_LEN positions, 206080 bytes), one copy per GPU for the life of
+// the process. Host code never passes the symbol itself to a kernel: it
+// takes the device address from hipGetSymbolAddress, per device.
+constexpr size_t NOALLOC_SCRATCH_BYTES = mworkspace_bytes(SEL_MAX_LEN);
+static_assert(NOALLOC_SCRATCH_BYTES == 206080, "the size the header documents");
+__device__ __align__(256) char scratch[NOALLOC_SCRATCH_BYTES];
+
 MLayout mlayout(int64_t n) {
   MLayout L;
   L.G = ceil_div(n > 0 ? n : 1, MSEG);
@@ -1092,6 +1110,61 @@ extern "C" cab_status_t cab_evict_select(const float* importance_scores, int64_t
   if ((r = launch_status(fn)) != CAB_OK) return r;
   msel_compact_write_kernel<<<grid, MTHREADS, 0, s>>>(a);
   return launch_status(fn);
+}
+
+namespace {
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[NOALLOC_MAX_DEVICES] = {};
+
+// The device address of the current device's scratch, looked up once per
+// device (with that device current) and kept.
+cab_status_t scratch_of_current_device(const char* fn, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  CAB_REQUIRE(e == hipSuccess, CAB_EHIP, "%s: hipGetDevice failed: %s", fn, hipGetErrorString(e));
+  CAB_REQUIRE(dev >= 0 && dev < NOALLOC_MAX_DEVICES, CAB_EINVAL, "%s: device %d beyond %d", fn,
+              dev, NOALLOC_MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    CAB_REQUIRE(e == hipSuccess && p != nullptr, CAB_EHIP,
+                "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", fn, dev,
+                hipGetErrorString(e));
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return CAB_OK;
+}
+
+}  // namespace
+
+extern "C" cab_status_t cab_evict_select_noalloc(const float* importance_scores,
+                                                 int64_t n_scores, const float* bridge_scores,
+                                                 int64_t cache_len, int32_t local_budget,
+                                                 int32_t importance_budget, int32_t bridge_budget,
+                                                 int importance_fallback, int bridge_mode,
+                                                 int64_t* keep_indices, int32_t* counts,
+                                                 uint8_t* category, void* stream) {
+  const char* fn = "cab_evict_select_noalloc";
+  clear_error();
+  CAB_REQUIRE(cache_len >= 0 && cache_len <= SEL_MAX_LEN, CAB_ESHAPE,
+              "%s: cache_len %lld outside [0, %d] (the size of the built-in scratch)", fn,
+              (long long)cache_len, SEL_MAX_LEN);
+  void* ws = nullptr;
+  if (cache_len >= MULTI_MIN) {
+    const size_t need = mlayout(cache_len).total;
+    CAB_REQUIRE(need <= NOALLOC_SCRATCH_BYTES, CAB_EWORKSPACE,
+                "%s: %zu scratch bytes needed, %zu built in", fn, need, NOALLOC_SCRATCH_BYTES);
+    cab_status_t st = scratch_of_current_device(fn, &ws);
+    if (st != CAB_OK) return st;
+  }
+  return cab_evict_select(importance_scores, n_scores, bridge_scores, cache_len, local_budget,
+                          importance_budget, bridge_budget, importance_fallback, bridge_mode,
+                          keep_indices, counts, category, ws, ws ? NOALLOC_SCRATCH_BYTES : 0,
+                          stream);
 }
 
 extern "C" cab_status_t cab_evict_connectivity(const float* attention, int64_t cache_len,

@@ -49,7 +49,7 @@ enum { CAB_NORM_NONE = 0, CAB_NORM_MINMAX = 1 };
 /* FRC combination (experiments/longbench_qa/config.py:465; test.ipynb:111-145). */
 enum { CAB_FRC_ADDITIVE = 0, CAB_FRC_MULTIPLICATIVE = 1, CAB_FRC_AUGMENTED = 2 };
 
-#define CAB_ABI_VERSION 7
+#define CAB_ABI_VERSION 8
 
 int cab_abi_version(void);
 const char* cab_last_error(void);
@@ -304,6 +304,25 @@ cab_status_t cab_evict_select(const float* importance_scores, int64_t n_scores,
                               int32_t bridge_budget, int importance_fallback, int bridge_mode,
                               int64_t* keep_indices, int32_t* counts, uint8_t* category,
                               void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * cab_evict_select without a workspace argument: no counterpart in the
+ * reference. For callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops that forbid hipMalloc). Same arguments,
+ * rules and results as cab_evict_select; the multi-workgroup path (cache_len
+ * >= 32768) uses a built-in device scratch array of 206080 bytes (the
+ * workspace of the largest cache, 2^20 positions), one per GPU, held until
+ * the process ends; larger caches return CAB_ESHAPE. The call allocates
+ * nothing. Every call on one GPU shares that GPU's scratch: calls that
+ * overlap in time on one GPU (different streams or host threads without
+ * ordering) race and must be serialised by the caller.
+ */
+cab_status_t cab_evict_select_noalloc(const float* importance_scores, int64_t n_scores,
+                                      const float* bridge_scores, int64_t cache_len,
+                                      int32_t local_budget, int32_t importance_budget,
+                                      int32_t bridge_budget, int importance_fallback,
+                                      int bridge_mode, int64_t* keep_indices, int32_t* counts,
+                                      uint8_t* category, void* stream);
 
 /*
  * Bridge scores of the policy's attention-matrix mode (policy.py:122-131):

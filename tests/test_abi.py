@@ -249,6 +249,14 @@ def test_eviction_validation(lib):
     assert sel(n=big, ns=big, ws=FAKE, wsb=wsb - 1) == nat.CAB_EWORKSPACE
     assert sel(n=big, ns=big, ws=FAKE + 16, wsb=wsb) == nat.CAB_EWORKSPACE
     assert sel(n=(1 << 20) + 1) == nat.CAB_ESHAPE
+    # the no-allocation variant: same checks, its scratch holds 2^20 positions
+    noalloc = lambda **kw: lib.cab_evict_select_noalloc(
+        FAKE, 10, None, kw.get("n", 100), kw.get("loc", 1), 2, 3, 1, kw.get("mode", 1), FAKE,
+        FAKE, None, None)
+    assert noalloc(n=(1 << 20) + 1) == nat.CAB_ESHAPE
+    assert b"scratch" in lib.cab_last_error()
+    assert noalloc(loc=101) == nat.CAB_EINVAL
+    assert noalloc(mode=4) == nat.CAB_EINVAL
     assert sel(local=11) == nat.CAB_EINVAL
     assert sel(imp=-1) == nat.CAB_EINVAL
     assert sel(mode=4) == nat.CAB_EINVAL
