@@ -263,6 +263,20 @@ __device__ __forceinline__ void dma16(const char* g, char* l) {
   __builtin_amdgcn_global_load_lds(g, (lds_void*)l, 16, OFF, 0);
 }
 
+// 16-byte buffer load to LDS per lane: bytes [voff + soff, +16) of the buffer
+// r land at LDS l + 16 * lane. Offsets at or past the buffer's size read as
+// zero. The per-lane offset is a 32-bit register and the base a scalar
+// descriptor, so no per-lane 64-bit address arithmetic is spent on a load.
+typedef __amdgpu_buffer_rsrc_t brsrc_t;
+__device__ __forceinline__ brsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  // word 3 0x00020000: raw (untyped) dword access, the gfx9 buffer default
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ void bdma16(brsrc_t r, uint32_t voff, uint32_t soff, char* l) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)l, 16, voff, soff, 0, 0);
+}
+
 // gfx950 lane swaps between the two halves of two registers (v_permlane32_swap:
 // 32-lane halves; v_permlane16_swap: odd and even 16-lane rows), written as
 // inline asm because the compiler's builtins return the first result twice.
@@ -460,13 +474,15 @@ __device__ __forceinline__ void acc_block(WaveAcc<HD>& s, const WaveGeo<HD>& ge,
                                      __builtin_fmaxf(sc[1][qt][2], sc[1][qt][3]));
     mx[qt] = __builtin_fmaxf(m0, m1);
   }
-  colmax2(mx[0], mx[1]);
   // Rescale only when a query's maximum grew by more than 2^RESCALE_LOG2
-  // in exp2 units (always on its first non-empty block).
-  const bool grow0 = __builtin_fmaf(mx[0], c, s.nmc[0]) > RESCALE_LOG2;
-  const bool grow1 = __builtin_fmaf(mx[1], c, s.nmc[1]) > RESCALE_LOG2;
-  if (__builtin_amdgcn_ballot_w64(grow0 || grow1)) {
-    const bool grow[2] = {grow0, grow1};
+  // in exp2 units (always on its first non-empty block). A query's keys sit
+  // in the four lane groups l16 + 16 g: the lane-local maxima tell whether
+  // any query can have grown, and only then are the column maxima formed.
+  if (__builtin_amdgcn_ballot_w64(__builtin_fmaf(mx[0], c, s.nmc[0]) > RESCALE_LOG2 ||
+                                  __builtin_fmaf(mx[1], c, s.nmc[1]) > RESCALE_LOG2)) {
+    colmax2(mx[0], mx[1]);
+    const bool grow[2] = {__builtin_fmaf(mx[0], c, s.nmc[0]) > RESCALE_LOG2,
+                          __builtin_fmaf(mx[1], c, s.nmc[1]) > RESCALE_LOG2};
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
       const float m_new = grow[qt] ? mx[qt] : s.m_run[qt];
@@ -586,15 +602,7 @@ __device__ __forceinline__ uint32_t k_lane_off(int group, int lane, int64_t krow
   return static_cast<uint32_t>(row * krow_bytes + 16 * ((lane % G::CPR) ^ G::kswz(row)));
 }
 
-template <int HD>
-__device__ __forceinline__ const char* k_lane_ptr_clamped(const char* kbytes, int j, int group,
-                                                          int lane, int N, int64_t krow_bytes) {
-  using G = Dims<HD>;
-  const int rr = G::ROWS_PER_LOAD * group + lane / G::CPR;
-  const int row = j * BS + rr;
-  const int64_t rb = (row < N ? row : N - 1) * krow_bytes;
-  return kbytes + rb + 16 * ((lane % G::CPR) ^ G::kswz(rr));
-}
+
 
 // ---------------------------------------------------------------------------
 // attn_fwd_kernel: one query block per workgroup of 4 waves, two LDS stages;
@@ -666,9 +674,11 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
   };
 
   // Staging of key block j by the 4 waves: wave w fetches its NI KB of K
-  // rows (rows 16 w .. +15 at D = 128) and of the V^T tile, one 1 KB load
-  // each. fp32: the block image is a copy of the stage; wave w copies its
-  // quarter w (one tile's bytes).
+  // rows (rows 16 w .. +15 at D = 128) and of the V^T tile, one 1 KB buffer
+  // load each, through descriptors based at the block (K: its valid rows, so
+  // rows at or past Nk read as zero; V^T: the whole tile). fp32: the block
+  // image is a copy of the stage; wave w copies its quarter w (one tile's
+  // bytes).
   const int64_t krow_bytes = a.ks[2] * 2;
   const int64_t kblk_bytes = BS * krow_bytes;
   uint32_t koff[NI];
@@ -689,24 +699,14 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
       return;
     }
     char* kl = reinterpret_cast<char*>(kst) + w * NI * 1024;
-    if ((j + 1) * BS <= Nk) {
-      const char* kbj = kbytes + j * kblk_bytes;
+    const int rows = Nk - j * BS < BS ? Nk - j * BS : BS;
+    const brsrc_t krs = make_rsrc(kbytes + j * kblk_bytes, static_cast<uint32_t>(rows * krow_bytes));
 #pragma unroll
-      for (int r = 0; r < NI; ++r) dma16<0>(kbj + koff[r], kl + 1024 * r);
-    } else {
-#pragma unroll
-      for (int r = 0; r < NI; ++r)
-        dma16<0>(k_lane_ptr_clamped<HD>(kbytes, j, NI * w + r, ge.lane, Nk, krow_bytes),
-                 kl + 1024 * r);
-    }
-    const char* vp = vtbytes + static_cast<int64_t>(j) * TILE_BYTES + voff;
+    for (int r = 0; r < NI; ++r) bdma16(krs, koff[r], 0, kl + 1024 * r);
+    const brsrc_t vrs = make_rsrc(vtbytes + static_cast<int64_t>(j) * TILE_BYTES, TILE_BYTES);
     char* vl = reinterpret_cast<char*>(vst) + w * NI * 1024;
-    dma16<0>(vp, vl);
-    dma16<1024>(vp, vl);
-    if constexpr (NI == 4) {
-      dma16<2048>(vp, vl);
-      dma16<3072>(vp, vl);
-    }
+#pragma unroll
+    for (int r = 0; r < NI; ++r) bdma16(vrs, voff, 1024 * r, vl + 1024 * r);
   };
 
   WaveAcc<HD> st;
