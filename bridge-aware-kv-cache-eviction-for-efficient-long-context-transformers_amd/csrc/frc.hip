@@ -413,8 +413,11 @@ struct TriArgs {
 // LDS operand tile in MFMA order: slot (kk, sub, lane) of 16 bytes holds the
 // 8 consecutive k values lane needs for a 32x32x16 MFMA, so every operand
 // read is one 1 KB wave access. Inside each 64-slot group the slot of lane L
-// is stored at position L ^ (4 (2 kk + L / 32)): the threads that load one
-// row's bytes then write different LDS bank groups.
+// is stored at position L ^ swz(kk, L / 32), swz(kk, h) = 2 (2 kk + h): the
+// eight chunks of one row (kc = 2 kk + h) then land in eight different
+// 16-byte bank groups, and the two rows sixteen threads store fill all
+// sixteen (bit 0 of the position is the row's); a wave's reads stay a
+// permutation inside each 16-slot bank cycle.
 template <int TILE, int KD>
 constexpr int tri_slots() { return (KD / 16) * (TILE / 32) * 64; }
 
@@ -444,7 +447,7 @@ __device__ __forceinline__ void tri_store(u32x4* lds, const u32x4 (&reg)[tri_chu
     const int cid = threadIdx.x + THREADS * q;
     const int row = cid / CPR, kc = cid % CPR;
     const int kk = kc >> 1, hf = kc & 1, sub = row >> 5;
-    lds[(kk * (TILE / 32) + sub) * 64 + (((row & 31) + 32 * hf) ^ (4 * (2 * kk + hf)))] = reg[q];
+    lds[(kk * (TILE / 32) + sub) * 64 + (((row & 31) + 32 * hf) ^ (2 * (2 * kk + hf)))] = reg[q];
   }
 }
 
@@ -523,7 +526,7 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
     const u32x4* lb = la + NH * SA;
 #pragma unroll
     for (int kk = 0; kk < KD / 16; ++kk) {
-      const int lsw = lane ^ (4 * (2 * kk + (lane >> 5)));
+      const int lsw = lane ^ (2 * (2 * kk + (lane >> 5)));
       if constexpr (F16) {
         f16x8 b8[YS];
 #pragma unroll
@@ -614,13 +617,13 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
         for (int q = 0; q < CAH; ++q) {
           const int cid = tg + 256 * q, row = gp * HA + cid / CPR, kc = cid % CPR;
           const int kk = kc >> 1, hf = kc & 1, sub = row >> 5;
-          la[(kk * (TI / 32) + sub) * 64 + (((row & 31) + 32 * hf) ^ (4 * (2 * kk + hf)))] = pra[q];
+          la[(kk * (TI / 32) + sub) * 64 + (((row & 31) + 32 * hf) ^ (2 * (2 * kk + hf)))] = pra[q];
         }
 #pragma unroll
         for (int q = 0; q < CBH; ++q) {
           const int cid = tg + 256 * q, row = gp * HB + cid / CPR, kc = cid % CPR;
           const int kk = kc >> 1, hf = kc & 1, sub = row >> 5;
-          lb[(kk * (TJ / 32) + sub) * 64 + (((row & 31) + 32 * hf) ^ (4 * (2 * kk + hf)))] = prb[q];
+          lb[(kk * (TJ / 32) + sub) * 64 + (((row & 31) + 32 * hf) ^ (2 * (2 * kk + hf)))] = prb[q];
         }
       };
       pload(0);

@@ -81,8 +81,17 @@ __device__ __forceinline__ void for_chunks(int nch, F f) {
   }
 }
 
+// A key no real score maps to (order_key never returns all ones): it stands
+// for a column that is not a candidate, so that every candidate ranks below
+// it.
+constexpr uint32_t KEY_NONE = 0xffffffffu;
+
 // key(c) is this lane's key in chunk c: a register, or (NCH == 0) a load.
-template <int NCH, typename Key, typename Cand>
+// SENT: non-candidates already carry KEY_NONE (is_cand is not consulted), so
+// the histogram passes are branch-free: every key adds 1 to its bin when it
+// matches the prefix and 0 otherwise. A KEY_NONE key that matches the prefix
+// lands above every candidate of its bin and never decides a rank.
+template <int NCH, bool SENT, typename Key, typename Cand>
 __device__ __forceinline__ uint32_t kth_key(Key key, Cand is_cand, int nch, int64_t need,
                                             int64_t& need_eq, uint32_t* hist) {
   const int lane = lane_id();
@@ -90,7 +99,11 @@ __device__ __forceinline__ uint32_t kth_key(Key key, Cand is_cand, int nch, int6
   if (need <= 0) return 0u;
   uint32_t kand = 0xffffffffu, kor = 0u;
   for_chunks<NCH>(nch, [&](int c) {
-    if (is_cand(c)) {
+    if constexpr (SENT) {
+      const uint32_t kc = key(c);
+      kand &= kc;
+      kor |= kc != KEY_NONE ? kc : 0u;
+    } else if (is_cand(c)) {
       const uint32_t kc = key(c);
       kand &= kc;
       kor |= kc;
@@ -128,12 +141,19 @@ __device__ __forceinline__ uint32_t kth_key(Key key, Cand is_cand, int nch, int6
     wave_sync();
     const uint32_t sub = static_cast<uint32_t>(lane % HSUB);
     for_chunks<NCH>(nch, [&](int c) {
-      if (!is_cand(c)) return;
-      const uint32_t kc = key(c);
-      if ((kc & pmask) == prefix) {
+      if constexpr (SENT) {
+        const uint32_t kc = key(c);
         const uint32_t bn = (kc >> shift) & 255u;
         const uint32_t q = 2u * (bn & 3u) + (sub >> 2);
-        atomicAdd(&hist[4u * (64u * q + (bn >> 2)) + (sub & 3u)], 1u);
+        atomicAdd(&hist[4u * (64u * q + (bn >> 2)) + (sub & 3u)], (kc & pmask) == prefix ? 1u : 0u);
+      } else {
+        if (!is_cand(c)) return;
+        const uint32_t kc = key(c);
+        if ((kc & pmask) == prefix) {
+          const uint32_t bn = (kc >> shift) & 255u;
+          const uint32_t q = 2u * (bn & 3u) + (sub >> 2);
+          atomicAdd(&hist[4u * (64u * q + (bn >> 2)) + (sub & 3u)], 1u);
+        }
       }
     });
     wave_sync();
@@ -177,9 +197,9 @@ __device__ __forceinline__ uint32_t kth_key(Key key, Cand is_cand, int nch, int6
       // One candidate left (rem == 1): theta is its key.
       uint32_t kv = 0u;
       for_chunks<NCH>(nch, [&](int c) {
-        if (!is_cand(c)) return;
+        if (!SENT && !is_cand(c)) return;
         const uint32_t kc = key(c);
-        if ((kc & pmask) == prefix) kv = kc;
+        if ((kc & pmask) == prefix && (!SENT || kc != KEY_NONE)) kv = kc;
       });
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1)
@@ -209,8 +229,14 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   uint32_t* hist = hist_all[threadIdx.x >> 6];
 
   // Loads are unconditional (the index is clamped) so that all NCH are in
-  // flight together; columns past M get the largest key.
+  // flight together; columns that are no candidate (past M, past the causal
+  // limit, the forced diagonal) get KEY_NONE.
   const int Mi = static_cast<int>(a.M);
+  const int ncand_i = static_cast<int>(ncand), i_i = static_cast<int>(i);
+  auto is_cand = [&](int c) {
+    const int j = 64 * c + lane;
+    return j < ncand_i && !(kd && j == i_i);
+  };
   uint32_t key[NCH];
   {
     float v[NCH];
@@ -222,13 +248,8 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
 #pragma unroll
     for (int c = 0; c < NCH; ++c) asm volatile("" ::"v"(v[c]));  // keeps the loads unconditional
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) key[c] = 64 * c + lane < Mi ? order_key(v[c], high) : 0xffffffffu;
+    for (int c = 0; c < NCH; ++c) key[c] = is_cand(c) ? order_key(v[c], high) : KEY_NONE;
   }
-  const int ncand_i = static_cast<int>(ncand), i_i = static_cast<int>(i);
-  auto is_cand = [&](int c) {
-    const int j = 64 * c + lane;
-    return j < ncand_i && !(kd && j == i_i);
-  };
 
   // Hybrid: the need_m candidates of highest magnitude first (bit c of msel
   // marks register c of this lane as taken).
@@ -250,15 +271,15 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
 #pragma unroll
       for (int c = 0; c < NCH; ++c) asm volatile("" ::"v"(v[c]));
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) mkey[c] = 64 * c + lane < Mi ? order_key(v[c], true) : 0xffffffffu;
+      for (int c = 0; c < NCH; ++c) mkey[c] = is_cand(c) ? order_key(v[c], true) : KEY_NONE;
     }
     int64_t meq = 0;
     const uint32_t mtheta =
-        kth_key<NCH>([&](int c) { return mkey[c]; }, is_cand, NCH, need_m, meq, hist);
+        kth_key<NCH, true>([&](int c) { return mkey[c]; }, is_cand, NCH, need_m, meq, hist);
     int64_t eq_seen = 0;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      const bool cand = is_cand(c) && need_m > 0;
+      const bool cand = mkey[c] != KEY_NONE && need_m > 0;
       const bool eq = cand && mkey[c] == mtheta;
       const uint64_t eqb = ballot64(eq);
       const int64_t eq_rank = eq_seen + __popcll(eqb & lt_mask);
@@ -267,20 +288,23 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
     }
   }
   auto taken = [&](int c) { return ((msel[c >> 6] >> (c & 63)) & 1ull) != 0; };
-  auto is_cand_f = [&](int c) { return is_cand(c) && !taken(c); };
+  if constexpr (HYB) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) key[c] = taken(c) ? KEY_NONE : key[c];
+  }
 
-  // FRC order for the rest of the row.
+  // FRC order for the rest of the row (taken columns now carry KEY_NONE).
   const int64_t need_f = need - need_m;
   int64_t need_eq = 0;
   const uint32_t theta =
-      kth_key<NCH>([&](int c) { return key[c]; }, is_cand_f, NCH, need_f, need_eq, hist);
+      kth_key<NCH, true>([&](int c) { return key[c]; }, is_cand, NCH, need_f, need_eq, hist);
 
   int64_t pos = 0, eq_seen = 0;
   int32_t* out = a.kv_idx + row * a.k;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int64_t j = 64 * c + lane;
-    const bool cand = is_cand_f(c) && need_f > 0;
+    const bool cand = key[c] != KEY_NONE && need_f > 0;
     const bool eq = cand && key[c] == theta;
     const uint64_t eqb = ballot64(eq);
     const int64_t eq_rank = eq_seen + __popcll(eqb & lt_mask);
@@ -338,7 +362,7 @@ __global__ __launch_bounds__(256) void topk_stream_kernel(TopkArgs a) {
   if constexpr (HYB) {
     need_m = min(static_cast<int64_t>(a.kmag), need);
     int64_t meq = 0;
-    mtheta = kth_key<0>(mkey, is_cand, nch, need_m, meq, hist);
+    mtheta = kth_key<0, false>(mkey, is_cand, nch, need_m, meq, hist);
     if (need_m > 0 && meq > 0) {
       int64_t seen = 0;
       for (int c = 0; c < nch && jm_last < 0; ++c) {  // uniform: ballots only
@@ -362,7 +386,7 @@ __global__ __launch_bounds__(256) void topk_stream_kernel(TopkArgs a) {
 
   const int64_t need_f = need - need_m;
   int64_t need_eq = 0;
-  const uint32_t theta = kth_key<0>(fkey, is_cand_f, nch, need_f, need_eq, hist);
+  const uint32_t theta = kth_key<0, false>(fkey, is_cand_f, nch, need_f, need_eq, hist);
 
   int64_t pos = 0, eq_seen = 0;
   int32_t* out = a.kv_idx + row * a.k;

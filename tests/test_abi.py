@@ -304,3 +304,31 @@ def test_token_frc_validation(lib):
     assert fk(f=None) == nat.CAB_EINVAL
     assert fk(wsb=ws - 1) == nat.CAB_EWORKSPACE
     assert fk(ws=FAKE + 16) == nat.CAB_EWORKSPACE
+
+
+def test_visualize_frc_statistics_on_host(tmp_path):
+    """visualize_frc_statistics (README.md:106-111) is host-only: its
+    summary equals numpy's over the same diagnostics, and with matplotlib
+    present it writes the histogram figure."""
+    import numpy as np
+    from cab_attention.kernels.frc_kernel import visualize_frc_statistics
+    from oracle import cab_oracle as O
+    rng = np.random.default_rng(12)
+    qc = rng.standard_normal((1, 2, 40, 32)).astype(np.float32)
+    kc = rng.standard_normal((1, 2, 40, 32)).astype(np.float32)
+    f, a, t = O.compute_block_frc(qc, kc, lambda_redundancy=0.5)
+    path = tmp_path / "frc.png"
+    st = visualize_frc_statistics(torch.from_numpy(f), torch.from_numpy(a), torch.from_numpy(t),
+                                  save_path=str(path))
+    f32 = f.astype(np.float32).astype(np.float64)
+    assert st["frc_mean"] == pytest.approx(f32.mean(), rel=1e-5)
+    assert st["frc_std"] == pytest.approx(f32.std(ddof=1), rel=1e-4)
+    assert st["frc_min"] == pytest.approx(f32.min()) and st["frc_max"] == pytest.approx(f32.max())
+    assert st["frc_negative_fraction"] == pytest.approx((f < 0).mean())
+    assert st["affinity_mean"] == pytest.approx(a.mean(), rel=1e-5)
+    assert st["triangles_mean"] == pytest.approx(t.mean(), rel=1e-5)
+    try:
+        import matplotlib  # noqa: F401
+    except ImportError:
+        return
+    assert path.exists() and path.stat().st_size > 1000

@@ -116,6 +116,38 @@ def test_frc_from_keys_matches_oracle(cuda, dt, B, H, N, D):
     assert np.all(np.abs(f64(got["frc"]) - want["frc"]) <= 3 * tol_t + 4e-6)
 
 
+@pytest.mark.parametrize("dt", ["fp32", "bf16", "fp16"])
+def test_frc_from_keys_element_wise_loads(cuda, dt):
+    """Layouts the 16-byte load path cannot take run the element-wise prep
+    path (keys_prep_kernel<T, false>): D not a multiple of 8, a last-dim
+    strided view, and keys starting one element past a 16-byte boundary;
+    each is checked against the oracle as the contiguous case is."""
+    from cab_attention.kernels import frc_from_keys
+    g = torch.Generator().manual_seed(77)
+    B, H, N = 1, 2, 301
+    cases = []
+    k100 = torch.randn((B, H, N, 100), generator=g).to(DTYPES[dt])
+    cases.append(("D=100", k100, k100.to(cuda)))
+    wide = torch.randn((B, H, N, 2 * 64), generator=g).to(DTYPES[dt])
+    strided = wide.to(cuda)[..., ::2]
+    assert strided.stride(-1) == 2
+    cases.append(("last-dim stride 2", wide[..., ::2], strided))
+    flat = torch.randn(B * H * N * 64 + 1, generator=g).to(DTYPES[dt])
+    off = flat.to(cuda)[1:].view(B, H, N, 64)
+    assert off.data_ptr() % 16 != 0
+    cases.append(("offset by one element", flat[1:].view(B, H, N, 64), off))
+    for name, host, dev in cases:
+        got = frc_from_keys(dev, return_parts=True)
+        kd = f64(host)
+        want = O.frc_from_keys(kd)
+        bound = _gram_bound(kd)
+        r = f64(got["row_sums"])
+        assert np.all(np.abs(r - want["row_sums"]) <= bound), name
+        tol_t = 2 * bound / want["row_sums"] + 2e-6
+        assert np.all(np.abs(f64(got["triangles"]) - want["triangles"]) <= tol_t), name
+        assert np.all(np.abs(f64(got["frc"]) - want["frc"]) <= 3 * tol_t + 4e-6), name
+
+
 def test_frc_from_keys_special_inputs(cuda):
     """Zero keys score 0; parallel and antipodal keys give the closed-form
     all-ones and identity graphs; a [B, N, H, D] layout passed as a
