@@ -12,9 +12,11 @@
 //     two workgroups per CU. Wave (kh, qh) owns key half kh (keys 32 kh ..
 //     32 kh + 31) of every kept key block and query half qh (32 queries).
 //     The 4 waves stage each kept key block (K rows and the packed V^T tile,
-//     32 KB) into one of two LDS stages with direct-to-LDS loads
-//     (global_load_lds_dwordx4), one block ahead; per block each wave reads
-//     its K half and V^T half from LDS and computes
+//     32 KB) into one of two LDS stages with 16-byte buffer loads to LDS,
+//     one block ahead: the loads of block p + 1 are issued two at a time
+//     between the score MFMAs of block p (a load waits for a free slot in the
+//     CU's 64 B/clk load path; spread out, the wait does not hold MFMAs back).
+//     Per block each wave reads its K half and V^T half from LDS and computes
 //       S^T = K_kh Q^T    (16 MFMA 16x16x32: A = K rows, B = Q in registers)
 //       online softmax over its 32 keys, fp32, log2 domain
 //       O^T += V_kh^T P^T (16 MFMA 16x16x32: A = packed V^T, B = P)
@@ -406,10 +408,10 @@ __device__ __forceinline__ bool block_needs_mask(int j, int i, bool valid, int N
 // fp32 (split operands, the lo halves 16 KB past the hi ones in LDS):
 // 48 + 48 + 4 MFMA. Keys at or past Nk and (causal) keys after t + qoff for
 // query t are dropped.
-template <cab_dtype_t DT, int HD>
+template <cab_dtype_t DT, int HD, typename Stager>
 __device__ __forceinline__ void acc_block(WaveAcc<HD>& s, const WaveGeo<HD>& ge, const char* ks,
                                           const u32x4* vts, int j, int i, bool valid, int Nk,
-                                          bool causal, int qoff, float c) {
+                                          bool causal, int qoff, float c, const Stager& stg) {
   using G = Dims<HD>;
   constexpr int NDS = G::NDS, NDT = G::NDT;
   constexpr int TT_BYTES = 16 * G::ROW_BYTES;  // 16 K rows
@@ -441,7 +443,7 @@ __device__ __forceinline__ void acc_block(WaveAcc<HD>& s, const WaveGeo<HD>& ge,
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) sc[tt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int ds = 0; ds < NDS; ++ds)
+  for (int ds = 0; ds < NDS; ++ds) {
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -452,6 +454,13 @@ __device__ __forceinline__ void acc_block(WaveAcc<HD>& s, const WaveGeo<HD>& ge,
         }
         sc[tt][qt] = mfma16<BF16>(kop[ds][tt], s.qreg[qt][ds], sc[tt][qt]);
       }
+    if constexpr (!SPLIT) {
+      // the next block's staging loads, spread between the score MFMAs
+      __builtin_amdgcn_sched_barrier(0);
+      stg(ds);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
 
   if (block_needs_mask(j, i, valid, Nk, causal, qoff)) {
 #pragma unroll
@@ -685,6 +694,23 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
 #pragma unroll
   for (int r = 0; r < NI; ++r) koff[r] = k_lane_off<HD>(NI * w + r, ge.lane, krow_bytes);
   const int voff = w * NI * 1024 + 16 * ge.lane;
+  // Loads 2 NI / NDS of the 2 NI staging loads of block j (part ds of NDS).
+  auto stage_part = [&](int j, u32x4* kst, u32x4* vst, int ds) {
+    constexpr int PER = 2 * NI / G::NDS;
+    char* kl = reinterpret_cast<char*>(kst) + w * NI * 1024;
+    const int rows = Nk - j * BS < BS ? Nk - j * BS : BS;
+    const brsrc_t krs = make_rsrc(kbytes + j * kblk_bytes, static_cast<uint32_t>(rows * krow_bytes));
+    const brsrc_t vrs = make_rsrc(vtbytes + static_cast<int64_t>(j) * TILE_BYTES, TILE_BYTES);
+    char* vl = reinterpret_cast<char*>(vst) + w * NI * 1024;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int r = ds * PER + q;
+      if (r < NI)
+        bdma16(krs, koff[r], 0, kl + 1024 * r);
+      else
+        bdma16(vrs, voff, 1024 * (r - NI), vl + 1024 * (r - NI));
+    }
+  };
   auto stage = [&](int j, u32x4* kst, u32x4* vst) {
     if constexpr (SPLIT) {
       const char* gp = vtbytes + j * BLOCK_BYTES + w * TILE_BYTES + 16 * ge.lane;
@@ -727,12 +753,23 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
       __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's staging of block p landed
       __builtin_amdgcn_s_barrier();        // ... and every wave's; stage PAR ^ 1 is free
       int jnext = 0;
-      if (p + 1 < cnt) {
-        jnext = entry(p + 1);
-        stage(block_of(jnext), stage_k(PAR ^ 1), stage_v(PAR ^ 1));
+      if constexpr (SPLIT) {
+        if (p + 1 < cnt) {
+          jnext = entry(p + 1);
+          stage(block_of(jnext), stage_k(PAR ^ 1), stage_v(PAR ^ 1));
+        }
+        acc_block<DT, HD>(st, ge, reinterpret_cast<const char*>(stage_k(PAR)), stage_v(PAR), j,
+                          i, valid, Nk, a.causal, a.qoff, c, [](int) {});
+      } else {
+        // unconditional (the last step re-stages a valid block into the free
+        // stage; waited for after the loop) so that the loads sit between the MFMAs
+        const int e = entry(p + 1 < cnt ? p + 1 : cnt - 1);
+        jnext = p + 1 < cnt ? e : 0;
+        const int js = block_of(jnext);
+        acc_block<DT, HD>(st, ge, reinterpret_cast<const char*>(stage_k(PAR)), stage_v(PAR), j,
+                          i, valid, Nk, a.causal, a.qoff, c,
+                          [&](int ds) { stage_part(js, stage_k(PAR ^ 1), stage_v(PAR ^ 1), ds); });
       }
-      acc_block<DT, HD>(st, ge, reinterpret_cast<const char*>(stage_k(PAR)), stage_v(PAR), j,
-                        i, valid, Nk, a.causal, a.qoff, c);
       jraw = jnext;
     };
     for (int p = 0; p < cnt; p += 2) {
@@ -741,6 +778,7 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
     }
   }
 
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the last step's staging landed
   __syncthreads();
   static_assert(2 * G::XCHG_FLOATS * 4 <= 2 * STAGE_SLOTS * 16, "merge buffer fits the stages");
   float* xo = reinterpret_cast<float*>(smem) + ge.qh * G::XCHG_FLOATS;
