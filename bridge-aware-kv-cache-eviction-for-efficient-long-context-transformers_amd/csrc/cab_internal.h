@@ -136,4 +136,24 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// ----------------------------------------------------------------------------
+// Buffer loads to LDS
+// ----------------------------------------------------------------------------
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// 16-byte buffer load to LDS per lane: bytes [voff + soff, +16) of the buffer
+// r land at LDS l + 16 * lane. Offsets at or past the buffer's size read as
+// zero. The per-lane offset is a 32-bit register and the base a scalar
+// descriptor, so no per-lane 64-bit address arithmetic is spent on a load.
+typedef __amdgpu_buffer_rsrc_t brsrc_t;
+__device__ __forceinline__ brsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  // word 3 0x00020000: raw (untyped) dword access, the gfx9 buffer default
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ void bdma16(brsrc_t r, uint32_t voff, uint32_t soff, char* l) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)l, 16, voff, soff, 0, 0);
+}
+
 }  // namespace cab

@@ -1,11 +1,11 @@
 // Coarse Forman-Ricci curvature (cab_block_frc).
 //
 // Pipeline per (b, h), Mp = M rounded up to 128:
-//  1. affinity_stats_kernel: A = qc kc^T * alpha on MFMA (256x256 tile per
-//     workgroup, 64x128 of eight 32x32 tiles per wave), per-tile min/max
-//     partials.
+//  1. STATS: A = qc kc^T * alpha on MFMA, per-tile min/max partials
+//     (aff_tile_kernel for 16-bit inputs with D <= 128: LDS-staged 128 x 128
+//     tiles; affinity_stats_kernel otherwise: operands straight from memory).
 //  2. minmax_finalize_kernel: per-(b,h) min/max from the partials.
-//  3. affinity_kernel (EMIT): recomputes the A tile, normalises it, and writes
+//  3. EMIT (aff_tile_kernel / affinity_kernel): recomputes the A tile, normalises it, and writes
 //     Ahat in row-major X and transposed XT planes (zero outside M), the fp32
 //     Ahat diagnostic and, for the augmented formula, row-sum partials. The
 //     planes hold either
@@ -252,7 +252,8 @@ __global__ __launch_bounds__(256) void affinity_kernel(AffArgs a) {
       for (int e = 0; e < 16; ++e) {
         float v = 0.f;
         if (row0 + qrow(x, e) < a.M && col0 + qcol(y) < a.M) {
-          v = acc[x][y][e] * a.alpha;
+#pragma clang fp contract(off)
+          v = acc[x][y][e] * a.alpha;  // rounded as in STATS (no fused multiply-add)
           if (a.normalization == CAB_NORM_MINMAX) v = normalize_minmax(v, mn, mx);
         }
         acc[x][y][e] = v;
@@ -355,6 +356,285 @@ __global__ __launch_bounds__(256) void affinity_kernel(AffArgs a) {
         const int64_t i = ti0 + r, jj = tj0 + c;
         if (i < a.M && jj < a.M) a.affinity[(static_cast<size_t>(bh) * a.M + i) * a.M + jj] = stile[r][c];
       }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// aff_tile_kernel: the STATS and EMIT passes for 16-bit inputs with D <= 128,
+// one 128 x 128 tile of A per workgroup of NW waves, two workgroups per CU
+// (one stages its panels while the other computes).
+// Both 128-row panels (Qc rows i, Kc rows j of the tile) are staged once into
+// LDS with buffer loads, 256 bytes per row, 16-byte chunk c of row R at chunk
+// position c ^ (R % 16) (the 16 rows one operand read touches fall into 16
+// distinct bank groups); rows at or past M and dims at or past D read as zero.
+// Wave w computes rows j 64 (w / (NW / 2)) .. +64 (two MFMA tiles) and NY
+// tiles of 32 columns i of C = Kc Qc^T (C[j][i] = A[i][j] / alpha) with
+// 32x32x16 MFMAs; lane l then holds column i = l % 32 of each tile and rows
+// j = 8 (e / 4) + 4 (l / 32) + e % 4 of element e: runs of four consecutive
+// j of one row i of A.
+// STATS: min / max of A over i, j < M per tile.
+// EMIT: both plane orientations go through LDS tiles (reusing the panels'
+// space) so that every global store is a whole 16-byte piece of a row:
+//   X tile [128 i][128 j]: 8-byte writes of the runs, chunk c of row il at
+//     chunk position c ^ (il % 16);
+//   XT tile [128 j][128 i]: 2-byte writes (a wave's 32 lanes of one row j
+//     are consecutive i).
+// Row-sum partials per 64 columns for the augmented formula.
+// Work per tile: 2 128^2 D flops; EMIT writes 32 KB per plane.
+// ---------------------------------------------------------------------------
+constexpr int AGT = 128;                 // tile edge and panel rows
+constexpr int AG_PANEL = AGT * 256;      // bytes of one staged panel
+constexpr int AG_DMAX = 128;             // largest D a panel holds
+constexpr int AG_WAVES = 8;              // waves per tile workgroup (4 or 8)
+
+template <typename T, bool EMIT, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void aff_tile_kernel(AffArgs a) {
+  constexpr bool BF = std::is_same<T, bf16_t>::value;
+  constexpr int NY = 8 / NW;              // 32-column tiles per wave (2 row tiles of 32 j)
+  constexpr int NT = 64 * NW;             // threads
+  __shared__ __attribute__((aligned(16))) char lds[2 * AG_PANEL];  // [Q panel][K panel]; EMIT: X, XT tiles
+  __shared__ float red[NW][2];
+  const int64_t ns = a.Mp / AGT;  // Mp is a multiple of 128
+  const int64_t logical = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x));
+  const int64_t bh = logical / (ns * ns);
+  const int64_t tile = logical - bh * ns * ns;
+  const int64_t ti = tile / ns, tj = tile - (tile / ns) * ns;
+  const int64_t i0 = ti * AGT, j0 = tj * AGT;
+  const int w = threadIdx.x >> 6, lane = lane_id(), tid = threadIdx.x;
+  const int kch = a.D / 8;
+  const uint32_t rowb = static_cast<uint32_t>(a.D) * 2;
+
+  {
+    // Staging: 32 loads of 4 rows per panel, spread over the waves.
+    const char* qb = static_cast<const char*>(a.qc) + (bh * a.M + i0) * rowb;
+    const char* kb = static_cast<const char*>(a.kc) + (bh * a.M + j0) * rowb;
+    const int64_t qrows = a.M - i0, krows = a.M - j0;  // > 0: tiles start below M
+    const brsrc_t qrs = make_rsrc(qb, static_cast<uint32_t>((qrows < AGT ? qrows : AGT) * rowb));
+    const brsrc_t krs = make_rsrc(kb, static_cast<uint32_t>((krows < AGT ? krows : AGT) * rowb));
+#pragma unroll
+    for (int n = 0; n < 32 / NW; ++n) {
+      const int blk = (32 / NW) * w + n;
+      const int R = 4 * blk + (lane >> 4);
+      const int c = (lane & 15) ^ (R & 15);
+      const uint32_t voff = c < kch ? static_cast<uint32_t>(R) * rowb + 16u * c : 0x80000000u;
+      bdma16(qrs, voff, 0, lds + blk * 1024);
+      bdma16(krs, voff, 0, lds + AG_PANEL + blk * 1024);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+  __syncthreads();
+
+  const int jr0 = 64 * (w / (NW / 2)), ic0 = 32 * NY * (w % (NW / 2));
+  f32x16 acc[2][NY];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < NY; ++y) acc[x][y] = f32x16{};
+  const int h = lane >> 5;
+  const int ksteps = (a.D + 15) / 16;
+  for (int ks = 0; ks < ksteps; ++ks) {
+    const int c = 2 * ks + h;
+    u32x4 av[2], bv[NY];
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const int R = jr0 + 32 * x + (lane & 31);
+      av[x] = *reinterpret_cast<const u32x4*>(lds + AG_PANEL + R * 256 + ((c ^ (R & 15)) << 4));
+    }
+#pragma unroll
+    for (int y = 0; y < NY; ++y) {
+      const int R = ic0 + 32 * y + (lane & 31);
+      bv[y] = *reinterpret_cast<const u32x4*>(lds + R * 256 + ((c ^ (R & 15)) << 4));
+    }
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int y = 0; y < NY; ++y) {
+        if constexpr (BF)
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8, av[x]), __builtin_bit_cast(bf16x8, bv[y]), acc[x][y], 0, 0, 0);
+        else
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+              __builtin_bit_cast(f16x8, av[x]), __builtin_bit_cast(f16x8, bv[y]), acc[x][y], 0, 0, 0);
+      }
+  }
+
+  // Tile-local coordinates: column i = li0 + 32 y of tile y, rows
+  // j = lj0 + 32 x + 8 g + r of run g (elements 4 g + r) of tile x.
+  const int li0 = ic0 + (lane & 31), lj0 = jr0 + 4 * h;
+  auto extent = [](int64_t n) { return static_cast<int>(n < 0 ? 0 : (n < AGT ? n : AGT)); };
+  const int mi = extent(a.M - i0), mj = extent(a.M - j0);
+  const bool interior = mi == AGT && mj == AGT;
+  auto inside = [&](int x, int y, int e) {
+    return li0 + 32 * y < mi && lj0 + 32 * x + 8 * (e >> 2) + (e & 3) < mj;
+  };
+
+  if constexpr (!EMIT) {
+    // Extremes of the raw products: rounding alpha x is monotonic in x, so
+    // the extremes of alpha A are alpha times these (swapped for alpha < 0),
+    // rounded once, as the EMIT pass rounds every entry.
+    float lo = INFINITY, hi = -INFINITY;
+    if (interior) {
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < NY; ++y)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            lo = fminf(lo, acc[x][y][e]);
+            hi = fmaxf(hi, acc[x][y][e]);
+          }
+    } else {
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < NY; ++y)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if (inside(x, y, e)) {
+              lo = fminf(lo, acc[x][y][e]);
+              hi = fmaxf(hi, acc[x][y][e]);
+            }
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      lo = fminf(lo, shfl_xor_f32(lo, off));
+      hi = fmaxf(hi, shfl_xor_f32(hi, off));
+    }
+    if (lane == 0) {
+      red[w][0] = lo;
+      red[w][1] = hi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      float m0 = red[0][0], m1 = red[0][1];
+#pragma unroll
+      for (int q = 1; q < NW; ++q) {
+        m0 = fminf(m0, red[q][0]);
+        m1 = fmaxf(m1, red[q][1]);
+      }
+      const float e0 = m0 * a.alpha, e1 = m1 * a.alpha;
+      float* p = a.mmpart + (bh * ns * ns + tile) * 2;
+      p[0] = a.alpha < 0.f ? e1 : e0;
+      p[1] = a.alpha < 0.f ? e0 : e1;
+    }
+  } else {
+    float mn = 0.f, scale = 1.f;  // Ahat = (alpha A - mn) * scale
+    if (a.normalization == CAB_NORM_MINMAX) {
+      mn = a.mm[bh * 2 + 0];
+      const float mx = a.mm[bh * 2 + 1];
+      if (mx > mn) scale = 1.0f / (mx - mn + 1e-8f);
+      else mn = 0.f;  // constant A: left as is
+    }
+    {
+      // alpha A rounded on its own, as in the STATS pass (no fused
+      // multiply-add with the subtraction): the minimum maps to exactly 0.
+#pragma clang fp contract(off)
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < NY; ++y)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const float v = (acc[x][y][e] * a.alpha - mn) * scale;
+            acc[x][y][e] = interior || inside(x, y, e) ? v : 0.f;
+          }
+    }
+    const size_t pbase = static_cast<size_t>(bh) * a.Mp * a.Mp;
+    const int Mp = static_cast<int>(a.Mp);
+    if (a.affinity) {
+      // fp32 diagnostic [M][M] (runs of four j of one row i)
+#pragma unroll
+      for (int y = 0; y < NY; ++y) {
+        if (li0 + 32 * y >= mi) continue;
+        float* ar = a.affinity + (static_cast<size_t>(bh) * a.M + i0 + li0 + 32 * y) * a.M + j0;
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int jl = lj0 + 32 * x + 8 * (e >> 2) + (e & 3);
+            if (jl < mj) ar[jl] = acc[x][y][e];
+          }
+      }
+    }
+    if (a.rspart) {
+      // Row sums over the wave's 64 columns j (one AT column block).
+      const int64_t jb = (j0 + jr0) / AT;
+#pragma unroll
+      for (int y = 0; y < NY; ++y) {
+        float sum = 0.f;
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) sum += acc[x][y][e];
+        sum += shfl_xor_f32(sum, 32);
+        if (h == 0) a.rspart[(static_cast<size_t>(bh) * a.nta + jb) * a.Mp + i0 + li0 + 32 * y] = sum;
+      }
+    }
+    // One pass fills one plane of each orientation (either may be absent)
+    // and stores both; tiles lie inside the padded planes (Mp is a multiple
+    // of 128), so every store is in range.
+    uint16_t* tx = reinterpret_cast<uint16_t*>(lds);
+    uint16_t* tt = reinterpret_cast<uint16_t*>(lds + AG_PANEL);
+    const bool diag_tile = i0 == j0;
+    auto emit_pass = [&](uint16_t* xplane, auto xval, uint16_t* tplane, auto tval) {
+      __syncthreads();  // the panels' (or the last pass's) readers are done
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < NY; ++y) {
+          const int il = li0 + 32 * y;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int jl = lj0 + 32 * x + 8 * g;  // a multiple of 4
+            if (xplane) {
+              const uint32_t w0 = static_cast<uint32_t>(xval(acc[x][y][4 * g])) |
+                                  (static_cast<uint32_t>(xval(acc[x][y][4 * g + 1])) << 16);
+              const uint32_t w1 = static_cast<uint32_t>(xval(acc[x][y][4 * g + 2])) |
+                                  (static_cast<uint32_t>(xval(acc[x][y][4 * g + 3])) << 16);
+              *reinterpret_cast<u32x2*>(tx + il * AGT + ((((jl >> 3) ^ (il & 15)) << 3) | (jl & 4))) =
+                  u32x2{w0, w1};
+            }
+            if (tplane) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) tt[(jl + r) * AGT + il] = tval(acc[x][y][4 * g + r], il, jl + r);
+            }
+          }
+        }
+      __syncthreads();
+      uint16_t* xo = xplane + pbase + static_cast<size_t>(i0) * a.Mp + j0;
+      uint16_t* to = tplane + pbase + static_cast<size_t>(j0) * a.Mp + i0;
+#pragma unroll
+      for (int n = 0; n < AGT * AGT / 8 / NT; ++n) {
+        const int t = tid + NT * n;
+        const int rl = t >> 4, c = t & 15;
+        if (xplane)
+          *reinterpret_cast<u32x4*>(xo + rl * Mp + 8 * c) =
+              *reinterpret_cast<const u32x4*>(tx + rl * AGT + ((c ^ (rl & 15)) << 3));
+        if (tplane)
+          *reinterpret_cast<u32x4*>(to + rl * Mp + 8 * c) = *reinterpret_cast<const u32x4*>(tt + rl * AGT + 8 * c);
+      }
+    };
+    uint16_t* const none = nullptr;  // an absent plane
+    auto f16v = [](float v) { return f32_to_f16(v); };
+    auto f16lo = [](float v) { return f32_to_f16(v - f16_to_f32(f32_to_f16(v))); };
+    auto bf16v = [](float v) { return f32_to_bf16(v); };
+    auto bf16lo = [](float v) { return f32_to_bf16(v - bf16_to_f32(f32_to_bf16(v))); };
+    if (a.fused) {
+      // X = f16(Ahat); XT[j][i] = delta_ij - lambda Ahat[i][j] (delta only inside M)
+      const float lam = a.lambda;
+      if (diag_tile)
+        emit_pass(a.xhi, f16v, a.xthi, [&](float v, int il, int jl) {
+          return f32_to_f16((il == jl && il < mi ? 1.f : 0.f) - lam * v);
+        });
+      else
+        emit_pass(a.xhi, f16v, a.xthi, [&](float v, int, int) { return f32_to_f16(-lam * v); });
+    } else if (a.f16_planes) {
+      emit_pass(a.xhi, f16v, a.xthi, [&](float v, int, int) { return f32_to_f16(v); });
+      emit_pass(a.xlo, f16lo, none, [&](float, int, int) { return uint16_t(0); });
+    } else {
+      emit_pass(a.xhi, bf16v, a.xthi, [&](float v, int, int) { return f32_to_bf16(v); });
+      emit_pass(a.xlo, bf16lo, a.xtlo, [&](float v, int, int) { return bf16lo(v); });
     }
   }
 }
@@ -768,16 +1048,30 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
     epilogue(std::integral_constant<int, CAB_FRC_AUGMENTED>{});
 }
 
+// Launches the STATS (emit = false) or EMIT pass; returns the number of
+// min / max partials per (b, h) the STATS pass writes.
 template <typename T>
-void launch_affinity(const AffArgs& a, int64_t BH, bool emit, hipStream_t s) {
+int64_t launch_affinity(const AffArgs& a, int64_t BH, bool emit, hipStream_t s) {
+  if constexpr (sizeof(T) == 2) {  // bf16_t, f16_t
+    if (a.D <= AG_DMAX) {
+      const int64_t ns = a.Mp / AGT;  // Mp is a multiple of 128
+      const unsigned grid = static_cast<unsigned>(BH * ns * ns);
+      if (emit)
+        aff_tile_kernel<T, true, AG_WAVES><<<grid, 64 * AG_WAVES, 0, s>>>(a);
+      else
+        aff_tile_kernel<T, false, AG_WAVES><<<grid, 64 * AG_WAVES, 0, s>>>(a);
+      return ns * ns;
+    }
+  }
+  const int64_t ns = ceil_div(a.Mp, AS);
   if (emit) {
     affinity_kernel<T><<<dim3(static_cast<unsigned>(a.ntw * a.ntw), static_cast<unsigned>(BH)), 256, 0,
                          s>>>(a);
   } else {
-    const int64_t ns = ceil_div(a.Mp, AS);
     affinity_stats_kernel<T><<<dim3(static_cast<unsigned>(ns * ns), static_cast<unsigned>(BH)), 512, 0,
                                s>>>(a);
   }
+  return ns * ns;
 }
 
 }  // namespace
@@ -858,15 +1152,16 @@ extern "C" cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_
   a.lambda = lambda_redundancy;
 
   if (normalization == CAB_NORM_MINMAX) {
+    int64_t nparts = 0;
     switch (dtype) {
-      case CAB_BF16: launch_affinity<bf16_t>(a, BH, false, s); break;
-      case CAB_F16: launch_affinity<f16_t>(a, BH, false, s); break;
-      default: launch_affinity<float>(a, BH, false, s); break;
+      case CAB_BF16: nparts = launch_affinity<bf16_t>(a, BH, false, s); break;
+      case CAB_F16: nparts = launch_affinity<f16_t>(a, BH, false, s); break;
+      default: nparts = launch_affinity<float>(a, BH, false, s); break;
     }
     cab_status_t st = launch_status("cab_block_frc/affinity_stats");
     if (st != CAB_OK) return st;
     minmax_finalize_kernel<<<static_cast<unsigned>(BH), 256, 0, s>>>(
-        a.mmpart, ceil_div(L.Mp, AS) * ceil_div(L.Mp, AS), reinterpret_cast<float*>(ws + L.off_mm));
+        a.mmpart, nparts, reinterpret_cast<float*>(ws + L.off_mm));
     st = launch_status("cab_block_frc/minmax_finalize");
     if (st != CAB_OK) return st;
   }

@@ -254,8 +254,6 @@ __global__ __launch_bounds__(256) void pack_split_kernel(SplitPackArgs a) {
   }
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 // 16-byte direct-to-LDS load per lane: global g + OFF, LDS l + OFF + 16 * lane.
 // OFF is the instruction's immediate, a 13-bit signed field: the compiler
 // wraps larger constants without a diagnostic, so they are refused here.
@@ -263,20 +261,6 @@ template <int OFF>
 __device__ __forceinline__ void dma16(const char* g, char* l) {
   static_assert(OFF >= 0 && OFF < 4096, "global_load_lds immediate offset must be in [0, 4096)");
   __builtin_amdgcn_global_load_lds(g, (lds_void*)l, 16, OFF, 0);
-}
-
-// 16-byte buffer load to LDS per lane: bytes [voff + soff, +16) of the buffer
-// r land at LDS l + 16 * lane. Offsets at or past the buffer's size read as
-// zero. The per-lane offset is a 32-bit register and the base a scalar
-// descriptor, so no per-lane 64-bit address arithmetic is spent on a load.
-typedef __amdgpu_buffer_rsrc_t brsrc_t;
-__device__ __forceinline__ brsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  // word 3 0x00020000: raw (untyped) dword access, the gfx9 buffer default
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
-                                           static_cast<int>(bytes), 0x00020000);
-}
-__device__ __forceinline__ void bdma16(brsrc_t r, uint32_t voff, uint32_t soff, char* l) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)l, 16, voff, soff, 0, 0);
 }
 
 // gfx950 lane swaps between the two halves of two registers (v_permlane32_swap:

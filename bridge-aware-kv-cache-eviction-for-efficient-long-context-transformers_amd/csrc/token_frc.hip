@@ -315,7 +315,6 @@ struct GramArgs {
   int64_t Np, tiles, col_tiles, rb;
 };
 
-typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int GRAM_STAGES = 3;
 

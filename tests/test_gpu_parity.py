@@ -258,6 +258,43 @@ def test_frc_fused_constant_affinity(cuda):
     np.testing.assert_allclose(np32(f), of, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("dt", ["bf16", "fp16"])
+@pytest.mark.parametrize("D", [64, 72, 128, 256])
+@pytest.mark.parametrize("mode", ["diag", "fused", "mult", "none", "aug", "aug_minmax"])
+def test_frc_plane_layouts_and_head_dims(cuda, dt, D, mode):
+    """Every plane layout the affinity pass writes for 16-bit inputs (fp16
+    Ahat with and without I - lambda Ahat, bf16 hi/lo pairs, row-sum partials
+    of the augmented formula), at head dims 64, 72 (a half 16-dim step), 128
+    (the LDS-staged 256 x 256 tile kernel) and 256 (the direct-load kernels);
+    M = 300, so the 256-row tiles overhang the 384-row padding."""
+    from cab_attention.kernels import compute_block_frc
+    formula, normalization, diag = {
+        "diag": ("additive", "minmax", True), "fused": ("additive", "minmax", False),
+        "mult": ("multiplicative", "minmax", True), "none": ("additive", "none", True),
+        "aug": ("augmented", "none", True), "aug_minmax": ("augmented", "minmax", True)}[mode]
+    B, H, M, lam = 1, 2, 300, 0.5
+    scale = 3.0 if normalization == "minmax" else 1.0
+    qc = seeded((B, H, M, D), 41 + D, DTYPES[dt], scale=scale)
+    kc = seeded((B, H, M, D), 42 + D, DTYPES[dt], scale=scale)
+    f, a, t = compute_block_frc(qc.to(cuda), kc.to(cuda), lambda_redundancy=lam, formula=formula,
+                                normalization=normalization, diagnostics=diag)
+    of, oa, ot = O.compute_block_frc(np32(qc), np32(kc), lambda_redundancy=lam, formula=formula,
+                                     normalization=normalization)
+    if diag:
+        np.testing.assert_allclose(np32(a), oa, rtol=1e-5, atol=1e-5 * max(1.0, np.abs(oa).max()))
+        assert_tri_close(t, ot, oa, normalization)
+    if formula == "multiplicative":
+        np.testing.assert_allclose(np32(f), of, rtol=1e-3, atol=1e-5)
+    elif formula == "augmented":
+        # F is 1000 where Ahat == 0 (no edge): with minmax normalisation the
+        # minimum of A must map to exactly 0 (the EMIT pass rounds alpha A
+        # as the STATS pass did), so the step lands on the oracle's entries.
+        np.testing.assert_array_equal(np32(a) == 0, oa == 0)
+        np.testing.assert_allclose(np32(f), of, rtol=1e-4, atol=1e-4 * np.abs(of).max())
+    else:
+        assert_frc_close(f, of, oa, ot, lam)
+
+
 def test_bridge_known_answer_on_gpu(cuda):
     """test.ipynb:19-25 through the GPU FRC path: adjacency as qc, identity
     as kc (fp32, D=104), unit scale, no normalisation, augmented formula."""
