@@ -1,14 +1,17 @@
 // Per-row block selection (cab_block_topk).
 //
 // One wave64 per FRC row. The row's M scores are read once (coalesced, lane l
-// holds columns j = 64 c + l) and mapped to order-preserving uint32 keys in
-// registers. The k-th smallest key is found by a radix select (one pass per
-// key byte that the candidates do not all share, a 256-bin LDS histogram per
-// wave, a wave-wide prefix scan, ending early at a bin of one key).
-// A last pass in ascending j keeps every key below the threshold and the
-// first (in j) keys equal to it, assigns output slots with a prefix
-// popcount, and writes the compact ascending index list and, optionally, the
-// dense 0/1 row.
+// holds columns j = 64 c + l, through a buffer descriptor: no per-lane 64-bit
+// addresses, columns past M read as zero) and mapped branch-free to
+// order-preserving uint32 keys in registers, non-candidates to a sentinel.
+// The k-th smallest key is found by a radix select (one pass per key byte
+// that the candidates do not all share, a 256-bin LDS histogram per wave with
+// four copies per bin, a wave-wide prefix scan, ending early at a bin of one
+// key). A last pass in ascending j keeps every key below the threshold and
+// the first (in j) keys equal to it -- when every key equal to the threshold
+// is kept, simply every key at most the threshold -- assigns output slots
+// with a prefix popcount, and writes the compact ascending index list and,
+// optionally, the dense 0/1 row.
 //
 // Hybrid selection (cab_block_topk_hybrid) first runs the same search on
 // the row's magnitude keys for its magnitude quota, marks those blocks taken,
@@ -212,6 +215,130 @@ __device__ __forceinline__ uint32_t kth_key(Key key, Cand is_cand, int nch, int6
   return prefix;
 }
 
+// Register-path form of kth_key for keys held in registers with KEY_NONE for
+// non-candidates. The histogram keeps HSUB_REG copies of every bin, copy s of bin
+// b at word s * HSTRIDE + b: copies of one bin fall into different LDS banks
+// (HSTRIDE % 64 == 4), and lane l clears and sums bins 4 l .. 4 l + 3 of a
+// copy with one 16-byte access. The first counting pass counts every key
+// (all candidates share the bytes above it; a KEY_NONE key lands in bin 255,
+// above every candidate of that bin); later passes count the keys matching
+// the prefix. eq_total returns how many keys equal theta.
+constexpr int HSTRIDE = 260;
+constexpr int HSUB_REG = 4;  // copies per bin (fewer copies: more waves per CU fit the LDS)
+
+template <int NCH>
+__device__ __forceinline__ uint32_t kth_key_reg(const uint32_t (&key)[NCH], int64_t need,
+                                                int64_t& need_eq, uint32_t& eq_total, uint32_t* hist) {
+  const int lane = lane_id();
+  need_eq = 0;
+  eq_total = 0;
+  if (need <= 0) return 0u;
+  uint32_t kand = 0xffffffffu, kor = 0u;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    kand &= key[c];
+    kor |= key[c] != KEY_NONE ? key[c] : 0u;
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    kand &= static_cast<uint32_t>(__shfl_xor(static_cast<int>(kand), off, 64));
+    kor |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(kor), off, 64));
+  }
+  const uint32_t diff = kand ^ kor;
+  if (diff == 0u) {  // every candidate holds the same key
+    need_eq = need;
+    eq_total = 0xffffffffu;  // unknown: the caller ranks the ties
+    return kand;
+  }
+  uint32_t prefix = 0u, pmask = 0u;
+  int64_t rem = need;
+  bool first = true;
+  char* hb = reinterpret_cast<char*>(hist) + (lane % HSUB_REG) * HSTRIDE * 4;
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    if (((diff >> shift) & 255u) == 0u) {  // every candidate shares this byte
+      prefix |= kand & (255u << shift);
+      pmask |= 255u << shift;
+      continue;
+    }
+    wave_sync();  // the previous pass's reads are done
+#pragma unroll
+    for (int q = 0; q < HSUB_REG; ++q)
+      *reinterpret_cast<u32x4*>(hist + q * HSTRIDE + 4 * lane) = u32x4{0u, 0u, 0u, 0u};
+    wave_sync();
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const uint32_t kc = key[c];
+      const uint32_t inc = first ? 1u : ((kc & pmask) == prefix ? 1u : 0u);
+      atomicAdd(reinterpret_cast<uint32_t*>(hb + (((kc >> shift) & 255u) << 2)), inc);
+    }
+    first = false;
+    wave_sync();
+    uint32_t hv[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int q = 0; q < HSUB_REG; ++q) {
+      const u32x4 x = *reinterpret_cast<const u32x4*>(hist + q * HSTRIDE + 4 * lane);
+      hv[0] += x[0];
+      hv[1] += x[1];
+      hv[2] += x[2];
+      hv[3] += x[3];
+    }
+    const uint32_t mine = hv[0] + hv[1] + hv[2] + hv[3];
+    uint32_t incl = mine;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t up = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += up;
+    }
+    const uint32_t excl = incl - mine;
+    const uint64_t reach = ballot64(static_cast<int64_t>(incl) >= rem);
+    const int src = __builtin_ctzll(reach);
+    uint32_t run = excl, bin = 0u, bcnt = 0u;
+    bool found = false;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (!found && static_cast<int64_t>(run + hv[q]) >= rem) {
+        found = true;
+        bin = 4u * lane + q;
+        bcnt = hv[q];
+      } else if (!found) {
+        run += hv[q];
+      }
+    }
+    const uint32_t sel_bin = __shfl(bin, src, 64);
+    const uint32_t below = __shfl(run, src, 64);
+    const uint32_t sel_cnt = __shfl(bcnt, src, 64);
+    rem -= below;
+    prefix |= sel_bin << shift;
+    pmask |= 255u << shift;
+    eq_total = sel_cnt;
+    if (sel_cnt == 1u && shift > 0) {
+      // One candidate left (rem == 1): theta is its key.
+      uint32_t kv = 0u;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+        if ((key[c] & pmask) == prefix && key[c] != KEY_NONE) kv = key[c];
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1)
+        kv |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(kv), off, 64));
+      need_eq = rem;
+      return kv;
+    }
+  }
+  need_eq = rem;  // keys below theta: need - rem; the rest are ties at theta
+  return prefix;
+}
+
+// Order key of the score bits u (see order_key), branch-free.
+__device__ __forceinline__ uint32_t order_key_bits(uint32_t u, uint32_t flip) {
+  const uint32_t mag = u & 0x7fffffffu;
+  u = mag == 0u ? 0u : u;                     // -0 == +0
+  u = mag > 0x7f800000u ? 0x7fc00000u : u;    // one NaN, above +inf
+  u ^= static_cast<uint32_t>(static_cast<int32_t>(u) >> 31) | 0x80000000u;
+  return u ^ flip;
+}
+
 template <int NCH, bool HYB>
 __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -222,33 +349,28 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   const int64_t krow = min(static_cast<int64_t>(a.k), ncand);
   const bool kd = a.keep_diagonal != 0;
   const int64_t need = kd ? krow - 1 : krow;
-  const float* f = a.frc + row * a.M;
-  const bool high = a.select_high != 0;
+  const uint32_t flip = a.select_high ? 0xffffffffu : 0u;
   const uint64_t lt_mask = lanemask_lt();
-  __shared__ uint32_t hist_all[4][256 * HSUB];
+  __shared__ __attribute__((aligned(16))) uint32_t hist_all[4][HSUB_REG * HSTRIDE];
   uint32_t* hist = hist_all[threadIdx.x >> 6];
 
-  // Loads are unconditional (the index is clamped) so that all NCH are in
-  // flight together; columns that are no candidate (past M, past the causal
-  // limit, the forced diagonal) get KEY_NONE.
-  const int Mi = static_cast<int>(a.M);
-  const int ncand_i = static_cast<int>(ncand), i_i = static_cast<int>(i);
-  auto is_cand = [&](int c) {
-    const int j = 64 * c + lane;
-    return j < ncand_i && !(kd && j == i_i);
-  };
+  // Lane l holds column j = 64 c + l of chunk c. Column j is a candidate when
+  // j < ncand (c < climit) and it is not the forced diagonal; the rest get
+  // KEY_NONE. The row is read through a buffer descriptor (columns past M
+  // read as zero and are no candidates), all NCH loads in flight together.
+  const int climit = static_cast<int>((ncand - lane + 63) >> 6);
+  const int dc = static_cast<int>(i >> 6);
+  const bool dlane = kd && lane == static_cast<int>(i & 63);
+  auto is_cand = [&](int c) { return c < climit && !(c == dc && dlane); };
+  const brsrc_t frs = make_rsrc(a.frc + row * a.M, static_cast<uint32_t>(a.M * 4));
   uint32_t key[NCH];
   {
-    float v[NCH];
+    uint32_t u[NCH];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const int j = 64 * c + lane;
-      v[c] = f[j < Mi ? j : Mi - 1];
-    }
+    for (int c = 0; c < NCH; ++c)
+      u[c] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(frs, 4u * lane, 256u * c, 0));
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) asm volatile("" ::"v"(v[c]));  // keeps the loads unconditional
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) key[c] = is_cand(c) ? order_key(v[c], high) : KEY_NONE;
+    for (int c = 0; c < NCH; ++c) key[c] = is_cand(c) ? order_key_bits(u[c], flip) : KEY_NONE;
   }
 
   // Hybrid: the need_m candidates of highest magnitude first (bit c of msel
@@ -259,23 +381,19 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   int64_t need_m = 0;
   if constexpr (HYB) {
     need_m = min(static_cast<int64_t>(a.kmag), need);
-    const float* mg = a.mag + row * a.M;
+    const brsrc_t mrs = make_rsrc(a.mag + row * a.M, static_cast<uint32_t>(a.M * 4));
     uint32_t mkey[NCH];
     {
-      float v[NCH];
+      uint32_t u[NCH];
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        const int j = 64 * c + lane;
-        v[c] = mg[j < Mi ? j : Mi - 1];
-      }
+      for (int c = 0; c < NCH; ++c)
+        u[c] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(mrs, 4u * lane, 256u * c, 0));
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) asm volatile("" ::"v"(v[c]));
-#pragma unroll
-      for (int c = 0; c < NCH; ++c) mkey[c] = is_cand(c) ? order_key(v[c], true) : KEY_NONE;
+      for (int c = 0; c < NCH; ++c) mkey[c] = is_cand(c) ? order_key_bits(u[c], 0xffffffffu) : KEY_NONE;
     }
     int64_t meq = 0;
-    const uint32_t mtheta =
-        kth_key<NCH, true>([&](int c) { return mkey[c]; }, is_cand, NCH, need_m, meq, hist);
+    uint32_t mtot = 0;
+    const uint32_t mtheta = kth_key_reg<NCH>(mkey, need_m, meq, mtot, hist);
     int64_t eq_seen = 0;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
@@ -296,25 +414,43 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   // FRC order for the rest of the row (taken columns now carry KEY_NONE).
   const int64_t need_f = need - need_m;
   int64_t need_eq = 0;
-  const uint32_t theta =
-      kth_key<NCH, true>([&](int c) { return key[c]; }, is_cand, NCH, need_f, need_eq, hist);
+  uint32_t eq_total = 0;
+  const uint32_t theta = kth_key_reg<NCH>(key, need_f, need_eq, eq_total, hist);
 
-  int64_t pos = 0, eq_seen = 0;
+  int64_t pos = 0;
   int32_t* out = a.kv_idx + row * a.k;
+  uint8_t* drow = a.dense ? a.dense + row * a.M : nullptr;
+  const int Mi = static_cast<int>(a.M);
+  if (need_f <= 0 || need_eq == static_cast<int64_t>(eq_total)) {
+    // Every key equal to theta is kept: a key is selected iff it is at most
+    // theta (KEY_NONE ranks above every real theta).
+    const bool any = need_f > 0;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int64_t j = 64 * c + lane;
-    const bool cand = key[c] != KEY_NONE && need_f > 0;
-    const bool eq = cand && key[c] == theta;
-    const uint64_t eqb = ballot64(eq);
-    const int64_t eq_rank = eq_seen + __popcll(eqb & lt_mask);
-    const bool sel = (cand && key[c] < theta) || (eq && eq_rank < need_eq) || taken(c) ||
-                     (kd && j == i);
-    const uint64_t selb = ballot64(sel);
-    if (sel) out[pos + __popcll(selb & lt_mask)] = static_cast<int32_t>(j);
-    if (a.dense && j < a.M) a.dense[row * a.M + j] = sel ? 1 : 0;
-    pos += __popcll(selb);
-    eq_seen += __popcll(eqb);
+    for (int c = 0; c < NCH; ++c) {
+      const int j = 64 * c + lane;
+      const bool sel = (any && key[c] <= theta) || (HYB && taken(c)) || (c == dc && dlane);
+      const uint64_t selb = ballot64(sel);
+      if (sel) out[pos + __popcll(selb & lt_mask)] = j;
+      if (drow && j < Mi) drow[j] = sel ? 1 : 0;
+      pos += __popcll(selb);
+    }
+  } else {
+    int64_t eq_seen = 0;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int j = 64 * c + lane;
+      const bool cand = key[c] != KEY_NONE;
+      const bool eq = cand && key[c] == theta;
+      const uint64_t eqb = ballot64(eq);
+      const int64_t eq_rank = eq_seen + __popcll(eqb & lt_mask);
+      const bool sel = (cand && key[c] < theta) || (eq && eq_rank < need_eq) || (HYB && taken(c)) ||
+                       (c == dc && dlane);
+      const uint64_t selb = ballot64(sel);
+      if (sel) out[pos + __popcll(selb & lt_mask)] = j;
+      if (drow && j < Mi) drow[j] = sel ? 1 : 0;
+      pos += __popcll(selb);
+      eq_seen += __popcll(eqb);
+    }
   }
   for (int64_t p = pos + lane; p < a.k; p += 64) out[p] = -1;
   if (lane == 0) a.kv_cnt[row] = static_cast<int32_t>(pos);
@@ -339,7 +475,7 @@ __global__ __launch_bounds__(256) void topk_stream_kernel(TopkArgs a) {
   const float* mg = HYB ? a.mag + row * a.M : nullptr;
   const bool high = a.select_high != 0;
   const uint64_t lt_mask = lanemask_lt();
-  __shared__ uint32_t hist_all[4][256 * HSUB];
+  __shared__ __attribute__((aligned(16))) uint32_t hist_all[4][256 * HSUB];
   uint32_t* hist = hist_all[threadIdx.x >> 6];
   const int Mi = static_cast<int>(a.M), nch = (Mi + 63) / 64;
   const int ncand_i = static_cast<int>(ncand), i_i = static_cast<int>(i);
