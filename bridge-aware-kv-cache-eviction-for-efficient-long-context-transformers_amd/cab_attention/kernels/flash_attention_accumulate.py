@@ -85,7 +85,7 @@ def key_scores(q: torch.Tensor, k: torch.Tensor, lse: torch.Tensor, scale: float
                accumulate: bool = False) -> torch.Tensor:
     """``scores[b, h, s] (+)= sum_t exp(q_t . k_s * scale - lse[b, h, t])``
     (``cab_attn_key_scores``), with the lse of :func:`flash_attention` on the
-    same q, k. bf16 or fp16."""
+    same q, k. bf16, fp16 or fp32."""
     B, H, N_q, D = q.shape
     H_kv, N_k = k.shape[1], k.shape[2]
     if tuple(lse.shape) != (B, H, N_q) or lse.dtype != torch.float32:
@@ -128,7 +128,7 @@ def flash_attention_with_cumulative_scores(
 
     Args:
         q: ``[B, H, N_q, D]``; k, v: ``[B, H_kv, N_k, D]`` (``H_kv`` divides
-            ``H``). bf16 or fp16, D = 64 or 128.
+            ``H``). bf16, fp16 or fp32, D = 64 or 128.
         cumulative_scores: optional fp32 ``[B, H, N_old]`` running totals. They
             are added to (not reset); when ``N_old < N_k`` they are first
             extended with zeros for the new key positions, as in the

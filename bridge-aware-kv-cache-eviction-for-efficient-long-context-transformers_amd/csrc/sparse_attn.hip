@@ -792,10 +792,14 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
 //   column sums over the tile's queries, kept per lane.
 // The lane partials are added once at the end in a fixed order (no
 // atomics) and written to, or added into, score[b, h, keys of the block].
+// fp32 inputs: the Q tile is staged in fp32 (two loads per stager lane) and
+// every operand is split into bf16 hi / lo halves in registers; S takes
+// three bf16 products per site, q_hi k_hi + q_lo k_hi + q_hi k_lo, as the
+// executor's fp32 path does.
 // ---------------------------------------------------------------------------
 struct KeyScoreArgs {
-  const uint16_t* q;
-  const uint16_t* k;
+  const void* q;
+  const void* k;
   const float* lse;  // [B, H, Nq] contiguous
   float* score;      // score[b * ss0 + h * ss1 + token]
   int64_t qs[3], ks[3], ss[2];
@@ -806,15 +810,21 @@ struct KeyScoreArgs {
 constexpr int KS_STAGES = 4;
 constexpr int KS_WAVES = 4;  // key blocks (waves) sharing each staged query tile (8 measured slower)
 
-// One ring stage: the Q tile (16 queries x D, 32 D bytes), then one 64-float
-// lse copy per wave.
-template <int HD>
-constexpr int ks_stage_bytes() { return 32 * HD + 4 * 256; }
+// One ring stage: the Q tile (16 queries x D, 2 or 4 bytes per value), then
+// one 64-float lse copy per wave.
+template <int HD, bool F32>
+constexpr int ks_q_bytes() { return (F32 ? 64 : 32) * HD; }
+template <int HD, bool F32>
+constexpr int ks_stage_bytes() { return ks_q_bytes<HD, F32>() + 4 * 256; }
 
-template <bool BF16, int NW, int HD>
+template <cab_dtype_t DT, int NW, int HD>
 __global__ __launch_bounds__(64 * NW) void key_score_kernel(KeyScoreArgs a) {
   constexpr int NDS = Dims<HD>::NDS;
-  constexpr int KS_STAGE_BYTES = ks_stage_bytes<HD>();
+  constexpr bool F32 = DT == CAB_F32;
+  constexpr bool BF16 = DT != CAB_F16;
+  constexpr int KS_STAGE_BYTES = ks_stage_bytes<HD, F32>();
+  constexpr int QB = ks_q_bytes<HD, F32>();
+  constexpr int ESZ = F32 ? 4 : 2;
   __shared__ __attribute__((aligned(16))) char ring[KS_STAGES * KS_STAGE_BYTES];
   const int logical = static_cast<int>(xcd_remap(blockIdx.x, static_cast<int64_t>(a.BH) * a.Mkg));
   const int bh = logical / a.Mkg;
@@ -827,19 +837,29 @@ __global__ __launch_bounds__(64 * NW) void key_score_kernel(KeyScoreArgs a) {
   const float c = a.scale_log2;
   constexpr float LOG2E = 1.4426950408889634f;
 
-  const uint16_t* qb = a.q + b * a.qs[0] + hh * a.qs[1];
-  const uint16_t* kb = a.k + b * a.ks[0] + hk * a.ks[1];
+  const char* qb = static_cast<const char*>(a.q) + (b * a.qs[0] + hh * a.qs[1]) * ESZ;
+  const char* kb = static_cast<const char*>(a.k) + (b * a.ks[0] + hk * a.ks[1]) * ESZ;
   const float* lb = a.lse + static_cast<int64_t>(bh) * a.Nq;
 
-  // K^T operand: kop[kt][ds] = K[16 kt + l16][32 ds + 8 g .. +8] (zero past Nk).
+  // K^T operand: kop[kt][ds] = K[16 kt + l16][32 ds + 8 g .. +8] (zero past
+  // Nk); fp32: its hi half, klo the lo half.
   u32x4 kop[4][NDS];
+  u32x4 klo[4][F32 ? NDS : 1];
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt) {
     const int key = j * BS + 16 * kt + l16;
 #pragma unroll
-    for (int ds = 0; ds < NDS; ++ds)
-      kop[kt][ds] = key < a.Nk ? *reinterpret_cast<const u32x4*>(kb + key * a.ks[2] + 32 * ds + 8 * g)
-                               : u32x4{0u, 0u, 0u, 0u};
+    for (int ds = 0; ds < NDS; ++ds) {
+      const char* kp = kb + (key * a.ks[2] + 32 * ds + 8 * g) * ESZ;
+      if constexpr (F32) {
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        const f32x4 x0 = key < a.Nk ? *reinterpret_cast<const f32x4*>(kp) : zero;
+        const f32x4 x1 = key < a.Nk ? *reinterpret_cast<const f32x4*>(kp + 16) : zero;
+        split8(x0, x1, kop[kt][ds], klo[kt][ds]);
+      } else {
+        kop[kt][ds] = key < a.Nk ? *reinterpret_cast<const u32x4*>(kp) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
   }
 
   // Query tiles that see the group's first block, and this wave's first.
@@ -857,9 +877,10 @@ __global__ __launch_bounds__(64 * NW) void key_score_kernel(KeyScoreArgs a) {
   auto tile_of = [&](int it) { return ntiles - 1 - it; };
   // Staging of tile tile_of(it): wave w < NDS moves Q dims 32 w .. 32 w + 31
   // of the tile's 16 queries (lane L: query L % 16, dims 32 w + 8 (L / 16)
-  // .. + 7, landing at 16 L: the A operand of MFMA k-step w); waves w < 4
-  // move lse copy w (one load per tile for waves NDS .. 3); waves 4 .. 7
-  // (NW = 8) stage nothing and read lse copy w % 4.
+  // .. + 7, landing at 16 L: the A operand of MFMA k-step w; fp32: dims
+  // .. + 3 at 2048 w + 16 L and .. + 4 .. + 7 at 1024 bytes past them); waves
+  // w < 4 move lse copy w (one load per tile for waves NDS .. 3); waves
+  // 4 .. 7 (NW = 8) stage nothing and read lse copy w % 4.
   const bool stager = w < 4;
   const bool qstager = w < NDS;
   auto issue = [&](int it) {
@@ -867,10 +888,16 @@ __global__ __launch_bounds__(64 * NW) void key_score_kernel(KeyScoreArgs a) {
     char* st = ring + (it % KS_STAGES) * KS_STAGE_BYTES;
     const int q = 16 * tile_of(it) + l16;
     const int qc = q < a.Nq ? q : a.Nq - 1;  // clamped, masked below
-    if (qstager)
-      __builtin_amdgcn_global_load_lds(qb + qc * a.qs[2] + 32 * w + 8 * g,
-                                       (lds_void*)(st + 1024 * w), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(lb + qc, (lds_void*)(st + 32 * HD + 256 * w), 4, 0, 0);
+    if (qstager) {
+      const char* src = qb + (qc * a.qs[2] + 32 * w + 8 * g) * ESZ;
+      if constexpr (F32) {
+        __builtin_amdgcn_global_load_lds(src, (lds_void*)(st + 2048 * w), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(src + 16, (lds_void*)(st + 2048 * w + 1024), 16, 0, 0);
+      } else {
+        __builtin_amdgcn_global_load_lds(src, (lds_void*)(st + 1024 * w), 16, 0, 0);
+      }
+    }
+    __builtin_amdgcn_global_load_lds(lb + qc, (lds_void*)(st + QB + 256 * w), 4, 0, 0);
   };
 
   float colsum[4] = {0.f, 0.f, 0.f, 0.f};
@@ -881,15 +908,16 @@ __global__ __launch_bounds__(64 * NW) void key_score_kernel(KeyScoreArgs a) {
   auto step = [&](int it, auto stage_tag) {
     constexpr int S = decltype(stage_tag)::value;
     const int ahead = stager ? nt - 1 - it : 0;  // tiles it + 1, it + 2 may be in flight
-    // A Q stager has two loads per tile in flight, an lse-only stager one.
+    // A Q stager has two loads per tile in flight (fp32: three), an
+    // lse-only stager one.
     if (ahead >= 2) {
       if (qstager)
-        __builtin_amdgcn_s_waitcnt(0x0f74);  // vmcnt(4)
+        __builtin_amdgcn_s_waitcnt(F32 ? 0x0f76 : 0x0f74);  // vmcnt(6) / vmcnt(4)
       else
         __builtin_amdgcn_s_waitcnt(0x0f72);  // vmcnt(2)
     } else if (ahead == 1) {
       if (qstager)
-        __builtin_amdgcn_s_waitcnt(0x0f72);  // vmcnt(2)
+        __builtin_amdgcn_s_waitcnt(F32 ? 0x0f73 : 0x0f72);  // vmcnt(3) / vmcnt(2)
       else
         __builtin_amdgcn_s_waitcnt(0x0f71);  // vmcnt(1)
     } else {
@@ -901,9 +929,18 @@ __global__ __launch_bounds__(64 * NW) void key_score_kernel(KeyScoreArgs a) {
     if (!has_keys || tile < my0) return;
     const char* st = ring + S * KS_STAGE_BYTES;
     u32x4 qop[NDS];
+    u32x4 qlo[F32 ? NDS : 1];
 #pragma unroll
-    for (int ds = 0; ds < NDS; ++ds) qop[ds] = reinterpret_cast<const u32x4*>(st + 1024 * ds)[lane];
-    const f32x4 lv = reinterpret_cast<const f32x4*>(st + 32 * HD + 256 * (w & 3))[g];
+    for (int ds = 0; ds < NDS; ++ds) {
+      if constexpr (F32) {
+        const f32x4 x0 = reinterpret_cast<const f32x4*>(st + 2048 * ds)[lane];
+        const f32x4 x1 = reinterpret_cast<const f32x4*>(st + 2048 * ds + 1024)[lane];
+        split8(x0, x1, qop[ds], qlo[ds]);
+      } else {
+        qop[ds] = reinterpret_cast<const u32x4*>(st + 1024 * ds)[lane];
+      }
+    }
+    const f32x4 lv = reinterpret_cast<const f32x4*>(st + QB + 256 * (w & 3))[g];
     float nl[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) nl[r] = -lv[r] * LOG2E;
@@ -912,7 +949,13 @@ __global__ __launch_bounds__(64 * NW) void key_score_kernel(KeyScoreArgs a) {
     for (int kt = 0; kt < 4; ++kt) {
       sc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ds = 0; ds < NDS; ++ds) sc[kt] = mfma16<BF16>(qop[ds], kop[kt][ds], sc[kt]);
+      for (int ds = 0; ds < NDS; ++ds) {
+        if constexpr (F32) {
+          sc[kt] = mfma16<true>(qlo[ds], kop[kt][ds], sc[kt]);
+          sc[kt] = mfma16<true>(qop[ds], klo[kt][ds], sc[kt]);
+        }
+        sc[kt] = mfma16<BF16>(qop[ds], kop[kt][ds], sc[kt]);
+      }
     }
     // sc[kt][r]: query 16 tile + 4 g + r, key j BS + 16 kt + l16.
     const int t0 = 16 * tile + 4 * g;
@@ -1310,24 +1353,25 @@ extern "C" cab_status_t cab_attn_key_scores(
     const int64_t score_strides[3], int accumulate, void* stream) {
   const char* fn = "cab_attn_key_scores";
   clear_error();
-  cab_status_t st = check_dense(fn, dtype, false, B, H, H_kv, N_q, N_k, D);
+  cab_status_t st = check_dense(fn, dtype, true, B, H, H_kv, N_q, N_k, D);
   if (st != CAB_OK) return st;
   CAB_REQUIRE(std::isfinite(scale) && scale > 0.f, CAB_EINVAL, "%s: scale must be finite and > 0",
               fn);
   CAB_REQUIRE(q_strides && k_strides && score_strides, CAB_EINVAL, "%s: null stride array", fn);
+  const int64_t esize = dtype == CAB_F32 ? 4 : 2;
   if (B == 0 || H == 0 || N_k == 0) return CAB_OK;
   CAB_REQUIRE(scores != nullptr, CAB_EINVAL, "%s: null scores", fn);
   CAB_REQUIRE(score_strides[2] == 1 && score_strides[0] >= 0 && score_strides[1] >= 0,
               CAB_ESHAPE, "%s: scores must have a contiguous token dim", fn);
   if (N_q > 0) {
-    if ((st = check_tensor(fn, "q", q, q_strides, 2)) != CAB_OK) return st;
+    if ((st = check_tensor(fn, "q", q, q_strides, esize)) != CAB_OK) return st;
     CAB_REQUIRE(lse != nullptr && reinterpret_cast<uintptr_t>(lse) % 4 == 0, CAB_EINVAL,
                 "%s: lse must be the fp32 [B, H, N_q] rows cab_flash_attn_fwd wrote", fn);
   }
-  if ((st = check_tensor(fn, "k", k, k_strides, 2)) != CAB_OK) return st;
+  if ((st = check_tensor(fn, "k", k, k_strides, esize)) != CAB_OK) return st;
   KeyScoreArgs a;
-  a.q = static_cast<const uint16_t*>(q);
-  a.k = static_cast<const uint16_t*>(k);
+  a.q = q;
+  a.k = k;
   a.lse = lse;
   a.score = scores;
   for (int d = 0; d < 3; ++d) {
@@ -1349,16 +1393,17 @@ extern "C" cab_status_t cab_attn_key_scores(
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   const dim3 grid(static_cast<unsigned>(B * H * a.Mkg));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (D == 64) {
-    if (dtype == CAB_BF16)
-      key_score_kernel<true, KS_WAVES, 64><<<grid, 64 * KS_WAVES, 0, s>>>(a);
-    else
-      key_score_kernel<false, KS_WAVES, 64><<<grid, 64 * KS_WAVES, 0, s>>>(a);
-  } else {
-    if (dtype == CAB_BF16)
-      key_score_kernel<true, KS_WAVES, 128><<<grid, 64 * KS_WAVES, 0, s>>>(a);
-    else
-      key_score_kernel<false, KS_WAVES, 128><<<grid, 64 * KS_WAVES, 0, s>>>(a);
-  }
+  auto launch = [&](auto hd_tag) {
+    constexpr int HDT = decltype(hd_tag)::value;
+    switch (dtype) {
+      case CAB_BF16: key_score_kernel<CAB_BF16, KS_WAVES, HDT><<<grid, 64 * KS_WAVES, 0, s>>>(a); break;
+      case CAB_F16: key_score_kernel<CAB_F16, KS_WAVES, HDT><<<grid, 64 * KS_WAVES, 0, s>>>(a); break;
+      default: key_score_kernel<CAB_F32, KS_WAVES, HDT><<<grid, 64 * KS_WAVES, 0, s>>>(a); break;
+    }
+  };
+  if (D == 64)
+    launch(std::integral_constant<int, 64>{});
+  else
+    launch(std::integral_constant<int, 128>{});
   return launch_status(fn);
 }

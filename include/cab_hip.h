@@ -243,7 +243,9 @@ cab_status_t cab_block_sparse_attn_fwd_packed(const void* q, const void* k, cons
  * key s receives from the N_q queries (same masking), with the lse rows of
  * cab_flash_attn_fwd on the same q, k. Written when accumulate == 0, added
  * to the existing values otherwise (the reference's running total across
- * calls). scores: fp32 [B,H,N_k] with strides {b, h, 1}. bf16 or fp16.
+ * calls). scores: fp32 [B,H,N_k] with strides {b, h, 1}. bf16, fp16 or fp32
+ * (fp32: each product as three bf16 MFMA products of split operands, as in
+ * cab_flash_attn_fwd).
  * Each key's total is summed in a fixed order (no atomics): the result is
  * deterministic. The reference's kernel adds exp(s - running maximum)
  * instead, a value that depends on its tiling; this is the quantity its

@@ -229,9 +229,14 @@ def test_dense_attention_validation(lib):
     assert fwd(ws=None) == nat.CAB_EWORKSPACE
     ss = _s4(8 * 64, 64, 1, 0)
     sc = lambda **kw: lib.cab_attn_key_scores(
-        FAKE, FAKE, kw.get("lse", FAKE), kw.get("dt", nat.CAB_BF16), 1, 8, 2, 64, 64, 128, st, st,
-        0.088, 1, kw.get("scores", FAKE), kw.get("ss", ss), 0, None)
-    assert sc(dt=nat.CAB_F32) == nat.CAB_EDTYPE
+        FAKE, FAKE, kw.get("lse", FAKE), kw.get("dt", nat.CAB_BF16), 1, 8, 2, 64, 64, 128,
+        kw.get("st", st), kw.get("st", st), 0.088, 1, kw.get("scores", FAKE), kw.get("ss", ss), 0, None)
+    assert sc(dt=9) == nat.CAB_EDTYPE
+    # fp32 is accepted; its rows must stay 16-byte aligned at 4 bytes per
+    # element (130-element rows are 260 bytes in bf16, 520 in fp32)
+    st130 = _s4(8 * 64 * 130, 64 * 130, 130, 1)
+    assert sc(dt=nat.CAB_F32, st=st130) == nat.CAB_ESHAPE
+    assert b"16-byte" in lib.cab_last_error()
     assert sc(lse=None) == nat.CAB_EINVAL
     assert sc(scores=None) == nat.CAB_EINVAL
     assert sc(ss=_s4(8 * 64, 64, 2, 0)) == nat.CAB_ESHAPE

@@ -63,9 +63,8 @@ def test_flash_attention_and_key_scores(cuda, dt, causal, H, Hkv, Nq, Nk, D):
     fin = np.isfinite(w_lse)
     assert np.array_equal(np.isfinite(got_lse), fin)
     np.testing.assert_allclose(got_lse[fin], w_lse[fin], atol=LSE_ATOL[dt], rtol=1e-4)
-    if dt != "fp32":
-        sc = key_scores(q.to(cuda), k.to(cuda), lse, causal=causal)
-        assert_scores_close(sc, w_sc, Nq)
+    sc = key_scores(q.to(cuda), k.to(cuda), lse, causal=causal)
+    assert_scores_close(sc, w_sc, Nq)
 
 
 @pytest.mark.parametrize("causal", [False, True])
