@@ -507,6 +507,9 @@ __device__ __forceinline__ void acc_block(WaveAcc<HD>& s, const WaveGeo<HD>& ge,
       pb[qt][3] = pack2<BF16>(pv[1][2], pv[1][3]);
     }
   }
+  // The P V products run at raised wave priority: the other wave of the SIMD
+  // then fills the MFMA gaps with its own softmax work, not the reverse.
+  if constexpr (!SPLIT) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -522,6 +525,7 @@ __device__ __forceinline__ void acc_block(WaveAcc<HD>& s, const WaveGeo<HD>& ge,
     if constexpr (SPLIT) s.lacc[qt] = mfma16<true>(ones, pl[qt], s.lacc[qt]);
     s.lacc[qt] = mfma16<BF16>(ones, pb[qt], s.lacc[qt]);
   }
+  if constexpr (!SPLIT) __builtin_amdgcn_s_setprio(0);
 }
 
 // Merge of the two key halves of a query half through LDS: the kh = 1 wave
