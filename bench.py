@@ -17,7 +17,7 @@ TFLOP/s, % of roofline".
 - ``bridge``: config 5 (structured bridge stress test, B=1 H=8 N=131072,
   sparsity 0.99): planted bridges kept, mask agreement with the CPU oracle on
   two heads, predictor + attention latency.
-- ``cpu_baseline``: the float64 numpy oracle on a bounded sample of the
+- ``cpu_baseline``: the numpy oracle (in float32) on a bounded sample of the
   config-4 attention workload, on this host's cores.
 - ``fp32_executor``, ``eviction_path``, ``token_frc``: config 4 with fp32
   inputs; dense attention + per-key totals, eviction selection and the

@@ -14,7 +14,7 @@ import threading
 import torch
 
 LIB_PATH = pathlib.Path(__file__).resolve().with_name("libcab_hip.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 CAB_OK, CAB_EINVAL, CAB_EDTYPE, CAB_ESHAPE, CAB_EWORKSPACE, CAB_EHIP = range(6)
 CAB_F32, CAB_F16, CAB_BF16 = 0, 1, 2

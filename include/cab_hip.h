@@ -49,7 +49,7 @@ enum { CAB_NORM_NONE = 0, CAB_NORM_MINMAX = 1 };
 /* FRC combination (experiments/longbench_qa/config.py:465; test.ipynb:111-145). */
 enum { CAB_FRC_ADDITIVE = 0, CAB_FRC_MULTIPLICATIVE = 1, CAB_FRC_AUGMENTED = 2 };
 
-#define CAB_ABI_VERSION 8
+#define CAB_ABI_VERSION 9
 
 int cab_abi_version(void);
 const char* cab_last_error(void);
