@@ -4,14 +4,15 @@
 // holds columns j = 64 c + l, through a buffer descriptor: no per-lane 64-bit
 // addresses, columns past M read as zero) and mapped branch-free to
 // order-preserving uint32 keys in registers, non-candidates to a sentinel.
-// The k-th smallest key is found by a radix select (one pass per key byte
-// that the candidates do not all share, a 256-bin LDS histogram per wave with
-// four copies per bin, a wave-wide prefix scan, ending early at a bin of one
-// key). A last pass in ascending j keeps every key below the threshold and
-// the first (in j) keys equal to it -- when every key equal to the threshold
-// is kept, simply every key at most the threshold -- assigns output slots
-// with a prefix popcount, and writes the compact ascending index list and,
-// optionally, the dense 0/1 row.
+// The k-th smallest key is found by a radix select (8-bit digit windows
+// from the highest bit where two candidates differ, a 256-bin LDS histogram
+// per wave with four copies per bin, a wave-wide prefix scan, ending early at
+// a bin of one key). A last pass in ascending j keeps every key below the
+// threshold and the first (in j) keys equal to it -- when every key equal to
+// the threshold is kept, simply every key at most the threshold -- assigns
+// output slots with v_mbcnt over the selection mask, and writes the compact
+// ascending index list and, optionally, the dense 0/1 row through buffer
+// stores.
 //
 // Hybrid selection (cab_block_topk_hybrid) first runs the same search on
 // the row's magnitude keys for its magnitude quota, marks those blocks taken,
@@ -216,13 +217,18 @@ __device__ __forceinline__ uint32_t kth_key(Key key, Cand is_cand, int nch, int6
 }
 
 // Register-path form of kth_key for keys held in registers with KEY_NONE for
-// non-candidates. The histogram keeps HSUB_REG copies of every bin, copy s of bin
-// b at word s * HSTRIDE + b: copies of one bin fall into different LDS banks
-// (HSTRIDE % 64 == 4), and lane l clears and sums bins 4 l .. 4 l + 3 of a
-// copy with one 16-byte access. The first counting pass counts every key
-// (all candidates share the bytes above it; a KEY_NONE key lands in bin 255,
-// above every candidate of that bin); later passes count the keys matching
-// the prefix. eq_total returns how many keys equal theta.
+// non-candidates. The digit windows are not byte-aligned: the first covers
+// the 8 bits below and at the highest bit where two candidates differ (the
+// candidates share every bit above it), each later one the next 8 bits down,
+// so the first pass spreads a narrow range of scores over up to 256 bins
+// (fewer same-bin LDS atomics, fewer keys left in the chosen bin). The
+// histogram keeps HSUB_REG copies of every bin, copy s of bin b at word
+// s * HSTRIDE + b: copies of one bin fall into different LDS banks (HSTRIDE %
+// 64 == 4), and lane l clears and sums bins 4 l .. 4 l + 3 of a copy with one
+// 16-byte access. The first pass counts every key (a KEY_NONE key lands in the
+// top bin, after every candidate of that bin: it is the largest key); later
+// passes count the keys matching the prefix. eq_total returns how many keys
+// equal theta.
 constexpr int HSTRIDE = 260;
 constexpr int HSUB_REG = 4;  // copies per bin (fewer copies: more waves per CU fit the LDS)
 
@@ -250,28 +256,31 @@ __device__ __forceinline__ uint32_t kth_key_reg(const uint32_t (&key)[NCH], int6
     eq_total = 0xffffffffu;  // unknown: the caller ranks the ties
     return kand;
   }
-  uint32_t prefix = 0u, pmask = 0u;
+  int hb = 31 - __builtin_clz(diff);          // highest bit where candidates differ
+  uint32_t pmask = ~((2u << hb) - 1u);        // the bits above it (none for hb = 31)
+  uint32_t prefix = kand & pmask;
   int64_t rem = need;
   bool first = true;
-  char* hb = reinterpret_cast<char*>(hist) + (lane % HSUB_REG) * HSTRIDE * 4;
-#pragma unroll
-  for (int pass = 0; pass < 4; ++pass) {
-    const int shift = 24 - 8 * pass;
-    if (((diff >> shift) & 255u) == 0u) {  // every candidate shares this byte
-      prefix |= kand & (255u << shift);
-      pmask |= 255u << shift;
-      continue;
-    }
+  char* hp = reinterpret_cast<char*>(hist) + (lane % HSUB_REG) * HSTRIDE * 4;
+  while (hb >= 0) {  // at most four windows
+    const int lo = hb >= 7 ? hb - 7 : 0;
+    const uint32_t wmask = (2u << (hb - lo)) - 1u;
     wave_sync();  // the previous pass's reads are done
 #pragma unroll
     for (int q = 0; q < HSUB_REG; ++q)
       *reinterpret_cast<u32x4*>(hist + q * HSTRIDE + 4 * lane) = u32x4{0u, 0u, 0u, 0u};
     wave_sync();
+    if (first) {
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const uint32_t kc = key[c];
-      const uint32_t inc = first ? 1u : ((kc & pmask) == prefix ? 1u : 0u);
-      atomicAdd(reinterpret_cast<uint32_t*>(hb + (((kc >> shift) & 255u) << 2)), inc);
+      for (int c = 0; c < NCH; ++c)
+        atomicAdd(reinterpret_cast<uint32_t*>(hp + (((key[c] >> lo) & wmask) << 2)), 1u);
+    } else {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const uint32_t kc = key[c];
+        atomicAdd(reinterpret_cast<uint32_t*>(hp + (((kc >> lo) & wmask) << 2)),
+                  (kc & pmask) == prefix ? 1u : 0u);
+      }
     }
     first = false;
     wave_sync();
@@ -310,10 +319,10 @@ __device__ __forceinline__ uint32_t kth_key_reg(const uint32_t (&key)[NCH], int6
     const uint32_t below = __shfl(run, src, 64);
     const uint32_t sel_cnt = __shfl(bcnt, src, 64);
     rem -= below;
-    prefix |= sel_bin << shift;
-    pmask |= 255u << shift;
+    prefix |= sel_bin << lo;
+    pmask |= wmask << lo;
     eq_total = sel_cnt;
-    if (sel_cnt == 1u && shift > 0) {
+    if (sel_cnt == 1u && lo > 0) {
       // One candidate left (rem == 1): theta is its key.
       uint32_t kv = 0u;
 #pragma unroll
@@ -325,9 +334,16 @@ __device__ __forceinline__ uint32_t kth_key_reg(const uint32_t (&key)[NCH], int6
       need_eq = rem;
       return kv;
     }
+    hb = lo - 1;
   }
   need_eq = rem;  // keys below theta: need - rem; the rest are ties at theta
   return prefix;
+}
+
+// Number of set bits of the wave mask m below this lane (v_mbcnt).
+__device__ __forceinline__ uint32_t rank_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
 }
 
 // Order key of the score bits u (see order_key), branch-free.
@@ -341,7 +357,10 @@ __device__ __forceinline__ uint32_t order_key_bits(uint32_t u, uint32_t flip) {
 
 template <int NCH, bool HYB>
 __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  // The wave index through readfirstlane: the row and everything derived
+  // from it (descriptors, limits, the histogram) stay in scalar registers.
+  const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wv;
   if (row >= a.rows) return;  // uniform per wave
   const int lane = lane_id();
   const int64_t i = row % a.M;
@@ -350,18 +369,18 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   const bool kd = a.keep_diagonal != 0;
   const int64_t need = kd ? krow - 1 : krow;
   const uint32_t flip = a.select_high ? 0xffffffffu : 0u;
-  const uint64_t lt_mask = lanemask_lt();
   __shared__ __attribute__((aligned(16))) uint32_t hist_all[4][HSUB_REG * HSTRIDE];
-  uint32_t* hist = hist_all[threadIdx.x >> 6];
+  uint32_t* hist = hist_all[wv];
 
   // Lane l holds column j = 64 c + l of chunk c. Column j is a candidate when
   // j < ncand (c < climit) and it is not the forced diagonal; the rest get
   // KEY_NONE. The row is read through a buffer descriptor (columns past M
   // read as zero and are no candidates), all NCH loads in flight together.
   const int climit = static_cast<int>((ncand - lane + 63) >> 6);
-  const int dc = static_cast<int>(i >> 6);
-  const bool dlane = kd && lane == static_cast<int>(i & 63);
-  auto is_cand = [&](int c) { return c < climit && !(c == dc && dlane); };
+  // dcl: the chunk holding the forced diagonal on its lane, -1 on the other
+  // lanes (one compare per chunk, no per-chunk masks kept across passes).
+  const int dcl = kd && lane == static_cast<int>(i & 63) ? static_cast<int>(i >> 6) : -1;
+  auto is_cand = [&](int c) { return c < climit && c != dcl; };
   const brsrc_t frs = make_rsrc(a.frc + row * a.M, static_cast<uint32_t>(a.M * 4));
   uint32_t key[NCH];
   {
@@ -370,7 +389,8 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
     for (int c = 0; c < NCH; ++c)
       u[c] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(frs, 4u * lane, 256u * c, 0));
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) key[c] = is_cand(c) ? order_key_bits(u[c], flip) : KEY_NONE;
+    for (int c = 0; c < NCH; ++c)  // branch-free: KEY_NONE is all ones
+      key[c] = order_key_bits(u[c], flip) | (is_cand(c) ? 0u : KEY_NONE);
   }
 
   // Hybrid: the need_m candidates of highest magnitude first (bit c of msel
@@ -400,7 +420,7 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
       const bool cand = mkey[c] != KEY_NONE && need_m > 0;
       const bool eq = cand && mkey[c] == mtheta;
       const uint64_t eqb = ballot64(eq);
-      const int64_t eq_rank = eq_seen + __popcll(eqb & lt_mask);
+      const int64_t eq_rank = eq_seen + rank_below(eqb);
       if ((cand && mkey[c] < mtheta) || (eq && eq_rank < meq)) msel[c >> 6] |= 1ull << (c & 63);
       eq_seen += __popcll(eqb);
     }
@@ -417,38 +437,38 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   uint32_t eq_total = 0;
   const uint32_t theta = kth_key_reg<NCH>(key, need_f, need_eq, eq_total, hist);
 
-  int64_t pos = 0;
+  // The compact list and the dense row go out through buffer stores: a lane
+  // with nothing to store passes an offset past the buffer, which the
+  // hardware drops (as it drops dense columns past M), so the stores need no
+  // branches and no 64-bit addresses.
+  uint32_t pos = 0;
   int32_t* out = a.kv_idx + row * a.k;
-  uint8_t* drow = a.dense ? a.dense + row * a.M : nullptr;
-  const int Mi = static_cast<int>(a.M);
+  const brsrc_t ors = make_rsrc(out, static_cast<uint32_t>(a.k * 4));
+  const bool dense = a.dense != nullptr;
+  const brsrc_t drs = make_rsrc(dense ? a.dense + row * a.M : nullptr, dense ? static_cast<uint32_t>(a.M) : 0u);
+  constexpr uint32_t DROP = 0x80000000u;
+  auto emit = [&](int c, bool sel) {
+    const uint64_t selb = ballot64(sel);
+    const uint32_t j = 64u * c + lane;
+    __builtin_amdgcn_raw_buffer_store_b32(j, ors, sel ? 4u * (pos + rank_below(selb)) : DROP, 0u, 0);
+    if (dense) __builtin_amdgcn_raw_buffer_store_b8(static_cast<unsigned char>(sel ? 1 : 0), drs, j, 0u, 0);
+    pos += static_cast<uint32_t>(__popcll(selb));
+  };
   if (need_f <= 0 || need_eq == static_cast<int64_t>(eq_total)) {
     // Every key equal to theta is kept: a key is selected iff it is at most
     // theta (KEY_NONE ranks above every real theta).
     const bool any = need_f > 0;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const int j = 64 * c + lane;
-      const bool sel = (any && key[c] <= theta) || (HYB && taken(c)) || (c == dc && dlane);
-      const uint64_t selb = ballot64(sel);
-      if (sel) out[pos + __popcll(selb & lt_mask)] = j;
-      if (drow && j < Mi) drow[j] = sel ? 1 : 0;
-      pos += __popcll(selb);
-    }
+    for (int c = 0; c < NCH; ++c) emit(c, (any && key[c] <= theta) || (HYB && taken(c)) || c == dcl);
   } else {
     int64_t eq_seen = 0;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      const int j = 64 * c + lane;
       const bool cand = key[c] != KEY_NONE;
       const bool eq = cand && key[c] == theta;
       const uint64_t eqb = ballot64(eq);
-      const int64_t eq_rank = eq_seen + __popcll(eqb & lt_mask);
-      const bool sel = (cand && key[c] < theta) || (eq && eq_rank < need_eq) || (HYB && taken(c)) ||
-                       (c == dc && dlane);
-      const uint64_t selb = ballot64(sel);
-      if (sel) out[pos + __popcll(selb & lt_mask)] = j;
-      if (drow && j < Mi) drow[j] = sel ? 1 : 0;
-      pos += __popcll(selb);
+      const int64_t eq_rank = eq_seen + rank_below(eqb);
+      emit(c, (cand && key[c] < theta) || (eq && eq_rank < need_eq) || (HYB && taken(c)) || c == dcl);
       eq_seen += __popcll(eqb);
     }
   }
@@ -463,7 +483,10 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
 // than the last tie the quota keeps.
 template <bool HYB>
 __global__ __launch_bounds__(256) void topk_stream_kernel(TopkArgs a) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  // The wave index through readfirstlane: the row and everything derived
+  // from it (descriptors, limits, the histogram) stay in scalar registers.
+  const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wv;
   if (row >= a.rows) return;  // uniform per wave
   const int lane = lane_id();
   const int64_t i = row % a.M;
@@ -476,7 +499,7 @@ __global__ __launch_bounds__(256) void topk_stream_kernel(TopkArgs a) {
   const bool high = a.select_high != 0;
   const uint64_t lt_mask = lanemask_lt();
   __shared__ __attribute__((aligned(16))) uint32_t hist_all[4][256 * HSUB];
-  uint32_t* hist = hist_all[threadIdx.x >> 6];
+  uint32_t* hist = hist_all[wv];
   const int Mi = static_cast<int>(a.M), nch = (Mi + 63) / 64;
   const int ncand_i = static_cast<int>(ncand), i_i = static_cast<int>(i);
   auto is_cand = [&](int c) {
