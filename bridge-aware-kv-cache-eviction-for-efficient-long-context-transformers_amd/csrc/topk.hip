@@ -56,10 +56,11 @@ __device__ __forceinline__ uint32_t order_key(float f, bool high) {
 
 // theta = the need-th smallest key among the candidates (the largest theta
 // with count(key < theta) < need), by a radix select over the key bits, most
-// significant byte first. A byte every candidate shares (a wave-wide AND /
-// OR) needs no pass; otherwise a pass histograms that byte of the candidates
-// that match the prefix chosen so far in the wave's LDS histogram, and a
-// wave-wide scan picks the bin where the running count reaches need. A bin
+// significant first. Bits every candidate shares (a wave-wide AND / OR) need
+// no pass; from the highest bit where two candidates differ, each pass
+// histograms the next 8 bits of the candidates that match the prefix chosen
+// so far in the wave's LDS histogram, and a wave-wide scan picks the bin
+// where the running count reaches need. A bin
 // holding a single key ends the search: that key is theta. The histogram keeps HSUB interleaved copies of every bin
 // (lane % HSUB picks one), so that keys of a row that share the digit do not
 // all update one LDS word. Returns in need_eq how many keys equal to theta
@@ -123,18 +124,15 @@ __device__ __forceinline__ uint32_t kth_key(Key key, Cand is_cand, int nch, int6
     need_eq = need;
     return kand;
   }
-  uint32_t prefix = 0u, pmask = 0u;
+  // Digit windows of 8 bits from the highest bit where two candidates differ
+  // down (the candidates share every bit above it).
+  int hb = 31 - __builtin_clz(diff);
+  uint32_t pmask = ~((2u << hb) - 1u);
+  uint32_t prefix = kand & pmask;
   int64_t rem = need;  // rank still to find among the keys matching the prefix
-  bool done = false;
-#pragma unroll
-  for (int pass = 0; pass < 4; ++pass) {
-    const int shift = 24 - 8 * pass;
-    if (done) break;
-    if (((diff >> shift) & 255u) == 0u) {  // every candidate shares this byte
-      prefix |= kand & (255u << shift);
-      pmask |= 255u << shift;
-      continue;
-    }
+  while (hb >= 0) {  // at most four windows
+    const int lo = hb >= 7 ? hb - 7 : 0;
+    const uint32_t wmask = (2u << (hb - lo)) - 1u;
     wave_sync();  // the previous pass's reads are done
     // Layout: 16-byte slot (q, l) at index 64 q + l holds copies 4 (q % 2) .. +3
     // of bin 4 l + q / 2, so lane l clears and sums its own four bins with
@@ -147,14 +145,14 @@ __device__ __forceinline__ uint32_t kth_key(Key key, Cand is_cand, int nch, int6
     for_chunks<NCH>(nch, [&](int c) {
       if constexpr (SENT) {
         const uint32_t kc = key(c);
-        const uint32_t bn = (kc >> shift) & 255u;
+        const uint32_t bn = (kc >> lo) & wmask;
         const uint32_t q = 2u * (bn & 3u) + (sub >> 2);
         atomicAdd(&hist[4u * (64u * q + (bn >> 2)) + (sub & 3u)], (kc & pmask) == prefix ? 1u : 0u);
       } else {
         if (!is_cand(c)) return;
         const uint32_t kc = key(c);
         if ((kc & pmask) == prefix) {
-          const uint32_t bn = (kc >> shift) & 255u;
+          const uint32_t bn = (kc >> lo) & wmask;
           const uint32_t q = 2u * (bn & 3u) + (sub >> 2);
           atomicAdd(&hist[4u * (64u * q + (bn >> 2)) + (sub & 3u)], 1u);
         }
@@ -195,9 +193,9 @@ __device__ __forceinline__ uint32_t kth_key(Key key, Cand is_cand, int nch, int6
     const uint32_t below = __shfl(run, src, 64);
     const uint32_t sel_cnt = __shfl(bcnt, src, 64);
     rem -= below;
-    prefix |= sel_bin << shift;
-    pmask |= 255u << shift;
-    if (sel_cnt == 1u && shift > 0) {
+    prefix |= sel_bin << lo;
+    pmask |= wmask << lo;
+    if (sel_cnt == 1u && lo > 0) {
       // One candidate left (rem == 1): theta is its key.
       uint32_t kv = 0u;
       for_chunks<NCH>(nch, [&](int c) {
@@ -209,8 +207,9 @@ __device__ __forceinline__ uint32_t kth_key(Key key, Cand is_cand, int nch, int6
       for (int off = 1; off < 64; off <<= 1)
         kv |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(kv), off, 64));
       prefix = kv;
-      done = true;
+      break;
     }
+    hb = lo - 1;
   }
   need_eq = rem;  // keys below theta: need - rem; the rest are ties at theta
   return prefix;
