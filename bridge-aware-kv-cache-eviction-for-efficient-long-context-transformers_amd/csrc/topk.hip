@@ -274,11 +274,14 @@ __device__ __forceinline__ uint32_t kth_key_reg(const uint32_t (&key)[NCH], int6
       for (int c = 0; c < NCH; ++c)
         atomicAdd(reinterpret_cast<uint32_t*>(hp + (((key[c] >> lo) & wmask) << 2)), 1u);
     } else {
+      // After the first window few keys still match the prefix: a chunk with
+      // no matching lane (a uniform branch) skips its LDS atomic.
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
         const uint32_t kc = key[c];
-        atomicAdd(reinterpret_cast<uint32_t*>(hp + (((kc >> lo) & wmask) << 2)),
-                  (kc & pmask) == prefix ? 1u : 0u);
+        const bool m = (kc & pmask) == prefix;
+        if (ballot64(m) != 0u)
+          atomicAdd(reinterpret_cast<uint32_t*>(hp + (((kc >> lo) & wmask) << 2)), m ? 1u : 0u);
       }
     }
     first = false;
