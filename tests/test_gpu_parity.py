@@ -365,6 +365,35 @@ def test_topk_shared_key_bytes(cuda, M, flags):
         np.testing.assert_array_equal(mask.cpu().numpy(), omask)
 
 
+@pytest.mark.parametrize("M", [5, 100, 2000])
+@pytest.mark.parametrize("flags", [(False, True, False), (True, False, True), (False, False, True)])
+def test_topk_narrow_and_straddling_windows(cuda, M, flags):
+    """The digit windows start at the highest bit where two candidates
+    differ: rows whose keys differ only in the lowest 2, 3 or 7 bits (one
+    window narrower than 8 bits), in bits 7 .. 14 (a window straddling a byte
+    boundary, then a 7-bit one), in the sign alone (+x / -x), and rows whose
+    first window holds real keys in the top bin beside the non-candidates."""
+    from cab_attention.kernels import generate_block_index
+    select_high, keep_diag, causal = flags
+    g = torch.Generator().manual_seed(300 + M)
+    f = torch.empty(1, 6, M, M)
+    f[0, 0] = 1.0 + torch.randint(0, 4, (M, M), generator=g).float() * 2.0 ** -23    # bits 0 .. 1
+    f[0, 1] = 1.0 + torch.randint(0, 8, (M, M), generator=g).float() * 2.0 ** -23    # bits 0 .. 2
+    f[0, 2] = 1.0 + torch.randint(0, 128, (M, M), generator=g).float() * 2.0 ** -23  # bits 0 .. 6
+    f[0, 3] = 1.0 + torch.randint(0, 2 ** 15, (M, M), generator=g).float() * 2.0 ** -23  # bits 0 .. 14
+    f[0, 4] = 0.75 * (2.0 * torch.randint(0, 2, (M, M), generator=g).float() - 1.0)  # sign only
+    top = torch.full((M, M), -1.0)                                      # the top key (low scores kept)
+    top[torch.rand(M, M, generator=g) < 0.5] = float("nan")             # or NaN, above +inf
+    f[0, 5] = top
+    for sp in (0.95, 0.5):
+        idx, cnt, mask = generate_block_index(f.to(cuda), sp, select_high=select_high,
+                                              keep_diagonal=keep_diag, causal=causal, dense=True)
+        omask, oidx, ocnt = O.generate_block_mask(f.numpy(), sp, select_high, keep_diag, causal)
+        np.testing.assert_array_equal(cnt.cpu().numpy(), ocnt)
+        np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
+        np.testing.assert_array_equal(mask.cpu().numpy(), omask)
+
+
 @pytest.mark.parametrize("M", [7, 100, 513, 2000])
 @pytest.mark.parametrize("ratio", [0.0, 0.3, 0.5, 1.0])
 @pytest.mark.parametrize("flags", [(True, True, False), (False, True, True), (True, False, True)])
