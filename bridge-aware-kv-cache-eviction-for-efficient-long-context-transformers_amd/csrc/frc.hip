@@ -2,10 +2,12 @@
 //
 // Pipeline per (b, h), Mp = M rounded up to 128:
 //  1. STATS: A = qc kc^T * alpha on MFMA, per-tile min/max partials
-//     (aff_tile_kernel for 16-bit inputs with D <= 128: LDS-staged 128 x 128
-//     tiles; affinity_stats_kernel otherwise: operands straight from memory).
-//  2. minmax_finalize_kernel: per-(b,h) min/max from the partials.
-//  3. EMIT (aff_tile_kernel / affinity_kernel): recomputes the A tile, normalises it, and writes
+//     (aff_strip_kernel for 16-bit inputs with D <= 128: strips of LDS-staged
+//     128 x 128 tiles; affinity_stats_kernel otherwise: operands straight
+//     from memory).
+//  2. per-(b,h) min/max from the partials: inside aff_strip_kernel's EMIT
+//     pass, minmax_finalize_kernel ahead of affinity_kernel.
+//  3. EMIT (aff_strip_kernel / affinity_kernel): recomputes the A tile, normalises it, and writes
 //     Ahat in row-major X and transposed XT planes (zero outside M), the fp32
 //     Ahat diagnostic and, for the augmented formula, row-sum partials. The
 //     planes hold either
@@ -24,6 +26,8 @@
 //     dropped lo*lo term is below 2^-16 relative); LDS double-buffered, with
 //     the FRC combination fused into the epilogue.
 // Algorithmic work: 2 M^2 D flops (affinity) + 2 M^3 flops (triangles).
+#include <atomic>
+
 #include "cab_internal.h"
 
 namespace cab {
@@ -72,8 +76,9 @@ struct AffArgs {
   int32_t D;
   float alpha;
   int normalization;
-  float* mmpart;       // [BH][ns*ns][2], ns = ceil(Mp / 256) STATS tiles per dim
-  const float* mm;     // [BH][2]
+  float* mmpart;       // [BH][nparts][2] min / max partials, nparts <= (Mp / 128)^2
+  float* mm;           // [BH][2] min / max of alpha A
+  int64_t nparts;      // min / max partials per (b, h)
   uint16_t* xhi;       // [BH][Mp][Mp]
   uint16_t* xlo;
   uint16_t* xthi;
@@ -83,6 +88,7 @@ struct AffArgs {
   int f16_planes;      // X = f16, xlo = f16 low part of X, XT = f16 (xtlo unused)
   int fused;           // with f16_planes: XT = f16(I - lambda Ahat^T), xlo unused
   float lambda;
+  int64_t strip;       // aff_strip_kernel: 128 x 128 tiles per workgroup
 };
 
 // One wave computes a 64 x 32 YT block of qc kc^T (fp32 accumulate) as
@@ -361,112 +367,127 @@ __global__ __launch_bounds__(256) void affinity_kernel(AffArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// aff_tile_kernel: the STATS and EMIT passes for 16-bit inputs with D <= 128,
-// one 128 x 128 tile of A per workgroup of NW waves, two workgroups per CU
-// (one stages its panels while the other computes).
-// Both 128-row panels (Qc rows i, Kc rows j of the tile) are staged once into
-// LDS with buffer loads, 256 bytes per row, 16-byte chunk c of row R at chunk
-// position c ^ (R % 16) (the 16 rows one operand read touches fall into 16
-// distinct bank groups); rows at or past M and dims at or past D read as zero.
-// Wave w computes rows j 64 (w / (NW / 2)) .. +64 (two MFMA tiles) and NY
-// tiles of 32 columns i of C = Kc Qc^T (C[j][i] = A[i][j] / alpha) with
-// 32x32x16 MFMAs; lane l then holds column i = l % 32 of each tile and rows
-// j = 8 (e / 4) + 4 (l / 32) + e % 4 of element e: runs of four consecutive
-// j of one row i of A.
-// STATS: min / max of A over i, j < M per tile.
-// EMIT: both plane orientations go through LDS tiles (reusing the panels'
-// space) so that every global store is a whole 16-byte piece of a row:
-//   X tile [128 i][128 j]: 8-byte writes of the runs, chunk c of row il at
-//     chunk position c ^ (il % 16);
-//   XT tile [128 j][128 i]: 2-byte writes (a wave's 32 lanes of one row j
-//     are consecutive i).
-// Row-sum partials per 64 columns for the augmented formula.
-// Work per tile: 2 128^2 D flops; EMIT writes 32 KB per plane.
+// aff_strip_kernel: the STATS and EMIT passes for 16-bit inputs with D <= 128.
+// A workgroup walks a strip of up to `strip` consecutive 128 x 128 tiles of A
+// along j, all in one 128-row band i0 of one (b, h):
+//  - the band's Qc panel (128 rows x 256 bytes; 16-byte chunk c of row R at
+//    chunk position c ^ (R % 16), so that the 16 rows one operand read
+//    touches fall into 16 distinct bank groups; rows at or past M and dims at
+//    or past D read as zero) is staged into LDS once, and each compute wave
+//    then keeps its MFMA operands of it in registers for the whole strip;
+//  - the Kc panel of every tile is staged in turn, double-buffered (the Qc
+//    panel's space is the second buffer once its operands are in registers),
+//    so that the next tile's panel is in flight while a tile is computed;
+//  - eight compute waves split a tile 2 (64 rows j) x 4 (32 columns i) and
+//    compute C = Kc Qc^T (C[j][i] = A[i][j] / alpha) with 32x32x16 MFMAs;
+//    lane l then holds column i = l % 32 of each of its two 32 x 32 tiles and
+//    rows j = 8 (e / 4) + 4 (l / 32) + e % 4 of element e: runs of four
+//    consecutive j of one row i of A.
+// STATS (8 waves, two workgroups per CU): min / max of A over i, j < M per
+// strip.
+// EMIT (8 compute + 4 store waves, one workgroup per CU): the compute waves
+// normalise a tile into two LDS tiles, X [128 i][128 j] (8-byte writes of the
+// runs, chunk c of row il at chunk position c ^ (il % 16)) and XT
+// [128 j][128 i] (2-byte writes: a wave's 32 lanes of one row j are
+// consecutive i); the store waves copy both to the planes as whole 16-byte row
+// pieces while the compute waves go on with the next tile. Loads and stores
+// are thus issued by different waves: vmcnt counts both, so a wave that
+// stored would wait for its stores whenever it waits for a panel.
+// Row-sum partials (augmented formula) per 64 columns j.
+// Work per tile: 2 128^2 D flops; EMIT writes 32 KB per plane and tile.
 // ---------------------------------------------------------------------------
 constexpr int AGT = 128;                 // tile edge and panel rows
 constexpr int AG_PANEL = AGT * 256;      // bytes of one staged panel
 constexpr int AG_DMAX = 128;             // largest D a panel holds
-constexpr int AG_WAVES = 8;              // waves per tile workgroup (4 or 8)
+constexpr int AG_CW = 8;                 // compute waves
+constexpr int AG_SW = 4;                 // store waves (EMIT)
 
-template <typename T, bool EMIT, int NW>
-__global__ __launch_bounds__(64 * NW, 2) void aff_tile_kernel(AffArgs a) {
+// Stages rows [0, 128) of a row-major [rows][D] 16-bit panel at `base` (the
+// first `rows` of them exist) into LDS `dst` in the swizzled layout; issued
+// by the eight compute waves, four 1 KB buffer loads each.
+__device__ __forceinline__ void ag_stage(const char* base, int64_t rows, uint32_t rowb, int kch,
+                                         int w, int lane, char* dst) {
+  const brsrc_t rs = make_rsrc(base, static_cast<uint32_t>((rows < AGT ? rows : AGT) * rowb));
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    const int blk = 4 * w + n;
+    const int R = 4 * blk + (lane >> 4);
+    const int c = (lane & 15) ^ (R & 15);
+    const uint32_t voff = c < kch ? static_cast<uint32_t>(R) * rowb + 16u * c : 0x80000000u;
+    bdma16(rs, voff, 0, dst + blk * 1024);
+  }
+}
+
+template <typename T, bool EMIT, int KS>
+__global__ __launch_bounds__(EMIT ? 64 * (AG_CW + AG_SW) : 64 * AG_CW, EMIT ? 3 : 4) void aff_strip_kernel(
+    AffArgs a) {
   constexpr bool BF = std::is_same<T, bf16_t>::value;
-  constexpr int NY = 8 / NW;              // 32-column tiles per wave (2 row tiles of 32 j)
-  constexpr int NT = 64 * NW;             // threads
-  __shared__ __attribute__((aligned(16))) char lds[2 * AG_PANEL];  // [Q panel][K panel]; EMIT: X, XT tiles
-  __shared__ float red[NW][2];
+  // [panel buffer 0 (Qc, then Kc)][panel buffer 1]; EMIT: [X tile][XT tile]
+  __shared__ __attribute__((aligned(16))) char lds[(EMIT ? 4 : 2) * AG_PANEL];
+  __shared__ float red[EMIT ? 2 * AGT : 2 * AG_CW];  // EMIT: row-sum partials; STATS: min / max
   const int64_t ns = a.Mp / AGT;  // Mp is a multiple of 128
+  const int64_t strip = a.strip;
+  const int64_t nstrip = (ns + strip - 1) / strip;
   const int64_t logical = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x));
-  const int64_t bh = logical / (ns * ns);
-  const int64_t tile = logical - bh * ns * ns;
-  const int64_t ti = tile / ns, tj = tile - (tile / ns) * ns;
-  const int64_t i0 = ti * AGT, j0 = tj * AGT;
-  const int w = threadIdx.x >> 6, lane = lane_id(), tid = threadIdx.x;
+  const int64_t bh = logical / (ns * nstrip);
+  const int64_t part = logical - bh * ns * nstrip;  // strip index within (b, h)
+  const int64_t ti = part / nstrip;
+  const int64_t tj0 = (part - ti * nstrip) * strip;
+  const int cnt = static_cast<int>(ns - tj0 < strip ? ns - tj0 : strip);
+  const int64_t i0 = ti * AGT;
+  // The wave index is uniform within a wave: the role branches below are scalar.
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = lane_id(), tid = threadIdx.x;
+  const bool compute = w < AG_CW;
   const int kch = a.D / 8;
   const uint32_t rowb = static_cast<uint32_t>(a.D) * 2;
-
-  {
-    // Staging: 32 loads of 4 rows per panel, spread over the waves.
-    const char* qb = static_cast<const char*>(a.qc) + (bh * a.M + i0) * rowb;
-    const char* kb = static_cast<const char*>(a.kc) + (bh * a.M + j0) * rowb;
-    const int64_t qrows = a.M - i0, krows = a.M - j0;  // > 0: tiles start below M
-    const brsrc_t qrs = make_rsrc(qb, static_cast<uint32_t>((qrows < AGT ? qrows : AGT) * rowb));
-    const brsrc_t krs = make_rsrc(kb, static_cast<uint32_t>((krows < AGT ? krows : AGT) * rowb));
-#pragma unroll
-    for (int n = 0; n < 32 / NW; ++n) {
-      const int blk = (32 / NW) * w + n;
-      const int R = 4 * blk + (lane >> 4);
-      const int c = (lane & 15) ^ (R & 15);
-      const uint32_t voff = c < kch ? static_cast<uint32_t>(R) * rowb + 16u * c : 0x80000000u;
-      bdma16(qrs, voff, 0, lds + blk * 1024);
-      bdma16(krs, voff, 0, lds + AG_PANEL + blk * 1024);
-    }
+  const char* const kbase = static_cast<const char*>(a.kc) + bh * a.M * rowb;
+  // The Kc panel of tile t sits in buffer (t + 1) % 2.
+  auto kbuf = [&](int t) { return lds + ((t + 1) & 1) * AG_PANEL; };
+  auto stage_k = [&](int t) {
+    const int64_t j0 = (tj0 + t) * AGT;
+    ag_stage(kbase + j0 * rowb, a.M - j0, rowb, kch, w, lane, kbuf(t));
+  };
+  if (compute) {
+    ag_stage(static_cast<const char*>(a.qc) + (bh * a.M + i0) * rowb, a.M - i0, rowb, kch, w, lane, lds);
+    stage_k(0);
   }
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-  __syncthreads();
 
-  const int jr0 = 64 * (w / (NW / 2)), ic0 = 32 * NY * (w % (NW / 2));
-  f32x16 acc[2][NY];
-#pragma unroll
-  for (int x = 0; x < 2; ++x)
-#pragma unroll
-    for (int y = 0; y < NY; ++y) acc[x][y] = f32x16{};
   const int h = lane >> 5;
-  const int ksteps = (a.D + 15) / 16;
-  for (int ks = 0; ks < ksteps; ++ks) {
-    const int c = 2 * ks + h;
-    u32x4 av[2], bv[NY];
-#pragma unroll
-    for (int x = 0; x < 2; ++x) {
-      const int R = jr0 + 32 * x + (lane & 31);
-      av[x] = *reinterpret_cast<const u32x4*>(lds + AG_PANEL + R * 256 + ((c ^ (R & 15)) << 4));
-    }
-#pragma unroll
-    for (int y = 0; y < NY; ++y) {
-      const int R = ic0 + 32 * y + (lane & 31);
-      bv[y] = *reinterpret_cast<const u32x4*>(lds + R * 256 + ((c ^ (R & 15)) << 4));
-    }
-#pragma unroll
-    for (int x = 0; x < 2; ++x)
-#pragma unroll
-      for (int y = 0; y < NY; ++y) {
-        if constexpr (BF)
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8, av[x]), __builtin_bit_cast(bf16x8, bv[y]), acc[x][y], 0, 0, 0);
-        else
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-              __builtin_bit_cast(f16x8, av[x]), __builtin_bit_cast(f16x8, bv[y]), acc[x][y], 0, 0, 0);
-      }
-  }
-
-  // Tile-local coordinates: column i = li0 + 32 y of tile y, rows
-  // j = lj0 + 32 x + 8 g + r of run g (elements 4 g + r) of tile x.
+  const int jr0 = 64 * ((w >> 2) & 1), ic0 = 32 * (w & 3);
+  // Tile-local coordinates: column i = li0, rows j = lj0 + 32 x + 8 g + r of
+  // run g (elements 4 g + r) of tile x.
   const int li0 = ic0 + (lane & 31), lj0 = jr0 + 4 * h;
   auto extent = [](int64_t n) { return static_cast<int>(n < 0 ? 0 : (n < AGT ? n : AGT)); };
-  const int mi = extent(a.M - i0), mj = extent(a.M - j0);
-  const bool interior = mi == AGT && mj == AGT;
-  auto inside = [&](int x, int y, int e) {
-    return li0 + 32 * y < mi && lj0 + 32 * x + 8 * (e >> 2) + (e & 3) < mj;
+  const int mi = extent(a.M - i0);
+  u32x4 qf[KS];  // the wave's Qc operands: rows i of its column tile
+  auto load_q = [&]() {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int R = li0, c = 2 * ks + h;
+      qf[ks] = *reinterpret_cast<const u32x4*>(lds + R * 256 + ((c ^ (R & 15)) << 4));
+    }
+  };
+  f32x16 acc[2];
+  auto product = [&](int t) {
+    const char* kb = kbuf(t);
+    acc[0] = f32x16{};
+    acc[1] = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int c = 2 * ks + h;
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const int R = jr0 + 32 * x + (lane & 31);
+        const u32x4 av = *reinterpret_cast<const u32x4*>(kb + R * 256 + ((c ^ (R & 15)) << 4));
+        if constexpr (BF)
+          acc[x] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, qf[ks]), acc[x], 0, 0, 0);
+        else
+          acc[x] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+              __builtin_bit_cast(f16x8, av), __builtin_bit_cast(f16x8, qf[ks]), acc[x], 0, 0, 0);
+      }
+    }
   };
 
   if constexpr (!EMIT) {
@@ -474,27 +495,36 @@ __global__ __launch_bounds__(64 * NW, 2) void aff_tile_kernel(AffArgs a) {
     // the extremes of alpha A are alpha times these (swapped for alpha < 0),
     // rounded once, as the EMIT pass rounds every entry.
     float lo = INFINITY, hi = -INFINITY;
-    if (interior) {
+    for (int t = 0; t < cnt; ++t) {
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's panel loads have landed
+      lds_barrier();                       // ... and every wave's; tile t - 1 is done
+      if (t == 0) {
+        load_q();
+        lds_barrier();  // every wave holds its Qc operands: buffer 0 is free
+      }
+      if (t + 1 < cnt) stage_k(t + 1);  // into the buffer tile t - 1 used
+      product(t);
+      const int mj = extent(a.M - (tj0 + t) * AGT);
+      if (mi == AGT && mj == AGT) {
 #pragma unroll
-      for (int x = 0; x < 2; ++x)
-#pragma unroll
-        for (int y = 0; y < NY; ++y)
+        for (int x = 0; x < 2; ++x)
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
-            lo = fminf(lo, acc[x][y][e]);
-            hi = fmaxf(hi, acc[x][y][e]);
+            lo = fminf(lo, acc[x][e]);
+            hi = fmaxf(hi, acc[x][e]);
           }
-    } else {
+      } else {
+        // Entries outside M enter as the identities: selects, not branches.
+        const int jlim = li0 < mi ? mj - lj0 : 0;  // rows lj0 + o of the lane inside M: o < jlim
 #pragma unroll
-      for (int x = 0; x < 2; ++x)
+        for (int x = 0; x < 2; ++x)
 #pragma unroll
-        for (int y = 0; y < NY; ++y)
-#pragma unroll
-          for (int e = 0; e < 16; ++e)
-            if (inside(x, y, e)) {
-              lo = fminf(lo, acc[x][y][e]);
-              hi = fmaxf(hi, acc[x][y][e]);
-            }
+          for (int e = 0; e < 16; ++e) {
+            const bool in = 32 * x + 8 * (e >> 2) + (e & 3) < jlim;
+            lo = fminf(lo, in ? acc[x][e] : INFINITY);
+            hi = fmaxf(hi, in ? acc[x][e] : -INFINITY);
+          }
+      }
     }
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -502,140 +532,219 @@ __global__ __launch_bounds__(64 * NW, 2) void aff_tile_kernel(AffArgs a) {
       hi = fmaxf(hi, shfl_xor_f32(hi, off));
     }
     if (lane == 0) {
-      red[w][0] = lo;
-      red[w][1] = hi;
+      red[2 * w] = lo;
+      red[2 * w + 1] = hi;
     }
-    __syncthreads();
+    lds_barrier();
     if (tid == 0) {
-      float m0 = red[0][0], m1 = red[0][1];
+      float m0 = red[0], m1 = red[1];
 #pragma unroll
-      for (int q = 1; q < NW; ++q) {
-        m0 = fminf(m0, red[q][0]);
-        m1 = fmaxf(m1, red[q][1]);
+      for (int q = 1; q < AG_CW; ++q) {
+        m0 = fminf(m0, red[2 * q]);
+        m1 = fmaxf(m1, red[2 * q + 1]);
       }
       const float e0 = m0 * a.alpha, e1 = m1 * a.alpha;
-      float* p = a.mmpart + (bh * ns * ns + tile) * 2;
+      float* p = a.mmpart + (bh * ns * nstrip + part) * 2;
       p[0] = a.alpha < 0.f ? e1 : e0;
       p[1] = a.alpha < 0.f ? e0 : e1;
     }
   } else {
+    // min / max of alpha A over (b, h) from the STATS partials, reduced by
+    // the store waves while the first panels load; the first strip of each
+    // (b, h) also stores them for the triangle pass.
+    __shared__ float mmred[AG_SW][2];
+    const bool minmax = a.normalization == CAB_NORM_MINMAX;
+    if (minmax && !compute) {
+      float lo = INFINITY, hi = -INFINITY;
+      for (int64_t q = tid - 64 * AG_CW; q < a.nparts; q += 64 * AG_SW) {
+        lo = fminf(lo, a.mmpart[(bh * a.nparts + q) * 2 + 0]);
+        hi = fmaxf(hi, a.mmpart[(bh * a.nparts + q) * 2 + 1]);
+      }
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        lo = fminf(lo, shfl_xor_f32(lo, off));
+        hi = fmaxf(hi, shfl_xor_f32(hi, off));
+      }
+      if (lane == 0) {
+        mmred[w - AG_CW][0] = lo;
+        mmred[w - AG_CW][1] = hi;
+      }
+    }
     float mn = 0.f, scale = 1.f;  // Ahat = (alpha A - mn) * scale
-    if (a.normalization == CAB_NORM_MINMAX) {
-      mn = a.mm[bh * 2 + 0];
-      const float mx = a.mm[bh * 2 + 1];
-      if (mx > mn) scale = 1.0f / (mx - mn + 1e-8f);
-      else mn = 0.f;  // constant A: left as is
-    }
-    {
-      // alpha A rounded on its own, as in the STATS pass (no fused
-      // multiply-add with the subtraction): the minimum maps to exactly 0.
-#pragma clang fp contract(off)
+    auto take_minmax = [&]() {
+      float m0 = mmred[0][0], m1 = mmred[0][1];
 #pragma unroll
-      for (int x = 0; x < 2; ++x)
-#pragma unroll
-        for (int y = 0; y < NY; ++y)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const float v = (acc[x][y][e] * a.alpha - mn) * scale;
-            acc[x][y][e] = interior || inside(x, y, e) ? v : 0.f;
-          }
-    }
+      for (int q = 1; q < AG_SW; ++q) {
+        m0 = fminf(m0, mmred[q][0]);
+        m1 = fmaxf(m1, mmred[q][1]);
+      }
+      if (part == 0 && tid == 64 * AG_CW) {
+        a.mm[bh * 2 + 0] = m0;
+        a.mm[bh * 2 + 1] = m1;
+      }
+      if (m1 > m0) {
+        mn = m0;
+        scale = 1.0f / (m1 - m0 + 1e-8f);
+      }  // else constant A: left as is
+    };
     const size_t pbase = static_cast<size_t>(bh) * a.Mp * a.Mp;
-    const int Mp = static_cast<int>(a.Mp);
-    if (a.affinity) {
-      // fp32 diagnostic [M][M] (runs of four j of one row i)
+    const uint32_t Mp2 = static_cast<uint32_t>(a.Mp) * 2;  // bytes per plane row
+    uint16_t* const sx = reinterpret_cast<uint16_t*>(lds + 2 * AG_PANEL);
+    uint16_t* const st = reinterpret_cast<uint16_t*>(lds + 3 * AG_PANEL);
+    // Pass 0 fills X = xhi and XT = xthi; the unfused forms add pass 1:
+    // xlo (fp16) or xlo and xtlo (bf16).
+    const int npass = a.fused ? 1 : 2;
+    auto xplane = [&](int p) { return p == 0 ? a.xhi : a.xlo; };
+    auto tplane = [&](int p) { return p == 0 ? a.xthi : (a.f16_planes ? nullptr : a.xtlo); };
+
+    // Store waves: copy the staged tiles of pass p of tile t to the planes.
+    auto flush = [&](int t, int p) {
+      const int ts = tid - 64 * AG_CW;  // 0 .. 255
+      const int rl0 = ts >> 4, c = ts & 15;
+      const int64_t j0 = (tj0 + t) * AGT;
+      const uint32_t voff = static_cast<uint32_t>(rl0) * Mp2 + 16u * c;
+      const brsrc_t xr = make_rsrc(xplane(p) + pbase + i0 * a.Mp + j0, AGT * Mp2);
 #pragma unroll
-      for (int y = 0; y < NY; ++y) {
-        if (li0 + 32 * y >= mi) continue;
-        float* ar = a.affinity + (static_cast<size_t>(bh) * a.M + i0 + li0 + 32 * y) * a.M + j0;
-#pragma unroll
-        for (int x = 0; x < 2; ++x)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int jl = lj0 + 32 * x + 8 * (e >> 2) + (e & 3);
-            if (jl < mj) ar[jl] = acc[x][y][e];
-          }
+      for (int n = 0; n < AGT / 16; ++n) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(sx + (rl0 + 16 * n) * AGT + ((c ^ (rl0 & 15)) << 3));
+        __builtin_amdgcn_raw_buffer_store_b128(v, xr, voff, static_cast<uint32_t>(16 * n) * Mp2, 0);
       }
-    }
-    if (a.rspart) {
-      // Row sums over the wave's 64 columns j (one AT column block).
-      const int64_t jb = (j0 + jr0) / AT;
+      uint16_t* const tp = tplane(p);
+      if (tp) {
+        const brsrc_t tr = make_rsrc(tp + pbase + j0 * a.Mp + i0, AGT * Mp2);
 #pragma unroll
-      for (int y = 0; y < NY; ++y) {
-        float sum = 0.f;
-#pragma unroll
-        for (int x = 0; x < 2; ++x)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) sum += acc[x][y][e];
-        sum += shfl_xor_f32(sum, 32);
-        if (h == 0) a.rspart[(static_cast<size_t>(bh) * a.nta + jb) * a.Mp + i0 + li0 + 32 * y] = sum;
-      }
-    }
-    // One pass fills one plane of each orientation (either may be absent)
-    // and stores both; tiles lie inside the padded planes (Mp is a multiple
-    // of 128), so every store is in range.
-    uint16_t* tx = reinterpret_cast<uint16_t*>(lds);
-    uint16_t* tt = reinterpret_cast<uint16_t*>(lds + AG_PANEL);
-    const bool diag_tile = i0 == j0;
-    auto emit_pass = [&](uint16_t* xplane, auto xval, uint16_t* tplane, auto tval) {
-      __syncthreads();  // the panels' (or the last pass's) readers are done
-#pragma unroll
-      for (int x = 0; x < 2; ++x)
-#pragma unroll
-        for (int y = 0; y < NY; ++y) {
-          const int il = li0 + 32 * y;
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int jl = lj0 + 32 * x + 8 * g;  // a multiple of 4
-            if (xplane) {
-              const uint32_t w0 = static_cast<uint32_t>(xval(acc[x][y][4 * g])) |
-                                  (static_cast<uint32_t>(xval(acc[x][y][4 * g + 1])) << 16);
-              const uint32_t w1 = static_cast<uint32_t>(xval(acc[x][y][4 * g + 2])) |
-                                  (static_cast<uint32_t>(xval(acc[x][y][4 * g + 3])) << 16);
-              *reinterpret_cast<u32x2*>(tx + il * AGT + ((((jl >> 3) ^ (il & 15)) << 3) | (jl & 4))) =
-                  u32x2{w0, w1};
-            }
-            if (tplane) {
-#pragma unroll
-              for (int r = 0; r < 4; ++r) tt[(jl + r) * AGT + il] = tval(acc[x][y][4 * g + r], il, jl + r);
-            }
-          }
+        for (int n = 0; n < AGT / 16; ++n) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(st + (rl0 + 16 * n) * AGT + 8 * c);
+          __builtin_amdgcn_raw_buffer_store_b128(v, tr, voff, static_cast<uint32_t>(16 * n) * Mp2, 0);
         }
-      __syncthreads();
-      uint16_t* xo = xplane + pbase + static_cast<size_t>(i0) * a.Mp + j0;
-      uint16_t* to = tplane + pbase + static_cast<size_t>(j0) * a.Mp + i0;
-#pragma unroll
-      for (int n = 0; n < AGT * AGT / 8 / NT; ++n) {
-        const int t = tid + NT * n;
-        const int rl = t >> 4, c = t & 15;
-        if (xplane)
-          *reinterpret_cast<u32x4*>(xo + rl * Mp + 8 * c) =
-              *reinterpret_cast<const u32x4*>(tx + rl * AGT + ((c ^ (rl & 15)) << 3));
-        if (tplane)
-          *reinterpret_cast<u32x4*>(to + rl * Mp + 8 * c) = *reinterpret_cast<const u32x4*>(tt + rl * AGT + 8 * c);
+      }
+      if (a.rspart && p == npass - 1) {
+        // Row sums over the 64 columns j of each half of the tile.
+        const int q = ts >> 7, il = ts & 127;
+        a.rspart[(static_cast<size_t>(bh) * a.nta + j0 / AT + q) * a.Mp + i0 + il] = red[q * AGT + il];
       }
     };
-    uint16_t* const none = nullptr;  // an absent plane
+
+    // Compute waves: write pass p of the normalised tile t into the LDS tiles.
     auto f16v = [](float v) { return f32_to_f16(v); };
     auto f16lo = [](float v) { return f32_to_f16(v - f16_to_f32(f32_to_f16(v))); };
     auto bf16v = [](float v) { return f32_to_bf16(v); };
     auto bf16lo = [](float v) { return f32_to_bf16(v - bf16_to_f32(f32_to_bf16(v))); };
-    if (a.fused) {
-      // X = f16(Ahat); XT[j][i] = delta_ij - lambda Ahat[i][j] (delta only inside M)
-      const float lam = a.lambda;
-      if (diag_tile)
-        emit_pass(a.xhi, f16v, a.xthi, [&](float v, int il, int jl) {
-          return f32_to_f16((il == jl && il < mi ? 1.f : 0.f) - lam * v);
-        });
-      else
-        emit_pass(a.xhi, f16v, a.xthi, [&](float v, int, int) { return f32_to_f16(-lam * v); });
-    } else if (a.f16_planes) {
-      emit_pass(a.xhi, f16v, a.xthi, [&](float v, int, int) { return f32_to_f16(v); });
-      emit_pass(a.xlo, f16lo, none, [&](float, int, int) { return uint16_t(0); });
-    } else {
-      emit_pass(a.xhi, bf16v, a.xthi, [&](float v, int, int) { return f32_to_bf16(v); });
-      emit_pass(a.xlo, bf16lo, a.xtlo, [&](float v, int, int) { return bf16lo(v); });
+    // tval(v, k) gives the XT entry of element k = 16 x + e of the lane.
+    auto stage_pass = [&](auto xval, bool with_t, auto tval) {
+      const int il = li0;
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int jl = lj0 + 32 * x + 8 * g;  // a multiple of 4
+          const uint32_t w0 = static_cast<uint32_t>(xval(acc[x][4 * g])) |
+                              (static_cast<uint32_t>(xval(acc[x][4 * g + 1])) << 16);
+          const uint32_t w1 = static_cast<uint32_t>(xval(acc[x][4 * g + 2])) |
+                              (static_cast<uint32_t>(xval(acc[x][4 * g + 3])) << 16);
+          *reinterpret_cast<u32x2*>(sx + il * AGT + ((((jl >> 3) ^ (il & 15)) << 3) | (jl & 4))) =
+              u32x2{w0, w1};
+          if (with_t) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) st[(jl + r) * AGT + il] = tval(acc[x][4 * g + r], 16 * x + 4 * g + r);
+          }
+        }
+      }
+    };
+    // Element of the lane on the diagonal of a diagonal tile (j = i < M), or
+    // -1: il - lj0 = 32 x + 8 g + r with r < 4.
+    const int dd = li0 - lj0;
+    const int ediag = li0 < mi && dd >= 0 && dd < 64 && (dd & 4) == 0
+                          ? 16 * (dd >> 5) + 4 * ((dd >> 3) & 3) + (dd & 3)
+                          : -1;
+    auto stage = [&](int t, int p) {
+      const int64_t j0 = (tj0 + t) * AGT;
+      if (a.fused) {
+        // X = f16(Ahat); XT[j][i] = delta_ij - lambda Ahat[i][j] (delta only inside M)
+        const float lam = a.lambda;
+        if (i0 == j0) {
+          int ed = ediag;
+          asm volatile("" : "+v"(ed));  // compared per tile, not held as 32 masks
+          stage_pass(f16v, true, [&](float v, int k) {
+            return f32_to_f16((k == ed ? 1.f : 0.f) - lam * v);
+          });
+        } else {
+          stage_pass(f16v, true, [&](float v, int) { return f32_to_f16(-lam * v); });
+        }
+      } else if (a.f16_planes) {
+        if (p == 0) stage_pass(f16v, true, [&](float v, int) { return f32_to_f16(v); });
+        else stage_pass(f16lo, false, [&](float, int) { return uint16_t(0); });
+      } else {
+        if (p == 0) stage_pass(bf16v, true, [&](float v, int) { return f32_to_bf16(v); });
+        else stage_pass(bf16lo, true, [&](float v, int) { return bf16lo(v); });
+      }
+    };
+
+    if (minmax) {
+      lds_barrier();  // the store waves' partial extremes are in (the panels still load)
+      take_minmax();
     }
+    for (int t = 0; t < cnt; ++t) {
+      if (compute) __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's panel loads
+      lds_barrier();  // tile t's panel is in; the tiles of t - 1 are staged
+      if (compute) {
+        if (t == 0) load_q();
+        else if (t + 1 < cnt) stage_k(t + 1);  // into the buffer tile t - 1 used
+        product(t);
+      } else if (t > 0) {
+        flush(t - 1, npass - 1);
+      }
+      lds_barrier();  // the panel buffer and the LDS tiles are free
+      if (compute) {
+        if (t == 0 && cnt > 1) stage_k(1);  // buffer 0: the Qc operands are in registers
+        const int64_t j0 = (tj0 + t) * AGT;
+        const int mj = extent(a.M - j0);
+        // rows lj0 + o of the lane inside M: o < jlim (all of them inside the interior)
+        const int jlim = li0 < mi ? mj - lj0 : 0;
+        {
+          // alpha A rounded on its own, as in the STATS pass (no fused
+          // multiply-add with the subtraction): the minimum maps to exactly 0.
+#pragma clang fp contract(off)
+#pragma unroll
+          for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const float v = (acc[x][e] * a.alpha - mn) * scale;
+              acc[x][e] = 32 * x + 8 * (e >> 2) + (e & 3) < jlim ? v : 0.f;
+            }
+        }
+        if (a.affinity && li0 < mi) {
+          // fp32 diagnostic [M][M] (runs of four j of one row i)
+          float* ar = a.affinity + (static_cast<size_t>(bh) * a.M + i0 + li0) * a.M + j0;
+#pragma unroll
+          for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int jl = lj0 + 32 * x + 8 * (e >> 2) + (e & 3);
+              if (jl < mj) ar[jl] = acc[x][e];
+            }
+        }
+        if (a.rspart) {
+          // Row sums over the wave's 64 rows j (one AT column block), per column i.
+          float sum = 0.f;
+#pragma unroll
+          for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) sum += acc[x][e];
+          sum += shfl_xor_f32(sum, 32);
+          if (h == 0) red[(jr0 / 64) * AGT + li0] = sum;
+        }
+        stage(t, 0);
+      }
+      for (int p = 1; p < npass; ++p) {
+        lds_barrier();  // pass p - 1 is staged
+        if (!compute) flush(t, p - 1);
+        lds_barrier();  // ... and copied out
+        if (compute) stage(t, p);
+      }
+    }
+    lds_barrier();
+    if (!compute) flush(cnt - 1, npass - 1);
   }
 }
 
@@ -1048,19 +1157,47 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
     epilogue(std::integral_constant<int, CAB_FRC_AUGMENTED>{});
 }
 
+// Compute units of the current device (queried once per device).
+int device_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 // Launches the STATS (emit = false) or EMIT pass; returns the number of
 // min / max partials per (b, h) the STATS pass writes.
+// Inputs the strip kernel takes (the others use the direct-load kernels).
+bool strip_path(int dtype, int64_t D) { return dtype != CAB_F32 && D <= AG_DMAX; }
+
 template <typename T>
 int64_t launch_affinity(const AffArgs& a, int64_t BH, bool emit, hipStream_t s) {
   if constexpr (sizeof(T) == 2) {  // bf16_t, f16_t
-    if (a.D <= AG_DMAX) {
+    if (a.D <= AG_DMAX) {  // strip_path()
+      // Strips as long as keeps every CU busy: two STATS or one EMIT workgroup
+      // per CU (their LDS footprints), each walking `strip` tiles.
       const int64_t ns = a.Mp / AGT;  // Mp is a multiple of 128
-      const unsigned grid = static_cast<unsigned>(BH * ns * ns);
-      if (emit)
-        aff_tile_kernel<T, true, AG_WAVES><<<grid, 64 * AG_WAVES, 0, s>>>(a);
-      else
-        aff_tile_kernel<T, false, AG_WAVES><<<grid, 64 * AG_WAVES, 0, s>>>(a);
-      return ns * ns;
+      const int64_t slots = (emit ? 1 : 2) * static_cast<int64_t>(device_cus());
+      int64_t strip = ceil_div(BH * ns * ns, slots);
+      strip = strip < 1 ? 1 : (strip > ns ? ns : strip);
+      const int64_t nstrip = ceil_div(ns, strip);
+      AffArgs b = a;
+      b.strip = strip;
+      const unsigned grid = static_cast<unsigned>(BH * ns * nstrip);
+      const unsigned threads = 64 * (emit ? AG_CW + AG_SW : AG_CW);
+      if (a.D <= 64) {
+        if (emit) aff_strip_kernel<T, true, 4><<<grid, threads, 0, s>>>(b);
+        else aff_strip_kernel<T, false, 4><<<grid, threads, 0, s>>>(b);
+      } else {
+        if (emit) aff_strip_kernel<T, true, 8><<<grid, threads, 0, s>>>(b);
+        else aff_strip_kernel<T, false, 8><<<grid, threads, 0, s>>>(b);
+      }
+      return ns * nstrip;
     }
   }
   const int64_t ns = ceil_div(a.Mp, AS);
@@ -1133,7 +1270,7 @@ extern "C" cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_
   a.alpha = static_cast<float>(static_cast<double>(scale) / static_cast<double>(temperature));
   a.normalization = normalization;
   a.mmpart = reinterpret_cast<float*>(ws + L.off_mmpart);
-  a.mm = reinterpret_cast<const float*>(ws + L.off_mm);
+  a.mm = reinterpret_cast<float*>(ws + L.off_mm);
   a.xhi = reinterpret_cast<uint16_t*>(ws + L.off_xhi);
   a.xlo = reinterpret_cast<uint16_t*>(ws + L.off_xlo);
   a.xthi = reinterpret_cast<uint16_t*>(ws + L.off_xthi);
@@ -1150,20 +1287,23 @@ extern "C" cab_status_t cab_block_frc(const void* qc, const void* kc, cab_dtype_
                      std::fabs(lambda_redundancy) <= 1024.f;
   a.fused = fused ? 1 : 0;
   a.lambda = lambda_redundancy;
+  a.strip = 1;
 
+  a.nparts = 0;
   if (normalization == CAB_NORM_MINMAX) {
-    int64_t nparts = 0;
     switch (dtype) {
-      case CAB_BF16: nparts = launch_affinity<bf16_t>(a, BH, false, s); break;
-      case CAB_F16: nparts = launch_affinity<f16_t>(a, BH, false, s); break;
-      default: nparts = launch_affinity<float>(a, BH, false, s); break;
+      case CAB_BF16: a.nparts = launch_affinity<bf16_t>(a, BH, false, s); break;
+      case CAB_F16: a.nparts = launch_affinity<f16_t>(a, BH, false, s); break;
+      default: a.nparts = launch_affinity<float>(a, BH, false, s); break;
     }
     cab_status_t st = launch_status("cab_block_frc/affinity_stats");
     if (st != CAB_OK) return st;
-    minmax_finalize_kernel<<<static_cast<unsigned>(BH), 256, 0, s>>>(
-        a.mmpart, nparts, reinterpret_cast<float*>(ws + L.off_mm));
-    st = launch_status("cab_block_frc/minmax_finalize");
-    if (st != CAB_OK) return st;
+    // aff_strip_kernel's EMIT pass reduces the partials itself.
+    if (!strip_path(dtype, D)) {
+      minmax_finalize_kernel<<<static_cast<unsigned>(BH), 256, 0, s>>>(a.mmpart, a.nparts, a.mm);
+      st = launch_status("cab_block_frc/minmax_finalize");
+      if (st != CAB_OK) return st;
+    }
   }
   switch (dtype) {
     case CAB_BF16: launch_affinity<bf16_t>(a, BH, true, s); break;

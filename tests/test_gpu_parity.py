@@ -265,14 +265,18 @@ def test_frc_plane_layouts_and_head_dims(cuda, dt, D, mode):
     """Every plane layout the affinity pass writes for 16-bit inputs (fp16
     Ahat with and without I - lambda Ahat, bf16 hi/lo pairs, row-sum partials
     of the augmented formula), at head dims 64, 72 (a half 16-dim step), 128
-    (the LDS-staged 256 x 256 tile kernel) and 256 (the direct-load kernels);
-    M = 300, so the 256-row tiles overhang the 384-row padding."""
+    (the LDS-staged 128 x 128 tile strips) and 256 (the direct-load kernels);
+    M = 300, so the last 128-row tiles overhang M."""
+    _plane_case(cuda, dt, D, mode, 1, 2, 300)
+
+
+def _plane_case(cuda, dt, D, mode, B, H, M):
     from cab_attention.kernels import compute_block_frc
     formula, normalization, diag = {
         "diag": ("additive", "minmax", True), "fused": ("additive", "minmax", False),
         "mult": ("multiplicative", "minmax", True), "none": ("additive", "none", True),
         "aug": ("augmented", "none", True), "aug_minmax": ("augmented", "minmax", True)}[mode]
-    B, H, M, lam = 1, 2, 300, 0.5
+    lam = 0.5
     scale = 3.0 if normalization == "minmax" else 1.0
     qc = seeded((B, H, M, D), 41 + D, DTYPES[dt], scale=scale)
     kc = seeded((B, H, M, D), 42 + D, DTYPES[dt], scale=scale)
@@ -293,6 +297,17 @@ def test_frc_plane_layouts_and_head_dims(cuda, dt, D, mode):
         np.testing.assert_allclose(np32(f), of, rtol=1e-4, atol=1e-4 * np.abs(of).max())
     else:
         assert_frc_close(f, of, oa, ot, lam)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("mode", ["diag", "fused", "mult", "none", "aug_minmax"])
+def test_frc_tile_strips(cuda, D, mode):
+    """Workgroups that walk strips of several 128 x 128 affinity tiles, with a
+    short last strip: M = 2900 (Mp = 2944, 23 tiles per dim, 529 tiles) on a
+    256-CU device gives EMIT strips of 3 tiles (the last of 2) and STATS
+    strips of 2 (the last of 1); the last tile row and column overhang M.
+    Every plane layout, at both operand depths (D <= 64 and D <= 128)."""
+    _plane_case(cuda, "bf16", D, mode, 1, 1, 2900)
 
 
 def test_bridge_known_answer_on_gpu(cuda):
