@@ -1,7 +1,7 @@
 // Coarse Forman-Ricci curvature (cab_block_frc).
 //
 // Pipeline per (b, h), Mp = M rounded up to 128:
-//  1. STATS: A = qc kc^T * alpha on MFMA, per-tile min/max partials
+//  1. STATS: A = qc kc^T * alpha on MFMA, min/max partials per tile or strip
 //     (aff_strip_kernel for 16-bit inputs with D <= 128: strips of LDS-staged
 //     128 x 128 tiles; affinity_stats_kernel otherwise: operands straight
 //     from memory).
@@ -378,10 +378,11 @@ __global__ __launch_bounds__(256) void affinity_kernel(AffArgs a) {
 //  - the Kc panel of every tile is staged in turn, double-buffered (the Qc
 //    panel's space is the second buffer once its operands are in registers),
 //    so that the next tile's panel is in flight while a tile is computed;
-//  - eight compute waves split a tile 2 (64 rows j) x 4 (32 columns i) and
-//    compute C = Kc Qc^T (C[j][i] = A[i][j] / alpha) with 32x32x16 MFMAs;
-//    lane l then holds column i = l % 32 of each of its two 32 x 32 tiles and
-//    rows j = 8 (e / 4) + 4 (l / 32) + e % 4 of element e: runs of four
+//  - eight compute waves split a tile into blocks of 64 rows j x 32 columns
+//    i (EMIT) or 32 x 64 (STATS) and compute C = Kc Qc^T (C[j][i] =
+//    A[i][j] / alpha) with 32x32x16 MFMAs; lane l then holds column
+//    i = l % 32 of each of its two 32 x 32 tiles and rows
+//    j = 8 (e / 4) + 4 (l / 32) + e % 4 of element e: runs of four
 //    consecutive j of one row i of A.
 // STATS (8 waves, two workgroups per CU): min / max of A over i, j < M per
 // strip.
@@ -454,38 +455,49 @@ __global__ __launch_bounds__(EMIT ? 64 * (AG_CW + AG_SW) : 64 * AG_CW, EMIT ? 3 
   }
 
   const int h = lane >> 5;
-  const int jr0 = 64 * ((w >> 2) & 1), ic0 = 32 * (w & 3);
-  // Tile-local coordinates: column i = li0, rows j = lj0 + 32 x + 8 g + r of
-  // run g (elements 4 g + r) of tile x.
+  // A wave's block is XW 32-row tiles (j) by YW 32-column tiles (i):
+  // 64 x 32 for EMIT, whose staging code needs the registers, and 32 x 64
+  // for STATS, which reads each Kc operand once for two MFMAs (half the LDS
+  // reads of 64 x 32).
+  constexpr int XW = EMIT ? 2 : 1, YW = EMIT ? 1 : 2, NI = 4 / YW;
+  const int jr0 = 32 * XW * ((w / NI) & (4 / XW - 1)), ic0 = 32 * YW * (w % NI);
+  // Tile-local coordinates: column i = li0 + 32 y of tile (x, y), rows
+  // j = lj0 + 32 x + 8 g + r of run g (elements 4 g + r).
   const int li0 = ic0 + (lane & 31), lj0 = jr0 + 4 * h;
   auto extent = [](int64_t n) { return static_cast<int>(n < 0 ? 0 : (n < AGT ? n : AGT)); };
   const int mi = extent(a.M - i0);
-  u32x4 qf[KS];  // the wave's Qc operands: rows i of its column tile
+  u32x4 qf[YW][KS];  // the wave's Qc operands: rows i of its column tiles
   auto load_q = [&]() {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int R = li0, c = 2 * ks + h;
-      qf[ks] = *reinterpret_cast<const u32x4*>(lds + R * 256 + ((c ^ (R & 15)) << 4));
-    }
+    for (int y = 0; y < YW; ++y)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int R = li0 + 32 * y, c = 2 * ks + h;
+        qf[y][ks] = *reinterpret_cast<const u32x4*>(lds + R * 256 + ((c ^ (R & 15)) << 4));
+      }
   };
-  f32x16 acc[2];
+  f32x16 acc[XW * YW];  // tile (x, y) at x * YW + y
   auto product = [&](int t) {
     const char* kb = kbuf(t);
-    acc[0] = f32x16{};
-    acc[1] = f32x16{};
+#pragma unroll
+    for (int q = 0; q < XW * YW; ++q) acc[q] = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int c = 2 * ks + h;
 #pragma unroll
-      for (int x = 0; x < 2; ++x) {
+      for (int x = 0; x < XW; ++x) {
         const int R = jr0 + 32 * x + (lane & 31);
         const u32x4 av = *reinterpret_cast<const u32x4*>(kb + R * 256 + ((c ^ (R & 15)) << 4));
-        if constexpr (BF)
-          acc[x] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, qf[ks]), acc[x], 0, 0, 0);
-        else
-          acc[x] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-              __builtin_bit_cast(f16x8, av), __builtin_bit_cast(f16x8, qf[ks]), acc[x], 0, 0, 0);
+#pragma unroll
+        for (int y = 0; y < YW; ++y) {
+          f32x16& d = acc[x * YW + y];
+          if constexpr (BF)
+            d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av),
+                                                        __builtin_bit_cast(bf16x8, qf[y][ks]), d, 0, 0, 0);
+          else
+            d = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, av),
+                                                       __builtin_bit_cast(f16x8, qf[y][ks]), d, 0, 0, 0);
+        }
       }
     }
   };
@@ -507,23 +519,27 @@ __global__ __launch_bounds__(EMIT ? 64 * (AG_CW + AG_SW) : 64 * AG_CW, EMIT ? 3 
       const int mj = extent(a.M - (tj0 + t) * AGT);
       if (mi == AGT && mj == AGT) {
 #pragma unroll
-        for (int x = 0; x < 2; ++x)
+        for (int q = 0; q < XW * YW; ++q)
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
-            lo = fminf(lo, acc[x][e]);
-            hi = fmaxf(hi, acc[x][e]);
+            lo = fminf(lo, acc[q][e]);
+            hi = fmaxf(hi, acc[q][e]);
           }
       } else {
         // Entries outside M enter as the identities: selects, not branches.
-        const int jlim = li0 < mi ? mj - lj0 : 0;  // rows lj0 + o of the lane inside M: o < jlim
 #pragma unroll
-        for (int x = 0; x < 2; ++x)
+        for (int y = 0; y < YW; ++y) {
+          // rows lj0 + o of column li0 + 32 y inside M: o < jlim
+          const int jlim = li0 + 32 * y < mi ? mj - lj0 : 0;
 #pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const bool in = 32 * x + 8 * (e >> 2) + (e & 3) < jlim;
-            lo = fminf(lo, in ? acc[x][e] : INFINITY);
-            hi = fmaxf(hi, in ? acc[x][e] : -INFINITY);
-          }
+          for (int x = 0; x < XW; ++x)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const bool in = 32 * x + 8 * (e >> 2) + (e & 3) < jlim;
+              lo = fminf(lo, in ? acc[x * YW + y][e] : INFINITY);
+              hi = fmaxf(hi, in ? acc[x * YW + y][e] : -INFINITY);
+            }
+        }
       }
     }
 #pragma unroll
