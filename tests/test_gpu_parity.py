@@ -299,15 +299,21 @@ def _plane_case(cuda, dt, D, mode, B, H, M):
         assert_frc_close(f, of, oa, ot, lam)
 
 
-@pytest.mark.parametrize("D", [64, 128])
-@pytest.mark.parametrize("mode", ["diag", "fused", "mult", "none", "aug_minmax"])
-def test_frc_tile_strips(cuda, D, mode):
+@pytest.mark.parametrize("dt,D,mode,H", [
+    ("bf16", 128, "fused", 1), ("bf16", 128, "diag", 1), ("bf16", 64, "mult", 1),
+    ("bf16", 128, "none", 1), ("bf16", 64, "aug_minmax", 1), ("bf16", 128, "fused", 2),
+    ("fp16", 64, "diag", 2), ("fp16", 128, "aug", 1), ("fp16", 128, "mult", 1),
+    ("fp16", 64, "fused", 1),
+])
+def test_frc_tile_strips(cuda, dt, D, mode, H):
     """Workgroups that walk strips of several 128 x 128 affinity tiles, with a
-    short last strip: M = 2900 (Mp = 2944, 23 tiles per dim, 529 tiles) on a
-    256-CU device gives EMIT strips of 3 tiles (the last of 2) and STATS
-    strips of 2 (the last of 1); the last tile row and column overhang M.
-    Every plane layout, at both operand depths (D <= 64 and D <= 128)."""
-    _plane_case(cuda, "bf16", D, mode, 1, 1, 2900)
+    short last strip: M = 2900 (Mp = 2944, 23 tiles per dim, 529 tiles per
+    head) on a 256-CU device gives, for one head, EMIT strips of 3 tiles (the
+    last of 2) and STATS strips of 2 (the last of 1), and for two heads EMIT
+    strips of 5 (the last of 3) and STATS strips of 3 (the last of 2); the
+    last tile row and column overhang M. Every plane layout, both 16-bit
+    types and both operand depths (D <= 64 and D <= 128)."""
+    _plane_case(cuda, dt, D, mode, 1, H, 2900)
 
 
 def test_bridge_known_answer_on_gpu(cuda):
