@@ -392,12 +392,13 @@ def test_topk_narrow_and_straddling_windows(cuda, M, flags):
     """The digit windows start at the highest bit where two candidates
     differ: rows whose keys differ only in the lowest 2, 3 or 7 bits (one
     window narrower than 8 bits), in bits 7 .. 14 (a window straddling a byte
-    boundary, then a 7-bit one), in the sign alone (+x / -x), and rows whose
-    first window holds real keys in the top bin beside the non-candidates."""
+    boundary, then a 7-bit one), in the sign alone (+x / -x), rows whose
+    first window holds real keys in the top bin beside the non-candidates,
+    and rows of fp32 denormals of both signs beside +0 and -0 (equal)."""
     from cab_attention.kernels import generate_block_index
     select_high, keep_diag, causal = flags
     g = torch.Generator().manual_seed(300 + M)
-    f = torch.empty(1, 6, M, M)
+    f = torch.empty(1, 7, M, M)
     f[0, 0] = 1.0 + torch.randint(0, 4, (M, M), generator=g).float() * 2.0 ** -23    # bits 0 .. 1
     f[0, 1] = 1.0 + torch.randint(0, 8, (M, M), generator=g).float() * 2.0 ** -23    # bits 0 .. 2
     f[0, 2] = 1.0 + torch.randint(0, 128, (M, M), generator=g).float() * 2.0 ** -23  # bits 0 .. 6
@@ -406,6 +407,10 @@ def test_topk_narrow_and_straddling_windows(cuda, M, flags):
     top = torch.full((M, M), -1.0)                                      # the top key (low scores kept)
     top[torch.rand(M, M, generator=g) < 0.5] = float("nan")             # or NaN, above +inf
     f[0, 5] = top
+    den = torch.randint(-20, 21, (M, M), generator=g).float() * 2.0 ** -149  # k * 2^-149
+    den[(den == 0) & (torch.rand(M, M, generator=g) < 0.5)] = -0.0
+    assert (den.view(torch.int32) & 0x7f800000 == 0).all() and (den.abs() > 0).any()
+    f[0, 6] = den
     for sp in (0.95, 0.5):
         idx, cnt, mask = generate_block_index(f.to(cuda), sp, select_high=select_high,
                                               keep_diagonal=keep_diag, causal=causal, dense=True)
