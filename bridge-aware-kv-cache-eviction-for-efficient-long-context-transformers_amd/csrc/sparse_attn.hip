@@ -297,6 +297,24 @@ __device__ __forceinline__ void colmax2(float& x0, float& x1) {
 // finite and exp2(s * c - max * c) of a masked score (-inf) is exactly 0.
 constexpr float M_EMPTY = -1.0e30f;
 
+// Softmax modes of one block step.
+//  SM_ONLINE: online softmax with the lazy rescale (the maximum may grow).
+//  SM_FIRST:  first block of a fixed-maximum walk: each query's maximum is
+//             set to its largest score in this block (the accumulators are
+//             still zero, so nothing is rescaled); queries with no finite
+//             score keep M_EMPTY.
+//  SM_FIXED:  later blocks of that walk: p = exp2(s c - m c) with the
+//             maximum of the first block, no maxima, no rescale. A score
+//             far above that maximum makes p (and the row sum) large or
+//             infinite; the walk's end check (row_sums_ok) then sends the
+//             row through an SM_ONLINE walk instead.
+constexpr int SM_ONLINE = 0, SM_FIRST = 1, SM_FIXED = 2;
+// Largest row sum a fixed-maximum walk may end with (2^64): every p is then
+// at most 2^64, far inside fp32 and bf16 range, and the first block's
+// maximum gives each query with a finite score a p of exactly 1, so no p
+// that matters underflows.
+constexpr uint32_t FIXED_SUM_MAX_BITS = 0x5f800000u;
+
 // Online-softmax state of one wave: 32 queries (two tiles of 16, query on
 // the lane axis) against one key half of every kept block.
 template <int HD>
@@ -366,6 +384,38 @@ __device__ __forceinline__ void acc_init(WaveAcc<HD>& s, const WaveGeo<HD>& ge, 
   }
 }
 
+// Clears the accumulators and maxima (the queries stay loaded).
+template <int HD>
+__device__ __forceinline__ void acc_reset(WaveAcc<HD>& s, float c) {
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    s.lacc[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dt = 0; dt < Dims<HD>::NDT; ++dt) s.oacc[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    s.m_run[qt] = M_EMPTY;
+    s.nmc[qt] = -M_EMPTY * c;
+  }
+}
+
+// Whether a fixed-maximum walk left this lane's state usable: both row sums
+// finite and at most 2^64, and the accumulators finite (their sum is; an
+// overflow of the sum alone only costs a needless online walk). Tested on
+// the bits: the file's device code is compiled without NaN semantics.
+template <int HD>
+__device__ __forceinline__ bool row_sums_ok(const WaveAcc<HD>& s) {
+  float t = 0.f;
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int dt = 0; dt < Dims<HD>::NDT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) t += s.oacc[dt][qt][r];
+  const uint32_t l0 = __builtin_bit_cast(uint32_t, s.lacc[0][0]) & 0x7fffffffu;
+  const uint32_t l1 = __builtin_bit_cast(uint32_t, s.lacc[1][0]) & 0x7fffffffu;
+  const uint32_t te = __builtin_bit_cast(uint32_t, t) & 0x7f800000u;
+  return l0 <= FIXED_SUM_MAX_BITS && l1 <= FIXED_SUM_MAX_BITS && te != 0x7f800000u;
+}
+
 // Marks the queries as loaded: later waits in the block loop then never
 // have to cover the Q loads.
 template <cab_dtype_t DT, int HD>
@@ -392,7 +442,7 @@ __device__ __forceinline__ bool block_needs_mask(int j, int i, bool valid, int N
 // fp32 (split operands, the lo halves 16 KB past the hi ones in LDS):
 // 48 + 48 + 4 MFMA. Keys at or past Nk and (causal) keys after t + qoff for
 // query t are dropped.
-template <cab_dtype_t DT, int HD, typename Stager>
+template <cab_dtype_t DT, int HD, int SM, typename Stager>
 __device__ __forceinline__ void acc_block(WaveAcc<HD>& s, const WaveGeo<HD>& ge, const char* ks,
                                           const u32x4* vts, int j, int i, bool valid, int Nk,
                                           bool causal, int qoff, float c, const Stager& stg) {
@@ -459,19 +509,30 @@ __device__ __forceinline__ void acc_block(WaveAcc<HD>& s, const WaveGeo<HD>& ge,
         }
   }
   float mx[2];
+  if constexpr (SM != SM_FIXED) {
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const float m0 = __builtin_fmaxf(__builtin_fmaxf(sc[0][qt][0], sc[0][qt][1]),
-                                     __builtin_fmaxf(sc[0][qt][2], sc[0][qt][3]));
-    const float m1 = __builtin_fmaxf(__builtin_fmaxf(sc[1][qt][0], sc[1][qt][1]),
-                                     __builtin_fmaxf(sc[1][qt][2], sc[1][qt][3]));
-    mx[qt] = __builtin_fmaxf(m0, m1);
+    for (int qt = 0; qt < 2; ++qt) {
+      const float m0 = __builtin_fmaxf(__builtin_fmaxf(sc[0][qt][0], sc[0][qt][1]),
+                                       __builtin_fmaxf(sc[0][qt][2], sc[0][qt][3]));
+      const float m1 = __builtin_fmaxf(__builtin_fmaxf(sc[1][qt][0], sc[1][qt][1]),
+                                       __builtin_fmaxf(sc[1][qt][2], sc[1][qt][3]));
+      mx[qt] = __builtin_fmaxf(m0, m1);
+    }
+  }
+  if constexpr (SM == SM_FIRST) {
+    colmax2(mx[0], mx[1]);
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      s.m_run[qt] = mx[qt] > M_EMPTY ? mx[qt] : M_EMPTY;
+      s.nmc[qt] = -s.m_run[qt] * c;
+    }
   }
   // Rescale only when a query's maximum grew by more than 2^RESCALE_LOG2
   // in exp2 units (always on its first non-empty block). A query's keys sit
   // in the four lane groups l16 + 16 g: the lane-local maxima tell whether
   // any query can have grown, and only then are the column maxima formed.
-  if (__builtin_amdgcn_ballot_w64(__builtin_fmaf(mx[0], c, s.nmc[0]) > RESCALE_LOG2 ||
+  if (SM == SM_ONLINE &&
+      __builtin_amdgcn_ballot_w64(__builtin_fmaf(mx[0], c, s.nmc[0]) > RESCALE_LOG2 ||
                                   __builtin_fmaf(mx[1], c, s.nmc[1]) > RESCALE_LOG2)) {
     colmax2(mx[0], mx[1]);
     const bool grow[2] = {__builtin_fmaf(mx[0], c, s.nmc[0]) > RESCALE_LOG2,
@@ -725,17 +786,23 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
 
   WaveAcc<HD> st;
   acc_init<DT, HD>(st, ge, qb, a.qs[2], i * BS + 32 * ge.qh, N, c);
+  __shared__ int wave_bad[4];
+  auto block_of = [&](int j) { return (j >= 0 && j < Mk) ? j : 0; };
 
-  if (cnt > 0) {
+  // One walk over the row's blocks. FAST: the first block sets each query's
+  // maximum and the rest use it unchanged (SM_FIRST, then SM_FIXED);
+  // otherwise the online softmax with the lazy rescale (SM_ONLINE).
+  auto walk = [&](auto fast_tag) {
+    constexpr bool FAST = decltype(fast_tag)::value;
     int jraw = entry(0);
-    auto block_of = [&](int j) { return (j >= 0 && j < Mk) ? j : 0; };
     stage(block_of(jraw), stage_k(0), stage_v(0));
     acc_q_ready<DT, HD>(st);
 
     // Block p lives in LDS stage PAR = p % 2 (compile time, so the compiler
     // sees the staging of block p + 1 into the other stage cannot alias).
-    auto step = [&](int p, auto par_tag) {
+    auto step = [&](int p, auto par_tag, auto sm_tag) {
       constexpr int PAR = decltype(par_tag)::value;
+      constexpr int SM = decltype(sm_tag)::value;
       const bool valid = jraw >= 0 && jraw < Mk;
       const int j = valid ? jraw : 0;
       __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's staging of block p landed
@@ -746,23 +813,48 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
           jnext = entry(p + 1);
           stage(block_of(jnext), stage_k(PAR ^ 1), stage_v(PAR ^ 1));
         }
-        acc_block<DT, HD>(st, ge, reinterpret_cast<const char*>(stage_k(PAR)), stage_v(PAR), j,
-                          i, valid, Nk, a.causal, a.qoff, c, [](int) {});
+        acc_block<DT, HD, SM>(st, ge, reinterpret_cast<const char*>(stage_k(PAR)), stage_v(PAR),
+                              j, i, valid, Nk, a.causal, a.qoff, c, [](int) {});
       } else {
         // unconditional (the last step re-stages a valid block into the free
         // stage; waited for after the loop) so that the loads sit between the MFMAs
         const int e = entry(p + 1 < cnt ? p + 1 : cnt - 1);
         jnext = p + 1 < cnt ? e : 0;
         const int js = block_of(jnext);
-        acc_block<DT, HD>(st, ge, reinterpret_cast<const char*>(stage_k(PAR)), stage_v(PAR), j,
-                          i, valid, Nk, a.causal, a.qoff, c,
-                          [&](int ds) { stage_part(js, stage_k(PAR ^ 1), stage_v(PAR ^ 1), ds); });
+        acc_block<DT, HD, SM>(st, ge, reinterpret_cast<const char*>(stage_k(PAR)), stage_v(PAR),
+                              j, i, valid, Nk, a.causal, a.qoff, c,
+                              [&](int ds) { stage_part(js, stage_k(PAR ^ 1), stage_v(PAR ^ 1), ds); });
       }
       jraw = jnext;
     };
-    for (int p = 0; p < cnt; p += 2) {
-      step(p, std::integral_constant<int, 0>{});
-      if (p + 1 < cnt) step(p + 1, std::integral_constant<int, 1>{});
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    if constexpr (FAST) {
+      step(0, P0{}, std::integral_constant<int, SM_FIRST>{});
+      for (int p = 1; p < cnt; p += 2) {
+        step(p, P1{}, std::integral_constant<int, SM_FIXED>{});
+        if (p + 1 < cnt) step(p + 1, P0{}, std::integral_constant<int, SM_FIXED>{});
+      }
+    } else {
+      for (int p = 0; p < cnt; p += 2) {
+        step(p, P0{}, std::integral_constant<int, SM_ONLINE>{});
+        if (p + 1 < cnt) step(p + 1, P1{}, std::integral_constant<int, SM_ONLINE>{});
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the last step's staging landed
+  };
+
+  if (cnt > 0) {
+    walk(std::true_type{});
+    // Every wave reports whether its fixed-maximum state is usable; if any
+    // is not, the whole row is walked again with the online softmax (the
+    // barrier also frees both stages for that walk's first loads).
+    const bool bad = __builtin_amdgcn_ballot_w64(!row_sums_ok<HD>(st)) != 0;
+    if (threadIdx.x % 64 == 0) wave_bad[w] = bad ? 1 : 0;
+    __syncthreads();
+    if ((wave_bad[0] | wave_bad[1] | wave_bad[2] | wave_bad[3]) != 0) {
+      acc_reset<HD>(st, c);
+      walk(std::false_type{});
     }
   }
 

@@ -378,6 +378,11 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   // j < ncand (c < climit) and it is not the forced diagonal; the rest get
   // KEY_NONE. The row is read through a buffer descriptor (columns past M
   // read as zero and are no candidates), all NCH loads in flight together.
+  // The whole byte offset 4 (64 c + lane) goes in the per-lane offset (the
+  // compiler folds 256 c into the instruction's immediate): the descriptor's
+  // range check covers the per-lane offset plus the immediate, while a
+  // scalar offset is not range-checked on gfx9, so chunks past M must not
+  // be addressed through it.
   const int climit = static_cast<int>((ncand - lane + 63) >> 6);
   // dcl: the chunk holding the forced diagonal on its lane, -1 on the other
   // lanes (one compare per chunk, no per-chunk masks kept across passes).
@@ -389,7 +394,7 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
     uint32_t u[NCH];
 #pragma unroll
     for (int c = 0; c < NCH; ++c)
-      u[c] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(frs, 4u * lane, 256u * c, 0));
+      u[c] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(frs, 4u * (64u * c + lane), 0u, 0));
 #pragma unroll
     for (int c = 0; c < NCH; ++c)  // branch-free: KEY_NONE is all ones
       key[c] = order_key_bits(u[c], flip) | (is_cand(c) ? 0u : KEY_NONE);
@@ -409,7 +414,7 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
       uint32_t u[NCH];
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
-        u[c] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(mrs, 4u * lane, 256u * c, 0));
+        u[c] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(mrs, 4u * (64u * c + lane), 0u, 0));
 #pragma unroll
       for (int c = 0; c < NCH; ++c) mkey[c] = is_cand(c) ? order_key_bits(u[c], 0xffffffffu) : KEY_NONE;
     }
