@@ -122,6 +122,12 @@ __device__ __forceinline__ uint64_t ballot64(bool p) {
   return __ballot(p);
 }
 
+// Number of set bits of the wave mask m below this lane (v_mbcnt).
+__device__ __forceinline__ uint32_t rank_below64(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+}
+
 __device__ __forceinline__ uint64_t lanemask_lt() {
   const int l = lane_id();
   return l == 0 ? 0ull : (~0ull >> (64 - l));
@@ -154,6 +160,34 @@ __device__ __forceinline__ brsrc_t make_rsrc(const void* base, uint32_t bytes) {
 }
 __device__ __forceinline__ void bdma16(brsrc_t r, uint32_t voff, uint32_t soff, char* l) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)l, 16, voff, soff, 0, 0);
+}
+
+// The same load issued as inline asm on a descriptor held in four scalar
+// registers (base, size; raw dword access). The compiler does not see this
+// load write LDS, so it adds no wait for it before later LDS reads: for a
+// builtin LDS load it makes every later LDS read wait for all outstanding
+// loads, whatever address they read. Callers wait (vmcnt(0)) and pass a
+// workgroup barrier before any wave reads the bytes such a load writes, and
+// never read a region while a load into it may be in flight.
+typedef uint32_t sgpr_rsrc_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ sgpr_rsrc_t make_sgpr_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  auto uni = [](uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x)));
+  };
+  return sgpr_rsrc_t{uni(static_cast<uint32_t>(p)), uni(static_cast<uint32_t>(p >> 32) & 0xffffu),
+                     uni(bytes), 0x00020000u};
+}
+__device__ __forceinline__ void bdma16_untracked(const sgpr_rsrc_t& r, uint32_t voff, uint32_t soff,
+                                                 const void* l) {
+  const uint32_t lds = static_cast<uint32_t>(
+      __builtin_amdgcn_readfirstlane(static_cast<int>(reinterpret_cast<uintptr_t>(l))));
+  // M0 (the LDS base of the load) is an input the compiler sets; the s_nop
+  // is the wait state an LDS load needs after an M0 write.
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(r), "s"(soff), "{m0}"(lds)
+               : "memory");
 }
 
 }  // namespace cab

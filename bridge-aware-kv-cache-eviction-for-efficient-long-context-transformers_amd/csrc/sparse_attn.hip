@@ -46,6 +46,8 @@
 //
 // Algorithmic work per kept tile: 4 * 64 * 64 * 128 flops (2 * 64 * 65 * 128
 // on a causal diagonal tile). Bound: MFMA.
+#include <cstdlib>
+
 #include "cab_internal.h"
 
 namespace cab {
@@ -873,6 +875,404 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
 }
 
 // ---------------------------------------------------------------------------
+// attn_pair_kernel: two adjacent query blocks (rows i = 2 p and 2 p + 1 of
+// the block mask) per workgroup of 4 waves, two workgroups per CU.
+//
+// Adjacent rows keep most of the same key blocks (about 62 % at config 4),
+// so the workgroup walks the union of the two rows' lists and stages each
+// block once for both rows: 0.62 staged blocks per kept tile there instead
+// of 1. Wave w owns queries 16 w .. 16 w + 15 of each row, so every wave has
+// the same work in every step (both rows' 16-query tiles for a block both
+// rows keep, one tile otherwise) and keeps its own queries' softmax state
+// for all 64 keys: no split of the key dimension and no merge at the end.
+// Per union entry and wave:
+//   S^T_r = K Q_r^T    (16 MFMA 16x16x32 per present row r; each K operand
+//                       read from LDS once and used for both rows)
+//   softmax of the row's 16 x 64 scores (fixed-maximum walk, as above)
+//   O^T_r += V^T P_r^T (16 MFMA per row; each V^T operand read once)
+//   row sums = 1 P_r^T (2 MFMA per row)
+// The union walk is built in the prologue from the rows' lists: entries
+// outside [0, Mk) are dropped, and two strictly ascending lists are merged
+// (each entry tagged with the rows that keep it); other lists (unsorted or
+// with repeats, whose blocks count once per occurrence) are walked one
+// after the other, untagged for the other row. 16-bit inputs, lists of at
+// most PAIR_KMAX entries.
+// ---------------------------------------------------------------------------
+constexpr int PAIR_KMAX = 512;
+constexpr uint32_t TAG_A = 1u << 30, TAG_B = 1u << 31, TAG_BLOCK = TAG_A - 1u;
+
+template <int HD>
+struct PairAcc {
+  static constexpr int NDS = Dims<HD>::NDS, NDT = Dims<HD>::NDT;
+  u32x4 qreg[2][NDS];  // row r: Q[q0_r + l % 16][32 ds + 8 g .. +8]
+  f32x4 oacc[2][NDT];  // row r: O^T[16 dt + 4 g + r'][q0_r + l % 16]
+  f32x4 lacc[2];       // row sums (all four entries equal)
+  float m_run[2];      // each lane's query maximum (raw scores)
+  float nmc[2];        // -m_run * c
+};
+
+template <int HD>
+__device__ __forceinline__ void pair_reset(PairAcc<HD>& s, float c) {
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    s.lacc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dt = 0; dt < Dims<HD>::NDT; ++dt) s.oacc[r][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    s.m_run[r] = M_EMPTY;
+    s.nmc[r] = -M_EMPTY * c;
+  }
+}
+
+// The fixed-maximum walk's end check for both rows of a lane (row_sums_ok).
+template <int HD>
+__device__ __forceinline__ bool pair_sums_ok(const PairAcc<HD>& s) {
+  float t = 0.f;
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int dt = 0; dt < Dims<HD>::NDT; ++dt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) t += s.oacc[r][dt][q];
+  const uint32_t l0 = __builtin_bit_cast(uint32_t, s.lacc[0][0]) & 0x7fffffffu;
+  const uint32_t l1 = __builtin_bit_cast(uint32_t, s.lacc[1][0]) & 0x7fffffffu;
+  const uint32_t te = __builtin_bit_cast(uint32_t, t) & 0x7f800000u;
+  return l0 <= FIXED_SUM_MAX_BITS && l1 <= FIXED_SUM_MAX_BITS && te != 0x7f800000u;
+}
+
+// Softmax of one row's 16 x 64 score tile held by a wave (lane: query
+// l % 16, keys 16 kt + 4 g + r') into its P^T operands. FAST: fixed maximum,
+// set from the first block the row meets (mset); otherwise the online
+// softmax with the lazy rescale.
+template <bool FAST, bool BF16, int HD>
+__device__ __forceinline__ void pair_softmax(PairAcc<HD>& s, int r, f32x4 (&sc)[4], float c,
+                                             bool& mset, u32x4 (&pb)[2]) {
+  constexpr int NDT = Dims<HD>::NDT;
+  if (!FAST || !mset) {
+    float mx = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(sc[0][0], sc[0][1]),
+                                               __builtin_fmaxf(sc[0][2], sc[0][3])),
+                               __builtin_fmaxf(__builtin_fmaxf(sc[1][0], sc[1][1]),
+                                               __builtin_fmaxf(sc[1][2], sc[1][3])));
+    mx = __builtin_fmaxf(mx, __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(sc[2][0], sc[2][1]),
+                                                             __builtin_fmaxf(sc[2][2], sc[2][3])),
+                                             __builtin_fmaxf(__builtin_fmaxf(sc[3][0], sc[3][1]),
+                                                             __builtin_fmaxf(sc[3][2], sc[3][3]))));
+    if constexpr (FAST) {
+      float m2 = mx;
+      colmax2(mx, m2);
+      s.m_run[r] = mx > M_EMPTY ? mx : M_EMPTY;
+      s.nmc[r] = -s.m_run[r] * c;
+      mset = true;
+    } else if (__builtin_amdgcn_ballot_w64(__builtin_fmaf(mx, c, s.nmc[r]) > RESCALE_LOG2)) {
+      float m2 = mx;
+      colmax2(mx, m2);
+      const bool grow = __builtin_fmaf(mx, c, s.nmc[r]) > RESCALE_LOG2;
+      const float m_new = grow ? mx : s.m_run[r];
+      const float alpha = __builtin_amdgcn_exp2f((s.m_run[r] - m_new) * c);
+      s.lacc[r] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) s.oacc[r][dt] *= alpha;
+      s.m_run[r] = m_new;
+      s.nmc[r] = -m_new * c;
+    }
+  }
+  float p[4][4];
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) p[kt][q] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][q], c, s.nmc[r]));
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    pb[ks][0] = pack2<BF16>(p[2 * ks][0], p[2 * ks][1]);
+    pb[ks][1] = pack2<BF16>(p[2 * ks][2], p[2 * ks][3]);
+    pb[ks][2] = pack2<BF16>(p[2 * ks + 1][0], p[2 * ks + 1][1]);
+    pb[ks][3] = pack2<BF16>(p[2 * ks + 1][2], p[2 * ks + 1][3]);
+  }
+}
+
+template <cab_dtype_t DT, int HD>
+__global__ __launch_bounds__(256, 2) void attn_pair_kernel(AttnArgs a) {
+  static_assert(DT != CAB_F32, "16-bit inputs only");
+  using G = Dims<HD>;
+  constexpr int NDS = G::NDS, NDT = G::NDT;
+  constexpr int TILE_SLOTS = G::TILE_SLOTS, TILE_BYTES = G::TILE_BYTES, NI = G::NI;
+  constexpr int STAGE_SLOTS = 2 * TILE_SLOTS;
+  constexpr int TT_BYTES = 16 * G::ROW_BYTES;  // 16 K rows
+  constexpr bool BF16 = DT == CAB_BF16;
+  __shared__ u32x4 smem[2 * STAGE_SLOTS];  // [stage 0: K, V^T][stage 1: K, V^T]
+  __shared__ int32_t lst[2][PAIR_KMAX];    // each row's valid entries, in list order
+  __shared__ uint32_t uni[2 * PAIR_KMAX];  // the walk: block | TAG_A | TAG_B
+  __shared__ int meta[8];                  // n_A, n_B, sorted_A, sorted_B, U, -, -, -
+  __shared__ int wave_bad[4];
+  auto stage_k = [&](int st) { return smem + st * STAGE_SLOTS; };
+  auto stage_v = [&](int st) { return smem + st * STAGE_SLOTS + TILE_SLOTS; };
+
+  const int M = a.M, N = a.N, Mk = a.Mk, Nk = a.Nk;
+  const int MP = (M + 1) / 2;
+  const int logical = static_cast<int>(xcd_remap(blockIdx.x, static_cast<int64_t>(a.BH) * MP));
+  const int bh = logical / MP;
+  const int pr = MP - 1 - (logical - bh * MP);  // longest causal pairs first
+  const int irow[2] = {2 * pr, 2 * pr + 1};     // irow[1] == M: no second row
+  const int b = bh / a.H, hh = bh - (bh / a.H) * a.H;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int lane = lane_id(), g = lane >> 4, l16 = lane & 15;
+  const float c = a.scale_log2;
+
+  const uint16_t* qb = static_cast<const uint16_t*>(a.q) + b * a.qs[0] + hh * a.qs[1];
+  const char* kbytes = reinterpret_cast<const char*>(a.k + b * a.ks[0] + hh * a.ks[1]);
+  const char* vtbytes = reinterpret_cast<const char*>(a.vt) + static_cast<int64_t>(bh) * Mk * TILE_BYTES;
+
+  // Queries (issued first; they land while the walk is built).
+  PairAcc<HD> st;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int qtok = 64 * irow[r] + 16 * w + l16;
+    const bool in = irow[r] < M && qtok < N;
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds)
+      st.qreg[r][ds] = in ? *reinterpret_cast<const u32x4*>(qb + qtok * a.qs[2] + 32 * ds + 8 * g)
+                          : u32x4{0u, 0u, 0u, 0u};
+  }
+  pair_reset<HD>(st, c);
+
+  // The walk. Waves 0 and 1 each compact one row's list (valid entries, in
+  // order) and test it for strict ascent; then each places its row's
+  // entries: merged by rank when both lists ascend, else one after the other.
+  if (w < 2) {
+    const int r = w;
+    int cnt = 0;
+    if (irow[r] < M) {
+      cnt = a.kv_cnt[static_cast<int64_t>(bh) * M + irow[r]];
+      cnt = cnt < 0 ? 0 : (cnt > a.kmax ? a.kmax : cnt);
+    }
+    const int32_t* gl = a.kv_idx + (static_cast<int64_t>(bh) * M + irow[r]) * a.kmax;
+    int n = 0;
+    for (int base = 0; base < cnt; base += 64) {
+      const int x = base + lane < cnt ? gl[base + lane] : -1;
+      const bool valid = x >= 0 && x < Mk;
+      const uint64_t bal = ballot64(valid);
+      if (valid) lst[r][n + static_cast<int>(rank_below64(bal))] = x;
+      n += __popcll(bal);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's list writes landed
+    bool asc = true;
+    for (int base = 0; base + 1 < n; base += 64) {
+      const int i = base + lane;
+      const bool ok = i + 1 >= n || lst[r][i] < lst[r][i + 1 < n ? i + 1 : i];
+      asc = asc && ballot64(!ok) == 0;
+    }
+    if (lane == 0) {
+      meta[r] = n;
+      meta[2 + r] = asc ? 1 : 0;
+    }
+  }
+  __syncthreads();
+  const int nrow[2] = {meta[0], meta[1]};
+  const bool merge = meta[2] != 0 && meta[3] != 0;
+  if (w < 2) {
+    const int r = w, n = nrow[r], no = nrow[r ^ 1];
+    const int32_t* other = lst[r ^ 1];
+    const uint32_t tag = r == 0 ? TAG_A : TAG_B;
+    int common = 0;  // entries of this row below the chunk that the other row keeps too
+    for (int base = 0; base < n; base += 64) {
+      const int i = base + lane;
+      const int x = i < n ? lst[r][i] : 0;
+      int pos = r == 0 ? i : nrow[0] + i;
+      bool shared = false;
+      if (merge) {
+        int lo = 0, hi = no;  // lower bound of x in the other row's list
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (other[mid] < x) lo = mid + 1; else hi = mid;
+        }
+        shared = lo < no && other[lo] == x;
+        const uint64_t sb = ballot64(i < n && shared);
+        pos = i + lo - common - static_cast<int>(rank_below64(sb));
+        common += __popcll(sb);
+      }
+      if (i < n && !(r == 1 && shared))
+        uni[pos] = static_cast<uint32_t>(x) | tag | (shared ? TAG_B : 0u);
+    }
+    if (r == 0 && lane == 0) meta[4] = nrow[0] + nrow[1] - (merge ? common : 0);
+  }
+  __syncthreads();
+  const int U = meta[4];
+
+  // Staging (as in attn_fwd_kernel): wave w fetches its NI KB of K rows and
+  // of the V^T tile of a block, one 1 KB buffer load each.
+  const int64_t krow_bytes = a.ks[2] * 2;
+  const int64_t kblk_bytes = BS * krow_bytes;
+  uint32_t koff[NI];
+#pragma unroll
+  for (int r = 0; r < NI; ++r) koff[r] = k_lane_off<HD>(NI * w + r, lane, krow_bytes);
+  const int voff = w * NI * 1024 + 16 * lane;
+  auto stage_part = [&](int j, u32x4* kst, u32x4* vst, int part) {
+    constexpr int PER = 2 * NI / NDS;
+    char* kl = reinterpret_cast<char*>(kst) + w * NI * 1024;
+    char* vl = reinterpret_cast<char*>(vst) + w * NI * 1024;
+    const int rows = Nk - j * BS < BS ? Nk - j * BS : BS;
+    const sgpr_rsrc_t krs =
+        make_sgpr_rsrc(kbytes + j * kblk_bytes, static_cast<uint32_t>(rows * krow_bytes));
+    const sgpr_rsrc_t vrs = make_sgpr_rsrc(vtbytes + static_cast<int64_t>(j) * TILE_BYTES, TILE_BYTES);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int r = part * PER + q;
+      if (r < NI)
+        bdma16_untracked(krs, koff[r], 0u, kl + 1024 * r);
+      else
+        bdma16_untracked(vrs, voff + 1024u * (r - NI), 0u, vl + 1024 * (r - NI));
+    }
+  };
+  // K operand offset of (key tile kt, k-step ds) inside a K stage.
+  uint32_t kread[NDS];
+#pragma unroll
+  for (int ds = 0; ds < NDS; ++ds)
+    kread[ds] = G::ROW_BYTES * l16 + 16 * ((4 * ds + g) ^ G::kswz(l16));
+  const uint32_t one2 = BF16 ? 0x3f803f80u : 0x3c003c00u;
+  const u32x4 ones = {one2, one2, one2, one2};
+
+  // One union entry (block j, rows ROWS: bit 0 row A, bit 1 row B) from LDS
+  // stage PAR, with the next entry's staging spread between its S MFMAs.
+  auto entry_step = [&](int j, auto rows_tag, auto par_tag, auto fast_tag, int jn, bool (&mset)[2]) {
+    constexpr int ROWS = decltype(rows_tag)::value;
+    constexpr int PAR = decltype(par_tag)::value;
+    constexpr bool FAST = decltype(fast_tag)::value;
+    const char* ks = reinterpret_cast<const char*>(stage_k(PAR));
+    const u32x4* vts = stage_v(PAR);
+    f32x4 sc[2][4];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) sc[r][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // K operands one k-step ahead of their MFMAs (two register sets), so an
+    // LDS read's latency overlaps the previous k-step's products.
+    u32x4 kf[2][4];
+    auto read_k = [&](int ds, u32x4 (&dst)[4]) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+        dst[kt] = *reinterpret_cast<const u32x4*>(ks + kread[ds] + TT_BYTES * kt);
+    };
+    read_k(0, kf[0]);
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) {
+      if (ds + 1 < NDS) read_k(ds + 1, kf[(ds + 1) & 1]);
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+          if (ROWS & (1 << r)) sc[r][kt] = mfma16<BF16>(kf[ds & 1][kt], st.qreg[r][ds], sc[r][kt]);
+      __builtin_amdgcn_sched_barrier(0);
+      stage_part(jn, stage_k(PAR ^ 1), stage_v(PAR ^ 1), ds);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // The first V^T operands are read before the softmax, the rest two
+    // O^T tiles ahead of their MFMAs.
+    constexpr int VAHEAD = 2;
+    u32x4 vf[NDT][2];
+    auto read_v = [&](int dt) {
+      vf[dt][0] = vts[(2 * dt + 0) * 64 + lane];
+      vf[dt][1] = vts[(2 * dt + 1) * 64 + lane];
+    };
+#pragma unroll
+    for (int dt = 0; dt < VAHEAD; ++dt) read_v(dt);
+    u32x4 pb[2][2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      if (!(ROWS & (1 << r))) continue;
+      if (block_needs_mask(j, irow[r], true, Nk, a.causal, a.qoff)) {
+        const int qtok = 64 * irow[r] + 16 * w + l16;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int ktok = j * BS + 16 * kt + 4 * g + q;
+            if (ktok >= Nk || (a.causal && ktok > qtok + a.qoff)) sc[r][kt][q] = -INFINITY;
+          }
+      }
+      pair_softmax<FAST, BF16, HD>(st, r, sc[r], c, mset[r], pb[r]);
+    }
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      if (dt + VAHEAD < NDT) read_v(dt + VAHEAD);
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+        if (ROWS & (1 << r)) {
+          st.oacc[r][dt] = mfma16<BF16>(vf[dt][0], pb[r][0], st.oacc[r][dt]);
+          st.oacc[r][dt] = mfma16<BF16>(vf[dt][1], pb[r][1], st.oacc[r][dt]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      if (ROWS & (1 << r)) {
+        st.lacc[r] = mfma16<BF16>(ones, pb[r][0], st.lacc[r]);
+        st.lacc[r] = mfma16<BF16>(ones, pb[r][1], st.lacc[r]);
+      }
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  auto walk = [&](auto fast_tag) {
+    bool mset[2] = {false, false};
+    auto ent = [&](int u) { return __builtin_amdgcn_readfirstlane(uni[u]); };
+    uint32_t e = ent(0);
+    {
+      const int j0 = static_cast<int>(e & TAG_BLOCK);
+#pragma unroll
+      for (int part = 0; part < NDS; ++part) stage_part(j0, stage_k(0), stage_v(0), part);
+    }
+    auto step = [&](int u, auto par_tag) {
+      const uint32_t en = ent(u + 1 < U ? u + 1 : U - 1);  // the last step re-stages its own block
+      const int j = static_cast<int>(e & TAG_BLOCK), jn = static_cast<int>(en & TAG_BLOCK);
+      // vmcnt(0): this wave's staging of entry u landed; the barrier: every
+      // wave's did, and the other stage is free. Written as one asm statement
+      // with a memory clobber, so no LDS access moves across it.
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      if ((e & TAG_A) && (e & TAG_B))
+        entry_step(j, std::integral_constant<int, 3>{}, par_tag, fast_tag, jn, mset);
+      else if (e & TAG_A)
+        entry_step(j, std::integral_constant<int, 1>{}, par_tag, fast_tag, jn, mset);
+      else
+        entry_step(j, std::integral_constant<int, 2>{}, par_tag, fast_tag, jn, mset);
+      e = en;
+    };
+    for (int u = 0; u < U; u += 2) {
+      step(u, std::integral_constant<int, 0>{});
+      if (u + 1 < U) step(u + 1, std::integral_constant<int, 1>{});
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last step's staging landed
+  };
+
+  if (U > 0) {
+    walk(std::true_type{});
+    const bool bad = ballot64(!pair_sums_ok<HD>(st)) != 0;
+    if (lane == 0) wave_bad[w] = bad ? 1 : 0;
+    __syncthreads();
+    if ((wave_bad[0] | wave_bad[1] | wave_bad[2] | wave_bad[3]) != 0) {
+      pair_reset<HD>(st, c);
+      walk(std::false_type{});
+    }
+  }
+
+  // Each wave writes its own queries: O = O^T / l, lse = (m c + log2 l) ln 2.
+  uint16_t* ob = static_cast<uint16_t*>(a.o) + b * a.os[0] + hh * a.os[1];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int qtok = 64 * irow[r] + 16 * w + l16;
+    if (irow[r] >= M || qtok >= N) continue;
+    const float l = st.lacc[r][0];
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const f32x4 o = st.oacc[r][dt] * inv;
+      *reinterpret_cast<u32x2*>(ob + qtok * a.os[2] + 16 * dt + 4 * g) =
+          u32x2{pack2<BF16>(o[0], o[1]), pack2<BF16>(o[2], o[3])};
+    }
+    if (a.lse && g == 0)
+      a.lse[static_cast<int64_t>(bh) * N + qtok] =
+          l > 0.f ? (st.m_run[r] * c + __log2f(l)) * 0.69314718055994531f : -INFINITY;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // key_score_kernel: per-key attention totals (cab_attn_key_scores).
 // score[k] = sum over queries t of softmax_t(k) = exp(s_tk - lse_t), with
 // the natural-log lse of attn_fwd_kernel's rows. One workgroup of 4 waves per
@@ -1203,6 +1603,16 @@ cab_status_t launch_pack_split(const char* fn, const void* k, const int64_t* k_s
   return launch_status(fn);
 }
 
+// Whether the row-pair kernel may run (development switch: CAB_ATTN_PAIR=0
+// keeps every call on attn_fwd_kernel).
+bool pair_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("CAB_ATTN_PAIR");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
 template <cab_dtype_t DT, int HD>
 void launch_attn_kernel(int list, dim3 grid, hipStream_t s, const AttnArgs& a) {
   if (list == LIST_LDS)
@@ -1251,6 +1661,22 @@ cab_status_t launch_attn(const char* fn, const void* q, const void* k, const voi
   a.kmax = kmax;
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   a.causal = causal ? 1 : 0;
+  if (g.list == LIST_LDS && dtype != CAB_F32 && g.H == g.Hkv && g.qoff == 0 &&
+      kmax <= PAIR_KMAX && pair_enabled()) {
+    const dim3 pgrid(static_cast<unsigned>(g.B * g.H * ((M + 1) / 2)));
+    if (g.D == 64) {
+      if (dtype == CAB_BF16)
+        attn_pair_kernel<CAB_BF16, 64><<<pgrid, 256, 0, s>>>(a);
+      else
+        attn_pair_kernel<CAB_F16, 64><<<pgrid, 256, 0, s>>>(a);
+    } else {
+      if (dtype == CAB_BF16)
+        attn_pair_kernel<CAB_BF16, 128><<<pgrid, 256, 0, s>>>(a);
+      else
+        attn_pair_kernel<CAB_F16, 128><<<pgrid, 256, 0, s>>>(a);
+    }
+    return launch_status(fn);
+  }
   const dim3 grid(static_cast<unsigned>(g.B * g.H * M));
   if (g.D == 64) {
     if (dtype == CAB_BF16)
