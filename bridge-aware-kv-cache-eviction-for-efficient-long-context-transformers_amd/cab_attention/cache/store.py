@@ -7,8 +7,16 @@ new rows after the active rows, so appending costs the new rows only, not a
 copy of the whole cache per token. A prune gathers the kept rows of every
 layer from the active buffers into the spares (``cab_kv_gather``: one launch
 per 32 tensors of one geometry) and swaps the two. Capacity doubles only when
-an append would overflow it. The tensors a layer hands out are views of its
-active buffer: valid until the next append or prune of that layer.
+an append would overflow it, and a prune that leaves a layer with less than
+half of its capacity in use (kept rows plus the caller's headroom) moves it
+into buffers of that size and releases the large ones: after a long prefill
+the cache holds about twice the kept rows plus headroom per layer, not the
+prefill's length.
+
+The tensors a layer hands out are views of its active buffer, valid until
+the next append or prune of that layer: a prune writes into the former
+active buffer, so a view kept across it changes. Callers that keep K or V
+across updates copy them.
 
 ``EvictingCache`` is the decision layer: it counts update calls, asks its
 ``selector`` for the positions to keep when an eviction is due, prunes the
@@ -96,20 +104,36 @@ class LayeredKV:
         L.v[:, :, L.length:need, :L.width].copy_(v)
         L.length = need
 
-    def prune(self, keep: torch.Tensor):
+    def capacity(self, layer: int) -> int:
+        """Rows the layer's active buffer holds (0 for an absent layer)."""
+        if layer >= len(self.layers) or self.layers[layer] is None:
+            return 0
+        return self.layers[layer].k.shape[2]
+
+    def prune(self, keep: torch.Tensor, headroom: int = 0):
         """Every present layer keeps its rows at ``keep`` (ascending int64
-        positions), in that order."""
+        positions), in that order. ``headroom``: rows the caller expects to
+        append before the next prune. A layer whose capacity exceeds twice
+        ``len(keep) + headroom`` (and the initial capacity) moves into new
+        buffers of that many rows; its old buffers are released."""
         n_keep = keep.numel()
+        target = max(self.initial_capacity, n_keep + max(0, int(headroom)))
         groups: Dict[tuple, List[_Layer]] = {}
+        shrunk = set()
         for L in self.layers:
             if L is None:
                 continue
-            if L.k_spare is None or L.k_spare.shape != L.k.shape:
+            if L.k.shape[2] > 2 * target:
+                B, H, _, W = L.k.shape
+                L.k_spare = L.k.new_empty((B, H, target, W))
+                L.v_spare = L.v.new_empty((B, H, target, W))
+                shrunk.add(id(L))
+            elif L.k_spare is None or L.k_spare.shape != L.k.shape:
                 L.k_spare, L.v_spare = torch.empty_like(L.k), torch.empty_like(L.v)
-            key = (tuple(L.k.shape), L.k.dtype, L.k.device, L.length)
+            key = (tuple(L.k.shape), tuple(L.k_spare.shape), L.k.dtype, L.k.device, L.length)
             groups.setdefault(key, []).append(L)
         idx = None
-        for (_, _, dev, length), members in groups.items():
+        for (_, _, _, dev, length), members in groups.items():
             if idx is None or idx.device != dev:
                 idx = keep.detach().reshape(-1).to(device=dev, dtype=torch.int64).contiguous()
             srcs = [L.k for L in members] + [L.v for L in members]
@@ -120,6 +144,8 @@ class LayeredKV:
                 continue
             L.k, L.k_spare = L.k_spare, L.k
             L.v, L.v_spare = L.v_spare, L.v
+            if id(L) in shrunk:
+                L.k_spare = L.v_spare = None  # the large buffers are released
             L.length = n_keep
 
     def clear(self):
@@ -150,22 +176,27 @@ class EvictingCache:
         self.device = device
         self._floor = floor
         self._selector = selector
-        slack = int(max_cache_size * 1.1) + max(1, eviction_interval) + 1
-        self._store = LayeredKV(initial_capacity=max(slack, 16))
+        # Kept rows plus the rows the update calls between two evictions
+        # append; larger appends (a prefill) grow a layer until its next prune.
+        self._headroom = max(1, eviction_interval) + 1
+        self._store = LayeredKV(initial_capacity=max(self.keep_size + self._headroom, 16))
         self.importance_tracker = ImportanceTracker(device=device)
         self.tokens_since_last_eviction = 0
         self.total_evictions = 0
         self.stats: Dict[str, Any] = {"total_tokens_processed": 0, "total_evictions": 0,
                                       "total_tokens_evicted": 0}
 
-    # The per-layer tensors, as lists of views (None for a layer never updated).
+    # The per-layer tensors as read-only tuples of views (None for a layer
+    # never updated): assigning an entry raises TypeError instead of being
+    # silently lost, and the views follow the store's lifetime rule (valid
+    # until the layer's next update or eviction).
     @property
-    def key_cache(self) -> List[Optional[torch.Tensor]]:
-        return [self._store.view(i)[0] for i in range(len(self._store.layers))]
+    def key_cache(self) -> Tuple[Optional[torch.Tensor], ...]:
+        return tuple(self._store.view(i)[0] for i in range(len(self._store.layers)))
 
     @property
-    def value_cache(self) -> List[Optional[torch.Tensor]]:
-        return [self._store.view(i)[1] for i in range(len(self._store.layers))]
+    def value_cache(self) -> Tuple[Optional[torch.Tensor], ...]:
+        return tuple(self._store.view(i)[1] for i in range(len(self._store.layers)))
 
     @property
     def keep_size(self) -> int:
@@ -196,7 +227,7 @@ class EvictingCache:
         if cache_len <= self.keep_size:
             return
         keep = self._selector(cache_len, self.keep_size)
-        self._store.prune(keep)
+        self._store.prune(keep, headroom=self._headroom)
         self.importance_tracker.prune(keep)
         self.tokens_since_last_eviction = 0
         self.total_evictions += 1

@@ -1105,8 +1105,11 @@ __global__ __launch_bounds__(256, 2) void attn_pair_kernel(AttnArgs a) {
 #pragma unroll
   for (int r = 0; r < NI; ++r) koff[r] = k_lane_off<HD>(NI * w + r, lane, krow_bytes);
   const int voff = w * NI * 1024 + 16 * lane;
+  // Loads 2 NI / NDS of the wave's 2 NI staging loads of block j (part
+  // 0 .. NDS - 1).
   auto stage_part = [&](int j, u32x4* kst, u32x4* vst, int part) {
     constexpr int PER = 2 * NI / NDS;
+    static_assert(NDS % 2 == 0 && NDT % (NDS / 2) == 0, "staging parts split over S and P V");
     char* kl = reinterpret_cast<char*>(kst) + w * NI * 1024;
     char* vl = reinterpret_cast<char*>(vst) + w * NI * 1024;
     const int rows = Nk - j * BS < BS ? Nk - j * BS : BS;
@@ -1160,13 +1163,18 @@ __global__ __launch_bounds__(256, 2) void attn_pair_kernel(AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < 2; ++r)
           if (ROWS & (1 << r)) sc[r][kt] = mfma16<BF16>(kf[ds & 1][kt], st.qreg[r][ds], sc[r][kt]);
-      __builtin_amdgcn_sched_barrier(0);
-      stage_part(jn, stage_k(PAR ^ 1), stage_v(PAR ^ 1), ds);
-      __builtin_amdgcn_sched_barrier(0);
+      // the next entry's staging: the first half of its loads here, between
+      // the S MFMAs, the second half between the P V MFMAs below
+      if (ds % 2 == 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        stage_part(jn, stage_k(PAR ^ 1), stage_v(PAR ^ 1), ds / 2);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    // The first V^T operands are read before the softmax, the rest two
+    // The first V^T operands are read before the softmax, the rest four
     // O^T tiles ahead of their MFMAs.
-    constexpr int VAHEAD = 2;
+    constexpr int VAHEAD = 4;
+    constexpr int PV_PART_EVERY = NDT / (NDS / 2);  // O^T tiles per staging part
     u32x4 vf[NDT][2];
     auto read_v = [&](int dt) {
       vf[dt][0] = vts[(2 * dt + 0) * 64 + lane];
@@ -1194,6 +1202,11 @@ __global__ __launch_bounds__(256, 2) void attn_pair_kernel(AttnArgs a) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       if (dt + VAHEAD < NDT) read_v(dt + VAHEAD);
+      if (dt % PV_PART_EVERY == 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        stage_part(jn, stage_k(PAR ^ 1), stage_v(PAR ^ 1), NDS / 2 + dt / PV_PART_EVERY);
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
       for (int r = 0; r < 2; ++r)
         if (ROWS & (1 << r)) {

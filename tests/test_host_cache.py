@@ -97,7 +97,7 @@ def test_cache_core_matches_the_reference_rules(monkeypatch, kind, D, dtype):
         assert 0 < st["avg_cache_size"] <= int(40 * 0.5 * 0.9)
         assert st["effective_sparsity"] == pytest.approx(1 - len(model.layers[0]) / 40)
     cache.reset()
-    assert len(cache) == 0 and cache.key_cache == [] and cache.get_seq_length(2) == 0
+    assert len(cache) == 0 and cache.key_cache == () and cache.get_seq_length(2) == 0
 
 
 def test_store_grows_and_pads_rows(monkeypatch):
@@ -119,3 +119,54 @@ def test_store_grows_and_pads_rows(monkeypatch):
     assert torch.equal(k[:, :, 2], y[:, :, 0]) and st.length(0) == 3
     with pytest.raises(ValueError):
         st.append(0, torch.ones(3, 2, 1, 4), torch.ones(3, 2, 1, 4))
+
+
+@pytest.mark.parametrize("kind", ["cab", "h2o"])
+def test_capacity_stays_bounded_after_a_long_prefill(monkeypatch, kind):
+    """A prefill far longer than the cache grows each layer to its length;
+    the first eviction moves every layer into buffers of about the kept rows
+    plus the eviction interval, and decode steps keep it there."""
+    monkeypatch.setattr(S, "gather_into", torch_gather_into)
+    cls = CABCache if kind == "cab" else H2OCache
+    cache = cls(max_cache_size=256, sparsity=0.5, eviction_interval=8, device="cpu")
+    cache._selector = every_other_newest
+    bound = 2 * (cache.keep_size + 8 + 1)
+    B, H, D, layers = 1, 2, 4, 3
+    for layer in range(layers):
+        x = torch.randn(B, H, 5000, D)
+        cache.update(x, x, layer, None)
+    for _ in range(40):
+        for layer in range(layers):
+            x = torch.randn(B, H, 1, D)
+            cache.update(x, x, layer, None)
+    assert cache.total_evictions >= 2
+    for layer in range(layers):
+        L = cache._store.layers[layer]
+        assert cache._store.capacity(layer) <= bound
+        assert L.k_spare is None or L.k_spare.shape[2] <= bound
+        assert cache.get_seq_length(layer) <= cache._store.capacity(layer)
+
+
+def test_cache_views_are_read_only_and_alias_the_store(monkeypatch):
+    """key_cache / value_cache are tuples (item assignment raises), and a view
+    kept across an eviction is overwritten by the next prune: the documented
+    lifetime (copy to keep)."""
+    monkeypatch.setattr(S, "gather_into", torch_gather_into)
+    cache = H2OCache(max_cache_size=40, sparsity=0.5, eviction_interval=3, device="cpu")
+    cache._selector = every_other_newest
+    # 20 rows fit the initial capacity (18 kept + 4 headroom), so no append
+    # reallocates and the view stays on one of the two store buffers
+    x = torch.arange(20, dtype=torch.float32).view(1, 1, 20, 1).expand(1, 2, 20, 4).contiguous()
+    cache.update(x, x, 0, None)
+    assert cache._store.capacity(0) == 22
+    with pytest.raises(TypeError):
+        cache.key_cache[0] = x
+    with pytest.raises(TypeError):
+        cache.value_cache[0] = x
+    kept = cache.key_cache[0]
+    snapshot = kept.clone()
+    for _ in range(6):
+        y = torch.full((1, 2, 1, 4), -1.0)
+        cache.update(y, y, 0, None)
+    assert cache.total_evictions >= 2
+    assert not torch.equal(kept, snapshot)  # the old view now shows a later prune's rows
