@@ -144,7 +144,7 @@ def canonical_sqnorm(x: np.ndarray) -> np.ndarray:
     return part[..., 0]
 
 
-def coarsen_max_l2(x: np.ndarray, block_size: int):
+def coarsen_max_l2(x: np.ndarray, block_size: int, compute_dtype=np.float64):
     """Max-L2 pooling: one representative token per block.
 
     ``idx[b,h,m] = argmax_{t in block m} ||x[b,h,t]||`` (first index on
@@ -153,10 +153,17 @@ def coarsen_max_l2(x: np.ndarray, block_size: int):
     Follows README.md:30-33 (Max-L2 pooling) and the coarsening contract of
     benchmarks/kernel_benchmark.py:82-85 and CAB_Attention_Colab.ipynb:109-141.
     Returns ``(xc, idx)``; idx is the absolute token index (int32).
+    ``compute_dtype=np.float32`` forms the norms as one float32 dot product
+    per token (the reference's torch path): the CPU baseline's timing mode,
+    not a checker (its ties and near-ties are not canonical).
     """
     b, h, n, d = x.shape
     m = num_blocks(n, block_size)
-    norms = canonical_sqnorm(x)
+    if compute_dtype == np.float64:
+        norms = canonical_sqnorm(x)
+    else:
+        xf = np.asarray(x, dtype=compute_dtype)
+        norms = np.einsum("...d,...d->...", xf, xf)
     padded = np.full((b, h, m * block_size), -np.inf, dtype=np.float64)
     padded[..., :n] = norms
     local = np.argmax(padded.reshape(b, h, m, block_size), axis=-1)
@@ -171,7 +178,7 @@ def coarsen_max_l2(x: np.ndarray, block_size: int):
 
 def compute_block_frc(q_coarse, k_coarse, temperature: float = 1.0,
                       lambda_redundancy: float = 0.5, formula: str = "additive",
-                      normalization: str = "minmax"):
+                      normalization: str = "minmax", compute_dtype=np.float64):
     """Block-level Forman-Ricci curvature, float64.
 
     - Affinity ``A = Qc Kc^T / sqrt(D) / temperature``
@@ -188,9 +195,12 @@ def compute_block_frc(q_coarse, k_coarse, temperature: float = 1.0,
       ``4 Ahat - S_i - S_j + 3 T`` on edges (Ahat > 0), 1000 elsewhere, with
       ``S`` the row sums of Ahat (test.ipynb:111-145).
     Returns ``(frc, affinity, redundancy)`` with affinity the normalised Ahat.
+    ``compute_dtype=np.float32`` runs the same steps in float32 (BLAS sgemm,
+    as the reference's torch path does): the CPU baseline's timing mode, not
+    a checker.
     """
-    qc = np.asarray(q_coarse, dtype=np.float64)
-    kc = np.asarray(k_coarse, dtype=np.float64)
+    qc = np.asarray(q_coarse, dtype=compute_dtype)
+    kc = np.asarray(k_coarse, dtype=compute_dtype)
     d = qc.shape[-1]
     a = np.matmul(qc, np.swapaxes(kc, -1, -2)) * (1.0 / math.sqrt(d)) / temperature
     if normalization == "minmax":
