@@ -14,7 +14,7 @@ import threading
 import torch
 
 LIB_PATH = pathlib.Path(__file__).resolve().with_name("libcab_hip.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 CAB_OK, CAB_EINVAL, CAB_EDTYPE, CAB_ESHAPE, CAB_EWORKSPACE, CAB_EHIP = range(6)
 CAB_F32, CAB_F16, CAB_BF16 = 0, 1, 2
@@ -43,6 +43,8 @@ SIGNATURES = {
                                              ctypes.c_int, ctypes.c_int, _ptr, _ptr, _ptr, _ptr]),
     "cab_block_sparse_attn_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, _i64, _i64, _i64, _i64,
                                                                 _i32]),
+    "cab_block_sparse_attn_workspace_bytes_k": (ctypes.c_size_t, [ctypes.c_int, _i64, _i64, _i64,
+                                                                  _i64, _i32, _i32]),
     "cab_block_sparse_attn_fwd": (ctypes.c_int, [_ptr, _ptr, _ptr, ctypes.c_int, _i64, _i64, _i64,
                                                  _i64, _i64x4, _i64x4, _i64x4, _i64x4, _i32, _ptr,
                                                  _ptr, _i32, _f32, ctypes.c_int, _ptr, _ptr, _ptr,

@@ -18,7 +18,9 @@ from .. import _native as nat
 # What the executor kernel is built for; anything else is rejected by the
 # C ABI (CAB_ESHAPE) rather than computed approximately.
 SUPPORTED_HEAD_DIMS = (64, 128)
-SUPPORTED_BLOCK_SIZES = (64,)
+# 64, its multiples 128 and 256 (lists expanded to 64-token tiles), and 8,
+# 16, 32 (64-token tiles with sub-tile masks); the packed-V path takes 64.
+SUPPORTED_BLOCK_SIZES = (8, 16, 32, 64, 128, 256)
 
 
 def _check_lists(kv_idx, kv_cnt, B, H, M):
@@ -48,7 +50,8 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     """``out[t] = softmax_s(q_t . k_s * scale) v_s`` over the key blocks
     ``kv_idx[b, h, i, :kv_cnt[b, h, i]]`` of the query block i holding t.
 
-    q, k, v: ``[B, H, N, D]`` bf16, fp16 or fp32 (D = 64 or 128, block_size = 64;
+    q, k, v: ``[B, H, N, D]`` bf16, fp16 or fp32 (D = 64 or 128, block_size in
+    ``SUPPORTED_BLOCK_SIZES``;
     fp32 runs on split bf16 hi + lo operands, three MFMA products each); causal
     drops keys s > t; a query with no key gets 0; ``scale`` (> 0) defaults to
     ``1/sqrt(D)``. Index entries outside ``[0, M)`` are skipped. ``out`` may be
@@ -74,7 +77,8 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     out, lse = _outputs(q, out, return_lse, dev)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    wbytes = lib.cab_block_sparse_attn_workspace_bytes(dt, B, H, N, D, int(block_size))
+    wbytes = lib.cab_block_sparse_attn_workspace_bytes_k(dt, B, H, N, D, int(block_size),
+                                                         int(kv_idx.shape[-1]))
     ws = torch.empty(max(int(wbytes), 16), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         st = lib.cab_block_sparse_attn_fwd(

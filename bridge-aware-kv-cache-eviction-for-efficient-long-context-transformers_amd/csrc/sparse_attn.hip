@@ -101,6 +101,11 @@ struct AttnArgs {
   int32_t kmax;
   float scale_log2;
   int causal;
+  // Block sizes below 64: per list entry, the 64-bit mask of the (bs x bs)
+  // sub-tiles of its 64 x 64 tile that are kept (bit (q / bs) * (64 / bs) +
+  // k / bs for query q and key k of the tile); null when every tile is whole.
+  const uint64_t* submask;
+  int sub_shift;  // log2(block_size) when submask is set
 };
 
 struct PackArgs {
@@ -447,7 +452,8 @@ __device__ __forceinline__ bool block_needs_mask(int j, int i, bool valid, int N
 template <cab_dtype_t DT, int HD, int SM, typename Stager>
 __device__ __forceinline__ void acc_block(WaveAcc<HD>& s, const WaveGeo<HD>& ge, const char* ks,
                                           const u32x4* vts, int j, int i, bool valid, int Nk,
-                                          bool causal, int qoff, float c, const Stager& stg) {
+                                          bool causal, int qoff, float c, uint64_t sm,
+                                          int sub_shift, const Stager& stg) {
   using G = Dims<HD>;
   constexpr int NDS = G::NDS, NDT = G::NDT;
   constexpr int TT_BYTES = 16 * G::ROW_BYTES;  // 16 K rows
@@ -498,16 +504,21 @@ __device__ __forceinline__ void acc_block(WaveAcc<HD>& s, const WaveGeo<HD>& ge,
     }
   }
 
-  if (block_needs_mask(j, i, valid, Nk, causal, qoff)) {
+  const bool subm = sm != ~0ull;  // a tile of smaller blocks, some of them dropped
+  if (block_needs_mask(j, i, valid, Nk, causal, qoff) || subm) {
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int ktok = j * BS + 32 * ge.kh + 16 * tt + 4 * ge.g + r;
-          const int qtok = i * BS + 32 * ge.qh + 16 * qt + ge.l16;
-          if (!valid || ktok >= Nk || (causal && ktok > qtok + qoff)) sc[tt][qt][r] = -INFINITY;
+          const int kl = 32 * ge.kh + 16 * tt + 4 * ge.g + r, ql = 32 * ge.qh + 16 * qt + ge.l16;
+          const int ktok = j * BS + kl, qtok = i * BS + ql;
+          bool drop = !valid || ktok >= Nk || (causal && ktok > qtok + qoff);
+          if (subm)
+            drop = drop || ((sm >> (((ql >> sub_shift) << (6 - sub_shift)) | (kl >> sub_shift))) &
+                            1ull) == 0;
+          if (drop) sc[tt][qt][r] = -INFINITY;
         }
   }
   float mx[2];
@@ -807,6 +818,8 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
       constexpr int SM = decltype(sm_tag)::value;
       const bool valid = jraw >= 0 && jraw < Mk;
       const int j = valid ? jraw : 0;
+      const uint64_t sm = a.submask ? a.submask[(static_cast<int64_t>(bh) * M + i) * a.kmax + p]
+                                    : ~0ull;
       __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's staging of block p landed
       __builtin_amdgcn_s_barrier();        // ... and every wave's; stage PAR ^ 1 is free
       int jnext = 0;
@@ -816,7 +829,7 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
           stage(block_of(jnext), stage_k(PAR ^ 1), stage_v(PAR ^ 1));
         }
         acc_block<DT, HD, SM>(st, ge, reinterpret_cast<const char*>(stage_k(PAR)), stage_v(PAR),
-                              j, i, valid, Nk, a.causal, a.qoff, c, [](int) {});
+                              j, i, valid, Nk, a.causal, a.qoff, c, sm, a.sub_shift, [](int) {});
       } else {
         // unconditional (the last step re-stages a valid block into the free
         // stage; waited for after the loop) so that the loads sit between the MFMAs
@@ -824,7 +837,7 @@ __global__ __launch_bounds__(256, DT == CAB_F32 ? 1 : 2) void attn_fwd_kernel(At
         jnext = p + 1 < cnt ? e : 0;
         const int js = block_of(jnext);
         acc_block<DT, HD, SM>(st, ge, reinterpret_cast<const char*>(stage_k(PAR)), stage_v(PAR),
-                              j, i, valid, Nk, a.causal, a.qoff, c,
+                              j, i, valid, Nk, a.causal, a.qoff, c, sm, a.sub_shift,
                               [&](int ds) { stage_part(js, stage_k(PAR ^ 1), stage_v(PAR ^ 1), ds); });
       }
       jraw = jnext;
@@ -1286,6 +1299,97 @@ __global__ __launch_bounds__(256, 2) void attn_pair_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Block sizes other than 64: the caller's lists over bs-token blocks become
+// lists over 64-token tiles, which the executors walk.
+//  relist_expand_kernel (bs = 64 r): entry jb of bs-row ib gives tiles
+//    jb r .. jb r + r - 1 to each of the r 64-rows of ib, in that order
+//    (entries outside [0, Mb) and tiles past the last key block stay -1,
+//    which the executors skip).
+//  relist_merge_kernel (bs = 64 / r): the r bs-rows of a 64-row give their
+//    entries jb as (tile jb / r, sub-tile bit u r + jb % r) for sub-row u.
+//    One wave merges them in list order: a pair joins the first entry of
+//    its tile that lacks its bit, or starts a new entry. A block listed
+//    twice therefore counts twice, as in the caller's lists. Each entry
+//    carries its 64-bit sub-tile mask (AttnArgs::submask).
+// ---------------------------------------------------------------------------
+struct RelistArgs {
+  const int32_t* idx;  // [BH, Mb, kmax]
+  const int32_t* cnt;  // [BH, Mb]
+  int32_t* idx64;      // [BH, M64, K64]
+  int32_t* cnt64;      // [BH, M64]
+  uint64_t* sub64;     // [BH, M64, K64] (merge only)
+  int32_t Mb, M64, Mk64, kmax, K64, r;
+};
+
+__global__ __launch_bounds__(64) void relist_expand_kernel(RelistArgs a) {
+  const int64_t row = blockIdx.x;  // bh * M64 + i64
+  const int64_t bh = row / a.M64, i64 = row - bh * a.M64;
+  const int64_t ib = i64 / a.r;
+  int cnt = a.cnt[bh * a.Mb + ib];
+  cnt = cnt < 0 ? 0 : (cnt > a.kmax ? a.kmax : cnt);
+  const int32_t* src = a.idx + (bh * a.Mb + ib) * a.kmax;
+  int32_t* dst = a.idx64 + row * a.K64;
+  for (int e = threadIdx.x; e < cnt * a.r; e += 64) {
+    const int jb = src[e / a.r];
+    const int64_t j64 = static_cast<int64_t>(jb) * a.r + e % a.r;
+    dst[e] = jb >= 0 && jb < a.Mb && j64 < a.Mk64 ? static_cast<int32_t>(j64) : -1;
+  }
+  if (threadIdx.x == 0) a.cnt64[row] = cnt * a.r;
+}
+
+__global__ __launch_bounds__(64) void relist_merge_kernel(RelistArgs a) {
+  extern __shared__ __align__(16) unsigned char relist_lds[];
+  uint64_t* lsub = reinterpret_cast<uint64_t*>(relist_lds);        // [K64]
+  int32_t* lidx = reinterpret_cast<int32_t*>(lsub + a.K64);         // [K64]
+  const int64_t row = blockIdx.x;
+  const int64_t bh = row / a.M64, i64 = row - bh * a.M64;
+  const int lane = lane_id();
+  int n = 0;  // entries so far (uniform)
+  for (int u = 0; u < a.r; ++u) {
+    const int64_t ib = i64 * a.r + u;
+    if (ib >= a.Mb) break;
+    int cnt = a.cnt[bh * a.Mb + ib];
+    cnt = cnt < 0 ? 0 : (cnt > a.kmax ? a.kmax : cnt);
+    const int32_t* src = a.idx + (bh * a.Mb + ib) * a.kmax;
+    for (int base = 0; base < cnt; base += 64) {
+      const int x = base + lane < cnt ? src[base + lane] : -1;
+      uint64_t vb = ballot64(x >= 0 && x < a.Mb);
+      while (vb) {
+        const int t = __builtin_ctzll(vb);
+        vb &= vb - 1;
+        const int jb = __builtin_amdgcn_readlane(x, t);
+        const int j64 = jb / a.r;
+        const uint64_t bit = 1ull << (u * a.r + jb % a.r);
+        int found = -1;
+        for (int ob = 0; ob < n && found < 0; ob += 64) {
+          const int e = ob + lane;
+          const bool hit = e < n && lidx[e] == j64 && (lsub[e] & bit) == 0;
+          const uint64_t hb = ballot64(hit);
+          if (hb) found = ob + __builtin_ctzll(hb);
+        }
+        if (lane == 0) {
+          if (found >= 0) {
+            lsub[found] |= bit;
+          } else {
+            lidx[n] = j64;
+            lsub[n] = bit;
+          }
+        }
+        n += found < 0 ? 1 : 0;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // visible to the next search
+      }
+    }
+  }
+  int32_t* didx = a.idx64 + row * a.K64;
+  uint64_t* dsub = a.sub64 + row * a.K64;
+  for (int e = lane; e < n; e += 64) {
+    didx[e] = lidx[e];
+    dsub[e] = lsub[e];
+  }
+  if (lane == 0) a.cnt64[row] = n;
+}
+
+// ---------------------------------------------------------------------------
 // key_score_kernel: per-key attention totals (cab_attn_key_scores).
 // score[k] = sum over queries t of softmax_t(k) = exp(s_tk - lse_t), with
 // the natural-log lse of attn_fwd_kernel's rows. One workgroup of 4 waves per
@@ -1516,8 +1620,15 @@ namespace {
 
 // Shape and scalar checks shared by the three entry points. fp32 is accepted
 // by cab_block_sparse_attn_fwd only (its packed form holds K as well as V).
+// Block sizes the executor takes: 64, its multiples 128 and 256 (lists
+// expanded to 64-token tiles) and 8, 16, 32 (tiles with sub-tile masks).
+bool executor_block_size(int64_t bs) {
+  return bs == 8 || bs == 16 || bs == 32 || bs == 64 || bs == 128 || bs == 256;
+}
+constexpr int64_t MERGE_K64_MAX = 4096;  // merged 64-tile entries per row (LDS of the merge)
+
 cab_status_t check_common(const char* fn, cab_dtype_t dtype, int64_t B, int64_t H, int64_t N,
-                          int64_t D, int32_t block_size, bool allow_f32) {
+                          int64_t D, int32_t block_size, bool allow_f32, bool any_bs = false) {
   if (allow_f32)
     CAB_REQUIRE(dtype == CAB_BF16 || dtype == CAB_F16 || dtype == CAB_F32, CAB_EDTYPE,
                 "%s: dtype %d unsupported (bf16, fp16 or fp32)", fn, (int)dtype);
@@ -1528,8 +1639,12 @@ cab_status_t check_common(const char* fn, cab_dtype_t dtype, int64_t B, int64_t 
   CAB_REQUIRE(B >= 0 && H >= 0 && N >= 0, CAB_ESHAPE, "%s: negative size", fn);
   CAB_REQUIRE(D == 64 || D == 128, CAB_ESHAPE, "%s: head dim %lld unsupported (64 or 128)", fn,
               (long long)D);
-  CAB_REQUIRE(block_size == BS, CAB_ESHAPE, "%s: block_size %d unsupported (64)", fn,
-              (int)block_size);
+  if (any_bs)
+    CAB_REQUIRE(executor_block_size(block_size), CAB_ESHAPE,
+                "%s: block_size %d unsupported (8, 16, 32, 64, 128 or 256)", fn, (int)block_size);
+  else
+    CAB_REQUIRE(block_size == BS, CAB_ESHAPE, "%s: block_size %d unsupported (64)", fn,
+                (int)block_size);
   const int64_t M = ceil_div(N, BS);
   CAB_REQUIRE(B * H * M <= INT32_MAX && B * H <= 65535 && N <= INT32_MAX - BS, CAB_ESHAPE,
               "%s: problem too large (B*H <= 65535, B*H*M < 2^31, N < 2^31 - 64)", fn);
@@ -1648,7 +1763,8 @@ cab_status_t launch_attn(const char* fn, const void* q, const void* k, const voi
                          cab_dtype_t dtype, const AttnGeom& g, const int64_t* q_strides,
                          const int64_t* k_strides, const int64_t* o_strides,
                          const int32_t* kv_idx, const int32_t* kv_cnt, int32_t kmax, float scale,
-                         int causal, void* out, float* lse, hipStream_t s) {
+                         int causal, void* out, float* lse, hipStream_t s,
+                         const uint64_t* submask = nullptr, int sub_shift = 0) {
   const int64_t M = ceil_div(g.Nq, BS);
   AttnArgs a;
   a.q = q;
@@ -1674,8 +1790,10 @@ cab_status_t launch_attn(const char* fn, const void* q, const void* k, const voi
   a.kmax = kmax;
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   a.causal = causal ? 1 : 0;
+  a.submask = submask;
+  a.sub_shift = sub_shift;
   if (g.list == LIST_LDS && dtype != CAB_F32 && g.H == g.Hkv && g.qoff == 0 &&
-      kmax <= PAIR_KMAX && pair_enabled()) {
+      kmax <= PAIR_KMAX && submask == nullptr && pair_enabled()) {
     const dim3 pgrid(static_cast<unsigned>(g.B * g.H * ((M + 1) / 2)));
     if (g.D == 64) {
       if (dtype == CAB_BF16)
@@ -1714,7 +1832,40 @@ AttnGeom sparse_geom(int64_t B, int64_t H, int64_t N, int64_t D, int32_t kmax) {
   return AttnGeom{B, H, H, N, N, D, 0, kmax <= LIST_MAX ? LIST_LDS : LIST_GLOBAL};
 }
 
+// The 64-tile lists of a block size other than 64, in the workspace after
+// the packed V: idx64 [BH, M64, K64], cnt64 [BH, M64], and for sizes below
+// 64 the sub-tile masks [BH, M64, K64], each part 256-byte aligned.
+struct TileLists {
+  int64_t r, K64, M64;
+  size_t off_idx, off_cnt, off_sub, end;
+};
+TileLists tile_lists(int64_t B, int64_t H, int64_t N, int32_t bs, int32_t kmax, size_t base) {
+  TileLists t;
+  t.r = bs >= BS ? bs / BS : BS / bs;
+  t.K64 = static_cast<int64_t>(kmax) * t.r;
+  t.M64 = ceil_div(N, BS);
+  const int64_t rows = B * H * t.M64;
+  t.off_idx = static_cast<size_t>(round_up(static_cast<int64_t>(base), 256));
+  t.off_cnt = t.off_idx + static_cast<size_t>(round_up(rows * t.K64 * 4, 256));
+  t.off_sub = t.off_cnt + static_cast<size_t>(round_up(rows * 4, 256));
+  t.end = t.off_sub + (bs < BS ? static_cast<size_t>(rows * t.K64 * 8) : 0);
+  return t;
+}
+
 }  // namespace
+
+extern "C" size_t cab_block_sparse_attn_workspace_bytes_k(cab_dtype_t dtype, int64_t B, int64_t H,
+                                                          int64_t N, int64_t D, int32_t block_size,
+                                                          int32_t kmax) {
+  if (dtype != CAB_BF16 && dtype != CAB_F16 && dtype != CAB_F32) return 0;
+  if (B <= 0 || H <= 0 || N <= 0 || (D != 64 && D != 128) || !executor_block_size(block_size) ||
+      kmax < 1)
+    return 0;
+  const size_t packed =
+      static_cast<size_t>(B * H * ceil_div(N, BS)) * block_bytes(dtype, static_cast<int>(D));
+  if (block_size == BS) return packed;
+  return tile_lists(B, H, N, block_size, kmax, packed).end;
+}
 
 extern "C" size_t cab_block_sparse_attn_workspace_bytes(cab_dtype_t dtype, int64_t B, int64_t H,
                                                         int64_t N, int64_t D, int32_t block_size) {
@@ -1768,9 +1919,16 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
     void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "cab_block_sparse_attn_fwd";
   clear_error();
-  cab_status_t st = check_common(fn, dtype, B, H, N, D, block_size, true);
+  cab_status_t st = check_common(fn, dtype, B, H, N, D, block_size, true, true);
   if (st != CAB_OK) return st;
   CAB_REQUIRE(kmax >= 1, CAB_EINVAL, "%s: kmax=%d must be >= 1", fn, (int)kmax);
+  if (block_size < BS)
+    CAB_REQUIRE(static_cast<int64_t>(kmax) * (BS / block_size) <= MERGE_K64_MAX, CAB_ESHAPE,
+                "%s: block_size %d takes lists of at most %lld entries (kmax=%d)", fn,
+                (int)block_size, (long long)(MERGE_K64_MAX / (BS / block_size)), (int)kmax);
+  if (block_size > BS)
+    CAB_REQUIRE(static_cast<int64_t>(kmax) * (block_size / BS) <= INT32_MAX / 2, CAB_ESHAPE,
+                "%s: kmax=%d too large for block_size %d", fn, (int)kmax, (int)block_size);
   CAB_REQUIRE(std::isfinite(scale) && scale > 0.f, CAB_EINVAL, "%s: scale must be finite and > 0",
               fn);
   CAB_REQUIRE(q_strides && k_strides && v_strides && o_strides, CAB_EINVAL,
@@ -1783,13 +1941,58 @@ extern "C" cab_status_t cab_block_sparse_attn_fwd(
     return st;
   if ((st = check_tensor(fn, "v", v, v_strides, esize)) != CAB_OK) return st;
   if ((st = check_packed(fn, workspace, workspace_bytes, B, H, M, dtype, D)) != CAB_OK) return st;
+  const size_t packed = static_cast<size_t>(B * H * M) * block_bytes(dtype, static_cast<int>(D));
+  TileLists tl{};
+  if (block_size != BS) {
+    tl = tile_lists(B, H, N, block_size, kmax, packed);
+    CAB_REQUIRE(workspace_bytes >= tl.end, CAB_EWORKSPACE,
+                "%s: workspace of %zu bytes given, %zu needed for block_size %d and kmax %d "
+                "(cab_block_sparse_attn_workspace_bytes_k)", fn, workspace_bytes, tl.end,
+                (int)block_size, (int)kmax);
+    CAB_REQUIRE(B * H * tl.M64 * tl.K64 <= INT64_C(1) << 40, CAB_ESHAPE, "%s: lists too large", fn);
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (block_size != BS) {
+    char* ws = static_cast<char*>(workspace);
+    RelistArgs ra;
+    ra.idx = kv_idx;
+    ra.cnt = kv_cnt;
+    ra.idx64 = reinterpret_cast<int32_t*>(ws + tl.off_idx);
+    ra.cnt64 = reinterpret_cast<int32_t*>(ws + tl.off_cnt);
+    ra.sub64 = block_size < BS ? reinterpret_cast<uint64_t*>(ws + tl.off_sub) : nullptr;
+    ra.Mb = static_cast<int32_t>(ceil_div(N, block_size));
+    ra.M64 = static_cast<int32_t>(tl.M64);
+    ra.Mk64 = static_cast<int32_t>(tl.M64);
+    ra.kmax = kmax;
+    ra.K64 = static_cast<int32_t>(tl.K64);
+    ra.r = static_cast<int32_t>(tl.r);
+    const dim3 rgrid(static_cast<unsigned>(B * H * tl.M64));
+    if (block_size > BS) {
+      relist_expand_kernel<<<rgrid, 64, 0, s>>>(ra);
+    } else {
+      const size_t lds = static_cast<size_t>(tl.K64) * 12;
+      relist_merge_kernel<<<rgrid, 64, lds, s>>>(ra);
+    }
+    if ((st = launch_status("cab_block_sparse_attn_fwd/relist")) != CAB_OK) return st;
+  }
   if (dtype == CAB_F32)
     st = launch_pack_split("cab_block_sparse_attn_fwd/pack_split", k, k_strides, v, v_strides, B,
                            H, N, D, workspace, s);
   else
     st = launch_pack("cab_block_sparse_attn_fwd/pack_v", v, v_strides, B, H, N, D, workspace, s);
   if (st != CAB_OK) return st;
+  if (block_size != BS) {
+    const char* ws = static_cast<const char*>(workspace);
+    int sh = 0;
+    while ((1 << sh) < block_size) ++sh;
+    return launch_attn(fn, q, k, workspace, dtype,
+                       sparse_geom(B, H, N, D, static_cast<int32_t>(tl.K64)), q_strides,
+                       k_strides, o_strides, reinterpret_cast<const int32_t*>(ws + tl.off_idx),
+                       reinterpret_cast<const int32_t*>(ws + tl.off_cnt),
+                       static_cast<int32_t>(tl.K64), scale, causal, out, lse, s,
+                       block_size < BS ? reinterpret_cast<const uint64_t*>(ws + tl.off_sub) : nullptr,
+                       sh);
+  }
   return launch_attn(fn, q, k, workspace, dtype, sparse_geom(B, H, N, D, kmax), q_strides, k_strides,
                      o_strides, kv_idx, kv_cnt, kmax, scale, causal, out, lse, s);
 }

@@ -49,7 +49,7 @@ enum { CAB_NORM_NONE = 0, CAB_NORM_MINMAX = 1 };
 /* FRC combination (experiments/longbench_qa/config.py:465; test.ipynb:111-145). */
 enum { CAB_FRC_ADDITIVE = 0, CAB_FRC_MULTIPLICATIVE = 1, CAB_FRC_AUGMENTED = 2 };
 
-#define CAB_ABI_VERSION 9
+#define CAB_ABI_VERSION 10
 
 int cab_abi_version(void);
 const char* cab_last_error(void);
@@ -160,6 +160,20 @@ size_t cab_block_sparse_attn_workspace_bytes(cab_dtype_t dtype, int64_t B, int64
                                              int64_t D, int32_t block_size);
 
 /*
+ * Workspace bytes cab_block_sparse_attn_fwd needs for any block size it
+ * takes and lists of `kmax` entries: the packed tiles above, and for a
+ * block size other than 64 the lists over 64-token tiles the call builds
+ * (block_size 128, 256: kmax * block_size / 64 entries per 64-token row;
+ * 8, 16, 32: kmax * 64 / block_size entries, each with a 64-bit sub-tile
+ * mask). Equal to cab_block_sparse_attn_workspace_bytes for block_size 64.
+ * 0 for unsupported arguments. Replaces nothing in the reference: its
+ * FlexAttention executor sizes its own buffers (config.block_size,
+ * experiments/longbench_qa/config.py:460; block sizes planned in TODO.md:117).
+ */
+size_t cab_block_sparse_attn_workspace_bytes_k(cab_dtype_t dtype, int64_t B, int64_t H, int64_t N,
+                                               int64_t D, int32_t block_size, int32_t kmax);
+
+/*
  * Block-sparse attention forward.
  * Replaces the executor inside CABAttention.forward of
  * cab_attention/cab_attention.py (absent; FlexAttention or the manual masked
@@ -174,12 +188,16 @@ size_t cab_block_sparse_attn_workspace_bytes(cab_dtype_t dtype, int64_t B, int64
  * products per product, fp32 output; relative error near 2^-16 per product).
  * q, k, v: [B,H,N,D] (strides), out: [B,H,N,D] (strides), dtype bf16, fp16
  * or fp32.
- * block_size == 64, D == 64 or 128, scale > 0. kv_idx: contiguous int32
- * [B,H,M,kmax], kv_cnt: contiguous int32 [B,H,M]. lse: fp32 [B,H,N]
+ * block_size 8, 16, 32, 64, 128 or 256 (M = ceil(N / block_size)); for
+ * 8, 16 and 32, kmax * 64 / block_size <= 4096. D == 64 or 128, scale > 0.
+ * kv_idx: contiguous int32 [B,H,M,kmax], kv_cnt: contiguous int32 [B,H,M].
+ * A block listed twice in a row counts twice. lse: fp32 [B,H,N]
  * natural-log log-sum-exp of the scaled scores (-inf for a query with no
- * key), or NULL. workspace: cab_block_sparse_attn_workspace_bytes(dtype, ...)
- * bytes, 16-byte aligned, overwritten (V, and for fp32 K, is repacked there
- * first).
+ * key), or NULL. workspace: cab_block_sparse_attn_workspace_bytes_k(dtype,
+ * ..., block_size, kmax) bytes (for block_size 64 also
+ * cab_block_sparse_attn_workspace_bytes()), 16-byte aligned, overwritten
+ * (V, and for fp32 K, is repacked there first; other block sizes' lists
+ * are rewritten there over 64-token tiles).
  */
 cab_status_t cab_block_sparse_attn_fwd(const void* q, const void* k, const void* v,
                                        cab_dtype_t dtype, int64_t B, int64_t H,
@@ -210,7 +228,7 @@ cab_status_t cab_block_sparse_attn_pack_v(const void* v, cab_dtype_t dtype, int6
 /*
  * cab_block_sparse_attn_fwd_packed: cab_block_sparse_attn_fwd with V given
  * as the tiles cab_block_sparse_attn_pack_v wrote (`vt`, `vt_bytes` bytes).
- * Same arguments, rules and result otherwise.
+ * Same arguments, rules and result otherwise; block_size 64 only.
  */
 cab_status_t cab_block_sparse_attn_fwd_packed(const void* q, const void* k, const void* vt,
                                               cab_dtype_t dtype, int64_t B, int64_t H, int64_t N,

@@ -133,6 +133,20 @@ def test_attention_validation(lib):
     assert call(dt=nat.CAB_F32, wsb=8 * 65536 - 1) == nat.CAB_EWORKSPACE
     assert call(D=96) == nat.CAB_ESHAPE
     assert call(bs=48) == nat.CAB_ESHAPE
+    assert call(bs=512) == nat.CAB_ESHAPE
+    # other block sizes: lists over 64-token tiles in the workspace after the
+    # packed V (256-byte aligned parts): idx [BH, M64, K64] int32, counts
+    # [BH, M64] int32 and, below 64, sub-tile masks [BH, M64, K64] uint64
+    wk = lib.cab_block_sparse_attn_workspace_bytes_k
+    base = 8 * 16384  # N = 64: one 64-token block per head
+    rup = lambda x: -(-x // 256) * 256
+    assert wk(nat.CAB_BF16, 1, 8, 64, 128, 64, 3) == base
+    assert wk(nat.CAB_BF16, 1, 8, 64, 128, 128, 3) == base + rup(8 * 6 * 4) + rup(8 * 4)
+    assert wk(nat.CAB_BF16, 1, 8, 64, 128, 16, 3) == base + rup(8 * 12 * 4) + rup(8 * 4) + 8 * 12 * 8
+    assert wk(nat.CAB_BF16, 1, 8, 64, 128, 48, 3) == 0 and wk(nat.CAB_BF16, 1, 8, 64, 128, 16, 0) == 0
+    assert call(bs=16, wsb=wk(nat.CAB_BF16, 1, 8, 64, 128, 16, 3) - 1) == nat.CAB_EWORKSPACE
+    assert call(bs=128, wsb=base) == nat.CAB_EWORKSPACE
+    assert call(bs=8, kmax=513) == nat.CAB_ESHAPE  # 513 * 8 merged entries > 4096
     assert call(kmax=0) == nat.CAB_EINVAL
     assert call(scale=-0.1) == nat.CAB_EINVAL
     assert call(os=_s4(1, 1, 1, 3)) == nat.CAB_ESHAPE
@@ -196,13 +210,15 @@ def test_module_contract_on_host():
     assert a.predictor.sparsity == 0.95
     with pytest.raises(ValueError):
         CABAttention(dim=500, num_heads=8)
-    # the executor runs head dims 64 and 128 and block size 64 only: rejected
-    # at construction, not in forward
+    # the executor runs head dims 64 and 128 and block sizes 8 ... 256: others
+    # are rejected at construction, not in forward
     CABAttention(dim=1024, num_heads=8)
+    for bs in (8, 16, 32, 128, 256):
+        assert CABAttention(dim=512, num_heads=8, block_size=bs).predictor.block_size == bs
     with pytest.raises(ValueError, match="head_dim"):
         CABAttention(dim=768, num_heads=8)
     with pytest.raises(ValueError, match="block_size"):
-        CABAttention(dim=512, num_heads=8, block_size=128)
+        CABAttention(dim=512, num_heads=8, block_size=48)
     with pytest.raises(ValueError):
         CoarseCurvaturePredictor(sparsity=1.5)
 

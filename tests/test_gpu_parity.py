@@ -849,6 +849,125 @@ def test_attention_row_pair_long_lists(cuda, dt, causal):
     assert np.abs(got - got_row).max() <= 2 * ATOL[dt]
 
 
+def _lists_with_repeats(f, sp, causal, seed):
+    """Predictor-style lists for scores ``f``, then in every 3rd row one
+    block listed a second time (it counts twice) and in every 4th row an
+    invalid entry (skipped). Returns the lists and the oracle's cleaned form."""
+    _, idx, cnt = O.generate_block_mask(f, sp, causal=causal)
+    B, H, M, k = idx.shape
+    rng = np.random.default_rng(seed)
+    kmax = k + 2
+    out = np.full((B, H, M, kmax), -1, np.int32)
+    ocnt = cnt.copy()
+    clean = np.full((B, H, M, kmax), 0, np.int32)
+    ccnt = cnt.copy()
+    for b in range(B):
+        for h in range(H):
+            for i in range(M):
+                row = list(idx[b, h, i, :cnt[b, h, i]])
+                crow = list(row)
+                if i % 3 == 0 and row:
+                    dup = row[int(rng.integers(len(row)))]
+                    row.append(dup)
+                    crow.append(dup)
+                if i % 4 == 1:
+                    row.insert(len(row) // 2, M + 1 if i % 8 == 1 else -3)
+                out[b, h, i, :len(row)] = row
+                ocnt[b, h, i] = len(row)
+                clean[b, h, i, :len(crow)] = crow
+                ccnt[b, h, i] = len(crow)
+    return out, ocnt, clean, ccnt
+
+
+@pytest.mark.parametrize("bs", [8, 16, 32, 128, 256])
+@pytest.mark.parametrize("dt", ["bf16", "fp32"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_block_sizes(cuda, bs, dt, causal):
+    """Block sizes other than 64 (lists over bs-token blocks, rewritten on
+    the device over 64-token tiles: whole tiles for 128 and 256, tiles with
+    sub-tile masks for 8, 16, 32), with a ragged last block, repeated and
+    invalid entries: output and lse against the oracle at that block size."""
+    from cab_attention.kernels import block_sparse_attention
+    B, H, D = 1, 2, 128
+    N = 1000 if bs < 128 else 2 * bs * 5 - 40
+    Mb = (N + bs - 1) // bs
+    q, k, v = (seeded((B, H, N, D), s, DTYPES[dt]) for s in (81 + bs, 82 + bs, 83 + bs))
+    f = np.random.default_rng(bs).standard_normal((B, H, Mb, Mb)).astype(np.float32)
+    idx, cnt, clean, ccnt = _lists_with_repeats(f, 0.6, causal, bs)
+    out, lse = block_sparse_attention(q.to(cuda), k.to(cuda), v.to(cuda), torch.from_numpy(idx).to(cuda),
+                                      torch.from_numpy(cnt).to(cuda), bs, causal=causal,
+                                      return_lse=True)
+    want = O.sparse_attention(np32(q), np32(k), np32(v), clean, ccnt, bs, causal=causal)
+    got = np32(out)
+    assert np.isfinite(got).all()
+    err = np.abs(got - want).max()
+    assert err <= ATOL[dt], f"bs {bs}: max abs error {err}"
+    # lse of head 1 from the token mask of the cleaned lists (a repeated block
+    # contributes its keys twice)
+    qs, ks = np32(q)[0, 1].astype(np.float64), np32(k)[0, 1].astype(np.float64)
+    gl = np32(lse)[0, 1]
+    for i in range(0, Mb, 3):
+        toks = np.concatenate([np.arange(bs * j, min(bs * j + bs, N)) for j in clean[0, 1, i, :ccnt[0, 1, i]]]
+                              + [np.zeros(0, np.int64)])
+        t0, t1 = bs * i, min(bs * i + bs, N)
+        if toks.size == 0:
+            assert np.all(np.isneginf(gl[t0:t1]))
+            continue
+        s = qs[t0:t1] @ ks[toks].T / math.sqrt(D)
+        if causal:
+            s = np.where(toks[None, :] > np.arange(t0, t1)[:, None], -np.inf, s)
+        mx = s.max(1)
+        wl = mx + np.log(np.exp(s - mx[:, None]).sum(1))
+        np.testing.assert_allclose(gl[t0:t1], wl, atol=LSE_ATOL[dt], rtol=1e-4)
+
+
+def test_attention_block_size_256_long_lists(cuda):
+    """Block size 256 with lists long enough that the 64-tile lists exceed
+    the row-pair limit (the one-row executor takes them), sampled rows
+    against the oracle."""
+    from cab_attention.kernels import block_sparse_attention
+    B, H, D, bs = 1, 1, 128, 256
+    N = 256 * 200 - 100
+    Mb = (N + bs - 1) // bs
+    q, k, v = (seeded((B, H, N, D), s, torch.bfloat16) for s in (91, 92, 93))
+    f = np.random.default_rng(5).standard_normal((B, H, Mb, Mb)).astype(np.float32)
+    _, idx, cnt = O.generate_block_mask(f, 0.3, causal=False)
+    assert idx.shape[-1] * 4 > 512
+    out = block_sparse_attention(q.to(cuda), k.to(cuda), v.to(cuda), torch.from_numpy(idx).to(cuda),
+                                 torch.from_numpy(cnt).to(cuda), bs)
+    rows = [0, 1, 77, Mb - 1]
+    want = O.sparse_attention(np32(q), np32(k), np32(v), idx, cnt, bs, query_blocks=rows)
+    got = np32(out)
+    for i in rows:
+        sl = slice(bs * i, min(bs * i + bs, N))
+        assert np.abs(got[0, 0, sl] - want[0, 0, sl]).max() <= ATOL["bf16"]
+
+
+@pytest.mark.parametrize("bs", [32, 128])
+def test_cab_attention_module_block_sizes(cuda, bs):
+    """CABAttention at block sizes 32 and 128: the predictor's lists at that
+    block size drive the executor; the module output matches the oracle's
+    attention over the same lists (and the predictor's mask matches the
+    oracle's selection except at near-ties)."""
+    from cab_attention import CABAttention
+    torch.manual_seed(3)
+    B, N, dim, heads = 1, 2048, 512, 4  # head dim 128
+    m = CABAttention(dim=dim, num_heads=heads, block_size=bs, sparsity=0.75, causal=True).to(cuda)
+    x = torch.randn(B, N, dim, device=cuda)
+    with torch.no_grad():
+        y = m(x)
+        qkv = m.qkv(x).view(B, N, 3, heads, dim // heads)
+        q, k, v = (qkv[:, :, t].transpose(1, 2).contiguous() for t in range(3))
+        idx, cnt = m.predictor.predict_index(q, k)
+    assert idx.shape[2] == (N + bs - 1) // bs
+    o = O.sparse_attention(np32(q), np32(k), np32(v), idx.cpu().numpy(), cnt.cpu().numpy(), bs,
+                           causal=True)
+    o = torch.from_numpy(o).float().transpose(1, 2).reshape(B, N, dim).to(cuda)
+    with torch.no_grad():
+        want = m.proj(o)
+    assert (y.float() - want).abs().max().item() <= ATOL["fp32"] * 10
+
+
 def test_attention_fixed_max_fallback(cuda):
     """A later block whose scores exceed a query's first-block maximum by far
     more than the fixed-maximum walk allows (p up to 2^64): the row is
