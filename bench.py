@@ -48,7 +48,7 @@ METRIC = "predictor ms @N=128k + block-sparse attn TFLOP/s, % of roofline"
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 PEAK_FP32_TFLOPS = 157.3    # MI355X dense fp32 MFMA
-TRAFFIC_FILE = ROOT / "profiles" / "attn_fwd_config4_traffic.md"
+TRAFFIC_FILE = ROOT / "profiles" / "attn_pair_config4_traffic.md"
 
 
 def log(msg: str) -> None:
