@@ -86,5 +86,56 @@ def build(verbose: bool = True) -> pathlib.Path:
     return LIB
 
 
+# Host code under AddressSanitizer and UndefinedBehaviorSanitizer (argument
+# validation, size arithmetic, error strings), for CPU tests of the C ABI.
+# Only host code is instrumented: every -fsanitize= goes through -Xarch_host,
+# and the link passes -fno-gpu-sanitize. The device code is the product's.
+SANITIZE_FLAGS = [
+    "-Xarch_host", "-fsanitize=address",
+    "-Xarch_host", "-fsanitize=undefined",
+    "-Xarch_host", "-fno-sanitize-recover=all",
+    "-fno-omit-frame-pointer", "-g", "-Xarch_device", "-g0",
+]
+
+
+def asan_runtime() -> pathlib.Path:
+    """The clang AddressSanitizer runtime the sanitized library needs preloaded."""
+    llvm = pathlib.Path(_hipcc()).resolve().parent.parent / "llvm" / "lib" / "clang"
+    for cand in sorted(llvm.glob("*/lib/linux/libclang_rt.asan-x86_64.so")):
+        return cand
+    raise RuntimeError(f"no libclang_rt.asan-x86_64.so under {llvm}")
+
+
+def build_host_sanitized(out_dir: pathlib.Path, verbose: bool = False) -> pathlib.Path:
+    """Compile every csrc/*.hip with sanitized host code into out_dir/libcab_hip_asan.so.
+    Load it with asan_runtime() in LD_PRELOAD (see tests/test_host_sanitizers.py)."""
+    hipcc = _hipcc()
+    out_dir = pathlib.Path(out_dir)
+    out_dir.mkdir(parents=True, exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+
+    def compile_one(src: pathlib.Path) -> pathlib.Path:
+        obj = out_dir / (src.stem + ".o")
+        cmd = [hipcc, *HIPCC_FLAGS, "-O1", "-Xarch_device", "-O3", *SANITIZE_FLAGS,
+               *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"sanitized build of {src.name} failed:\n{res.stderr[-4000:]}")
+        return obj
+
+    jobs = min(len(sources), int(os.environ.get("MAX_JOBS", "8")))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(compile_one, sources))
+    lib = out_dir / "libcab_hip_asan.so"
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-fsanitize=address,undefined",
+           "-fno-gpu-sanitize", "-shared-libsan", "-o", str(lib), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("link of libcab_hip_asan.so failed:\n" + res.stderr)
+    if verbose:
+        print(f"built {lib}")
+    return lib
+
+
 if __name__ == "__main__":
     build()

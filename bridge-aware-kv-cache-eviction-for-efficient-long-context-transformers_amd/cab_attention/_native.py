@@ -8,12 +8,16 @@ CPU tensor or an ABI error raises.
 from __future__ import annotations
 
 import ctypes
+import os
 import pathlib
 import threading
 
 import torch
 
-LIB_PATH = pathlib.Path(__file__).resolve().with_name("libcab_hip.so")
+# The in-tree build; CAB_HIP_LIB names another build of the same library (the
+# host-sanitized one that tests/test_host_sanitizers.py runs the ABI checks on).
+LIB_PATH = pathlib.Path(os.environ.get("CAB_HIP_LIB") or
+                        pathlib.Path(__file__).resolve().with_name("libcab_hip.so"))
 ABI_VERSION = 10
 
 CAB_OK, CAB_EINVAL, CAB_EDTYPE, CAB_ESHAPE, CAB_EWORKSPACE, CAB_EHIP = range(6)

@@ -32,16 +32,22 @@
 extern "C" {
 #endif
 
-typedef enum {
+/* Status codes, returned as cab_status_t. */
+enum {
   CAB_OK = 0,
   CAB_EINVAL = 1,     /* bad scalar argument or null pointer */
   CAB_EDTYPE = 2,     /* unsupported element type */
   CAB_ESHAPE = 3,     /* unsupported or inconsistent shape / stride / alignment */
   CAB_EWORKSPACE = 4, /* workspace too small */
   CAB_EHIP = 5        /* HIP runtime error at launch */
-} cab_status_t;
+};
+typedef int32_t cab_status_t;
 
-typedef enum { CAB_F32 = 0, CAB_F16 = 1, CAB_BF16 = 2 } cab_dtype_t;
+/* Element types, passed as cab_dtype_t. Both are plain 32-bit integers (an
+ * enum's size and calling convention): any value a caller passes is a defined
+ * value, which the validation rejects with CAB_EDTYPE unless it is one of these. */
+enum { CAB_F32 = 0, CAB_F16 = 1, CAB_BF16 = 2 };
+typedef int32_t cab_dtype_t;
 
 /* Affinity normalisation (experiments/longbench_qa/config.py:466). */
 enum { CAB_NORM_NONE = 0, CAB_NORM_MINMAX = 1 };
