@@ -1002,9 +1002,11 @@ __device__ __forceinline__ void pair_softmax(PairAcc<HD>& s, int r, f32x4 (&sc)[
   }
 }
 
-template <cab_dtype_t DT, int HD>
+template <cab_dtype_t DT, int LIST, int HD>
 __global__ __launch_bounds__(256, 2) void attn_pair_kernel(AttnArgs a) {
   static_assert(DT != CAB_F32, "16-bit inputs only");
+  static_assert(LIST == LIST_LDS || LIST == LIST_DENSE, "lists staged in LDS, or dense");
+  constexpr bool DENSE = LIST == LIST_DENSE;
   using G = Dims<HD>;
   constexpr int NDS = G::NDS, NDT = G::NDT;
   constexpr int TILE_SLOTS = G::TILE_SLOTS, TILE_BYTES = G::TILE_BYTES, NI = G::NI;
@@ -1012,8 +1014,9 @@ __global__ __launch_bounds__(256, 2) void attn_pair_kernel(AttnArgs a) {
   constexpr int TT_BYTES = 16 * G::ROW_BYTES;  // 16 K rows
   constexpr bool BF16 = DT == CAB_BF16;
   __shared__ u32x4 smem[2 * STAGE_SLOTS];  // [stage 0: K, V^T][stage 1: K, V^T]
-  __shared__ int32_t lst[2][PAIR_KMAX];    // each row's valid entries, in list order
-  __shared__ uint32_t uni[2 * PAIR_KMAX];  // the walk: block | TAG_A | TAG_B
+  constexpr int LISTN = DENSE ? 1 : PAIR_KMAX;  // dense rows need no list in LDS
+  __shared__ int32_t lst[2][LISTN];        // each row's valid entries, in list order
+  __shared__ uint32_t uni[2 * LISTN];      // the walk: block | TAG_A | TAG_B
   __shared__ int meta[8];                  // n_A, n_B, sorted_A, sorted_B, U, -, -, -
   __shared__ int wave_bad[4];
   auto stage_k = [&](int st) { return smem + st * STAGE_SLOTS; };
@@ -1026,13 +1029,15 @@ __global__ __launch_bounds__(256, 2) void attn_pair_kernel(AttnArgs a) {
   const int pr = MP - 1 - (logical - bh * MP);  // longest causal pairs first
   const int irow[2] = {2 * pr, 2 * pr + 1};     // irow[1] == M: no second row
   const int b = bh / a.H, hh = bh - (bh / a.H) * a.H;
+  const int hk = hh / a.group;                                  // K / V head
+  const int64_t bhk = static_cast<int64_t>(b) * (a.H / a.group) + hk;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int lane = lane_id(), g = lane >> 4, l16 = lane & 15;
   const float c = a.scale_log2;
 
   const uint16_t* qb = static_cast<const uint16_t*>(a.q) + b * a.qs[0] + hh * a.qs[1];
-  const char* kbytes = reinterpret_cast<const char*>(a.k + b * a.ks[0] + hh * a.ks[1]);
-  const char* vtbytes = reinterpret_cast<const char*>(a.vt) + static_cast<int64_t>(bh) * Mk * TILE_BYTES;
+  const char* kbytes = reinterpret_cast<const char*>(a.k + b * a.ks[0] + hk * a.ks[1]);
+  const char* vtbytes = reinterpret_cast<const char*>(a.vt) + bhk * Mk * TILE_BYTES;
 
   // Queries (issued first; they land while the walk is built).
   PairAcc<HD> st;
@@ -1047,68 +1052,84 @@ __global__ __launch_bounds__(256, 2) void attn_pair_kernel(AttnArgs a) {
   }
   pair_reset<HD>(st, c);
 
-  // The walk. Waves 0 and 1 each compact one row's list (valid entries, in
-  // order) and test it for strict ascent; then each places its row's
-  // entries: merged by rank when both lists ascend, else one after the other.
-  if (w < 2) {
-    const int r = w;
-    int cnt = 0;
-    if (irow[r] < M) {
-      cnt = a.kv_cnt[static_cast<int64_t>(bh) * M + irow[r]];
-      cnt = cnt < 0 ? 0 : (cnt > a.kmax ? a.kmax : cnt);
+  // The walk. Dense rows: key blocks 0 .. dcnt[r] - 1 of each row (up to the
+  // last block holding a key some query of the row sees), so the union is
+  // 0 .. max - 1, tagged arithmetically. Lists: waves 0 and 1 each compact
+  // one row's list (valid entries, in order) and test it for strict ascent;
+  // then each places its row's entries: merged by rank when both lists
+  // ascend, else one after the other.
+  int dcnt[2] = {0, 0};
+  int U = 0;
+  if constexpr (DENSE) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int last = irow[r] * BS + BS - 1 + a.qoff;
+      dcnt[r] = irow[r] >= M ? 0
+                : !a.causal ? Mk
+                            : (last < 0 ? 0 : (last / BS + 1 < Mk ? last / BS + 1 : Mk));
     }
-    const int32_t* gl = a.kv_idx + (static_cast<int64_t>(bh) * M + irow[r]) * a.kmax;
-    int n = 0;
-    for (int base = 0; base < cnt; base += 64) {
-      const int x = base + lane < cnt ? gl[base + lane] : -1;
-      const bool valid = x >= 0 && x < Mk;
-      const uint64_t bal = ballot64(valid);
-      if (valid) lst[r][n + static_cast<int>(rank_below64(bal))] = x;
-      n += __popcll(bal);
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's list writes landed
-    bool asc = true;
-    for (int base = 0; base + 1 < n; base += 64) {
-      const int i = base + lane;
-      const bool ok = i + 1 >= n || lst[r][i] < lst[r][i + 1 < n ? i + 1 : i];
-      asc = asc && ballot64(!ok) == 0;
-    }
-    if (lane == 0) {
-      meta[r] = n;
-      meta[2 + r] = asc ? 1 : 0;
-    }
-  }
-  __syncthreads();
-  const int nrow[2] = {meta[0], meta[1]};
-  const bool merge = meta[2] != 0 && meta[3] != 0;
-  if (w < 2) {
-    const int r = w, n = nrow[r], no = nrow[r ^ 1];
-    const int32_t* other = lst[r ^ 1];
-    const uint32_t tag = r == 0 ? TAG_A : TAG_B;
-    int common = 0;  // entries of this row below the chunk that the other row keeps too
-    for (int base = 0; base < n; base += 64) {
-      const int i = base + lane;
-      const int x = i < n ? lst[r][i] : 0;
-      int pos = r == 0 ? i : nrow[0] + i;
-      bool shared = false;
-      if (merge) {
-        int lo = 0, hi = no;  // lower bound of x in the other row's list
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if (other[mid] < x) lo = mid + 1; else hi = mid;
-        }
-        shared = lo < no && other[lo] == x;
-        const uint64_t sb = ballot64(i < n && shared);
-        pos = i + lo - common - static_cast<int>(rank_below64(sb));
-        common += __popcll(sb);
+    U = dcnt[0] > dcnt[1] ? dcnt[0] : dcnt[1];
+  } else {
+    if (w < 2) {
+      const int r = w;
+      int cnt = 0;
+      if (irow[r] < M) {
+        cnt = a.kv_cnt[static_cast<int64_t>(bh) * M + irow[r]];
+        cnt = cnt < 0 ? 0 : (cnt > a.kmax ? a.kmax : cnt);
       }
-      if (i < n && !(r == 1 && shared))
-        uni[pos] = static_cast<uint32_t>(x) | tag | (shared ? TAG_B : 0u);
+      const int32_t* gl = a.kv_idx + (static_cast<int64_t>(bh) * M + irow[r]) * a.kmax;
+      int n = 0;
+      for (int base = 0; base < cnt; base += 64) {
+        const int x = base + lane < cnt ? gl[base + lane] : -1;
+        const bool valid = x >= 0 && x < Mk;
+        const uint64_t bal = ballot64(valid);
+        if (valid) lst[r][n + static_cast<int>(rank_below64(bal))] = x;
+        n += __popcll(bal);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's list writes landed
+      bool asc = true;
+      for (int base = 0; base + 1 < n; base += 64) {
+        const int i = base + lane;
+        const bool ok = i + 1 >= n || lst[r][i] < lst[r][i + 1 < n ? i + 1 : i];
+        asc = asc && ballot64(!ok) == 0;
+      }
+      if (lane == 0) {
+        meta[r] = n;
+        meta[2 + r] = asc ? 1 : 0;
+      }
     }
-    if (r == 0 && lane == 0) meta[4] = nrow[0] + nrow[1] - (merge ? common : 0);
+    __syncthreads();
+    const int nrow[2] = {meta[0], meta[1]};
+    const bool merge = meta[2] != 0 && meta[3] != 0;
+    if (w < 2) {
+      const int r = w, n = nrow[r], no = nrow[r ^ 1];
+      const int32_t* other = lst[r ^ 1];
+      const uint32_t tag = r == 0 ? TAG_A : TAG_B;
+      int common = 0;  // entries of this row below the chunk that the other row keeps too
+      for (int base = 0; base < n; base += 64) {
+        const int i = base + lane;
+        const int x = i < n ? lst[r][i] : 0;
+        int pos = r == 0 ? i : nrow[0] + i;
+        bool shared = false;
+        if (merge) {
+          int lo = 0, hi = no;  // lower bound of x in the other row's list
+          while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (other[mid] < x) lo = mid + 1; else hi = mid;
+          }
+          shared = lo < no && other[lo] == x;
+          const uint64_t sb = ballot64(i < n && shared);
+          pos = i + lo - common - static_cast<int>(rank_below64(sb));
+          common += __popcll(sb);
+        }
+        if (i < n && !(r == 1 && shared))
+          uni[pos] = static_cast<uint32_t>(x) | tag | (shared ? TAG_B : 0u);
+      }
+      if (r == 0 && lane == 0) meta[4] = nrow[0] + nrow[1] - (merge ? common : 0);
+    }
+    __syncthreads();
+    U = meta[4];
   }
-  __syncthreads();
-  const int U = meta[4];
 
   // Staging (as in attn_fwd_kernel): wave w fetches its NI KB of K rows and
   // of the V^T tile of a block, one 1 KB buffer load each.
@@ -1238,7 +1259,12 @@ __global__ __launch_bounds__(256, 2) void attn_pair_kernel(AttnArgs a) {
 
   auto walk = [&](auto fast_tag) {
     bool mset[2] = {false, false};
-    auto ent = [&](int u) { return __builtin_amdgcn_readfirstlane(uni[u]); };
+    auto ent = [&](int u) -> uint32_t {
+      if constexpr (DENSE)
+        return static_cast<uint32_t>(u) | (u < dcnt[0] ? TAG_A : 0u) | (u < dcnt[1] ? TAG_B : 0u);
+      else
+        return __builtin_amdgcn_readfirstlane(uni[u]);
+    };
     uint32_t e = ent(0);
     {
       const int j0 = static_cast<int>(e & TAG_BLOCK);
@@ -1792,19 +1818,25 @@ cab_status_t launch_attn(const char* fn, const void* q, const void* k, const voi
   a.causal = causal ? 1 : 0;
   a.submask = submask;
   a.sub_shift = sub_shift;
-  if (g.list == LIST_LDS && dtype != CAB_F32 && g.H == g.Hkv && g.qoff == 0 &&
-      kmax <= PAIR_KMAX && submask == nullptr && pair_enabled()) {
+  if (dtype != CAB_F32 && submask == nullptr && pair_enabled() &&
+      ((g.list == LIST_LDS && kmax <= PAIR_KMAX) || g.list == LIST_DENSE)) {
     const dim3 pgrid(static_cast<unsigned>(g.B * g.H * ((M + 1) / 2)));
+    auto go = [&](auto dt_tag, auto hd_tag) {
+      constexpr cab_dtype_t DT = decltype(dt_tag)::value;
+      constexpr int HD = decltype(hd_tag)::value;
+      if (g.list == LIST_DENSE)
+        attn_pair_kernel<DT, LIST_DENSE, HD><<<pgrid, 256, 0, s>>>(a);
+      else
+        attn_pair_kernel<DT, LIST_LDS, HD><<<pgrid, 256, 0, s>>>(a);
+    };
+    using BF = std::integral_constant<cab_dtype_t, CAB_BF16>;
+    using FH = std::integral_constant<cab_dtype_t, CAB_F16>;
+    using D64 = std::integral_constant<int, 64>;
+    using D128 = std::integral_constant<int, 128>;
     if (g.D == 64) {
-      if (dtype == CAB_BF16)
-        attn_pair_kernel<CAB_BF16, 64><<<pgrid, 256, 0, s>>>(a);
-      else
-        attn_pair_kernel<CAB_F16, 64><<<pgrid, 256, 0, s>>>(a);
+      if (dtype == CAB_BF16) go(BF{}, D64{}); else go(FH{}, D64{});
     } else {
-      if (dtype == CAB_BF16)
-        attn_pair_kernel<CAB_BF16, 128><<<pgrid, 256, 0, s>>>(a);
-      else
-        attn_pair_kernel<CAB_F16, 128><<<pgrid, 256, 0, s>>>(a);
+      if (dtype == CAB_BF16) go(BF{}, D128{}); else go(FH{}, D128{});
     }
     return launch_status(fn);
   }
