@@ -1600,17 +1600,24 @@ __global__ __launch_bounds__(64 * NW) void key_score_kernel(KeyScoreArgs a) {
     const int t0 = 16 * tile + 4 * g;
     const bool edge = 16 * tile + 15 >= a.Nq || (j + 1) * BS > a.Nk ||
                       (a.causal && j * BS + BS - 1 > 16 * tile + a.qoff);
+    // Two loops behind one uniform branch: written as one loop with the
+    // edge test inside, the compiler branched around every element.
+    if (!edge) {
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      const int key = j * BS + 16 * kt + l16;
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][r], c, nl[r]));
-        if (edge) {
+        for (int r = 0; r < 4; ++r) colsum[kt] += __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][r], c, nl[r]));
+    } else {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const int key = j * BS + 16 * kt + l16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
           const int t = t0 + r;
-          if (t >= a.Nq || key >= a.Nk || (a.causal && key > t + a.qoff)) p = 0.f;
+          const bool drop = t >= a.Nq || key >= a.Nk || (a.causal && key > t + a.qoff);
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][r], c, nl[r]));
+          colsum[kt] += drop ? 0.f : p;
         }
-        colsum[kt] += p;
       }
     }
   };
