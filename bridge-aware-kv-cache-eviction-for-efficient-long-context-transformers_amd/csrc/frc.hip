@@ -1109,6 +1109,62 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
   const int64_t ib = ti * TI + wi * (TI / WI) + 4 * half;
   const int64_t jb = tj * TJ + wj * (TJ / WJ) + (lane & 31);
   const size_t obase = static_cast<size_t>(bh) * a.M * a.M;
+  // Fused additive form: the accumulator is F. Stores go through a buffer
+  // descriptor over this (b, h)'s F with 32-bit byte offsets (M <= 32767, so
+  // M^2 4 < 2^32; M = 32768 takes the general epilogue), so an element
+  // outside the M x M matrix (the padded rows and columns of edge tiles) takes
+  // an offset past the range, which the hardware drops: no branch per element.
+  auto epilogue_fused = [&]() {
+    const uint64_t fbytes = static_cast<uint64_t>(a.M) * static_cast<uint64_t>(a.M) * 4u;
+    // The base and size through readfirstlane: computed through 64-bit
+    // divisions, they would otherwise be taken for divergent, and every store
+    // wrapped in a loop over the lanes' descriptors.
+    auto uni = [](uint32_t x) {
+      return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x)));
+    };
+    const uint64_t fb = reinterpret_cast<uint64_t>(a.frc + obase);
+    float* const fbase = reinterpret_cast<float*>((static_cast<uint64_t>(uni(static_cast<uint32_t>(fb >> 32))) << 32) |
+                                                  uni(static_cast<uint32_t>(fb)));
+    const brsrc_t frs = make_rsrc(fbase, uni(static_cast<uint32_t>(fbytes)));
+    constexpr uint32_t DROP = 0xffffffffu;
+    const uint32_t m = static_cast<uint32_t>(a.M), rstep = 4u * m;
+    if (constant) {  // uniform: a constant A's F = c - lambda M c^2 everywhere
+      const float fconst = cval - a.lambda * (static_cast<float>(a.M) * cval * cval);
+#pragma unroll
+      for (int x = 0; x < XS; ++x)
+#pragma unroll
+        for (int y = 0; y < YS; ++y)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[x][y][e] = fconst;
+    }
+    // Whole tiles (every edge tile's padded rows and columns aside) store
+    // without a range test; edge tiles send the padding past the range.
+    auto store_all = [&](auto full_tag) {
+      constexpr bool FULL = decltype(full_tag)::value;
+#pragma unroll
+      for (int y = 0; y < YS; ++y) {
+        const uint32_t j = static_cast<uint32_t>(jb + y * 32);
+#pragma unroll
+        for (int x = 0; x < XS; ++x) {
+          const uint32_t i0 = static_cast<uint32_t>(ib + x * 32);
+          const uint32_t base = 4u * (i0 * m + j);  // wraps only for rows or columns past M
+          const uint32_t rows_left = j < m && i0 < m ? m - i0 : 0u;  // rows r < rows_left are in M
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const uint32_t r = 8 * (e >> 2) + (e & 3);
+            const float f = __builtin_isfinite(acc[x][y][e]) ? acc[x][y][e] : 0.f;
+            uint32_t off = base + r * rstep;
+            if constexpr (!FULL) off = r < rows_left ? off : DROP;
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, f), frs, off, 0u, 0);
+          }
+        }
+      }
+    };
+    if ((ti + 1) * TI <= a.M && (tj + 1) * TJ <= a.M)
+      store_all(std::true_type{});
+    else
+      store_all(std::false_type{});
+  };
   auto epilogue = [&](auto form_tag) {
     constexpr int FORM = decltype(form_tag)::value;
     constexpr bool FUSED = FORM < 0;  // F = X (I - lambda X) accumulated directly
@@ -1163,7 +1219,9 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
       }
     }
   };
-  if (a.fused)
+  if (a.fused && a.M <= 32767)  // M^2 4 bytes within the 32-bit offsets
+    epilogue_fused();
+  else if (a.fused)
     epilogue(std::integral_constant<int, -1>{});
   else if (a.formula == CAB_FRC_ADDITIVE)
     epilogue(std::integral_constant<int, CAB_FRC_ADDITIVE>{});
