@@ -373,6 +373,25 @@ def token_frc_section(args, dev):
     }
 
 
+def reference_gemm(dev, kern_tflops, n=8192, iters=20):
+    """torch.matmul on bf16 [n, n] x [n, n] (the vendor GEMM library PyTorch
+    ships), event-timed: what a dense MFMA workload reaches on this box."""
+    import torch
+    a = torch.randn(n, n, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(n, n, device=dev, dtype=torch.bfloat16)
+    f = lambda: torch.matmul(a, b)
+    for _ in range(3):
+        f()
+    ms = time_events(f, iters)
+    tf = 2 * n ** 3 / (ms * 1e-3) / 1e12
+    del a, b
+    torch.cuda.empty_cache()
+    log(f"reference GEMM bf16 {n}^3: {ms:.3f} ms = {tf:.1f} TFLOP/s")
+    return {"config": f"torch.matmul bf16 [{n}, {n}] x [{n}, {n}] (hipBLASLt), {iters} event-timed calls",
+            "ms": round(ms, 4), "TFLOPs": round(tf, 1), "frac_of_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+            "executor_kernel_over_gemm": round(kern_tflops / tf, 4)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -634,6 +653,11 @@ def main() -> int:
                          f"{secs:.1f} s)",
                "host_cpu_count": os.cpu_count(), "host_cpu_model": cpu_model()}
 
+    # The practical dense-MFMA ceiling of this box under the same sustained
+    # load: torch's own bf16 GEMM (hipBLASLt), for context beside the
+    # executor's roofline fraction. Not part of the measured path.
+    result_gemm = reference_gemm(dev, kern_tflops)
+
     traffic = read_traffic()
     line = {
         "metric": METRIC,
@@ -663,6 +687,7 @@ def main() -> int:
         "fp32_executor": result_fp32,
         "eviction_path": result_evict,
         "token_frc": result_tfrc,
+        "reference_gemm": result_gemm,
     }
     print(json.dumps(line), flush=True)
     return 0
