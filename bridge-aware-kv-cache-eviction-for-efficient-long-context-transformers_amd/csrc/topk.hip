@@ -238,41 +238,47 @@ __device__ __forceinline__ uint32_t kth_key_reg(const uint32_t (&key)[NCH], int6
   need_eq = 0;
   eq_total = 0;
   if (need <= 0) return 0u;
-  uint32_t kand = 0xffffffffu, kor = 0u;
+  // The smallest and the largest candidate key: every candidate lies between
+  // them, so the bits above the highest bit where the two differ are shared
+  // by all. KEY_NONE never decides the minimum, and KEY_NONE + 1 wraps to 0,
+  // so it never decides the maximum of key + 1 (need > 0: a candidate exists).
+  uint32_t kmin = 0xffffffffu, kmax1 = 0u;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    kand &= key[c];
-    kor |= key[c] != KEY_NONE ? key[c] : 0u;
+    kmin = min(kmin, key[c]);
+    kmax1 = max(kmax1, key[c] + 1u);
   }
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
-    kand &= static_cast<uint32_t>(__shfl_xor(static_cast<int>(kand), off, 64));
-    kor |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(kor), off, 64));
+    kmin = min(kmin, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmin), off, 64)));
+    kmax1 = max(kmax1, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmax1), off, 64)));
   }
-  const uint32_t diff = kand ^ kor;
+  const uint32_t diff = kmin ^ (kmax1 - 1u);
   if (diff == 0u) {  // every candidate holds the same key
     need_eq = need;
     eq_total = 0xffffffffu;  // unknown: the caller ranks the ties
-    return kand;
+    return kmin;
   }
   int hb = 31 - __builtin_clz(diff);          // highest bit where candidates differ
   uint32_t pmask = ~((2u << hb) - 1u);        // the bits above it (none for hb = 31)
-  uint32_t prefix = kand & pmask;
+  uint32_t prefix = kmin & pmask;
   int64_t rem = need;
   bool first = true;
   char* hp = reinterpret_cast<char*>(hist) + (lane % HSUB_REG) * HSTRIDE * 4;
   while (hb >= 0) {  // at most four windows
     const int lo = hb >= 7 ? hb - 7 : 0;
+    const uint32_t wbits = static_cast<uint32_t>(hb - lo + 1);
     const uint32_t wmask = (2u << (hb - lo)) - 1u;
     wave_sync();  // the previous pass's reads are done
 #pragma unroll
     for (int q = 0; q < HSUB_REG; ++q)
       *reinterpret_cast<u32x4*>(hist + q * HSTRIDE + 4 * lane) = u32x4{0u, 0u, 0u, 0u};
     wave_sync();
+    // Bin of key k: its bits lo .. hb (one bit-field extract).
+    auto bin_of = [&](uint32_t k) { return __builtin_amdgcn_ubfe(k, static_cast<uint32_t>(lo), wbits); };
     if (first) {
 #pragma unroll
-      for (int c = 0; c < NCH; ++c)
-        atomicAdd(reinterpret_cast<uint32_t*>(hp + (((key[c] >> lo) & wmask) << 2)), 1u);
+      for (int c = 0; c < NCH; ++c) atomicAdd(reinterpret_cast<uint32_t*>(hp + (bin_of(key[c]) << 2)), 1u);
     } else {
       // After the first window few keys still match the prefix: a chunk with
       // no matching lane (a uniform branch) skips its LDS atomic.
@@ -281,7 +287,7 @@ __device__ __forceinline__ uint32_t kth_key_reg(const uint32_t (&key)[NCH], int6
         const uint32_t kc = key[c];
         const bool m = (kc & pmask) == prefix;
         if (ballot64(m) != 0u)
-          atomicAdd(reinterpret_cast<uint32_t*>(hp + (((kc >> lo) & wmask) << 2)), m ? 1u : 0u);
+          atomicAdd(reinterpret_cast<uint32_t*>(hp + (bin_of(kc) << 2)), m ? 1u : 0u);
       }
     }
     first = false;
@@ -348,13 +354,14 @@ __device__ __forceinline__ uint32_t rank_below(uint64_t m) {
                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
 }
 
-// Order key of the score bits u (see order_key), branch-free.
-__device__ __forceinline__ uint32_t order_key_bits(uint32_t u, uint32_t flip) {
-  const uint32_t mag = u & 0x7fffffffu;
-  u = mag == 0u ? 0u : u;                     // -0 == +0
-  u = mag > 0x7f800000u ? 0x7fc00000u : u;    // one NaN, above +inf
-  u ^= static_cast<uint32_t>(static_cast<int32_t>(u) >> 31) | 0x80000000u;
-  return u ^ flip;
+// Order key of the score bits u (see order_key), branch-free: -0 becomes +0
+// through an fp32 add of +0 (fp32 denormals are kept, so no other value
+// changes), every NaN the one NaN above +inf.
+__device__ __forceinline__ uint32_t order_key_f(uint32_t u, uint32_t flip) {
+  const float f = __uint_as_float(u) + 0.0f;
+  uint32_t v = __builtin_isnan(f) ? 0x7fc00000u : __float_as_uint(f);
+  v ^= static_cast<uint32_t>(static_cast<int32_t>(v) >> 31) | 0x80000000u;
+  return v ^ flip;
 }
 
 template <int NCH, bool HYB>
@@ -374,20 +381,30 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t hist_all[4][HSUB_REG * HSTRIDE];
   uint32_t* hist = hist_all[wv];
 
-  // Lane l holds column j = 64 c + l of chunk c. Column j is a candidate when
-  // j < ncand (c < climit) and it is not the forced diagonal; the rest get
-  // KEY_NONE. The row is read through a buffer descriptor (columns past M
-  // read as zero and are no candidates), all NCH loads in flight together.
-  // The whole byte offset 4 (64 c + lane) goes in the per-lane offset (the
-  // compiler folds 256 c into the instruction's immediate): the descriptor's
-  // range check covers the per-lane offset plus the immediate, while a
-  // scalar offset is not range-checked on gfx9, so chunks past M must not
-  // be addressed through it.
-  const int climit = static_cast<int>((ncand - lane + 63) >> 6);
-  // dcl: the chunk holding the forced diagonal on its lane, -1 on the other
-  // lanes (one compare per chunk, no per-chunk masks kept across passes).
-  const int dcl = kd && lane == static_cast<int>(i & 63) ? static_cast<int>(i >> 6) : -1;
-  auto is_cand = [&](int c) { return c < climit && c != dcl; };
+  // Lane l holds column j = 64 c + l of chunk c. The row is read through a
+  // buffer descriptor (columns past M read as zero), all NCH loads in flight
+  // together. The whole byte offset 4 (64 c + lane) goes in the per-lane
+  // offset (the compiler folds 256 c into the instruction's immediate): the
+  // descriptor's range check covers the per-lane offset plus the immediate,
+  // while a scalar offset is not range-checked on gfx9, so chunks past M
+  // must not be addressed through it.
+  // Non-candidates (columns j >= ncand and the forced diagonal) carry
+  // KEY_NONE. Only the chunk holding the limit compares lanes, the chunks
+  // past it hold no candidate, and only the diagonal's chunk marks a lane;
+  // these chunk indices are the same for every lane, so marking is a few
+  // register-indexed moves after the mapping instead of a test per chunk.
+  const int lim = static_cast<int>(ncand);
+  const int cl = lim >> 6;                               // the chunk holding the limit
+  const int dch = static_cast<int>(i >> 6);              // the diagonal's chunk
+  const bool dlane = lane == static_cast<int>(i & 63);   // and lane
+  auto mark = [&](uint32_t (&kk)[NCH]) {
+    if (cl < NCH) {
+      kk[cl] = lane < lim - 64 * cl ? kk[cl] : KEY_NONE;
+#pragma nounroll
+      for (int c = cl + 1; c < NCH; ++c) kk[c] = KEY_NONE;
+    }
+    if (kd) kk[dch] = dlane ? KEY_NONE : kk[dch];
+  };
   const brsrc_t frs = make_rsrc(a.frc + row * a.M, static_cast<uint32_t>(a.M * 4));
   uint32_t key[NCH];
   {
@@ -396,8 +413,8 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
     for (int c = 0; c < NCH; ++c)
       u[c] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(frs, 4u * (64u * c + lane), 0u, 0));
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)  // branch-free: KEY_NONE is all ones
-      key[c] = order_key_bits(u[c], flip) | (is_cand(c) ? 0u : KEY_NONE);
+    for (int c = 0; c < NCH; ++c) key[c] = order_key_f(u[c], flip);
+    mark(key);
   }
 
   // Hybrid: the need_m candidates of highest magnitude first (bit c of msel
@@ -416,7 +433,8 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
       for (int c = 0; c < NCH; ++c)
         u[c] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(mrs, 4u * (64u * c + lane), 0u, 0));
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) mkey[c] = is_cand(c) ? order_key_bits(u[c], 0xffffffffu) : KEY_NONE;
+      for (int c = 0; c < NCH; ++c) mkey[c] = order_key_f(u[c], 0xffffffffu);
+      mark(mkey);
     }
     int64_t meq = 0;
     uint32_t mtot = 0;
@@ -448,6 +466,9 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   // with nothing to store passes an offset past the buffer, which the
   // hardware drops (as it drops dense columns past M), so the stores need no
   // branches and no 64-bit addresses.
+  // The forced diagonal takes key 0, below every real key (order_key_f
+  // never returns 0), so the selection tests below keep it.
+  if (kd) key[dch] = dlane ? 0u : key[dch];
   uint32_t pos = 0;
   int32_t* out = a.kv_idx + row * a.k;
   const brsrc_t ors = make_rsrc(out, static_cast<uint32_t>(a.k * 4));
@@ -464,9 +485,9 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   if (need_f <= 0 || need_eq == static_cast<int64_t>(eq_total)) {
     // Every key equal to theta is kept: a key is selected iff it is at most
     // theta (KEY_NONE ranks above every real theta).
-    const bool any = need_f > 0;
+    const uint32_t th = need_f > 0 ? theta : 0u;  // nothing but the diagonal when no candidate is kept
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) emit(c, (any && key[c] <= theta) || (HYB && taken(c)) || c == dcl);
+    for (int c = 0; c < NCH; ++c) emit(c, key[c] <= th || (HYB && taken(c)));
   } else {
     int64_t eq_seen = 0;
 #pragma unroll
@@ -475,7 +496,7 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
       const bool eq = cand && key[c] == theta;
       const uint64_t eqb = ballot64(eq);
       const int64_t eq_rank = eq_seen + rank_below(eqb);
-      emit(c, (cand && key[c] < theta) || (eq && eq_rank < need_eq) || (HYB && taken(c)) || c == dcl);
+      emit(c, (cand && key[c] < theta) || (eq && eq_rank < need_eq) || (HYB && taken(c)));
       eq_seen += __popcll(eqb);
     }
   }
