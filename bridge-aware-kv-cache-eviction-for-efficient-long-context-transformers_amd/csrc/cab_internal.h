@@ -158,6 +158,9 @@ __device__ __forceinline__ brsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
                                            static_cast<int>(bytes), 0x00020000);
 }
+// Cache-policy operand of the buffer load / store builtins on gfx950: the
+// non-temporal hint, for data written once and not read back soon.
+constexpr int CPOL_NT = 2;
 __device__ __forceinline__ void bdma16(brsrc_t r, uint32_t voff, uint32_t soff, char* l) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)l, 16, voff, soff, 0, 0);
 }

@@ -1109,7 +1109,9 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
   const int64_t ib = ti * TI + wi * (TI / WI) + 4 * half;
   const int64_t jb = tj * TJ + wj * (TJ / WJ) + (lane & 31);
   const size_t obase = static_cast<size_t>(bh) * a.M * a.M;
-  // Fused additive form: the accumulator is F. Stores go through a buffer
+  // Fused additive form: the accumulator is F. F is written once and read
+  // once, by the block selection, so its stores carry the non-temporal
+  // hint (FRC stage 4 % faster at config 3). Stores go through a buffer
   // descriptor over this (b, h)'s F with 32-bit byte offsets (M <= 32767, so
   // M^2 4 < 2^32; M = 32768 takes the general epilogue), so an element
   // outside the M x M matrix (the padded rows and columns of edge tiles) takes
@@ -1155,7 +1157,7 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
             const float f = __builtin_isfinite(acc[x][y][e]) ? acc[x][y][e] : 0.f;
             uint32_t off = base + r * rstep;
             if constexpr (!FULL) off = r < rows_left ? off : DROP;
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, f), frs, off, 0u, 0);
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, f), frs, off, 0u, CPOL_NT);
           }
         }
       }
