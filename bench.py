@@ -296,7 +296,7 @@ def eviction_prune(args, dev, importance, k_layer):
     the kept positions (cab_kv_gather), priced as HBM bytes moved."""
     import torch
     from cab_attention.eviction._select import BRIDGE_MEDIAN, select_positions
-    from cab_attention.cache.prune import gather_positions
+    from cab_attention.cache.prune import gather_into, gather_positions
     iters = max(5, args.steps)
 
     def budgets(n):
@@ -314,21 +314,27 @@ def eviction_prune(args, dev, importance, k_layer):
     sel_big_ms = time_events(lambda: sel(big_scores, big), iters)
     layers = 32
     tensors = [k_layer + i for i in range(2 * layers)]  # distinct K / V buffers
-    gather_positions(tensors, keep)
-    g_ms = time_events(lambda: gather_positions(tensors, keep), iters)
+    # the store's prune path: rows gathered into the spare buffers it owns
+    # (gather_positions, which allocates its outputs, is timed beside it)
+    outs = gather_positions(tensors, keep)
+    g_ms = time_events(lambda: gather_into(tensors, outs, keep, n, validate=False), iters)
+    g_alloc_ms = time_events(lambda: gather_positions(tensors, keep), iters)
     B, H, _, D = k_layer.shape
     moved = 2 * len(tensors) * B * H * keep.numel() * D * k_layer.element_size()
     gbs = moved / (g_ms * 1e-3) / 1e9
     log(f"eviction prune: select {sel_ms * 1e3:.1f} us (N={n}), {sel_big_ms * 1e3:.1f} us "
-        f"(N={big}); gather {g_ms * 1e3:.1f} us = {gbs:.0f} GB/s")
-    del tensors, big_scores
+        f"(N={big}); gather {g_ms * 1e3:.1f} us = {gbs:.0f} GB/s "
+        f"({g_alloc_ms * 1e3:.1f} us with output allocation)")
+    del tensors, big_scores, outs
     return {
         "select_config": f"cab_evict_select: keep {keep.numel()} of {n} (local/importance/"
                          f"bridge = {cnt}), median bridges, fp32 scores",
         "select_us": round(sel_ms * 1e3, 2),
         "select_us_at_2e20_positions": round(sel_big_ms * 1e3, 2),
         "gather_config": f"cab_kv_gather: {2 * layers} tensors [{B}, {H}, {n}, {D}] bf16 -> "
-                         f"{keep.numel()} positions",
+                         f"{keep.numel()} positions, into preallocated buffers (the store's "
+                         f"prune path)",
+        "gather_us_with_allocation": round(g_alloc_ms * 1e3, 2),
         "gather_us": round(g_ms * 1e3, 2),
         "gather_GBs": round(gbs, 1),
         "gather_frac_hbm": round(gbs / 8000.0, 4),
