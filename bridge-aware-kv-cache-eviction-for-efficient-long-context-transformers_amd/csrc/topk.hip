@@ -3,16 +3,18 @@
 // One wave64 per FRC row. The row's M scores are read once (coalesced, lane l
 // holds columns j = 64 c + l, through a buffer descriptor: no per-lane 64-bit
 // addresses, columns past M read as zero) and mapped branch-free to
-// order-preserving uint32 keys in registers, non-candidates to a sentinel.
+// order-preserving uint32 keys in registers (NaN scores in a second pass run
+// only for rows holding one), non-candidates to a sentinel.
 // The k-th smallest key is found by a radix select (8-bit digit windows
 // from the highest bit where two candidates differ, a 256-bin LDS histogram
-// per wave with four copies per bin, a wave-wide prefix scan, ending early at
-// a bin of one key). A last pass in ascending j keeps every key below the
-// threshold and the first (in j) keys equal to it -- when every key equal to
-// the threshold is kept, simply every key at most the threshold -- assigns
-// output slots with v_mbcnt over the selection mask, and writes the compact
-// ascending index list and, optionally, the dense 0/1 row through buffer
-// stores.
+// per wave with four copies per bin, a wave-wide DPP prefix scan, the bin
+// chosen in scalar registers, ending early at a bin of one key, whose largest
+// value then serves as the threshold). A last pass in ascending j keeps every
+// key below the threshold and the first (in j) keys equal to it -- when every
+// key equal to the threshold is kept, simply every key at most the threshold
+// -- assigns output slots with v_mbcnt over the selection mask, and writes the
+// compact ascending index list and, optionally, the dense 0/1 row through
+// buffer stores.
 //
 // Hybrid selection (cab_block_topk_hybrid) first runs the same search on
 // the row's magnitude keys for its magnitude quota, marks those blocks taken,
@@ -231,9 +233,49 @@ __device__ __forceinline__ uint32_t kth_key(Key key, Cand is_cand, int nch, int6
 constexpr int HSTRIDE = 260;
 constexpr int HSUB_REG = 4;  // copies per bin (fewer copies: more waves per CU fit the LDS)
 
+// Inclusive prefix sum over the 64 lanes of a wave: DPP row shifts by 1, 2,
+// 4 and 8 within each row of 16 lanes, then row_bcast:15 (a row's last lane
+// added to the next row, rows 1 and 3) and row_bcast:31 (lane 31 added to
+// rows 2 and 3). Lanes whose source is outside the row or whose row is
+// masked off add the old value 0. No LDS round trips.
+template <int CTRL, int ROW_MASK, int OLD>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(OLD, static_cast<int>(v), CTRL, ROW_MASK, 0xf, false));
+}
+__device__ __forceinline__ uint32_t wave_incl_sum(uint32_t x) {
+  x += dpp_u32<0x111, 0xf, 0>(x);  // row_shr:1
+  x += dpp_u32<0x112, 0xf, 0>(x);  // row_shr:2
+  x += dpp_u32<0x114, 0xf, 0>(x);  // row_shr:4
+  x += dpp_u32<0x118, 0xf, 0>(x);  // row_shr:8
+  x += dpp_u32<0x142, 0xa, 0>(x);  // row_bcast:15
+  x += dpp_u32<0x143, 0xc, 0>(x);  // row_bcast:31
+  return x;
+}
+
+// Wave-wide minimum (MAX false) or maximum of x, uniform: DPP row shifts by
+// 1, 2, 4 and 8 leave each row's result in its lane 15 (a lane whose source
+// is outside its row takes the identity), and the four rows' values are read
+// into scalars.
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_min_max(uint32_t x) {
+  constexpr int ID = MAX ? 0 : -1;
+  auto op = [](uint32_t a, uint32_t b) { return MAX ? max(a, b) : min(a, b); };
+  x = op(x, dpp_u32<0x111, 0xf, ID>(x));
+  x = op(x, dpp_u32<0x112, 0xf, ID>(x));
+  x = op(x, dpp_u32<0x114, 0xf, ID>(x));
+  x = op(x, dpp_u32<0x118, 0xf, ID>(x));
+  auto rl = [&](int l) { return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), l)); };
+  return op(op(rl(15), rl(31)), op(rl(47), rl(63)));
+}
+
+// The threshold it returns need not be a key of the row: when the search ends
+// at a bin holding a single key, it returns the largest key value of that bin
+// (the bin's prefix with every lower bit set), which selects the same keys by
+// "at most theta" (the bin's one key and everything below it) and equals no
+// other key; eq_total and need_eq are then 1. need is at most 64 NCH.
 template <int NCH>
-__device__ __forceinline__ uint32_t kth_key_reg(const uint32_t (&key)[NCH], int64_t need,
-                                                int64_t& need_eq, uint32_t& eq_total, uint32_t* hist) {
+__device__ __forceinline__ uint32_t kth_key_reg(const uint32_t (&key)[NCH], int32_t need,
+                                                int32_t& need_eq, uint32_t& eq_total, uint32_t* hist) {
   const int lane = lane_id();
   need_eq = 0;
   eq_total = 0;
@@ -248,11 +290,8 @@ __device__ __forceinline__ uint32_t kth_key_reg(const uint32_t (&key)[NCH], int6
     kmin = min(kmin, key[c]);
     kmax1 = max(kmax1, key[c] + 1u);
   }
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    kmin = min(kmin, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmin), off, 64)));
-    kmax1 = max(kmax1, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmax1), off, 64)));
-  }
+  kmin = wave_min_max<false>(kmin);
+  kmax1 = wave_min_max<true>(kmax1);
   const uint32_t diff = kmin ^ (kmax1 - 1u);
   if (diff == 0u) {  // every candidate holds the same key
     need_eq = need;
@@ -262,7 +301,7 @@ __device__ __forceinline__ uint32_t kth_key_reg(const uint32_t (&key)[NCH], int6
   int hb = 31 - __builtin_clz(diff);          // highest bit where candidates differ
   uint32_t pmask = ~((2u << hb) - 1u);        // the bits above it (none for hb = 31)
   uint32_t prefix = kmin & pmask;
-  int64_t rem = need;
+  int32_t rem = need;
   bool first = true;
   char* hp = reinterpret_cast<char*>(hist) + (lane % HSUB_REG) * HSTRIDE * 4;
   while (hb >= 0) {  // at most four windows
@@ -280,14 +319,13 @@ __device__ __forceinline__ uint32_t kth_key_reg(const uint32_t (&key)[NCH], int6
 #pragma unroll
       for (int c = 0; c < NCH; ++c) atomicAdd(reinterpret_cast<uint32_t*>(hp + (bin_of(key[c]) << 2)), 1u);
     } else {
-      // After the first window few keys still match the prefix: a chunk with
-      // no matching lane (a uniform branch) skips its LDS atomic.
+      // After the first window few keys still match the prefix: only the
+      // matching lanes add (exec-masked), and a chunk with none skips the
+      // atomic altogether.
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
         const uint32_t kc = key[c];
-        const bool m = (kc & pmask) == prefix;
-        if (ballot64(m) != 0u)
-          atomicAdd(reinterpret_cast<uint32_t*>(hp + (bin_of(kc) << 2)), m ? 1u : 0u);
+        if ((kc & pmask) == prefix) atomicAdd(reinterpret_cast<uint32_t*>(hp + (bin_of(kc) << 2)), 1u);
       }
     }
     first = false;
@@ -302,45 +340,32 @@ __device__ __forceinline__ uint32_t kth_key_reg(const uint32_t (&key)[NCH], int6
       hv[3] += x[3];
     }
     const uint32_t mine = hv[0] + hv[1] + hv[2] + hv[3];
-    uint32_t incl = mine;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const uint32_t up = __shfl_up(incl, d, 64);
-      if (lane >= d) incl += up;
-    }
-    const uint32_t excl = incl - mine;
-    const uint64_t reach = ballot64(static_cast<int64_t>(incl) >= rem);
+    const uint32_t incl = wave_incl_sum(mine);
+    // The first lane whose bins reach rank rem (a uniform index); its four
+    // bin counts and the count below them go to scalars, and the bin is
+    // found there.
+    const uint64_t reach = ballot64(static_cast<int32_t>(incl) >= rem);
     const int src = __builtin_ctzll(reach);
-    uint32_t run = excl, bin = 0u, bcnt = 0u;
-    bool found = false;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (!found && static_cast<int64_t>(run + hv[q]) >= rem) {
-        found = true;
-        bin = 4u * lane + q;
-        bcnt = hv[q];
-      } else if (!found) {
-        run += hv[q];
-      }
-    }
-    const uint32_t sel_bin = __shfl(bin, src, 64);
-    const uint32_t below = __shfl(run, src, 64);
-    const uint32_t sel_cnt = __shfl(bcnt, src, 64);
+    auto from_src = [&](uint32_t v) {
+      return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), src));
+    };
+    int32_t below = static_cast<int32_t>(from_src(incl - mine));
+    const uint32_t h[4] = {from_src(hv[0]), from_src(hv[1]), from_src(hv[2]), from_src(hv[3])};
+    uint32_t q = 0;
+    while (q < 3 && below + static_cast<int32_t>(h[q]) < rem) below += static_cast<int32_t>(h[q++]);
+    const uint32_t sel_bin = 4u * static_cast<uint32_t>(src) + q;
+    const uint32_t sel_cnt = h[q];
     rem -= below;
     prefix |= sel_bin << lo;
     pmask |= wmask << lo;
     eq_total = sel_cnt;
     if (sel_cnt == 1u && lo > 0) {
-      // One candidate left (rem == 1): theta is its key.
-      uint32_t kv = 0u;
-#pragma unroll
-      for (int c = 0; c < NCH; ++c)
-        if ((key[c] & pmask) == prefix && key[c] != KEY_NONE) kv = key[c];
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1)
-        kv |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(kv), off, 64));
-      need_eq = rem;
-      return kv;
+      // One key left in the bin (rem == 1): it is a candidate (a KEY_NONE
+      // key matching the prefix would share its bin), and every key of the
+      // row is either below the bin, the bin's one key, or above the bin's
+      // largest value.
+      need_eq = 1;
+      return prefix | ((1u << lo) - 1u);
     }
     hb = lo - 1;
   }
@@ -354,15 +379,25 @@ __device__ __forceinline__ uint32_t rank_below(uint64_t m) {
                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
 }
 
-// Order key of the score bits u (see order_key), branch-free: -0 becomes +0
-// through an fp32 add of +0 (fp32 denormals are kept, so no other value
-// changes), every NaN the one NaN above +inf.
-__device__ __forceinline__ uint32_t order_key_f(uint32_t u, uint32_t flip) {
-  const float f = __uint_as_float(u) + 0.0f;
-  uint32_t v = __builtin_isnan(f) ? 0x7fc00000u : __float_as_uint(f);
-  v ^= static_cast<uint32_t>(static_cast<int32_t>(v) >> 31) | 0x80000000u;
-  return v ^ flip;
+// Order key of the score bits u (see order_key) in three VALU operations,
+// for every score but NaN: f = s x + 0 with s = +1, or s = -1 when the highest
+// scores are wanted (-x orders as x reversed), turns -0 into +0 (fp32
+// denormals are kept, so no other value changes), and the sign-magnitude bits
+// of f become an unsigned order. Non-NaN scores map into [KEY_LO, KEY_HI]
+// (the keys of -inf and +inf), NaN scores outside it; the caller gives NaN
+// scores the key NaN takes in order_key (above +inf, or below -inf when the
+// order is reversed) in a pass that runs only for rows holding a NaN. The
+// keys order the scores exactly as order_key does.
+constexpr uint32_t KEY_LO = 0x007fffffu, KEY_HI = 0xff800000u;
+__device__ __forceinline__ uint32_t order_key_fast(uint32_t u, float s) {
+  const uint32_t v = __float_as_uint(__builtin_fmaf(__uint_as_float(u), s, 0.0f));
+  return v ^ (static_cast<uint32_t>(static_cast<int32_t>(v) >> 31) | 0x80000000u);
 }
+
+template <bool B>
+struct BoolC {
+  static constexpr bool value = B;
+};
 
 template <int NCH, bool HYB>
 __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
@@ -374,10 +409,9 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   const int lane = lane_id();
   const int64_t i = row % a.M;
   const int64_t ncand = a.causal ? i + 1 : a.M;
-  const int64_t krow = min(static_cast<int64_t>(a.k), ncand);
+  const int32_t krow = static_cast<int32_t>(min(static_cast<int64_t>(a.k), ncand));
   const bool kd = a.keep_diagonal != 0;
-  const int64_t need = kd ? krow - 1 : krow;
-  const uint32_t flip = a.select_high ? 0xffffffffu : 0u;
+  const int32_t need = kd ? krow - 1 : krow;
   __shared__ __attribute__((aligned(16))) uint32_t hist_all[4][HSUB_REG * HSTRIDE];
   uint32_t* hist = hist_all[wv];
 
@@ -405,47 +439,54 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
     }
     if (kd) kk[dch] = dlane ? KEY_NONE : kk[dch];
   };
-  const brsrc_t frs = make_rsrc(a.frc + row * a.M, static_cast<uint32_t>(a.M * 4));
-  uint32_t key[NCH];
-  {
+  // Loads a row's scores and maps them to keys (high: the order reversed).
+  // The keys' minimum and maximum show whether any lane holds a NaN; only
+  // then (a uniform branch) do the keys outside [KEY_LO, KEY_HI] take NaN's
+  // key, the one above every other (below every other when reversed).
+  auto load_keys = [&](const float* src, bool high, uint32_t (&kk)[NCH]) {
+    const brsrc_t rs = make_rsrc(src, static_cast<uint32_t>(a.M * 4));
     uint32_t u[NCH];
 #pragma unroll
     for (int c = 0; c < NCH; ++c)
-      u[c] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(frs, 4u * (64u * c + lane), 0u, 0));
+      u[c] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rs, 4u * (64u * c + lane), 0u, 0));
+    const float s = high ? -1.0f : 1.0f;
+    uint32_t kmn = 0xffffffffu, kmx = 0u;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) key[c] = order_key_f(u[c], flip);
-    mark(key);
-  }
+    for (int c = 0; c < NCH; ++c) {
+      kk[c] = order_key_fast(u[c], s);
+      kmn = min(kmn, kk[c]);
+      kmx = max(kmx, kk[c]);
+    }
+    if (ballot64(kmn < KEY_LO || kmx > KEY_HI) != 0u) {
+      const uint32_t nan_key = high ? ~0xffc00000u : 0xffc00000u;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) kk[c] = kk[c] - KEY_LO > KEY_HI - KEY_LO ? nan_key : kk[c];
+    }
+    mark(kk);
+  };
+  uint32_t key[NCH];
+  load_keys(a.frc + row * a.M, a.select_high != 0, key);
 
   // Hybrid: the need_m candidates of highest magnitude first (bit c of msel
   // marks register c of this lane as taken).
   uint64_t msel[(NCH + 63) / 64];
 #pragma unroll
   for (int w = 0; w < (NCH + 63) / 64; ++w) msel[w] = 0;
-  int64_t need_m = 0;
+  int32_t need_m = 0;
   if constexpr (HYB) {
-    need_m = min(static_cast<int64_t>(a.kmag), need);
-    const brsrc_t mrs = make_rsrc(a.mag + row * a.M, static_cast<uint32_t>(a.M * 4));
+    need_m = min(a.kmag, need);
     uint32_t mkey[NCH];
-    {
-      uint32_t u[NCH];
-#pragma unroll
-      for (int c = 0; c < NCH; ++c)
-        u[c] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(mrs, 4u * (64u * c + lane), 0u, 0));
-#pragma unroll
-      for (int c = 0; c < NCH; ++c) mkey[c] = order_key_f(u[c], 0xffffffffu);
-      mark(mkey);
-    }
-    int64_t meq = 0;
+    load_keys(a.mag + row * a.M, true, mkey);
+    int32_t meq = 0;
     uint32_t mtot = 0;
     const uint32_t mtheta = kth_key_reg<NCH>(mkey, need_m, meq, mtot, hist);
-    int64_t eq_seen = 0;
+    int32_t eq_seen = 0;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       const bool cand = mkey[c] != KEY_NONE && need_m > 0;
       const bool eq = cand && mkey[c] == mtheta;
       const uint64_t eqb = ballot64(eq);
-      const int64_t eq_rank = eq_seen + rank_below(eqb);
+      const int32_t eq_rank = eq_seen + static_cast<int32_t>(rank_below(eqb));
       if ((cand && mkey[c] < mtheta) || (eq && eq_rank < meq)) msel[c >> 6] |= 1ull << (c & 63);
       eq_seen += __popcll(eqb);
     }
@@ -457,16 +498,16 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   }
 
   // FRC order for the rest of the row (taken columns now carry KEY_NONE).
-  const int64_t need_f = need - need_m;
-  int64_t need_eq = 0;
+  const int32_t need_f = need - need_m;
+  int32_t need_eq = 0;
   uint32_t eq_total = 0;
   const uint32_t theta = kth_key_reg<NCH>(key, need_f, need_eq, eq_total, hist);
 
-  // The compact list and the dense row go out through buffer stores: a lane
-  // with nothing to store passes an offset past the buffer, which the
-  // hardware drops (as it drops dense columns past M), so the stores need no
-  // branches and no 64-bit addresses.
-  // The forced diagonal takes key 0, below every real key (order_key_f
+  // The compact list goes out through buffer stores from the selected lanes
+  // only (exec-masked: no offset to compute for the others), the dense row
+  // from every lane, through a descriptor that drops columns past M. Output
+  // slots come from v_mbcnt over the selection mask.
+  // The forced diagonal takes key 0, below every real key (order_key_fast
   // never returns 0), so the selection tests below keep it.
   if (kd) key[dch] = dlane ? 0u : key[dch];
   uint32_t pos = 0;
@@ -474,33 +515,42 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   const brsrc_t ors = make_rsrc(out, static_cast<uint32_t>(a.k * 4));
   const bool dense = a.dense != nullptr;
   const brsrc_t drs = make_rsrc(dense ? a.dense + row * a.M : nullptr, dense ? static_cast<uint32_t>(a.M) : 0u);
-  constexpr uint32_t DROP = 0x80000000u;
-  auto emit = [&](int c, bool sel) {
-    const uint64_t selb = ballot64(sel);
-    const uint32_t j = 64u * c + lane;
-    __builtin_amdgcn_raw_buffer_store_b32(j, ors, sel ? 4u * (pos + rank_below(selb)) : DROP, 0u, 0);
-    // the dense row is never read back here: non-temporal stores (4 % faster)
-    if (dense) __builtin_amdgcn_raw_buffer_store_b8(static_cast<unsigned char>(sel ? 1 : 0), drs, j, 0u, CPOL_NT);
-    pos += static_cast<uint32_t>(__popcll(selb));
-  };
-  if (need_f <= 0 || need_eq == static_cast<int64_t>(eq_total)) {
-    // Every key equal to theta is kept: a key is selected iff it is at most
-    // theta (KEY_NONE ranks above every real theta).
-    const uint32_t th = need_f > 0 ? theta : 0u;  // nothing but the diagonal when no candidate is kept
+  // One copy of the output pass with the dense row and one without, so the
+  // choice is one branch instead of one per chunk.
+  auto output_pass = [&](auto dense_c) {
+    constexpr bool DENSE = decltype(dense_c)::value;
+    auto emit = [&](int c, bool sel) {
+      const uint64_t selb = ballot64(sel);
+      const uint32_t j = 64u * c + lane;
+      if (sel) __builtin_amdgcn_raw_buffer_store_b32(j, ors, 4u * (pos + rank_below(selb)), 0u, 0);
+      // the dense row is never read back here: non-temporal stores (4 % faster)
+      if constexpr (DENSE)
+        __builtin_amdgcn_raw_buffer_store_b8(static_cast<unsigned char>(sel ? 1 : 0), drs, j, 0u, CPOL_NT);
+      pos += static_cast<uint32_t>(__popcll(selb));
+    };
+    if (need_f <= 0 || static_cast<uint32_t>(need_eq) == eq_total) {
+      // Every key equal to theta is kept: a key is selected iff it is at most
+      // theta (KEY_NONE ranks above every real theta).
+      const uint32_t th = need_f > 0 ? theta : 0u;  // nothing but the diagonal when no candidate is kept
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) emit(c, key[c] <= th || (HYB && taken(c)));
-  } else {
-    int64_t eq_seen = 0;
+      for (int c = 0; c < NCH; ++c) emit(c, key[c] <= th || (HYB && taken(c)));
+    } else {
+      int32_t eq_seen = 0;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const bool cand = key[c] != KEY_NONE;
-      const bool eq = cand && key[c] == theta;
-      const uint64_t eqb = ballot64(eq);
-      const int64_t eq_rank = eq_seen + rank_below(eqb);
-      emit(c, (cand && key[c] < theta) || (eq && eq_rank < need_eq) || (HYB && taken(c)));
-      eq_seen += __popcll(eqb);
+      for (int c = 0; c < NCH; ++c) {
+        const bool cand = key[c] != KEY_NONE;
+        const bool eq = cand && key[c] == theta;
+        const uint64_t eqb = ballot64(eq);
+        const int32_t eq_rank = eq_seen + static_cast<int32_t>(rank_below(eqb));
+        emit(c, (cand && key[c] < theta) || (eq && eq_rank < need_eq) || (HYB && taken(c)));
+        eq_seen += __popcll(eqb);
+      }
     }
-  }
+  };
+  if (dense)
+    output_pass(BoolC<true>{});
+  else
+    output_pass(BoolC<false>{});
   for (int64_t p = pos + lane; p < a.k; p += 64) out[p] = -1;
   if (lane == 0) a.kv_cnt[row] = static_cast<int32_t>(pos);
 }

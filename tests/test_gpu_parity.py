@@ -522,6 +522,47 @@ def test_topk_nan_inf(cuda):
         np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
 
 
+@pytest.mark.parametrize("M", [100, 2000])
+@pytest.mark.parametrize("flags", [(False, True, False), (True, True, True), (True, False, False)])
+def test_topk_nan_payloads(cuda, M, flags):
+    """Every NaN is one key above +inf (below -inf when the highest scores are
+    kept), whatever its sign and payload: quiet and signalling NaNs of both
+    signs, including the all-ones payloads, scattered over rows of ordinary
+    scores and +-inf, in the FRC and in the magnitude scores (hybrid)."""
+    from cab_attention.kernels import generate_block_index
+    select_high, keep_diag, causal = flags
+    g = torch.Generator().manual_seed(900 + M)
+    f = torch.randint(-20, 20, (1, 2, M, M), generator=g).float()
+    f[0, 1] = torch.randn(M, M, generator=g)
+    bits = f.view(torch.int32)
+    payloads = torch.tensor([0x7FC00000, 0xFFC00000, 0x7FFFFFFF, 0xFFFFFFFF, 0x7F800001,
+                             0xFF800001, 0x7FBFFFFF, 0xFFBFFFFF], dtype=torch.int64)
+    payloads = ((payloads + 2 ** 31) % 2 ** 32 - 2 ** 31).to(torch.int32)  # as int32 bits
+    pick = torch.rand(1, 2, M, M, generator=g)
+    which = torch.randint(0, len(payloads), (1, 2, M, M), generator=g)
+    bits[pick < 0.08] = payloads[which[pick < 0.08]]
+    f[(pick >= 0.08) & (pick < 0.1)] = float("inf")
+    f[(pick >= 0.1) & (pick < 0.12)] = -float("inf")
+    assert torch.isnan(f).float().mean() > 0.05
+    mag = torch.rand(1, 2, M, M, generator=g)
+    mag.view(torch.int32)[pick > 0.95] = payloads[which[pick > 0.95]]
+    for sp in (0.95, 0.5):
+        idx, cnt, mask = generate_block_index(f.to(cuda), sp, select_high=select_high,
+                                              keep_diagonal=keep_diag, causal=causal, dense=True)
+        omask, oidx, ocnt = O.generate_block_mask(f.numpy(), sp, select_high, keep_diag, causal)
+        np.testing.assert_array_equal(cnt.cpu().numpy(), ocnt)
+        np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
+        np.testing.assert_array_equal(mask.cpu().numpy(), omask)
+        idx, cnt, mask = generate_block_index(f.to(cuda), sp, select_high=select_high,
+                                              keep_diagonal=keep_diag, causal=causal, dense=True,
+                                              magnitude_scores=mag.to(cuda), magnitude_ratio=0.5)
+        omask, oidx, ocnt = O.generate_block_mask(f.numpy(), sp, select_high, keep_diag, causal,
+                                                  magnitude_scores=mag.numpy(), magnitude_ratio=0.5)
+        np.testing.assert_array_equal(cnt.cpu().numpy(), ocnt)
+        np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
+        np.testing.assert_array_equal(mask.cpu().numpy(), omask)
+
+
 # ---------------------------------------------------------------------------
 # Predictor end to end: mask identical except near the row threshold
 # ---------------------------------------------------------------------------
