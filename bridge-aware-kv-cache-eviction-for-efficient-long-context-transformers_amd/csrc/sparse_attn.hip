@@ -1521,23 +1521,29 @@ __global__ __launch_bounds__(64 * NW) void key_score_kernel(KeyScoreArgs a) {
   // .. + 3 at 2048 w + 16 L and .. + 4 .. + 7 at 1024 bytes past them); waves
   // w < 4 move lse copy w (one load per tile for waves NDS .. 3); waves
   // 4 .. 7 (NW = 8) stage nothing and read lse copy w % 4.
+  // The loads go through a buffer descriptor per tile (its 16 rows; rows
+  // past N_q read as zero and are masked below), so a lane's offsets are the
+  // same for every tile and the staging costs no vector instructions.
   const bool stager = w < 4;
   const bool qstager = w < NDS;
+  const uint32_t qrow = static_cast<uint32_t>(a.qs[2] * ESZ);  // below 2^27 (host check)
+  const uint32_t q_voff = static_cast<uint32_t>(l16) * qrow + static_cast<uint32_t>((32 * w + 8 * g) * ESZ);
   auto issue = [&](int it) {
     if (!stager) return;
     char* st = ring + (it % KS_STAGES) * KS_STAGE_BYTES;
-    const int q = 16 * tile_of(it) + l16;
-    const int qc = q < a.Nq ? q : a.Nq - 1;  // clamped, masked below
+    const int q0 = 16 * tile_of(it);
+    const uint32_t rows = static_cast<uint32_t>(min(16, a.Nq - q0));
     if (qstager) {
-      const char* src = qb + (qc * a.qs[2] + 32 * w + 8 * g) * ESZ;
+      const brsrc_t qrs = make_rsrc(qb + static_cast<int64_t>(q0) * a.qs[2] * ESZ, rows * qrow);
       if constexpr (F32) {
-        __builtin_amdgcn_global_load_lds(src, (lds_void*)(st + 2048 * w), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(src + 16, (lds_void*)(st + 2048 * w + 1024), 16, 0, 0);
+        bdma16(qrs, q_voff, 0, st + 2048 * w);
+        bdma16(qrs, q_voff + 16u, 0, st + 2048 * w + 1024);
       } else {
-        __builtin_amdgcn_global_load_lds(src, (lds_void*)(st + 1024 * w), 16, 0, 0);
+        bdma16(qrs, q_voff, 0, st + 1024 * w);
       }
     }
-    __builtin_amdgcn_global_load_lds(lb + qc, (lds_void*)(st + QB + 256 * w), 4, 0, 0);
+    const brsrc_t lrs = make_rsrc(lb + q0, 4u * rows);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(lrs, (lds_void*)(st + QB + 256 * w), 4, 4u * l16, 0, 0, 0);
   };
 
   float colsum[4] = {0.f, 0.f, 0.f, 0.f};
@@ -2145,6 +2151,10 @@ extern "C" cab_status_t cab_attn_key_scores(
     if ((st = check_tensor(fn, "q", q, q_strides, esize)) != CAB_OK) return st;
     CAB_REQUIRE(lse != nullptr && reinterpret_cast<uintptr_t>(lse) % 4 == 0, CAB_EINVAL,
                 "%s: lse must be the fp32 [B, H, N_q] rows cab_flash_attn_fwd wrote", fn);
+    // 16 query rows are staged through one buffer descriptor (32-bit offsets).
+    CAB_REQUIRE(q_strides[2] * esize < (int64_t{1} << 27), CAB_ESHAPE,
+                "%s: q token stride of %lld elements exceeds the 2^27-byte limit", fn,
+                (long long)q_strides[2]);
   }
   if ((st = check_tensor(fn, "k", k, k_strides, esize)) != CAB_OK) return st;
   KeyScoreArgs a;

@@ -256,6 +256,10 @@ def test_dense_attention_validation(lib):
     assert sc(lse=None) == nat.CAB_EINVAL
     assert sc(scores=None) == nat.CAB_EINVAL
     assert sc(ss=_s4(8 * 64, 64, 2, 0)) == nat.CAB_ESHAPE
+    # 16 query rows are staged through one buffer descriptor: a token stride
+    # of 2^27 bytes or more (2^26 bf16 elements) is refused
+    assert sc(st=_s4(0, 0, 1 << 26, 1)) == nat.CAB_ESHAPE
+    assert b"2^27" in lib.cab_last_error()
 
 
 def test_eviction_validation(lib):
