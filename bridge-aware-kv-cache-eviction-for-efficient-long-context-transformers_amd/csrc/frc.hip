@@ -1002,18 +1002,40 @@ __global__ __launch_bounds__(WI * WJ * 64, 1) void triangle_kernel(TriArgs a) {
       static_assert(CAH * 256 == HA * CPR && CBH * 256 == HB * CPR, "whole chunks per thread");
       const int gp = wi, tg = threadIdx.x & 255;
       u32x4 pra[CAH], prb[CBH];
+      // Loads through buffer descriptors over the tile's rows (Mp is a
+      // multiple of the tile edge, so every row exists; TI Mp 2 bytes fit 32
+      // bits): a lane's offsets are the same for every slice and the slice's
+      // k offset is the scalar offset, so the loads cost no vector address
+      // arithmetic.
+      // (The bases go through readfirstlane: they are uniform, which the
+      // compiler does not see, and a descriptor it takes for divergent is
+      // wrapped in a loop over the lanes' values.)
+      const uint32_t rowb = static_cast<uint32_t>(a.Mp) * 2u;
+      auto uniform = [](const uint16_t* p) {
+        const uint64_t u = reinterpret_cast<uint64_t>(p);
+        const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(u)));
+        const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(u >> 32)));
+        return reinterpret_cast<const uint16_t*>((static_cast<uint64_t>(hi) << 32) | lo);
+      };
+      const brsrc_t ars = make_rsrc(uniform(pa[0] + ra * a.Mp), static_cast<uint32_t>(TI) * rowb);
+      const brsrc_t brs = make_rsrc(uniform(pb[0] + rb * a.Mp), static_cast<uint32_t>(TJ) * rowb);
+      uint32_t aoff[CAH], boff[CBH];
+#pragma unroll
+      for (int q = 0; q < CAH; ++q) {
+        const int cid = tg + 256 * q, row = gp * HA + cid / CPR, kc = cid % CPR;
+        aoff[q] = static_cast<uint32_t>(row) * rowb + 16u * kc;
+      }
+#pragma unroll
+      for (int q = 0; q < CBH; ++q) {
+        const int cid = tg + 256 * q, row = gp * HB + cid / CPR, kc = cid % CPR;
+        boff[q] = static_cast<uint32_t>(row) * rowb + 16u * kc;
+      }
       auto pload = [&](int kt) {
-        const int64_t k0 = static_cast<int64_t>(kt) * KD;
+        const uint32_t k0b = static_cast<uint32_t>(kt) * (2u * KD);
 #pragma unroll
-        for (int q = 0; q < CAH; ++q) {
-          const int cid = tg + 256 * q, row = gp * HA + cid / CPR, kc = cid % CPR;
-          pra[q] = *reinterpret_cast<const u32x4*>(pa[0] + (ra + row) * a.Mp + k0 + 8 * kc);
-        }
+        for (int q = 0; q < CAH; ++q) pra[q] = __builtin_amdgcn_raw_buffer_load_b128(ars, aoff[q], k0b, 0);
 #pragma unroll
-        for (int q = 0; q < CBH; ++q) {
-          const int cid = tg + 256 * q, row = gp * HB + cid / CPR, kc = cid % CPR;
-          prb[q] = *reinterpret_cast<const u32x4*>(pb[0] + (rb + row) * a.Mp + k0 + 8 * kc);
-        }
+        for (int q = 0; q < CBH; ++q) prb[q] = __builtin_amdgcn_raw_buffer_load_b128(brs, boff[q], k0b, 0);
       };
       auto pstore = [&](int st) {
         u32x4* la = lds + st * STAGE;
