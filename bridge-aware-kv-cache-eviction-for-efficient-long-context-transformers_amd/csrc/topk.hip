@@ -431,13 +431,27 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   const int cl = lim >> 6;                               // the chunk holding the limit
   const int dch = static_cast<int>(i >> 6);              // the diagonal's chunk
   const bool dlane = lane == static_cast<int>(i & 63);   // and lane
+  // Rows of more than 32 chunks mark by a uniform test per chunk instead:
+  // register-indexed access to a longer key array makes the compiler keep the
+  // array in scratch memory.
   auto mark = [&](uint32_t (&kk)[NCH]) {
-    if (cl < NCH) {
-      kk[cl] = lane < lim - 64 * cl ? kk[cl] : KEY_NONE;
+    if constexpr (NCH <= 32) {
+      if (cl < NCH) {
+        kk[cl] = lane < lim - 64 * cl ? kk[cl] : KEY_NONE;
 #pragma nounroll
-      for (int c = cl + 1; c < NCH; ++c) kk[c] = KEY_NONE;
+        for (int c = cl + 1; c < NCH; ++c) kk[c] = KEY_NONE;
+      }
+      if (kd) kk[dch] = dlane ? KEY_NONE : kk[dch];
+    } else {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        if (c > cl)
+          kk[c] = KEY_NONE;
+        else if (c == cl)
+          kk[c] = lane < lim - 64 * cl ? kk[c] : KEY_NONE;
+        if (kd && c == dch) kk[c] = dlane ? KEY_NONE : kk[c];
+      }
     }
-    if (kd) kk[dch] = dlane ? KEY_NONE : kk[dch];
   };
   // Loads a row's scores and maps them to keys (high: the order reversed).
   // The keys' minimum and maximum show whether any lane holds a NaN; only
@@ -509,7 +523,13 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   // slots come from v_mbcnt over the selection mask.
   // The forced diagonal takes key 0, below every real key (order_key_fast
   // never returns 0), so the selection tests below keep it.
-  if (kd) key[dch] = dlane ? 0u : key[dch];
+  if constexpr (NCH <= 32) {
+    if (kd) key[dch] = dlane ? 0u : key[dch];
+  } else {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      if (kd && c == dch) key[c] = dlane ? 0u : key[c];
+  }
   uint32_t pos = 0;
   int32_t* out = a.kv_idx + row * a.k;
   const brsrc_t ors = make_rsrc(out, static_cast<uint32_t>(a.k * 4));

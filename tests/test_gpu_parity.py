@@ -484,6 +484,33 @@ def test_topk_hybrid_bit_exact(cuda, M, ratio, flags):
     assert torch.equal(m2.cpu(), torch.from_numpy(omask))
 
 
+@pytest.mark.parametrize("M", [2100, 4500, 8190])
+def test_topk_register_rows_above_2048(cuda, M):
+    """Rows of 33 .. 128 chunks (the 64- and 128-chunk register kernels,
+    whose chunk marking is a uniform test per chunk): ties, both selection
+    directions, causal rows, and the hybrid quota at one size, bit-exact."""
+    from cab_attention.kernels import generate_block_index
+    g = torch.Generator().manual_seed(M)
+    f = torch.randint(-50, 50, (1, 1, M, M), generator=g).float()
+    for select_high, keep_diag, causal in ((False, True, True), (True, False, False)):
+        idx, cnt, mask = generate_block_index(f.to(cuda), 0.95, select_high=select_high,
+                                              keep_diagonal=keep_diag, causal=causal, dense=True)
+        omask, oidx, ocnt = O.generate_block_mask(f.numpy(), 0.95, select_high, keep_diag, causal)
+        np.testing.assert_array_equal(cnt.cpu().numpy(), ocnt)
+        np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
+        np.testing.assert_array_equal(mask.cpu().numpy(), omask)
+        del mask, omask
+    if M == 4500:
+        mag = torch.randint(0, 10, (1, 1, M, M), generator=g).float()
+        idx, cnt, _ = generate_block_index(f.to(cuda), 0.95, select_high=False, keep_diagonal=True,
+                                           causal=True, magnitude_scores=mag.to(cuda),
+                                           magnitude_ratio=0.5)
+        _, oidx, ocnt = O.generate_block_mask(f.numpy(), 0.95, False, True, True,
+                                              magnitude_scores=mag.numpy(), magnitude_ratio=0.5)
+        np.testing.assert_array_equal(cnt.cpu().numpy(), ocnt)
+        np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
+
+
 @pytest.mark.parametrize("flags", [(False, True, False), (True, False, True)])
 def test_topk_long_rows(cuda, flags):
     """M > 8192 takes the streaming kernel (the row re-read on every pass):
