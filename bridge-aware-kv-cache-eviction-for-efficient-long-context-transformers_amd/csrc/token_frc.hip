@@ -324,7 +324,7 @@ constexpr int GRAM_STAGES = 3;
 // registers) and the waves walk the same column tiles 8 x + [y col_tiles,
 // (y + 1) col_tiles). Each column tile's B operands (hi and lo, 1 KB per
 // k-step and plane) and, in pass 1, its 32 weights are staged once per
-// workgroup into a ring of three LDS stages by global_load_lds, two tiles
+// workgroup into a ring of three LDS stages by buffer loads to LDS, two tiles
 // ahead (the waves split the 2 DK 1 KB loads evenly). Each 32x32 tile of
 // kn kn^T is folded into 16 per-lane row partials (lane l: column l % 32, rows
 // 8 (e / 4) + 4 (l / 32) + e % 4), added over the lanes at the end. A tile
@@ -374,17 +374,30 @@ __global__ __launch_bounds__(64 * GRAM_WAVES) void gram_kernel(GramArgs a) {
 
   const int plane = (w * PER_WAVE) / DK, s0 = (w * PER_WAVE) % DK;
   const u32x4* src_plane = plane == 0 ? a.hi : a.lo;
+  // The loads go through a buffer descriptor per column tile (its DK KB of
+  // one plane; pass 1: its 32 weights), so a lane's offsets are the same for
+  // every tile and the staging costs no vector address arithmetic. The bases
+  // are uniform; readfirstlane lets the compiler see it (a descriptor it
+  // takes for divergent is wrapped in a loop over the lanes' values).
+  auto uniform = [](const void* p) {
+    const uint64_t u = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(u)));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(u >> 32)));
+    return reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  };
   auto issue = [&](int it) {
     const int64_t ct = c0 + it;
     char* st = ring + (it % GRAM_STAGES) * STAGE_BYTES;
+    const brsrc_t prs = make_rsrc(uniform(src_plane + ct * DK * 64), static_cast<uint32_t>(DK * 1024));
 #pragma unroll
     for (int q = 0; q < PER_WAVE; ++q)
-      __builtin_amdgcn_global_load_lds(src_plane + (ct * DK + s0 + q) * 64 + lane,
-                                       (lds_void*)(st + plane * PLANE_BYTES + (s0 + q) * 1024), 16,
-                                       0, 0);
-    if constexpr (PASS == 1)
-      __builtin_amdgcn_global_load_lds(a.w + ct * 32 + (lane & 31),
-                                       (lds_void*)(st + 2 * PLANE_BYTES + 256 * w), 4, 0, 0);
+      bdma16(prs, static_cast<uint32_t>(((s0 + q) * 64 + lane) * 16), 0u,
+             st + plane * PLANE_BYTES + (s0 + q) * 1024);
+    if constexpr (PASS == 1) {
+      const brsrc_t wrs = make_rsrc(uniform(a.w + ct * 32), 128u);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void*)(st + 2 * PLANE_BYTES + 256 * w), 4,
+                                               4u * static_cast<uint32_t>(lane & 31), 0, 0, 0);
+    }
   };
   // Wave 0 adds the waves' column sums of tile it (staged in cbuf[S]).
   auto flush_cols = [&](int it, int S) {
