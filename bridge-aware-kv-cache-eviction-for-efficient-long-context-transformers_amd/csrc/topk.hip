@@ -56,17 +56,9 @@ __device__ __forceinline__ uint32_t order_key(float f, bool high) {
   return high ? ~u : u;
 }
 
-// theta = the need-th smallest key among the candidates (the largest theta
-// with count(key < theta) < need), by a radix select over the key bits, most
-// significant first. Bits every candidate shares (a wave-wide AND / OR) need
-// no pass; from the highest bit where two candidates differ, each pass
-// histograms the next 8 bits of the candidates that match the prefix chosen
-// so far in the wave's LDS histogram, and a wave-wide scan picks the bin
-// where the running count reaches need. A bin
-// holding a single key ends the search: that key is theta. The histogram keeps HSUB interleaved copies of every bin
+// The streaming kernel's histogram keeps HSUB interleaved copies of every bin
 // (lane % HSUB picks one), so that keys of a row that share the digit do not
-// all update one LDS word. Returns in need_eq how many keys equal to theta
-// (the first ones in j order) complete the selection.
+// all update one LDS word.
 constexpr int HSUB = 8;
 // Orders one wave's LDS accesses across its lanes (the histogram is shared
 // by the lanes of a wave; other waves of the workgroup may have exited).
@@ -75,149 +67,14 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_wave_barrier();
 }
 
-// Runs f(c) for the row's chunks c (lane l holds column 64 c + l): NCH
-// chunks unrolled (keys in registers), or nch chunks in a loop when NCH == 0.
-template <int NCH, typename F>
-__device__ __forceinline__ void for_chunks(int nch, F f) {
-  if constexpr (NCH > 0) {
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) f(c);
-  } else {
-#pragma unroll 4
-    for (int c = 0; c < nch; ++c) f(c);
-  }
-}
-
 // A key no real score maps to (order_key never returns all ones): it stands
 // for a column that is not a candidate, so that every candidate ranks below
 // it.
 constexpr uint32_t KEY_NONE = 0xffffffffu;
 
-// key(c) is this lane's key in chunk c: a register, or (NCH == 0) a load.
-// SENT: non-candidates already carry KEY_NONE (is_cand is not consulted), so
-// the histogram passes are branch-free: every key adds 1 to its bin when it
-// matches the prefix and 0 otherwise. A KEY_NONE key that matches the prefix
-// lands above every candidate of its bin and never decides a rank.
-template <int NCH, bool SENT, typename Key, typename Cand>
-__device__ __forceinline__ uint32_t kth_key(Key key, Cand is_cand, int nch, int64_t need,
-                                            int64_t& need_eq, uint32_t* hist) {
-  const int lane = lane_id();
-  need_eq = 0;
-  if (need <= 0) return 0u;
-  uint32_t kand = 0xffffffffu, kor = 0u;
-  for_chunks<NCH>(nch, [&](int c) {
-    if constexpr (SENT) {
-      const uint32_t kc = key(c);
-      kand &= kc;
-      kor |= kc != KEY_NONE ? kc : 0u;
-    } else if (is_cand(c)) {
-      const uint32_t kc = key(c);
-      kand &= kc;
-      kor |= kc;
-    }
-  });
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    kand &= static_cast<uint32_t>(__shfl_xor(static_cast<int>(kand), off, 64));
-    kor |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(kor), off, 64));
-  }
-  const uint32_t diff = kand ^ kor;
-  if (diff == 0u) {  // every candidate holds the same key
-    need_eq = need;
-    return kand;
-  }
-  // Digit windows of 8 bits from the highest bit where two candidates differ
-  // down (the candidates share every bit above it).
-  int hb = 31 - __builtin_clz(diff);
-  uint32_t pmask = ~((2u << hb) - 1u);
-  uint32_t prefix = kand & pmask;
-  int64_t rem = need;  // rank still to find among the keys matching the prefix
-  while (hb >= 0) {  // at most four windows
-    const int lo = hb >= 7 ? hb - 7 : 0;
-    const uint32_t wmask = (2u << (hb - lo)) - 1u;
-    wave_sync();  // the previous pass's reads are done
-    // Layout: 16-byte slot (q, l) at index 64 q + l holds copies 4 (q % 2) .. +3
-    // of bin 4 l + q / 2, so lane l clears and sums its own four bins with
-    // lane-contiguous (conflict-free) 16-byte accesses.
-    u32x4* slots = reinterpret_cast<u32x4*>(hist);
-#pragma unroll
-    for (int q = 0; q < HSUB; ++q) slots[64 * q + lane] = u32x4{0u, 0u, 0u, 0u};
-    wave_sync();
-    const uint32_t sub = static_cast<uint32_t>(lane % HSUB);
-    for_chunks<NCH>(nch, [&](int c) {
-      if constexpr (SENT) {
-        const uint32_t kc = key(c);
-        const uint32_t bn = (kc >> lo) & wmask;
-        const uint32_t q = 2u * (bn & 3u) + (sub >> 2);
-        atomicAdd(&hist[4u * (64u * q + (bn >> 2)) + (sub & 3u)], (kc & pmask) == prefix ? 1u : 0u);
-      } else {
-        if (!is_cand(c)) return;
-        const uint32_t kc = key(c);
-        if ((kc & pmask) == prefix) {
-          const uint32_t bn = (kc >> lo) & wmask;
-          const uint32_t q = 2u * (bn & 3u) + (sub >> 2);
-          atomicAdd(&hist[4u * (64u * q + (bn >> 2)) + (sub & 3u)], 1u);
-        }
-      }
-    });
-    wave_sync();
-    // Bins 4 lane .. 4 lane + 3: inclusive prefix counts across the wave.
-    uint32_t hv[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int q = 0; q < HSUB; ++q) {
-      const u32x4 x = slots[64 * q + lane];
-      hv[q / 2] += x[0] + x[1] + x[2] + x[3];
-    }
-    const uint32_t mine = hv[0] + hv[1] + hv[2] + hv[3];
-    uint32_t incl = mine;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const uint32_t up = __shfl_up(incl, d, 64);
-      if (lane >= d) incl += up;
-    }
-    const uint32_t excl = incl - mine;
-    // First lane whose bins reach rank rem; inside it, the first such bin.
-    const uint64_t reach = ballot64(static_cast<int64_t>(incl) >= rem);
-    const int src = __builtin_ctzll(reach);
-    uint32_t run = excl, bin = 0u, bcnt = 0u;
-    bool found = false;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (!found && static_cast<int64_t>(run + hv[q]) >= rem) {
-        found = true;
-        bin = 4u * lane + q;
-        bcnt = hv[q];
-      } else if (!found) {
-        run += hv[q];
-      }
-    }
-    const uint32_t sel_bin = __shfl(bin, src, 64);
-    const uint32_t below = __shfl(run, src, 64);
-    const uint32_t sel_cnt = __shfl(bcnt, src, 64);
-    rem -= below;
-    prefix |= sel_bin << lo;
-    pmask |= wmask << lo;
-    if (sel_cnt == 1u && lo > 0) {
-      // One candidate left (rem == 1): theta is its key.
-      uint32_t kv = 0u;
-      for_chunks<NCH>(nch, [&](int c) {
-        if (!SENT && !is_cand(c)) return;
-        const uint32_t kc = key(c);
-        if ((kc & pmask) == prefix && (!SENT || kc != KEY_NONE)) kv = kc;
-      });
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1)
-        kv |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(kv), off, 64));
-      prefix = kv;
-      break;
-    }
-    hb = lo - 1;
-  }
-  need_eq = rem;  // keys below theta: need - rem; the rest are ties at theta
-  return prefix;
-}
-
-// Register-path form of kth_key for keys held in registers with KEY_NONE for
+// theta = the need-th smallest key among the candidates (the largest theta
+// with count(key < theta) < need), by a radix select over the key bits, most
+// significant first, for keys held in registers with KEY_NONE for
 // non-candidates. The digit windows are not byte-aligned: the first covers
 // the 8 bits below and at the highest bit where two candidates differ (the
 // candidates share every bit above it), each later one the next 8 bits down,
@@ -228,8 +85,9 @@ __device__ __forceinline__ uint32_t kth_key(Key key, Cand is_cand, int nch, int6
 // 64 == 4), and lane l clears and sums bins 4 l .. 4 l + 3 of a copy with one
 // 16-byte access. The first pass counts every key (a KEY_NONE key lands in the
 // top bin, after every candidate of that bin: it is the largest key); later
-// passes count the keys matching the prefix. eq_total returns how many keys
-// equal theta.
+// passes count the keys matching the prefix. need_eq returns how many keys
+// equal to theta (the first ones in j order) complete the selection,
+// eq_total how many keys equal theta.
 constexpr int HSTRIDE = 260;
 constexpr int HSUB_REG = 4;  // copies per bin (fewer copies: more waves per CU fit the LDS)
 
@@ -364,6 +222,93 @@ __device__ __forceinline__ uint32_t kth_key_reg(const uint32_t (&key)[NCH], int3
       // key matching the prefix would share its bin), and every key of the
       // row is either below the bin, the bin's one key, or above the bin's
       // largest value.
+      need_eq = 1;
+      return prefix | ((1u << lo) - 1u);
+    }
+    hb = lo - 1;
+  }
+  need_eq = rem;  // keys below theta: need - rem; the rest are ties at theta
+  return prefix;
+}
+
+// kth_key_reg's search for rows read again from memory on every pass
+// (topk_stream_kernel): key(c) loads this lane's key of chunk c and
+// is_cand(c) tells whether it is a candidate. The candidates' minimum and
+// maximum fix the bits they share; each window of 8 bits from the highest bit
+// where two differ is counted in the wave's LDS histogram (HSUB copies per
+// bin: 16-byte slot (q, l) at index 64 q + l holds copies 4 (q % 2) .. +3 of
+// bin 4 l + q / 2, so lane l clears and sums its own four bins with
+// lane-contiguous accesses), a DPP scan and scalar registers pick the bin,
+// and a bin holding a single candidate ends the search with the bin's
+// largest value as theta, as in kth_key_reg. need_eq returns how many keys
+// equal to theta (the first ones in j order) complete the selection.
+template <typename Key, typename Cand>
+__device__ __forceinline__ uint32_t kth_key_stream(Key key, Cand is_cand, int nch, int32_t need,
+                                                   int32_t& need_eq, uint32_t* hist) {
+  const int lane = lane_id();
+  need_eq = 0;
+  if (need <= 0) return 0u;
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
+#pragma unroll 4
+  for (int c = 0; c < nch; ++c) {
+    if (!is_cand(c)) continue;
+    const uint32_t kc = key(c);
+    kmin = min(kmin, kc);
+    kmax = max(kmax, kc);
+  }
+  kmin = wave_min_max<false>(kmin);
+  kmax = wave_min_max<true>(kmax);
+  const uint32_t diff = kmin ^ kmax;
+  if (diff == 0u) {  // every candidate holds the same key
+    need_eq = need;
+    return kmin;
+  }
+  int hb = 31 - __builtin_clz(diff);
+  uint32_t pmask = ~((2u << hb) - 1u);
+  uint32_t prefix = kmin & pmask;
+  int32_t rem = need;  // rank still to find among the keys matching the prefix
+  u32x4* slots = reinterpret_cast<u32x4*>(hist);
+  const uint32_t sub = static_cast<uint32_t>(lane % HSUB);
+  while (hb >= 0) {  // at most four windows
+    const int lo = hb >= 7 ? hb - 7 : 0;
+    const uint32_t wmask = (2u << (hb - lo)) - 1u;
+    wave_sync();  // the previous pass's reads are done
+#pragma unroll
+    for (int q = 0; q < HSUB; ++q) slots[64 * q + lane] = u32x4{0u, 0u, 0u, 0u};
+    wave_sync();
+#pragma unroll 4
+    for (int c = 0; c < nch; ++c) {
+      if (!is_cand(c)) continue;
+      const uint32_t kc = key(c);
+      if ((kc & pmask) == prefix) {
+        const uint32_t bn = (kc >> lo) & wmask;
+        const uint32_t q = 2u * (bn & 3u) + (sub >> 2);
+        atomicAdd(&hist[4u * (64u * q + (bn >> 2)) + (sub & 3u)], 1u);
+      }
+    }
+    wave_sync();
+    uint32_t hv[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int q = 0; q < HSUB; ++q) {
+      const u32x4 x = slots[64 * q + lane];
+      hv[q / 2] += x[0] + x[1] + x[2] + x[3];
+    }
+    const uint32_t mine = hv[0] + hv[1] + hv[2] + hv[3];
+    const uint32_t incl = wave_incl_sum(mine);
+    const uint64_t reach = ballot64(static_cast<int32_t>(incl) >= rem);
+    const int src = __builtin_ctzll(reach);
+    auto from_src = [&](uint32_t v) {
+      return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), src));
+    };
+    int32_t below = static_cast<int32_t>(from_src(incl - mine));
+    const uint32_t h[4] = {from_src(hv[0]), from_src(hv[1]), from_src(hv[2]), from_src(hv[3])};
+    uint32_t q = 0;
+    while (q < 3 && below + static_cast<int32_t>(h[q]) < rem) below += static_cast<int32_t>(h[q++]);
+    const uint32_t sel_cnt = h[q];
+    rem -= below;
+    prefix |= (4u * static_cast<uint32_t>(src) + q) << lo;
+    pmask |= wmask << lo;
+    if (sel_cnt == 1u && lo > 0) {  // one candidate left in the bin (rem == 1)
       need_eq = 1;
       return prefix | ((1u << lo) - 1u);
     }
@@ -590,11 +535,9 @@ __global__ __launch_bounds__(256) void topk_stream_kernel(TopkArgs a) {
   const int lane = lane_id();
   const int64_t i = row % a.M;
   const int64_t ncand = a.causal ? i + 1 : a.M;
-  const int64_t krow = min(static_cast<int64_t>(a.k), ncand);
+  const int32_t krow = static_cast<int32_t>(min(static_cast<int64_t>(a.k), ncand));
   const bool kd = a.keep_diagonal != 0;
-  const int64_t need = kd ? krow - 1 : krow;
-  const float* f = a.frc + row * a.M;
-  const float* mg = HYB ? a.mag + row * a.M : nullptr;
+  const int32_t need = kd ? krow - 1 : krow;
   const bool high = a.select_high != 0;
   const uint64_t lt_mask = lanemask_lt();
   __shared__ __attribute__((aligned(16))) uint32_t hist_all[4][256 * HSUB];
@@ -605,28 +548,36 @@ __global__ __launch_bounds__(256) void topk_stream_kernel(TopkArgs a) {
     const int j = 64 * c + lane;
     return j < ncand_i && !(kd && j == i_i);
   };
-  auto fkey = [&](int c) {
-    const int j = 64 * c + lane;
-    return j < Mi ? order_key(f[j], high) : 0xffffffffu;
+  // Keys through one buffer descriptor per row (columns past M read as zero;
+  // they are never candidates), by the three-instruction map; a key outside
+  // [KEY_LO, KEY_HI] comes from a NaN score and takes NaN's key (the row is
+  // not held, so every load is tested).
+  auto load_key = [&](const brsrc_t& rs, int c, float sgn, uint32_t nan_key) {
+    const uint32_t u = static_cast<uint32_t>(
+        __builtin_amdgcn_raw_buffer_load_b32(rs, 4u * (64u * c + lane), 0u, 0));
+    const uint32_t kk = order_key_fast(u, sgn);
+    return kk - KEY_LO > KEY_HI - KEY_LO ? nan_key : kk;
   };
-  auto mkey = [&](int c) {
-    const int j = 64 * c + lane;
-    return j < Mi ? order_key(mg[j], true) : 0xffffffffu;
-  };
+  const brsrc_t frs = make_rsrc(a.frc + row * a.M, static_cast<uint32_t>(a.M * 4));
+  const float fsgn = high ? -1.0f : 1.0f;
+  const uint32_t fnan = high ? ~0xffc00000u : 0xffc00000u;
+  auto fkey = [&](int c) { return load_key(frs, c, fsgn, fnan); };
+  const brsrc_t mrs = make_rsrc(HYB ? a.mag + row * a.M : nullptr, HYB ? static_cast<uint32_t>(a.M * 4) : 0u);
+  auto mkey = [&](int c) { return load_key(mrs, c, -1.0f, ~0xffc00000u); };
 
-  int64_t need_m = 0;
+  int32_t need_m = 0;
   uint32_t mtheta = 0u;
   int jm_last = -1;  // the last tie at mtheta (in j) the quota keeps
   if constexpr (HYB) {
-    need_m = min(static_cast<int64_t>(a.kmag), need);
-    int64_t meq = 0;
-    mtheta = kth_key<0, false>(mkey, is_cand, nch, need_m, meq, hist);
+    need_m = min(a.kmag, need);
+    int32_t meq = 0;
+    mtheta = kth_key_stream(mkey, is_cand, nch, need_m, meq, hist);
     if (need_m > 0 && meq > 0) {
-      int64_t seen = 0;
+      int32_t seen = 0;
       for (int c = 0; c < nch && jm_last < 0; ++c) {  // uniform: ballots only
         const bool eq = is_cand(c) && mkey(c) == mtheta;
         const uint64_t eqb = ballot64(eq);
-        const int64_t r = meq - 1 - seen;  // its rank among this chunk's ties
+        const int32_t r = meq - 1 - seen;  // its rank among this chunk's ties
         if (r < __popcll(eqb)) {
           const uint64_t hit = ballot64(eq && __popcll(eqb & lt_mask) == r);
           jm_last = 64 * c + __builtin_ctzll(hit);
@@ -642,25 +593,31 @@ __global__ __launch_bounds__(256) void topk_stream_kernel(TopkArgs a) {
   };
   auto is_cand_f = [&](int c) { return is_cand(c) && !taken(c); };
 
-  const int64_t need_f = need - need_m;
-  int64_t need_eq = 0;
-  const uint32_t theta = kth_key<0, false>(fkey, is_cand_f, nch, need_f, need_eq, hist);
+  const int32_t need_f = need - need_m;
+  int32_t need_eq = 0;
+  const uint32_t theta = kth_key_stream(fkey, is_cand_f, nch, need_f, need_eq, hist);
 
-  int64_t pos = 0, eq_seen = 0;
+  // Output as in topk_kernel: list stores from the selected lanes, the dense
+  // row through a descriptor that drops columns past M.
+  uint32_t pos = 0;
+  int32_t eq_seen = 0;
   int32_t* out = a.kv_idx + row * a.k;
+  const brsrc_t ors = make_rsrc(out, static_cast<uint32_t>(a.k * 4));
+  const bool dense = a.dense != nullptr;
+  const brsrc_t drs = make_rsrc(dense ? a.dense + row * a.M : nullptr, dense ? static_cast<uint32_t>(a.M) : 0u);
   for (int c = 0; c < nch; ++c) {
-    const int j = 64 * c + lane;
+    const uint32_t j = 64u * c + lane;
     const bool tk = taken(c);
     const bool cand = need_f > 0 && is_cand(c) && !tk;
-    const uint32_t kc = cand ? fkey(c) : 0xffffffffu;
+    const uint32_t kc = cand ? fkey(c) : KEY_NONE;
     const bool eq = cand && kc == theta;
     const uint64_t eqb = ballot64(eq);
-    const int64_t eq_rank = eq_seen + __popcll(eqb & lt_mask);
-    const bool sel = (cand && kc < theta) || (eq && eq_rank < need_eq) || tk || (kd && j == i_i);
+    const int32_t eq_rank = eq_seen + static_cast<int32_t>(rank_below(eqb));
+    const bool sel = (cand && kc < theta) || (eq && eq_rank < need_eq) || tk || (kd && static_cast<int>(j) == i_i);
     const uint64_t selb = ballot64(sel);
-    if (sel) out[pos + __popcll(selb & lt_mask)] = j;
-    if (a.dense && j < Mi) a.dense[row * a.M + j] = sel ? 1 : 0;
-    pos += __popcll(selb);
+    if (sel) __builtin_amdgcn_raw_buffer_store_b32(j, ors, 4u * (pos + rank_below(selb)), 0u, 0);
+    if (dense) __builtin_amdgcn_raw_buffer_store_b8(static_cast<unsigned char>(sel ? 1 : 0), drs, j, 0u, CPOL_NT);
+    pos += static_cast<uint32_t>(__popcll(selb));
     eq_seen += __popcll(eqb);
   }
   for (int64_t p = pos + lane; p < a.k; p += 64) out[p] = -1;

@@ -484,6 +484,32 @@ def test_topk_hybrid_bit_exact(cuda, M, ratio, flags):
     assert torch.equal(m2.cpu(), torch.from_numpy(omask))
 
 
+def test_topk_stream_nan_payloads(cuda):
+    """M = 8200 (the streaming kernel, which tests every load for NaN): NaNs of
+    both signs and assorted payloads beside +-inf in the FRC and magnitude
+    scores, with the hybrid quota, causal, bit-exact."""
+    from cab_attention.kernels import generate_block_index
+    M = 8200
+    g = torch.Generator().manual_seed(8201)
+    f = torch.randint(-30, 30, (1, 1, M, M), generator=g).float()
+    payloads = torch.tensor([0x7FC00000, 0xFFC00000, 0x7FFFFFFF, 0xFFFFFFFF, 0x7F800001,
+                             0xFF800001], dtype=torch.int64)
+    payloads = ((payloads + 2 ** 31) % 2 ** 32 - 2 ** 31).to(torch.int32)
+    pick = torch.rand(1, 1, M, M, generator=g)
+    which = torch.randint(0, len(payloads), (1, 1, M, M), generator=g)
+    f.view(torch.int32)[pick < 0.05] = payloads[which[pick < 0.05]]
+    f[(pick >= 0.05) & (pick < 0.06)] = float("inf")
+    mag = torch.randint(0, 10, (1, 1, M, M), generator=g).float()
+    mag.view(torch.int32)[pick > 0.97] = payloads[which[pick > 0.97]]
+    idx, cnt, _ = generate_block_index(f.to(cuda), 0.95, select_high=False, keep_diagonal=True,
+                                       causal=True, magnitude_scores=mag.to(cuda),
+                                       magnitude_ratio=0.5)
+    _, oidx, ocnt = O.generate_block_mask(f.numpy(), 0.95, False, True, True,
+                                          magnitude_scores=mag.numpy(), magnitude_ratio=0.5)
+    np.testing.assert_array_equal(cnt.cpu().numpy(), ocnt)
+    np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
+
+
 @pytest.mark.parametrize("M", [2100, 4500, 8190])
 def test_topk_register_rows_above_2048(cuda, M):
     """Rows of 33 .. 128 chunks (the 64- and 128-chunk register kernels,
