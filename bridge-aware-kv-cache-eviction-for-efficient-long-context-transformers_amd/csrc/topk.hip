@@ -46,16 +46,6 @@ struct TopkArgs {
   int select_high, keep_diagonal, causal;
 };
 
-// Ascending key order == selection order: float order with -0 == +0 and NaN
-// above +inf, inverted when the highest scores are wanted.
-__device__ __forceinline__ uint32_t order_key(float f, bool high) {
-  uint32_t u = __float_as_uint(f);
-  if (f == 0.f) u = 0u;
-  if (isnan(f)) u = 0x7fc00000u;
-  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return high ? ~u : u;
-}
-
 // The streaming kernel's histogram keeps HSUB interleaved copies of every bin
 // (lane % HSUB picks one), so that keys of a row that share the digit do not
 // all update one LDS word.
@@ -67,7 +57,7 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_wave_barrier();
 }
 
-// A key no real score maps to (order_key never returns all ones): it stands
+// A key no real score maps to (order_key_fast never returns all ones): it stands
 // for a column that is not a candidate, so that every candidate ranks below
 // it.
 constexpr uint32_t KEY_NONE = 0xffffffffu;
@@ -324,15 +314,16 @@ __device__ __forceinline__ uint32_t rank_below(uint64_t m) {
                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
 }
 
-// Order key of the score bits u (see order_key) in three VALU operations,
-// for every score but NaN: f = s x + 0 with s = +1, or s = -1 when the highest
-// scores are wanted (-x orders as x reversed), turns -0 into +0 (fp32
-// denormals are kept, so no other value changes), and the sign-magnitude bits
-// of f become an unsigned order. Non-NaN scores map into [KEY_LO, KEY_HI]
-// (the keys of -inf and +inf), NaN scores outside it; the caller gives NaN
-// scores the key NaN takes in order_key (above +inf, or below -inf when the
-// order is reversed) in a pass that runs only for rows holding a NaN. The
-// keys order the scores exactly as order_key does.
+// Order key of the score bits u: ascending key order is the selection order,
+// float order with -0 == +0 and NaN above +inf, inverted when the highest
+// scores are wanted. Three VALU operations for every score but NaN: f = s x +
+// 0 with s = +1, or s = -1 when the highest scores are wanted (-x orders as x
+// reversed), turns -0 into +0 (fp32 denormals are kept, so no other value
+// changes), and the sign-magnitude bits of f become an unsigned order.
+// Non-NaN scores map into [KEY_LO, KEY_HI] (the keys of -inf and +inf), NaN
+// scores outside it; the caller gives NaN scores their own key, 0xffc00000
+// (the quiet NaN's bits as an unsigned order, above +inf) or its complement
+// when the order is reversed.
 constexpr uint32_t KEY_LO = 0x007fffffu, KEY_HI = 0xff800000u;
 __device__ __forceinline__ uint32_t order_key_fast(uint32_t u, float s) {
   const uint32_t v = __float_as_uint(__builtin_fmaf(__uint_as_float(u), s, 0.0f));
